@@ -1,0 +1,113 @@
+// Shared helpers for the SignRot gfx950 kernels and the C-ABI entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/signrot_hip.h"
+
+typedef _Float16 f16;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef unsigned int u32;
+
+#define SRQ_DEV __device__ __forceinline__
+
+// ----------------------------------------------------------- error reporting
+// The entry points never throw: they return an SRQ_E* code and leave a
+// message retrievable with srq_last_error() (thread-local).
+void srq_set_error(const char *fmt, ...);
+
+#define SRQ_CHECK_ARG(cond, ...)                                   \
+    do {                                                           \
+        if (!(cond)) {                                             \
+            srq_set_error(__VA_ARGS__);                            \
+            return SRQ_EINVAL;                                     \
+        }                                                          \
+    } while (0)
+
+#define SRQ_LAUNCH_CHECK(name)                                     \
+    do {                                                           \
+        hipError_t _e = hipGetLastError();                         \
+        if (_e != hipSuccess) {                                    \
+            srq_set_error("%s: launch failed: %s", name,           \
+                          hipGetErrorString(_e));                  \
+            return SRQ_ELAUNCH;                                    \
+        }                                                          \
+    } while (0)
+
+static inline bool srq_aligned(const void *p, size_t a) {
+    return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+static inline int64_t srq_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------------------ wave helpers
+SRQ_DEV float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+SRQ_DEV float wave_min(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+SRQ_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Reduction over a group of G consecutive lanes (G a power of two <= 64).
+template <int G>
+SRQ_DEV float group_max(float v) {
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int G>
+SRQ_DEV float group_min(float v) {
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+template <int G>
+SRQ_DEV float group_sum(float v) {
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ---------------------------------------------------------- int4 semantics
+// Symmetric code of one fp16 value given the fp16 scale, as the reference's
+// quantizers define it: q = clamp(round_half_even(fp16(x / s)), -8, 7), where
+// the fp16 quotient is the correctly rounded one (an IEEE fp32 division
+// rounded to fp16 is correctly rounded: 24 >= 2*11 + 2), NaN (0/0 on an
+// all-zero row) gives 0 and ±inf saturates.
+SRQ_DEV int sym_code(float x, float s) {
+    float quot = (float)(f16)(x / s);
+    float r = __builtin_rintf(quot);
+    if (r != r) return 0;
+    r = fminf(fmaxf(r, -8.f), 7.f);
+    return (int)r;
+}
+
+// Unsigned asymmetric KV code: clamp(round_half_even(fp16(fp16(x + z) / s)), 0, 15).
+SRQ_DEV int kv_code(float x, float zero, float scale) {
+    float shifted = (float)(f16)(x + zero);
+    float scaled = (float)(f16)(shifted / scale);
+    float r = __builtin_rintf(scaled);
+    if (r != r) return 0;
+    r = fminf(fmaxf(r, 0.f), 15.f);
+    return (int)r;
+}

@@ -1,0 +1,446 @@
+// Online Hadamard rotation for gfx950: Walsh-Hadamard transform of a 2^k
+// block (Sylvester order), the Kronecker factor hadK for n = K * 2^k, the
+// SignRot ±1 sign, and -- in the fused variant -- the per-token symmetric
+// int4 quantizer, all in one pass over HBM.
+//
+// Reference semantics (signrot/functional/hadamard.py:78-87,
+// signrot/nn/hadamard.py:26-42): y = fp16(FWHT_{n/K}(chunk) / sqrt(n)) per
+// chunk of the [K, n/K] view, out = fp16(hadK @ y), out *= sign.  With
+// fp32_had (OnlineHadamard(force_fp32=True)) both intermediate roundings are
+// skipped and the result is rounded to fp16 once at the end.
+//
+// Design: one block owns whole rows.  The row is staged once in LDS as
+// fp32; the FWHT runs as radix-16 passes (16 values per thread in
+// registers, 4 butterfly stages per pass, one LDS round trip per pass); the
+// first pass reads HBM directly.  The K-mix keeps one column of the [K, n/K]
+// view per thread in registers.  The result leaves LDS with coalesced
+// vector stores (fp16 out) or goes straight into the quantizer (fused).
+#include "common.h"
+
+#include <math.h>
+
+namespace {
+
+constexpr int kThreads = 256;
+
+struct RotArgs {
+    const void *x;
+    void *out;          // rotation output (mode 0)
+    int64_t rows;
+    int n;              // row length
+    int m;              // FWHT size = n / K
+    int K;              // Kronecker factor (1 = none)
+    const void *hadK;   // [K, K] f16 (or f32 when fp32_had)
+    const int8_t *sign; // [n] or null
+    float scale;        // fp32(1/sqrt(n)) or the caller's scale
+    int io_f32;         // input/output are fp32 (hadamard_transform dtype 1)
+    int fp32_had;       // keep fp32 between the two rotation stages
+    float clip;         // quant mode
+    uint32_t *q;        // quant mode: packed codes [rows, n/2] as u32 words
+    f16 *qscale;        // quant mode: [rows]
+    int rpb;            // rows per block
+};
+
+SRQ_DEV float round16(float v) { return (float)(f16)v; }
+
+template <int R>
+SRQ_DEV void fwht_regs(float (&v)[R]) {
+#pragma unroll
+    for (int h = 1; h < R; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            if (!(i & h)) {
+                const float a = v[i], b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+        }
+    }
+}
+
+// One radix-R pass over `total` LDS floats: butterflies on the index bits
+// [log2(s), log2(s) + log2(R)).  Group g covers base + j*s, j < R.
+template <int R>
+SRQ_DEV void fwht_pass_lds(float *buf, int total, int s_log2) {
+    const int s = 1 << s_log2;
+    const int groups = total / R;
+    for (int g = threadIdx.x; g < groups; g += kThreads) {
+        const int lo = g & (s - 1);
+        const int hi = g >> s_log2;
+        const int base = hi * s * R + lo;
+        float v[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) v[j] = buf[base + j * s];
+        fwht_regs<R>(v);
+#pragma unroll
+        for (int j = 0; j < R; ++j) buf[base + j * s] = v[j];
+    }
+    __syncthreads();
+}
+
+SRQ_DEV void fwht_pass_dispatch(float *buf, int total, int s_log2, int r_log2) {
+    switch (r_log2) {
+        case 1: fwht_pass_lds<2>(buf, total, s_log2); break;
+        case 2: fwht_pass_lds<4>(buf, total, s_log2); break;
+        case 3: fwht_pass_lds<8>(buf, total, s_log2); break;
+        default: fwht_pass_lds<16>(buf, total, s_log2); break;
+    }
+}
+
+// Load `rpb` rows (rpb * n values) into LDS as fp32 and run the first
+// radix-16 (or smaller) pass on the way.  Each thread takes R consecutive
+// values.  Returns the number of index bits already transformed.
+template <int R>
+SRQ_DEV void load_first_pass(const RotArgs &a, float *buf, int64_t row0, int nrows) {
+    const int total = nrows * a.n;
+    const int groups = total / R;
+    for (int g = threadIdx.x; g < groups; g += kThreads) {
+        const int64_t off = row0 * a.n + (int64_t)g * R;
+        float v[R];
+        if (a.io_f32) {
+            const float *src = reinterpret_cast<const float *>(a.x) + off;
+#pragma unroll
+            for (int j = 0; j < R; ++j) v[j] = src[j];
+        } else {
+            const f16 *src = reinterpret_cast<const f16 *>(a.x) + off;
+            if constexpr (R >= 8) {
+#pragma unroll
+                for (int j = 0; j < R; j += 8) {
+                    const v8h h = *reinterpret_cast<const v8h *>(src + j);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[j + i] = (float)h[i];
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < R; ++j) v[j] = (float)src[j];
+            }
+        }
+        fwht_regs<R>(v);
+#pragma unroll
+        for (int j = 0; j < R; ++j) buf[g * R + j] = v[j];
+    }
+    __syncthreads();
+}
+
+SRQ_DEV void fwht_rows(const RotArgs &a, float *buf, int64_t row0, int nrows) {
+    const int mlog = __builtin_ctz(a.m);
+    const int total = nrows * a.n;
+    int done;
+    if (mlog >= 4) {
+        load_first_pass<16>(a, buf, row0, nrows);
+        done = 4;
+    } else if (mlog == 3) {
+        load_first_pass<8>(a, buf, row0, nrows);
+        done = 3;
+    } else if (mlog == 2) {
+        load_first_pass<4>(a, buf, row0, nrows);
+        done = 2;
+    } else {
+        load_first_pass<2>(a, buf, row0, nrows);
+        done = 1;
+    }
+    while (done < mlog) {
+        const int r = (mlog - done) >= 4 ? 4 : (mlog - done);
+        fwht_pass_dispatch(buf, total, done, r);
+        done += r;
+    }
+}
+
+// K-mix with one column of the [K, m] view per thread, K <= KT in registers.
+// Applies the first rounding point (y = fp16(fwht * scale)) on load and the
+// second (fp16(hadK @ y)) on store, unless fp32_had.
+template <int KT>
+SRQ_DEV void kmix_regs(const RotArgs &a, float *buf, const float *hk, int nrows) {
+    const int cols = nrows * a.m;
+    for (int c = threadIdx.x; c < cols; c += kThreads) {
+        const int r = c / a.m;
+        const int j = c - r * a.m;
+        float *rb = buf + r * a.n + j;
+        float y[KT];
+#pragma unroll
+        for (int k = 0; k < KT; ++k) {
+            if (k < a.K) {
+                const float v = rb[k * a.m] * a.scale;
+                y[k] = a.fp32_had ? v : round16(v);
+            }
+        }
+        for (int k = 0; k < a.K; ++k) {
+            const float *h = hk + k * a.K;
+            float acc = 0.f;
+#pragma unroll
+            for (int kk = 0; kk < KT; ++kk) {
+                if (kk < a.K) acc = __builtin_fmaf(h[kk], y[kk], acc);
+            }
+            rb[k * a.m] = a.fp32_had ? acc : round16(acc);
+        }
+    }
+    __syncthreads();
+}
+
+// K-mix for K > 64: out-of-place into `dst`, hadK read from global memory.
+SRQ_DEV void kmix_generic(const RotArgs &a, const float *src, float *dst, int nrows) {
+    const int cols = nrows * a.m;
+    for (int c = threadIdx.x; c < cols; c += kThreads) {
+        const int r = c / a.m;
+        const int j = c - r * a.m;
+        const float *sb = src + r * a.n + j;
+        float *db = dst + r * a.n + j;
+        for (int k = 0; k < a.K; ++k) {
+            float acc = 0.f;
+            for (int kk = 0; kk < a.K; ++kk) {
+                const float h = a.fp32_had
+                                    ? reinterpret_cast<const float *>(a.hadK)[k * a.K + kk]
+                                    : (float)reinterpret_cast<const f16 *>(a.hadK)[k * a.K + kk];
+                float v = sb[kk * a.m] * a.scale;
+                if (!a.fp32_had) v = round16(v);
+                acc = __builtin_fmaf(h, v, acc);
+            }
+            db[k * a.m] = a.fp32_had ? acc : round16(acc);
+        }
+    }
+    __syncthreads();
+}
+
+// Final value of element i of a row (after the rotation stages).
+SRQ_DEV float finish(const RotArgs &a, const float *rb, int i) {
+    float v = rb[i];
+    if (a.K == 1) {
+        v *= a.scale;
+        if (!a.fp32_had && !a.io_f32) v = round16(v);
+    }
+    if (a.sign) v *= (float)a.sign[i];
+    return v;
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kThreads) void rotate_kernel(RotArgs a) {
+    extern __shared__ float lds[];
+    const int64_t row0 = (int64_t)blockIdx.x * a.rpb;
+    const int nrows = (int)((a.rows - row0) < a.rpb ? (a.rows - row0) : a.rpb);
+    float *buf = lds;
+    float *buf2 = nullptr;
+    float *hk = nullptr;
+    const int cap = a.rpb * a.n;
+    if (a.K > 64) {
+        buf2 = lds + cap;
+    } else if (a.K > 1) {
+        hk = lds + cap;
+        for (int i = threadIdx.x; i < a.K * a.K; i += kThreads)
+            hk[i] = a.fp32_had ? reinterpret_cast<const float *>(a.hadK)[i]
+                               : (float)reinterpret_cast<const f16 *>(a.hadK)[i];
+        // made visible by the barrier at the end of the FWHT passes
+    }
+
+    fwht_rows(a, buf, row0, nrows);
+
+    if (a.K > 64) {
+        kmix_generic(a, buf, buf2, nrows);
+        buf = buf2;
+    } else if (a.K > 32) {
+        kmix_regs<64>(a, buf, hk, nrows);
+    } else if (a.K > 1) {
+        kmix_regs<32>(a, buf, hk, nrows);
+    }
+
+    if constexpr (MODE == 0) {
+        const int total = nrows * a.n;
+        if (a.io_f32) {
+            float *dst = reinterpret_cast<float *>(a.out) + row0 * a.n;
+            for (int i = threadIdx.x; i < total; i += kThreads) {
+                const int r = i / a.n;
+                dst[i] = finish(a, buf + r * a.n, i - r * a.n);
+            }
+        } else {
+            f16 *dst = reinterpret_cast<f16 *>(a.out) + row0 * a.n;
+            for (int i = threadIdx.x * 8; i < total; i += kThreads * 8) {
+                const int r = i / a.n;
+                const float *rb = buf + r * a.n;
+                const int c = i - r * a.n;
+                v8h o;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = (f16)finish(a, rb, c + e);
+                *reinterpret_cast<v8h *>(dst + i) = o;
+            }
+        }
+    } else {
+        // Fused quantizer.  n >= 1024: the whole block shares one row; else
+        // wave w quantizes row w of the block.
+        __shared__ float red[4];
+        const int nw = a.n / 8;
+        if (a.rpb == 1) {
+            float amax = 0.f;
+            for (int w = threadIdx.x; w < nw; w += kThreads)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(round16(finish(a, buf, w * 8 + e))));
+            amax = wave_max(amax);
+            if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+            __syncthreads();
+            amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+            f16 s = (f16)(amax / 7.f);
+            if (a.clip != 1.f) s = (f16)((float)s * a.clip);
+            if (threadIdx.x == 0) a.qscale[row0] = s;
+            const float sf = (float)s;
+            uint32_t *qr = a.q + row0 * nw;
+            for (int w = threadIdx.x; w < nw; w += kThreads) {
+                uint32_t word = 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    word |= (uint32_t)(sym_code(round16(finish(a, buf, w * 8 + e)), sf) & 0xF) << (4 * e);
+                qr[w] = word;
+            }
+        } else {
+            const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+            if (wave < nrows) {
+                const float *rb = buf + wave * a.n;
+                float amax = 0.f;
+                for (int w = lane; w < nw; w += 64)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(round16(finish(a, rb, w * 8 + e))));
+                amax = wave_max(amax);
+                f16 s = (f16)(amax / 7.f);
+                if (a.clip != 1.f) s = (f16)((float)s * a.clip);
+                const int64_t row = row0 + wave;
+                if (lane == 0) a.qscale[row] = s;
+                const float sf = (float)s;
+                uint32_t *qr = a.q + row * nw;
+                for (int w = lane; w < nw; w += 64) {
+                    uint32_t word = 0;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        word |= (uint32_t)(sym_code(round16(finish(a, rb, w * 8 + e)), sf) & 0xF) << (4 * e);
+                    qr[w] = word;
+                }
+            }
+        }
+    }
+}
+
+bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+int launch_rotate(RotArgs a, int mode, hipStream_t st, const char *name) {
+    // rows per block: small rows share a block (<= 4, one wave each when
+    // quantizing), large rows get a block each
+    int rpb = 1;
+    if (a.n < 1024) {
+        rpb = 1024 / a.n;
+        if (rpb > 4) rpb = 4;
+    }
+    a.rpb = rpb;
+    size_t lds = (size_t)rpb * a.n * sizeof(float);
+    if (a.K > 64) lds *= 2;
+    else if (a.K > 1) lds += (size_t)a.K * a.K * sizeof(float);
+    if (lds > 160 * 1024) {
+        srq_set_error("%s: row of %d elements (K=%d) needs %zu bytes of LDS (> 160 KiB)",
+                      name, a.n, a.K, lds);
+        return SRQ_EUNSUPPORTED;
+    }
+    const dim3 grid((unsigned)srq_cdiv(a.rows, rpb));
+    const void *fn = mode == 0 ? (const void *)rotate_kernel<0> : (const void *)rotate_kernel<1>;
+    if (lds > 64 * 1024) {
+        hipError_t err = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (err != hipSuccess) {
+            srq_set_error("%s: cannot reserve %zu bytes of LDS: %s", name, lds,
+                          hipGetErrorString(err));
+            return SRQ_ELAUNCH;
+        }
+    }
+    if (mode == 0)
+        rotate_kernel<0><<<grid, dim3(kThreads), lds, st>>>(a);
+    else
+        rotate_kernel<1><<<grid, dim3(kThreads), lds, st>>>(a);
+    SRQ_LAUNCH_CHECK(name);
+    return SRQ_OK;
+}
+
+int check_rotation(const char *name, const void *x, int64_t rows, int64_t n, int64_t K,
+                   const void *hadK) {
+    SRQ_CHECK_ARG(rows >= 0 && n > 0, "%s: bad shape rows=%lld n=%lld", name, (long long)rows,
+                  (long long)n);
+    SRQ_CHECK_ARG(rows <= 0x7fffffffLL, "%s: rows > 2^31-1", name);
+    SRQ_CHECK_ARG(K >= 1 && n % K == 0 && is_pow2(n / K),
+                  "%s: n=%lld is not K=%lld times a power of two", name, (long long)n,
+                  (long long)K);
+    SRQ_CHECK_ARG(n / K >= 2 && n <= 65536, "%s: n=%lld outside [2K, 65536]", name,
+                  (long long)n);
+    SRQ_CHECK_ARG(n % 8 == 0 || K == 1, "%s: n must be a multiple of 8", name);
+    SRQ_CHECK_ARG(K == 1 || hadK != nullptr, "%s: hadK is null with K=%lld", name,
+                  (long long)K);
+    SRQ_CHECK_ARG(x != nullptr || rows == 0, "%s: null input", name);
+    return SRQ_OK;
+}
+
+}  // namespace
+
+extern "C" int srq_hadamard_transform(const void *x, void *out, int64_t rows, int64_t n,
+                                      float scale, int dtype, void *stream) {
+    SRQ_CHECK_ARG(dtype == 0 || dtype == 1, "hadamard_transform: dtype must be 0 (f16) or 1 (f32)");
+    SRQ_CHECK_ARG(is_pow2(n) && n >= 8 && n <= 32768,
+                  "hadamard_transform: n=%lld must be a power of two in [8, 32768]", (long long)n);
+    int rc = check_rotation("hadamard_transform", x, rows, n, 1, nullptr);
+    if (rc) return rc;
+    if (rows == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(out != nullptr, "hadamard_transform: null output");
+    SRQ_CHECK_ARG(srq_aligned(x, 16) && srq_aligned(out, 16),
+                  "hadamard_transform: x and out must be 16-byte aligned");
+    RotArgs a{};
+    a.x = x;
+    a.out = out;
+    a.rows = rows;
+    a.n = (int)n;
+    a.m = (int)n;
+    a.K = 1;
+    a.scale = scale;
+    a.io_f32 = dtype;
+    a.fp32_had = dtype;
+    return launch_rotate(a, 0, (hipStream_t)stream, "hadamard_transform");
+}
+
+extern "C" int srq_online_hadamard(const void *x, void *out, int64_t rows, int64_t n, int64_t K,
+                                   const void *hadK, const int8_t *sign, int fp32_had,
+                                   void *stream) {
+    int rc = check_rotation("online_hadamard", x, rows, n, K, hadK);
+    if (rc) return rc;
+    if (rows == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(out != nullptr, "online_hadamard: null output");
+    SRQ_CHECK_ARG(srq_aligned(x, 16) && srq_aligned(out, 16),
+                  "online_hadamard: x and out must be 16-byte aligned");
+    SRQ_CHECK_ARG(n % 8 == 0, "online_hadamard: n must be a multiple of 8");
+    RotArgs a{};
+    a.x = x;
+    a.out = out;
+    a.rows = rows;
+    a.n = (int)n;
+    a.K = (int)K;
+    a.m = (int)(n / K);
+    a.hadK = hadK;
+    a.sign = sign;
+    a.scale = 1.0f / sqrtf((float)n);
+    a.fp32_had = fp32_had ? 1 : 0;
+    return launch_rotate(a, 0, (hipStream_t)stream, "online_hadamard");
+}
+
+extern "C" int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_t K,
+                                  const void *hadK, const int8_t *sign, int fp32_had,
+                                  float clip_ratio, void *q, void *scale, void *stream) {
+    int rc = check_rotation("had_sign_quant", x, rows, n, K, hadK);
+    if (rc) return rc;
+    if (rows == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(q && scale, "had_sign_quant: null output");
+    SRQ_CHECK_ARG(srq_aligned(x, 16) && srq_aligned(q, 4),
+                  "had_sign_quant: x must be 16-byte and q 4-byte aligned");
+    SRQ_CHECK_ARG(n % 8 == 0, "had_sign_quant: n must be a multiple of 8");
+    RotArgs a{};
+    a.x = x;
+    a.rows = rows;
+    a.n = (int)n;
+    a.K = (int)K;
+    a.m = (int)(n / K);
+    a.hadK = hadK;
+    a.sign = sign;
+    a.scale = 1.0f / sqrtf((float)n);
+    a.fp32_had = fp32_had ? 1 : 0;
+    a.clip = clip_ratio;
+    a.q = (uint32_t *)q;
+    a.qscale = (f16 *)scale;
+    return launch_rotate(a, 1, (hipStream_t)stream, "had_sign_quant");
+}

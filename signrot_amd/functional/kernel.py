@@ -1,0 +1,123 @@
+"""Python wrappers over the HIP op table, mirroring
+signrot/functional/kernel.py:15-227 (flatten / view handling, the
+PackedQuantizedTensor carrier, dtype asserts)."""
+import torch
+
+from .. import _CUDA
+
+__all__ = [
+    "matmul_si4_si4",
+    "sym_quant",
+    "sym_quant_dynamic",
+    "sym_dequant",
+    "kv_quant_pack",
+    "w4a4_linear",
+    "had_sign_quant",
+    "PackedQuantizedTensor",
+]
+
+
+class ShapeHandler:
+    def __init__(self, x: torch.Tensor):
+        self.size_excl_last = x.numel() // x.shape[-1]
+        self.shape_excl_last = tuple(x.shape[:-1])
+
+    def flatten(self, x: torch.Tensor):
+        return x.view(self.size_excl_last, -1)
+
+    def unflatten(self, x: torch.Tensor):
+        return x.view(self.shape_excl_last + (-1,))
+
+    def unflatten_scale(self, x: torch.Tensor):
+        return x.view(self.shape_excl_last)
+
+
+class PackedQuantizedTensor:
+    """Quantized-activation carrier (kernel.py:32-52): packed int4 codes
+    [..., K/2] u8, per-token fp16 scales [..., 1], zeros (asym only)."""
+
+    def __init__(self, quantized_x: torch.Tensor, scales_x: torch.Tensor,
+                 zeros_x: torch.Tensor | None = None):
+        self.quantized_x = quantized_x
+        self.scales_x = scales_x
+        self.zeros_x = zeros_x
+
+    def size(self):
+        return self.quantized_x.size()
+
+    @property
+    def device(self):
+        return self.quantized_x.device
+
+    @property
+    def dtype(self):
+        return self.quantized_x.dtype
+
+
+def flatten_last_dim_and_return_shape(x: torch.Tensor):
+    shape_excl_last = x.shape[:-1]
+    x = x.view(-1, x.shape[-1])
+    return x, shape_excl_last
+
+
+def flatten_last_two_dim_and_return_shape(x: torch.Tensor):
+    shape_excl_last_two, shape_last_two = x.shape[:-2], x.shape[-2:]
+    x = x.view(-1, x.shape[-2], x.shape[-1])
+    return x, shape_excl_last_two, shape_last_two
+
+
+def matmul_si4_si4(A, B):
+    """int4 x int4 -> int32 over the last dim (kernel.py:67-73)."""
+    assert A.shape[-1] % 32 == 0, "A.shape[-1]: {} must be multiplication of 32".format(
+        A.shape[-1])
+    A, A_shape_excl_last = flatten_last_dim_and_return_shape(A)
+    B, B_shape_excl_last = flatten_last_dim_and_return_shape(B)
+    return _CUDA.matmul(A, B).view(*A_shape_excl_last, *B_shape_excl_last)
+
+
+def w4a4_linear(A, a_scale, B, b_scale, bias=None):
+    """Fused matmul_si4_si4 + sym_dequant (+ bias): fp16 [..., N]."""
+    A, A_shape_excl_last = flatten_last_dim_and_return_shape(A)
+    out = _CUDA.w4a4_linear(A, a_scale.reshape(-1), B, b_scale.reshape(-1),
+                            None if bias is None else bias.reshape(-1))
+    return out.view(*A_shape_excl_last, B.shape[0])
+
+
+def sym_quant(x, scale):
+    assert x.dtype == scale.dtype == torch.float16
+    x, x_shape_excl_last = flatten_last_dim_and_return_shape(x)
+    return _CUDA.sym_quant(x, scale.view(-1)).view(*x_shape_excl_last, -1)
+
+
+def sym_quant_dynamic(x, clip_ratio=1.0):
+    """Fused per-row amax + scale + symmetric int4 quantize/pack
+    (kernel.py:101-110).  Returns (packed_q, scale) with scale shaped
+    (*x.shape[:-1], 1)."""
+    assert x.dtype == torch.float16
+    x, shape_excl_last = flatten_last_dim_and_return_shape(x.contiguous())
+    q, scale = _CUDA.sym_quant_dynamic(x, clip_ratio)
+    return q.view(*shape_excl_last, -1), scale.view(*shape_excl_last, 1)
+
+
+def had_sign_quant(x, hadK, K, sign=None, clip_ratio=1.0, fp32_had=False):
+    """Fused OnlineHadamard -> sign -> sym_quant_dynamic (one launch)."""
+    assert x.dtype == torch.float16
+    x, shape_excl_last = flatten_last_dim_and_return_shape(x.contiguous())
+    q, scale = _CUDA.had_sign_quant(x, hadK, K, sign, clip_ratio, fp32_had)
+    return q.view(*shape_excl_last, -1), scale.view(*shape_excl_last, 1)
+
+
+def kv_quant_pack(x):
+    """Fused KV-cache asymmetric uint4 quantize + pack (kernel.py:148-155):
+    (packed_q, param) with param[..., 0] the scale and param[..., 1] the zero."""
+    assert x.dtype == torch.float16
+    return _CUDA.kv_quant_pack(x.contiguous())
+
+
+def sym_dequant(q, scale_row, scale_col, bits=32):
+    """(kernel.py:179-185)"""
+    assert q.dtype == torch.int32
+    assert scale_row.dtype == scale_col.dtype == torch.float16
+    q, q_shape_excl_last = flatten_last_dim_and_return_shape(q)
+    return _CUDA.sym_dequant(q, scale_row.view(-1), scale_col.view(-1), bits).view(
+        *q_shape_excl_last, -1)

@@ -1,0 +1,3 @@
+from .linear import Linear4bit
+from .quantization import Quantizer, SymQuantizer
+from .hadamard import OnlineHadamard, HadamardQuantizer, fuse_online_hadamard

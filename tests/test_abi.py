@@ -1,0 +1,63 @@
+"""CPU checks of the C-ABI library: it loads, exports every symbol that
+include/signrot_hip.h declares, and rejects bad arguments with an error code
+and message before touching a device (no compute call is made here)."""
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def _declared():
+    text = (ROOT / "include" / "signrot_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(srq_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from signrot_amd import _native
+    return _native.lib()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = _declared()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(lib, n), f"missing export {n}"
+
+
+def test_python_signatures_cover_header():
+    from signrot_amd import _native
+    declared = set(_declared()) - {"srq_last_error", "srq_abi_version"}
+    assert declared == set(_native.SIGNATURES), declared ^ set(_native.SIGNATURES)
+
+
+def test_abi_version(lib):
+    assert lib.srq_abi_version() >= 1
+
+
+@pytest.mark.parametrize("call,msg", [
+    (lambda L: L.srq_sym_quant_dynamic(None, -1, 4, 1.0, None, None, None), "negative"),
+    (lambda L: L.srq_kv_quant_pack(None, 4, 7, None, None, None), "even"),
+    (lambda L: L.srq_matmul_s4s4(None, None, 4, 4, 48, None, None), "multiple of 32"),
+    (lambda L: L.srq_matmul_s4s4(None, None, 4, 4, 262144, None, None), "131072"),
+    (lambda L: L.srq_hadamard_transform(None, None, 4, 24, 1.0, 0, None), "power of two"),
+    (lambda L: L.srq_online_hadamard(None, None, 4, 14336, 28, None, None, 0, None), "hadK"),
+    (lambda L: L.srq_had_sign_quant(None, 4, 21 * 64, 3, None, None, 0, 1.0, None, None,
+                                    None), "power of two"),
+    (lambda L: L.srq_w4a4_linear(ctypes.c_void_p(8), None, ctypes.c_void_p(16), None, None, 4,
+                                 4, 64, None, None), "aligned"),
+])
+def test_argument_errors(lib, call, msg):
+    rc = call(lib)
+    assert rc == -1
+    assert msg in lib.srq_last_error().decode()
+
+
+def test_empty_inputs_are_noops(lib):
+    assert lib.srq_sym_quant_dynamic(None, 0, 4096, 1.0, None, None, None) == 0
+    assert lib.srq_matmul_s4s4(None, None, 0, 16, 64, None, None) == 0
+    assert lib.srq_kv_quant_pack(None, 0, 128, None, None, None) == 0

@@ -1,0 +1,82 @@
+"""GPU parity: int4 GEMM (int32, bit-exact) and the fused W4A4 linear
+(fp16, bit-exact) vs the CPU oracle; fused == unfused on the GPU."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant as oq
+from tests.gpu_util import assert_bitexact, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def C():
+    from signrot_amd import _CUDA
+    return _CUDA
+
+
+GEMM_SHAPES = [
+    (1, 4096, 4096), (16, 4096, 4096), (1, 4096, 14336), (16, 4096, 14336),
+    (17, 100, 768), (32, 768, 2048), (33, 64, 32), (64, 2048, 768), (65, 130, 4096),
+    (128, 4096, 14336), (300, 513, 800), (513, 2048, 768), (2048, 4096, 14336),
+    (2, 16, 32), (5, 3, 64),
+]
+
+
+def _rand_packed(rng, r, k):
+    return rng.integers(0, 256, (r, k // 2)).astype(np.uint8)
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_matmul_bitexact(C, M, N, K):
+    rng = np.random.default_rng(M * 7 + N * 13 + K)
+    a, b = _rand_packed(rng, M, K), _rand_packed(rng, N, K)
+    c = C.matmul(to_dev(a), to_dev(b))
+    assert_bitexact(to_np(c), oq.matmul_s4s4(a, b), "int32 C")
+
+
+def test_matmul_extreme_values(C):
+    K = 28672
+    a = np.full((3, K // 2), 0x88, np.uint8)
+    b = np.full((17, K // 2), 0x88, np.uint8)
+    c = to_np(C.matmul(to_dev(a), to_dev(b)))
+    assert np.all(c == 64 * K)
+    b2 = np.full((17, K // 2), 0x77, np.uint8)
+    c2 = to_np(C.matmul(to_dev(a), to_dev(b2)))
+    assert np.all(c2 == -56 * K)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 4096, 4096), (33, 300, 768),
+                                   (128, 4096, 14336), (2048, 4096, 14336), (7, 5, 64)])
+@pytest.mark.parametrize("bias", [False, True])
+def test_w4a4_linear_bitexact(C, M, N, K, bias):
+    rng = np.random.default_rng(M + N + K + bias)
+    a, b = _rand_packed(rng, M, K), _rand_packed(rng, N, K)
+    sa = (np.abs(rng.standard_normal(M)) * 0.05 + 1e-3).astype(np.float16)
+    sb = (np.abs(rng.standard_normal(N)) * 0.01 + 1e-4).astype(np.float16)
+    bs = (rng.standard_normal(N) * 0.5).astype(np.float16) if bias else None
+    out = C.w4a4_linear(to_dev(a), to_dev(sa), to_dev(b), to_dev(sb),
+                        to_dev(bs) if bias else None)
+    want = oq.w4a4_linear(a, sa, b, sb, bs)
+    assert_bitexact(to_np(out), want, "fp16 out")
+    # the fused kernel equals the unfused GPU pair
+    unf = C.sym_dequant(C.matmul(to_dev(a), to_dev(b)), to_dev(sa), to_dev(sb))
+    if bias:
+        unf = unf + to_dev(bs)
+    assert torch.equal(out, unf)
+
+
+def test_matmul_rejects_bad_k(C):
+    a = torch.zeros(4, 8, dtype=torch.uint8, device="cuda")  # K = 16
+    with pytest.raises(RuntimeError):
+        C.matmul(a, a)
+    with pytest.raises(RuntimeError):
+        C.matmul(torch.zeros(4, 16, dtype=torch.uint8, device="cuda"),
+                 torch.zeros(4, 32, dtype=torch.uint8, device="cuda"))
+
+
+def test_matmul_empty(C):
+    a = torch.zeros(0, 16, dtype=torch.uint8, device="cuda")
+    b = torch.zeros(5, 16, dtype=torch.uint8, device="cuda")
+    assert C.matmul(a, b).shape == (0, 5)

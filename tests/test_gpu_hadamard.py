@@ -1,0 +1,104 @@
+"""GPU parity: the Hadamard rotation (tolerance vs the float64 closed form
+and vs the oracle's rounding points -- the reference FWHT's bits are not
+pinnable) and the fused rotation + sign + quant (bit-exact given the same
+rotated fp16 input)."""
+import math
+
+import numpy as np
+import pytest
+import scipy.linalg
+import torch
+
+from oracle import hadamard as oh
+from oracle import quant as oq
+from tests.gpu_util import assert_bitexact, outlier_input, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def C():
+    from signrot_amd import _CUDA
+    return _CUDA
+
+
+def _hadk(k, dtype=torch.float16):
+    return to_dev(oh.had_table(k).astype(np.float32)).to(dtype)
+
+
+@pytest.mark.parametrize("n", [8, 32, 128, 512, 4096, 16384, 32768])
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_hadamard_transform_closed_form(C, n, dtype):
+    rng = np.random.default_rng(n)
+    rows = 3 if n >= 16384 else 17
+    x = rng.standard_normal((rows, n)).astype(dtype)
+    scale = 1.0 / math.sqrt(n)
+    out = to_np(C.hadamard_transform(to_dev(x), scale))
+    want = oh.fwht(x.astype(np.float64)) * np.float64(np.float32(scale))
+    if dtype == np.float16:
+        ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+        # one fp16 rounding of an fp32-accumulated value: <= 1 ulp
+        assert np.all(np.abs(out.astype(np.float64) - want) <= ulp), "fp16 FWHT beyond 1 ulp"
+        # and almost always the correctly rounded value
+        exact = want.astype(np.float16)
+        assert np.mean(out != exact) < 1e-3
+    else:
+        np.testing.assert_allclose(out, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("n", [4096, 14336, 28672, 12 * 64, 11008, 128, 32])
+def test_online_hadamard_vs_oracle(C, n):
+    rng = np.random.default_rng(n + 1)
+    x = outlier_input(rng, 9, n, n_out=min(8, n // 4), mag=50.0)
+    had, k = oh.get_hadK(n)
+    sign = rng.choice([-1, 1], n).astype(np.int8)
+    hk = _hadk(k) if k > 1 else None
+    out = to_np(C.online_hadamard(to_dev(x), hk, k, to_dev(sign)))
+    want = oh.online_hadamard(x, sign)
+    exact = oh.matmul_hadU_f64(x.astype(np.float64)) * sign
+    # rtol 1e-2 / atol 1e-2 against the oracle ...
+    np.testing.assert_allclose(out.astype(np.float32), want.astype(np.float32),
+                               rtol=1e-2, atol=1e-2)
+    # ... and agreement in (nearly) every bit: differences only where fp32
+    # accumulation order moves a value across an fp16 rounding boundary
+    assert np.mean(out.view(np.uint16) != want.view(np.uint16)) < 5e-3
+    np.testing.assert_allclose(out.astype(np.float64), exact, rtol=1e-2, atol=1e-2)
+
+
+def test_online_hadamard_fp32_mode(C):
+    rng = np.random.default_rng(2)
+    n = 14336
+    x = outlier_input(rng, 4, n, n_out=8, mag=50.0)
+    out = to_np(C.online_hadamard(to_dev(x), _hadk(28, torch.float32), 28, None, True))
+    exact = oh.matmul_hadU_f64(x.astype(np.float64))
+    # a single rounding at the end: within 1 fp16 ulp of the exact rotation
+    ulp = np.spacing(np.abs(exact).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(out.astype(np.float64) - exact) <= ulp)
+
+
+@pytest.mark.parametrize("n,rows", [(4096, 16), (14336, 64), (28672, 5), (128, 33),
+                                    (11008, 3), (32, 10)])
+@pytest.mark.parametrize("use_sign", [False, True])
+def test_had_sign_quant_bitexact(C, n, rows, use_sign):
+    rng = np.random.default_rng(n + rows)
+    x = outlier_input(rng, rows, n, n_out=min(8, n // 4), mag=100.0)
+    _, k = oh.get_hadK(n)
+    hk = _hadk(k) if k > 1 else None
+    sign = to_dev(rng.choice([-1, 1], n).astype(np.int8)) if use_sign else None
+    xd = to_dev(x)
+    rot = C.online_hadamard(xd, hk, k, sign)
+    q, s = C.had_sign_quant(xd, hk, k, sign)
+    qw, sw = oq.sym_quant_dynamic(to_np(rot))
+    assert_bitexact(to_np(s), sw, "scale")
+    assert_bitexact(to_np(q), qw, "codes")
+    # same as the unfused GPU composition
+    q2, s2 = C.sym_quant_dynamic(rot.view(rows, n))
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+
+
+def test_zero_sign_raises_in_module():
+    from signrot_amd.nn import OnlineHadamard
+    m = OnlineHadamard(4096, had_adj=True).cuda()
+    m.had_adj_sign[5] = 0
+    with pytest.raises(RuntimeError):
+        m(torch.zeros(2, 4096, dtype=torch.float16, device="cuda"))
