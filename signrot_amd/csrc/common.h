@@ -88,6 +88,20 @@ SRQ_DEV float group_sum(float v) {
     return v;
 }
 
+// ------------------------------------------------------- fp16 rounding
+// Round an fp32 *result* to fp16 in two steps, as the reference does
+// (fp32 op, then __float2half).  The empty asm pins the fp32 value in a
+// register so the backend cannot fold `fptrunc(fmul/fma(...))` into a
+// v_fma_mix* instruction, which would round the exact product to fp16 once
+// -- a different value whenever the fp32 rounding moves it across an fp16
+// rounding boundary.
+SRQ_DEV f16 f16_rn(float v) {
+    asm volatile("" : "+v"(v));
+    return (f16)v;
+}
+
+SRQ_DEV float round16(float v) { return (float)f16_rn(v); }
+
 // ---------------------------------------------------------- int4 semantics
 // Symmetric code of one fp16 value given the fp16 scale, as the reference's
 // quantizers define it: q = clamp(round_half_even(fp16(x / s)), -8, 7), where
@@ -95,7 +109,7 @@ SRQ_DEV float group_sum(float v) {
 // rounded to fp16 is correctly rounded: 24 >= 2*11 + 2), NaN (0/0 on an
 // all-zero row) gives 0 and ±inf saturates.
 SRQ_DEV int sym_code(float x, float s) {
-    float quot = (float)(f16)(x / s);
+    float quot = round16(x / s);
     float r = __builtin_rintf(quot);
     if (r != r) return 0;
     r = fminf(fmaxf(r, -8.f), 7.f);
@@ -104,8 +118,8 @@ SRQ_DEV int sym_code(float x, float s) {
 
 // Unsigned asymmetric KV code: clamp(round_half_even(fp16(fp16(x + z) / s)), 0, 15).
 SRQ_DEV int kv_code(float x, float zero, float scale) {
-    float shifted = (float)(f16)(x + zero);
-    float scaled = (float)(f16)(shifted / scale);
+    float shifted = round16(x + zero);
+    float scaled = round16(shifted / scale);
     float r = __builtin_rintf(scaled);
     if (r != r) return 0;
     r = fminf(fmaxf(r, 0.f), 15.f);

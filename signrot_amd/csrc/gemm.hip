@@ -53,8 +53,8 @@ SRQ_DEV void store_one(const Epi &e, int64_t N, int64_t m, int64_t n, int acc256
         e.C[m * N + n] = v;
     } else {
         const float a = (float)v * (float)e.sa[m];
-        f16 o = (f16)(a * (float)e.sb[n]);
-        if (e.bias) o = (f16)((float)o + (float)e.bias[n]);
+        f16 o = f16_rn(a * (float)e.sb[n]);
+        if (e.bias) o = f16_rn((float)o + (float)e.bias[n]);
         e.out[m * N + n] = o;
     }
 }

@@ -41,8 +41,6 @@ struct RotArgs {
     int rpb;            // rows per block
 };
 
-SRQ_DEV float round16(float v) { return (float)(f16)v; }
-
 template <int R>
 SRQ_DEV void fwht_regs(float (&v)[R]) {
 #pragma unroll
@@ -258,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(RotArgs a) {
                 const int c = i - r * a.n;
                 v8h o;
 #pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = (f16)finish(a, rb, c + e);
+                for (int e = 0; e < 8; ++e) o[e] = f16_rn(finish(a, rb, c + e));
                 *reinterpret_cast<v8h *>(dst + i) = o;
             }
         }
@@ -276,8 +274,8 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(RotArgs a) {
             if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
             __syncthreads();
             amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-            f16 s = (f16)(amax / 7.f);
-            if (a.clip != 1.f) s = (f16)((float)s * a.clip);
+            f16 s = f16_rn(amax / 7.f);
+            if (a.clip != 1.f) s = f16_rn((float)s * a.clip);
             if (threadIdx.x == 0) a.qscale[row0] = s;
             const float sf = (float)s;
             uint32_t *qr = a.q + row0 * nw;
@@ -297,8 +295,8 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(RotArgs a) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(round16(finish(a, rb, w * 8 + e))));
                 amax = wave_max(amax);
-                f16 s = (f16)(amax / 7.f);
-                if (a.clip != 1.f) s = (f16)((float)s * a.clip);
+                f16 s = f16_rn(amax / 7.f);
+                if (a.clip != 1.f) s = f16_rn((float)s * a.clip);
                 const int64_t row = row0 + wave;
                 if (lane == 0) a.qscale[row] = s;
                 const float sf = (float)s;

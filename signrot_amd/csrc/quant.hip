@@ -44,8 +44,8 @@ SRQ_DEV float absmax8(const v8h &v, float m) {
 // Row scale from the exact fp32 max (fused.cu:93-95 order: divide, round to
 // fp16, then the clip multiply rounds again).
 SRQ_DEV f16 sym_row_scale(float amax, float clip) {
-    f16 s = (f16)(amax / 7.f);
-    if (clip != 1.f) s = (f16)((float)s * clip);
+    f16 s = f16_rn(amax / 7.f);
+    if (clip != 1.f) s = f16_rn((float)s * clip);
     return s;
 }
 
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(256) void sym_dequant_vec_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float a = (float)v[j] * r;
-            o[j] = (f16)(a * (float)sc[c4 * 4 + j]);
+            o[j] = f16_rn(a * (float)sc[c4 * 4 + j]);
         }
         out[i] = o;
     }
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(256) void sym_dequant_generic_kernel(
         const int64_t row = i / cols;
         const int64_t col = i - row * cols;
         const float a = (float)q[i] * (float)sr[row];
-        out[i] = (f16)(a * (float)sc[col]);
+        out[i] = f16_rn(a * (float)sc[col]);
     }
 }
 
@@ -308,9 +308,9 @@ __global__ __launch_bounds__(256) void kv_quant_pack_vec_kernel(
     if (row >= rows) return;
     // fused.cu:246-252: diff rounds to fp16, the clamp(min=1e-5) rounds to
     // fp16, the / 15 rounds again; zero = -min exactly.
-    f16 diff = (f16)((float)(f16)vmax - (float)(f16)vmin);
-    diff = (f16)fmaxf((float)diff, 1e-5f);
-    const f16 scale = (f16)((float)diff / 15.f);
+    f16 diff = f16_rn((float)(f16)vmax - (float)(f16)vmin);
+    diff = f16_rn(fmaxf((float)diff, 1e-5f));
+    const f16 scale = f16_rn((float)diff / 15.f);
     const f16 zero = -(f16)vmin;
     if (lt == 0) {
         param[row * 2 + 0] = scale;
@@ -336,9 +336,9 @@ __global__ __launch_bounds__(64) void kv_quant_pack_generic_kernel(
     }
     vmax = wave_max(vmax);
     vmin = wave_min(vmin);
-    f16 diff = (f16)((float)(f16)vmax - (float)(f16)vmin);
-    diff = (f16)fmaxf((float)diff, 1e-5f);
-    const f16 scale = (f16)((float)diff / 15.f);
+    f16 diff = f16_rn((float)(f16)vmax - (float)(f16)vmin);
+    diff = f16_rn(fmaxf((float)diff, 1e-5f));
+    const f16 scale = f16_rn((float)diff / 15.f);
     const f16 zero = -(f16)vmin;
     if (threadIdx.x == 0) {
         param[row * 2 + 0] = scale;
