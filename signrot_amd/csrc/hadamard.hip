@@ -369,6 +369,10 @@ int check_rotation(const char *name, const void *x, int64_t rows, int64_t n, int
 
 }  // namespace
 
+int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
+                    const int8_t *sign, float clip, void *q, void *qscale, void *out,
+                    hipStream_t st);
+
 extern "C" int srq_hadamard_transform(const void *x, void *out, int64_t rows, int64_t n,
                                       float scale, int dtype, void *stream) {
     SRQ_CHECK_ARG(dtype == 0 || dtype == 1, "hadamard_transform: dtype must be 0 (f16) or 1 (f32)");
@@ -414,6 +418,11 @@ extern "C" int srq_online_hadamard(const void *x, void *out, int64_t rows, int64
     a.sign = sign;
     a.scale = 1.0f / sqrtf((float)n);
     a.fp32_had = fp32_had ? 1 : 0;
+    if (!fp32_had &&
+        srq_had512_mfma(x, rows, n, K, hadK, sign, 1.f, nullptr, nullptr, out, (hipStream_t)stream)) {
+        SRQ_LAUNCH_CHECK("online_hadamard");
+        return SRQ_OK;
+    }
     return launch_rotate(a, 0, (hipStream_t)stream, "online_hadamard");
 }
 
@@ -440,5 +449,10 @@ extern "C" int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_
     a.clip = clip_ratio;
     a.q = (uint32_t *)q;
     a.qscale = (f16 *)scale;
+    if (!fp32_had && srq_had512_mfma(x, rows, n, K, hadK, sign, clip_ratio, q, scale, nullptr,
+                                     (hipStream_t)stream)) {
+        SRQ_LAUNCH_CHECK("had_sign_quant");
+        return SRQ_OK;
+    }
     return launch_rotate(a, 1, (hipStream_t)stream, "had_sign_quant");
 }

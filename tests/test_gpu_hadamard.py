@@ -49,7 +49,7 @@ def test_hadamard_transform_closed_form(C, n, dtype):
         assert np.all(np.abs(out.astype(np.float64) - want) <= acc + 1e-30)
 
 
-@pytest.mark.parametrize("n", [4096, 14336, 28672, 12 * 64, 11008, 128, 32])
+@pytest.mark.parametrize("n", [4096, 14336, 28672, 12 * 64, 11008, 128, 32, 6144, 10240])
 def test_online_hadamard_vs_oracle(C, n):
     rng = np.random.default_rng(n + 1)
     x = outlier_input(rng, 9, n, n_out=min(8, n // 4), mag=50.0)
@@ -83,7 +83,8 @@ def test_online_hadamard_fp32_mode(C):
 
 
 @pytest.mark.parametrize("n,rows", [(4096, 16), (14336, 64), (28672, 5), (128, 33),
-                                    (11008, 3), (32, 10)])
+                                    (11008, 3), (32, 10), (14336, 7), (14336, 3001),
+                                    (6144, 9), (10240, 13)])
 @pytest.mark.parametrize("use_sign", [False, True])
 def test_had_sign_quant_bitexact(C, n, rows, use_sign):
     rng = np.random.default_rng(n + rows)
@@ -108,3 +109,36 @@ def test_zero_sign_raises_in_module():
     m.had_adj_sign[5] = 0
     with pytest.raises(RuntimeError):
         m(torch.zeros(2, 4096, dtype=torch.float16, device="cuda"))
+
+
+@pytest.mark.parametrize("case", ["zeros", "tiny", "subnormal_scale", "clip", "huge"])
+def test_had_sign_quant_edge_cases(C, case):
+    """Rows the MFMA fast path (n = 28 x 512) must treat like the reference:
+    an all-zero row (scale 0, codes 0), tiny values (subnormal fp16 scale),
+    a row whose scale underflows to 0, clip < 1 (codes clamp at -8), and
+    large magnitudes."""
+    n, rows = 14336, 8
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((rows, n)).astype(np.float16)
+    clip = 1.0
+    if case == "zeros":
+        x[2] = 0
+        x[5] = 0
+    elif case == "tiny":
+        x = (x.astype(np.float32) * 1e-5).astype(np.float16)
+    elif case == "subnormal_scale":
+        x[:] = 0
+        x[1, 100] = np.float16(2 ** -24)
+        x[3, 7] = -np.float16(2 ** -23)
+    elif case == "clip":
+        clip = 0.8
+    else:
+        x = (x.astype(np.float32) * 300).astype(np.float16)
+    hk = _hadk(28)
+    sign = to_dev(rng.choice([-1, 1], n).astype(np.int8))
+    xd = to_dev(x)
+    rot = C.online_hadamard(xd, hk, 28, sign)
+    q, s = C.had_sign_quant(xd, hk, 28, sign, clip)
+    qw, sw = oq.sym_quant_dynamic(to_np(rot), clip)
+    assert_bitexact(to_np(s), sw, "scale")
+    assert_bitexact(to_np(q), qw, "codes")
