@@ -25,18 +25,40 @@ namespace {
 SRQ_DEV u32 lo4(u32 w) { return (w << 4) & 0xF0F0F0F0u; }
 SRQ_DEV u32 hi4(u32 w) { return w & 0xF0F0F0F0u; }
 
-// 8 packed bytes (16 int4) -> one MFMA operand of 16 int8
+// 8 packed bytes (16 int4) -> one MFMA operand of 16 int8.  The two low
+// nibble words come from one 64-bit shift (the nibble that crosses from w0
+// into w1 is masked off).
 SRQ_DEV v4i unpack8(u32 w0, u32 w1) {
+    const uint64_t sh = ((uint64_t)w1 << 32 | w0) << 4;
     v4i r;
-    r[0] = (int)lo4(w0);
+    r[0] = (int)((u32)sh & 0xF0F0F0F0u);
     r[1] = (int)hi4(w0);
-    r[2] = (int)lo4(w1);
+    r[2] = (int)((u32)(sh >> 32) & 0xF0F0F0F0u);
     r[3] = (int)hi4(w1);
     return r;
 }
 
 SRQ_DEV v4i mfma16(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Raw buffer loads: an offset at or past the resource's byte size returns
+// zeros in hardware, so tile edges and the K tail need no branches.
+SRQ_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t bytes) {
+    const uint32_t n = bytes > 0xFFFFFFF0LL ? 0xFFFFFFF0u : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)n, 0x00020000);
+}
+
+constexpr uint32_t kOob = 0xFFFFFFF0u;
+
+SRQ_DEV v4i bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// byte offset of 16-byte chunk (row, kbyte) of a [rows, KB] packed matrix,
+// or kOob when it lies outside
+SRQ_DEV uint32_t chunk_off(int64_t row, int64_t rows, int64_t kb, int64_t KB) {
+    return (row < rows && kb < KB) ? (uint32_t)(row * KB + kb) : kOob;
 }
 
 struct Epi {
@@ -57,6 +79,42 @@ SRQ_DEV void store_one(const Epi &e, int64_t N, int64_t m, int64_t n, int acc256
         if (e.bias) o = f16_rn((float)o + (float)e.bias[n]);
         e.out[m * N + n] = o;
     }
+}
+
+// Store a wave's FM x FN block of 16x16 accumulators (16x16 layout: lane
+// holds column lane & 15, rows 4 * (lane >> 4) + r), loading each row and
+// column scale once.
+template <int FM, int FN>
+SRQ_DEV void store_block(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t nb,
+                         const v4i (&acc)[FM][FN], int lane) {
+    float sbv[FN];
+    int64_t gnv[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        gnv[j] = nb + j * 16 + (lane & 15);
+        sbv[j] = (!e.C && gnv[j] < N) ? (float)e.sb[gnv[j]] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t gm = mb + i * 16 + 4 * (lane >> 4) + r;
+            if (gm >= M) continue;
+            const float sa = e.C ? 0.f : (float)e.sa[gm];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                if (gnv[j] >= N) continue;
+                const int v = acc[i][j][r] >> 8;
+                if (e.C) {
+                    e.C[gm * N + gnv[j]] = v;
+                } else {
+                    const float a = (float)v * sa;
+                    f16 o = f16_rn(a * sbv[j]);
+                    if (e.bias) o = f16_rn((float)o + (float)e.bias[gnv[j]]);
+                    e.out[gm * N + gnv[j]] = o;
+                }
+            }
+        }
 }
 
 // ---------------------------------------------------------------------------
@@ -99,6 +157,7 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t *__restric
     const int64_t KB = K / 2;  // bytes per row
     const int steps = (int)((K + kBK - 1) / kBK);
 
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
     v4i ra[A_CHUNKS], rb[B_CHUNKS];
     auto gload = [&](int s) {
         const int64_t kb0 = (int64_t)s * kBKB;
@@ -106,21 +165,13 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t *__restric
         for (int i = 0; i < A_CHUNKS; ++i) {
             const int c = tid + 256 * i;
             const int r = c / (kBKB / 16), col = (c % (kBKB / 16)) * 16;
-            const int64_t gm = m0 + r, gk = kb0 + col;
-            if (gm < M && gk < KB)
-                ra[i] = *reinterpret_cast<const v4i *>(A + gm * KB + gk);
-            else
-                ra[i] = (v4i){0, 0, 0, 0};
+            ra[i] = bload16(ar, chunk_off(m0 + r, M, kb0 + col, KB));
         }
 #pragma unroll
         for (int i = 0; i < B_CHUNKS; ++i) {
             const int c = tid + 256 * i;
             const int r = c / (kBKB / 16), col = (c % (kBKB / 16)) * 16;
-            const int64_t gn = n0 + r, gk = kb0 + col;
-            if (gn < N && gk < KB)
-                rb[i] = *reinterpret_cast<const v4i *>(B + gn * KB + gk);
-            else
-                rb[i] = (v4i){0, 0, 0, 0};
+            rb[i] = bload16(br, chunk_off(n0 + r, N, kb0 + col, KB));
         }
     };
     auto sstore = [&]() {
@@ -153,21 +204,26 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t *__restric
         sstore();
         __syncthreads();
         if (s + 1 < steps) gload(s + 1);
+        uint2 wa[2][FM], wb[2][FN];
+        auto fetch = [&](int kk, int slot) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                wa[slot][i] = *reinterpret_cast<const uint2 *>(
+                    As + (wm * WM + i * 16 + frow) * kLdsRow + kk * 32 + fk);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                wb[slot][j] = *reinterpret_cast<const uint2 *>(
+                    Bs + (wn * WN + j * 16 + frow) * kLdsRow + kk * 32 + fk);
+        };
+        fetch(0, 0);
 #pragma unroll
         for (int kk = 0; kk < kBKB / 32; ++kk) {
+            if (kk + 1 < kBKB / 32) fetch(kk + 1, (kk + 1) & 1);
             v4i fa[FM], fb[FN];
 #pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                const uint8_t *p = As + (wm * WM + i * 16 + frow) * kLdsRow + kk * 32 + fk;
-                const uint2 w = *reinterpret_cast<const uint2 *>(p);
-                fa[i] = unpack8(w.x, w.y);
-            }
+            for (int i = 0; i < FM; ++i) fa[i] = unpack8(wa[kk & 1][i].x, wa[kk & 1][i].y);
 #pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const uint8_t *p = Bs + (wn * WN + j * 16 + frow) * kLdsRow + kk * 32 + fk;
-                const uint2 w = *reinterpret_cast<const uint2 *>(p);
-                fb[j] = unpack8(w.x, w.y);
-            }
+            for (int j = 0; j < FN; ++j) fb[j] = unpack8(wb[kk & 1][j].x, wb[kk & 1][j].y);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -175,17 +231,188 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t *__restric
         }
     }
 
-    // 16x16 accumulator layout: lane holds column (lane & 15), rows
-    // 4 * (lane >> 4) + r, r = 0..3.
+    store_block<FM, FN>(e, M, N, m0 + wm * WM, n0 + wn * WN, acc, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Large-M kernel: 256 x 128 block per workgroup of 8 waves (4 x 2), each
+// wave 64 x 64 as 2 x 2 blocks of v_mfma_i32_32x32x32_i8 (the gfx950 int8
+// MFMA with the highest sustained rate); two waves per SIMD, so one wave's
+// nibble unpacking and LDS reads overlap the other's MFMAs.  K advances 256 codes (128 bytes)
+// per step through a 3-stage LDS ring filled by buffer -> LDS DMA
+// (buffer_load_dwordx4 ... lds): two steps of loads are in flight while one
+// is multiplied, without spending VGPRs, and out-of-range chunks (tile
+// edges, K tail) arrive as zeros.  The DMA is issued from inline asm and
+// its completion tracked explicitly with vmcnt, so the compiler does not
+// serialise the ring by waiting for every outstanding DMA before each LDS
+// read.  A stage holds the 256 A rows then the 128 B rows, 128 bytes each,
+// with 16-byte chunk j of row r at position j ^ (r & 7): the 16-byte
+// fragment reads (rows r .. r+15 of one chunk column) hit distinct banks.
+// A lane reads 16 bytes (32 codes) per fragment and feeds two MFMA K-slices
+// from it (half-wave g takes chunk 2p + g, bytes 0-7 then 8-15); A and B use
+// the same K mapping, so the dot products are exact.
+
+SRQ_DEV v16i mfma32i8(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+constexpr int kBigBM = 256, kBigBN = 128;
+constexpr int kBigRows = kBigBM + kBigBN;
+constexpr int kBigStage = kBigRows * kBKB;           // 48 KiB
+constexpr int kBigDma = kBigRows / 8;                 // 1 KiB DMA blocks per stage
+constexpr int kBigWaves = 8;                          // 4 (M) x 2 (N), 64 x 64 each
+constexpr int kBigDmaPerWave = kBigDma / kBigWaves;   // 6
+
+// One 1 KiB DMA block: lane l's 16 bytes land at lds + 16 l.
+SRQ_DEV void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds), "v"(voff), "s"(r) : "memory");
+}
+
+template <int FM, int FN>
+SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {
+    const int rr = lane & 31;
+    const int g = lane >> 5;
+    v4i fa[2][FM], fb[2][FN];
+    auto fetch = [&](int pp, int slot) {
+        const int j = 2 * pp + g;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int r = wm * (FM * 32) + i * 32 + rr;
+            fa[slot][i] = *reinterpret_cast<const v4i *>(stage + r * kBKB + ((j ^ (r & 7)) << 4));
+        }
+#pragma unroll
+        for (int jn = 0; jn < FN; ++jn) {
+            const int r = kBigBM + wn * (FN * 32) + jn * 32 + rr;
+            fb[slot][jn] = *reinterpret_cast<const v4i *>(stage + r * kBKB + ((j ^ (r & 7)) << 4));
+        }
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+        if (pp + 1 < 4) fetch(pp + 1, (pp + 1) & 1);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            v4i ua[FM], ub[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                ua[i] = unpack8((u32)fa[pp & 1][i][2 * h], (u32)fa[pp & 1][i][2 * h + 1]);
+#pragma unroll
+            for (int jn = 0; jn < FN; ++jn)
+                ub[jn] = unpack8((u32)fb[pp & 1][jn][2 * h], (u32)fb[pp & 1][jn][2 * h + 1]);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int jn = 0; jn < FN; ++jn) acc[i][jn] = mfma32i8(ua[i], ub[jn], acc[i][jn]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(512, 1) void gemm_big_kernel(const uint8_t *__restrict__ A,
+                                                         const uint8_t *__restrict__ B,
+                                                         int64_t M, int64_t N, int64_t K,
+                                                         Epi e) {
+    constexpr int FM = 2, FN = 2;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * kBigStage];
+
+    const int lane = threadIdx.x & 63;
+    // wave-uniform: keeps the DMA addressing in scalar registers
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves, 64 x 64 each
+    const int64_t tiles_n = (N + kBigBN - 1) / kBigBN;
+    const int64_t tiles = ((M + kBigBM - 1) / kBigBM) * tiles_n;
+    int64_t t = blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+    const int64_t m0 = (t / tiles_n) * kBigBM;
+    const int64_t n0 = (t % tiles_n) * kBigBN;
+    const int64_t KB = K / 2;
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
+    const int steps = (int)((K + kBK - 1) / kBK);
+    const uint32_t lds0 =
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)smem;
+
+    // DMA of K-step st into stage sl: block i = 6 wave + q covers stage rows
+    // 8i .. 8i+7; lane l fetches chunk (l % 8) ^ (r & 7) of row r = 8i + l/8.
+    // Per-lane row offsets are fixed for the whole K loop: rows outside the
+    // matrix get kOob (then every chunk reads as zero); a chunk past the K
+    // tail is redirected out of range the same way.
+    uint32_t roff[kBigDmaPerWave];
+    int jc[kBigDmaPerWave];
+#pragma unroll
+    for (int q = 0; q < kBigDmaPerWave; ++q) {
+        const int i = wave * kBigDmaPerWave + q;
+        const int r = 8 * i + (lane >> 3);
+        jc[q] = ((lane & 7) ^ (r & 7)) * 16;
+        const int64_t row = 8 * i < kBigBM ? m0 + r : n0 + r - kBigBM;
+        const int64_t rows = 8 * i < kBigBM ? M : N;
+        roff[q] = row < rows ? (uint32_t)(row * KB) : kOob;
+    }
+    auto issue = [&](int st, int sl) {
+        const int64_t kb0 = (int64_t)st * kBKB;
+        const bool tail = kb0 + kBKB > KB;
+#pragma unroll
+        for (int q = 0; q < kBigDmaPerWave; ++q) {
+            const int i = wave * kBigDmaPerWave + q;
+            const uint32_t dst = lds0 + sl * kBigStage + i * 1024;
+            uint32_t off = roff[q] == kOob ? kOob : roff[q] + (uint32_t)kb0 + jc[q];
+            if (tail && kb0 + jc[q] >= KB) off = kOob;
+            dma16(8 * i < kBigBM ? ar : br, off, dst);
+        }
+    };
+
+    v16i acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int64_t gn = n0 + wn * WN + j * 16 + (lane & 15);
+        for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){};
+
+    issue(0, 0);
+    if (steps > 1) issue(1, 1);
+    int sl = 0;
+    for (int s = 0; s < steps; ++s) {
+        // this wave's DMA of step s is done (step s + 1's may stay in flight)
+        if (s + 1 < steps) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kBigDmaPerWave) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        // all waves' DMA of step s has landed, and all waves are done with
+        // the stage that step s + 2 now overwrites (read in step s - 1)
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + 2 < steps) issue(s + 2, sl == 0 ? 2 : sl - 1);
+        big_compute<FM, FN>(smem + sl * kBigStage, wm, wn, lane, acc);
+        sl = sl == 2 ? 0 : sl + 1;
+    }
+
+    // 32x32 accumulator layout: lane holds column lane & 31, rows
+    // 8 (v / 4) + 4 (lane / 32) + v % 4
+    float sbv[FN];
+    int64_t gnv[FN];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t gm = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
-                if (gm < M && gn < N) store_one(e, N, gm, gn, acc[i][j][r]);
+    for (int j = 0; j < FN; ++j) {
+        gnv[j] = n0 + wn * (FN * 32) + j * 32 + (lane & 31);
+        sbv[j] = (!e.C && gnv[j] < N) ? (float)e.sb[gnv[j]] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t gm = m0 + wm * (FM * 32) + i * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+            if (gm >= M) continue;
+            const float sa = e.C ? 0.f : (float)e.sa[gm];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                if (gnv[j] >= N) continue;
+                const int val = acc[i][j][v] >> 8;
+                if (e.C) {
+                    e.C[gm * N + gnv[j]] = val;
+                } else {
+                    const float a = (float)val * sa;
+                    f16 o = f16_rn(a * sbv[j]);
+                    if (e.bias) o = f16_rn((float)o + (float)e.bias[gnv[j]]);
+                    e.out[gm * N + gnv[j]] = o;
+                }
             }
         }
 }
@@ -216,16 +443,7 @@ __global__ __launch_bounds__(KW * 64) void gemm_skinny_kernel(const uint8_t *__r
 
     const int64_t bn = n0 + (lane & 15);
     const int kb = (lane >> 4) * 16;  // byte offset inside the 64-byte step
-    const bool bvalid = bn < N;
-    const uint8_t *bp = B + (bvalid ? bn : 0) * KB + kb;
-    const uint8_t *ap[MB];
-    bool avalid[MB];
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-        const int64_t am = m0 + i * 16 + (lane & 15);
-        avalid[i] = am < M;
-        ap[i] = A + (avalid[i] ? am : 0) * KB + kb;
-    }
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
 
     v4i acc[MB];
 #pragma unroll
@@ -235,14 +453,11 @@ __global__ __launch_bounds__(KW * 64) void gemm_skinny_kernel(const uint8_t *__r
         v4i wb[U], wa[U][MB];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t off = (s + u) * 64;
-            const bool ok = (s + u) < s1 && off + kb < KB;
-            wb[u] = (ok && bvalid) ? __builtin_nontemporal_load(reinterpret_cast<const v4i *>(bp + off))
-                                   : (v4i){0, 0, 0, 0};
+            const int64_t kbyte = (s + u < s1) ? (s + u) * 64 + kb : KB;
+            wb[u] = bload16(br, chunk_off(bn, N, kbyte, KB));
 #pragma unroll
             for (int i = 0; i < MB; ++i)
-                wa[u][i] = (ok && avalid[i]) ? *reinterpret_cast<const v4i *>(ap[i] + off)
-                                             : (v4i){0, 0, 0, 0};
+                wa[u][i] = bload16(ar, chunk_off(m0 + i * 16 + (lane & 15), M, kbyte, KB));
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -282,6 +497,11 @@ int check_gemm(const char *name, const void *A, const void *B, int64_t M, int64_
     SRQ_CHECK_ARG(K <= 131072, "%s: K=%lld > 131072 (int32 accumulator bound)", name,
                   (long long)K);
     SRQ_CHECK_ARG(M <= 0x7fffffffLL && N <= 0x7fffffffLL, "%s: M or N > 2^31-1", name);
+    // operands are read through 32-bit-offset buffer resources
+    if (M * (K / 2) >= 0xFFFFFFF0LL || N * (K / 2) >= 0xFFFFFFF0LL) {
+        srq_set_error("%s: operand larger than 4 GiB", name);
+        return SRQ_EUNSUPPORTED;
+    }
     if (M && N && K) {
         SRQ_CHECK_ARG(A && B, "%s: null operand", name);
         SRQ_CHECK_ARG(srq_aligned(A, 16) && srq_aligned(B, 16),
@@ -315,6 +535,9 @@ int run_gemm(const char *name, const void *A, const void *B, int64_t M, int64_t 
     } else if (M <= 64) {
         gemm_skinny_kernel<4, 8, 2><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
+    } else if (M >= 1024) {
+        const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
+        gemm_big_kernel<<<dim3((unsigned)tiles), dim3(64 * kBigWaves), 0, st>>>(a, b, M, N, K, e);
     } else {
         constexpr int BM = 128, BN = 128;
         const int64_t tiles = srq_cdiv(M, BM) * srq_cdiv(N, BN);

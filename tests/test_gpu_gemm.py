@@ -20,7 +20,7 @@ GEMM_SHAPES = [
     (1, 4096, 4096), (16, 4096, 4096), (1, 4096, 14336), (16, 4096, 14336),
     (17, 100, 768), (32, 768, 2048), (33, 64, 32), (64, 2048, 768), (65, 130, 4096),
     (128, 4096, 14336), (300, 513, 800), (513, 2048, 768), (2048, 4096, 14336),
-    (2, 16, 32), (5, 3, 64),
+    (2, 16, 32), (5, 3, 64), (1100, 300, 4128), (1024, 128, 256), (4096, 256, 1024),
 ]
 
 
