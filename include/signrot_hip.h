@@ -117,6 +117,72 @@ int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_t K,
                        const void *hadK, const int8_t *sign, int fp32_had,
                        float clip_ratio, void *q, void *scale, void *stream);
 
+/* ----------------------------------------------------- paged int4 KV cache */
+/* Cache layout (signrot/kernels/include/flashinfer/page.cuh:18-112):
+ *   kv_data  u8  [pages, num_layers, 2, num_heads, page_size, head_dim/2]
+ *   kv_param f16 [pages, num_layers, 2, num_heads, page_size, 2] ([scale, zero])
+ * Request b owns pages kv_indices[kv_indptr[b] .. kv_indptr[b+1]) (int32,
+ * device); its length is (#pages - 1) * page_size + last_page_offset[b] and
+ * already counts the tokens being appended.  head_dim must be 128. */
+
+/* Append one token per request (k, v u8 [batch, num_heads, head_dim/2],
+ * k_param, v_param f16 [batch, num_heads, 2]) at position length - 1.
+ * Replaces _CUDA.append_kv_i4 (bindings.cpp:606-645, page.cuh:119-164). */
+int srq_append_kv_i4(void *kv_data, void *kv_param, const int32_t *kv_indptr,
+                     const int32_t *kv_indices, const int32_t *last_page_offset,
+                     const void *k, const void *v, const void *k_param, const void *v_param,
+                     int64_t batch, int64_t num_layers, int64_t layer_idx, int64_t num_heads,
+                     int64_t page_size, int64_t head_dim, void *stream);
+
+/* Prefill: request b's tokens seqlen_indptr[b] .. seqlen_indptr[b+1] of
+ * k, v u8 [total_tokens, num_heads, head_dim/2] (and the params) go to the
+ * last (seqlen_indptr[b+1] - seqlen_indptr[b]) positions of request b.
+ * Replaces _CUDA.init_kv_i4 (bindings.cpp:561-604, page.cuh:166-219). */
+int srq_init_kv_i4(void *kv_data, void *kv_param, const int32_t *kv_indptr,
+                   const int32_t *kv_indices, const int32_t *last_page_offset, const void *k,
+                   const void *v, const void *k_param, const void *v_param,
+                   const int32_t *seqlen_indptr, int64_t batch, int64_t total_tokens,
+                   int64_t num_layers, int64_t layer_idx, int64_t num_heads, int64_t page_size,
+                   int64_t head_dim, void *stream);
+
+/* Single-query decode attention over the int4 cache of one layer:
+ * o, q f16 [batch, num_qo_heads, 128]; query head h reads KV head
+ * h / (num_qo_heads / num_kv_heads) (1 to 8 query heads per KV head; the
+ * reference's kernel is the ratio-1 case).  k̂ = float(c) * scale - zero,
+ * logits q·k̂ / sqrt(128), softmax, o = Σ p v̂ / Σ p.  With tmp != NULL and
+ * num_chunks > 1 each request is split into num_chunks slices whose partial
+ * states (tmp f32 [batch, num_qo_heads, num_chunks, 132]) are merged by a
+ * second kernel.  Replaces _CUDA.batch_decode_i4 (bindings.cpp:508-559,
+ * flashinfer.cu:11-55, decode.cuh:493-751). */
+int srq_batch_decode_i4(void *o, const void *q, const void *kv_data, const void *kv_param,
+                        const int32_t *kv_indptr, const int32_t *kv_indices,
+                        const int32_t *last_page_offset, int64_t batch, int64_t num_qo_heads,
+                        int64_t num_kv_heads, int64_t num_layers, int64_t layer_idx,
+                        int64_t page_size, int64_t head_dim, float *tmp, int64_t num_chunks,
+                        void *stream);
+
+/* ------------------------------------------------------ decode-layer glue */
+
+/* out f16 [rows, cols] = fp16(x * 1/sqrt(Σ x² / mean_dim + eps)), the sum in
+ * fp32 (no gamma: it is folded into the next linear).
+ * Replaces _CUDA.rmsnorm (bindings.cpp:423-435, fused.cu:278-309; module
+ * signrot/nn/normalization.py:19-30). */
+int srq_rmsnorm(const void *x, int64_t rows, int64_t cols, float eps, int64_t mean_dim,
+                void *out, void *stream);
+
+/* In-place rotary embedding of q f16 [n_seqs, seq_len, n_q_heads, head_dim]
+ * and k f16 [n_seqs, seq_len, n_k_heads, head_dim] with cos, sin f16
+ * [cos_batch, seq_len, head_dim] (cos_batch 1 or n_seqs); each of the three
+ * ops of x * cos + rotate_half(x) * sin rounds to fp16.
+ * Replaces _CUDA.rope_qk (bindings.cpp:383-409, fused.cu:316-362). */
+int srq_rope_qk(void *q, void *k, const void *cos, const void *sin, int64_t n_seqs,
+                int64_t seq_len, int64_t cos_batch, int64_t n_q_heads, int64_t n_k_heads,
+                int64_t head_dim, void *stream);
+
+/* out f16 [n] = fp16(fp16(silu(gate)) * up).
+ * Replaces _CUDA.swiglu (bindings.cpp:411-421, fused.cu:367-390). */
+int srq_swiglu(const void *gate, const void *up, int64_t n, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -209,3 +209,138 @@ def _check_had(name, n, hadK, K, sign, fp32_had):
             raise RuntimeError(f"{name}: hadK must be {want}")
     if sign is not None and sign.numel() != n:
         raise RuntimeError(f"{name}: sign must have {n} elements")
+
+
+# ------------------------------------------------------ paged int4 KV cache
+
+def _check_cache(name, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset):
+    _check(name, [(kv_data, "kv_data"), (kv_param, "kv_param"), (kv_indptr, "kv_indptr"),
+                  (kv_indices, "kv_indices"), (last_page_offset, "last_page_offset")],
+           [torch.uint8, torch.float16, torch.int32, torch.int32, torch.int32])
+    if kv_data.dim() != 6 or kv_param.dim() != 6:
+        raise RuntimeError(f"{name}: kv_data and kv_param must be 6D [pages, L, 2, H, P, *]")
+    if tuple(kv_param.shape[:5]) != tuple(kv_data.shape[:5]) or kv_param.shape[5] != 2:
+        raise RuntimeError(f"{name}: kv_param must be {tuple(kv_data.shape[:5]) + (2,)}")
+    if kv_indptr.dim() != 1 or kv_indices.dim() != 1 or last_page_offset.dim() != 1:
+        raise RuntimeError(f"{name}: index tensors must be 1D")
+    head_dim = kv_data.shape[5] * 2
+    if head_dim != 128:
+        raise RuntimeError(f"CHECK_EQ(head_dim, 128) failed. {head_dim} vs 128")
+    return kv_data.shape[1], kv_data.shape[3], kv_data.shape[4], head_dim
+
+
+def init_kv_i4(kv_data, kv_param, kv_indptr, kv_indices, last_page_offset, k, v, k_param,
+               v_param, seqlen_indptr, layer_idx):
+    """Prefill fill of one layer of the paged int4 cache (bindings.cpp:561-604)."""
+    L, H, P, D = _check_cache("init_kv_i4", kv_data, kv_param, kv_indptr, kv_indices,
+                              last_page_offset)
+    _check("init_kv_i4", [(k, "k"), (v, "v"), (k_param, "k_param"), (v_param, "v_param"),
+                          (seqlen_indptr, "seqlen_indptr"), (kv_data, "kv_data")],
+           [torch.uint8, torch.uint8, torch.float16, torch.float16, torch.int32, None])
+    B = last_page_offset.shape[0]
+    if kv_indptr.shape[0] != B + 1 or seqlen_indptr.shape[0] != B + 1:
+        raise RuntimeError("init_kv_i4: kv_indptr and seqlen_indptr must have batch + 1 entries")
+    if k.dim() != 3 or tuple(k.shape[1:]) != (H, D // 2) or v.shape != k.shape:
+        raise RuntimeError(f"init_kv_i4: k and v must be [tokens, {H}, {D // 2}]")
+    if tuple(k_param.shape) != (k.shape[0], H, 2) or v_param.shape != k_param.shape:
+        raise RuntimeError(f"init_kv_i4: k_param and v_param must be [tokens, {H}, 2]")
+    _call("srq_init_kv_i4", _ptr(kv_data), _ptr(kv_param), _ptr(kv_indptr), _ptr(kv_indices),
+          _ptr(last_page_offset), _ptr(k), _ptr(v), _ptr(k_param), _ptr(v_param),
+          _ptr(seqlen_indptr), B, k.shape[0], L, int(layer_idx), H, P, D, _stream(kv_data))
+
+
+def append_kv_i4(kv_data, kv_param, kv_indptr, kv_indices, last_page_offset, k, v, k_param,
+                 v_param, layer_idx):
+    """Decode append of one token per request (bindings.cpp:606-645)."""
+    L, H, P, D = _check_cache("append_kv_i4", kv_data, kv_param, kv_indptr, kv_indices,
+                              last_page_offset)
+    _check("append_kv_i4", [(k, "k"), (v, "v"), (k_param, "k_param"), (v_param, "v_param"),
+                            (kv_data, "kv_data")],
+           [torch.uint8, torch.uint8, torch.float16, torch.float16, None])
+    if k.dim() != 3 or tuple(k.shape[1:]) != (H, D // 2) or v.shape != k.shape:
+        raise RuntimeError(f"append_kv_i4: k and v must be [batch, {H}, {D // 2}]")
+    B = k.shape[0]
+    if kv_indptr.shape[0] != B + 1 or last_page_offset.shape[0] != B:
+        raise RuntimeError("append_kv_i4: index tensors do not match the batch")
+    if tuple(k_param.shape) != (B, H, 2) or v_param.shape != k_param.shape:
+        raise RuntimeError(f"append_kv_i4: k_param and v_param must be [{B}, {H}, 2]")
+    _call("srq_append_kv_i4", _ptr(kv_data), _ptr(kv_param), _ptr(kv_indptr), _ptr(kv_indices),
+          _ptr(last_page_offset), _ptr(k), _ptr(v), _ptr(k_param), _ptr(v_param), B, L,
+          int(layer_idx), H, P, D, _stream(kv_data))
+
+
+def batch_decode_i4(o, q, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset,
+                    layer_idx, tmp=None, num_chunks=1):
+    """Single-query attention over the int4 cache into o [B, Hq, 128]
+    (bindings.cpp:508-559).  Hq may be 1..8 times the cache's head count."""
+    L, H, P, D = _check_cache("batch_decode_i4", kv_data, kv_param, kv_indptr, kv_indices,
+                              last_page_offset)
+    _check("batch_decode_i4", [(o, "o"), (q, "q"), (kv_data, "kv_data")],
+           [torch.float16, torch.float16, None])
+    if o.dim() != 3 or q.dim() != 3 or o.shape != q.shape:
+        raise RuntimeError("batch_decode_i4: o and q must be the same [B, N, D] shape")
+    B, Hq = q.shape[0], q.shape[1]
+    if q.shape[2] != D:
+        raise RuntimeError(f"batch_decode_i4: q head_dim {q.shape[2]} != cache head_dim {D}")
+    if kv_indptr.shape[0] != B + 1 or last_page_offset.shape[0] != B:
+        raise RuntimeError("batch_decode_i4: index tensors do not match the batch")
+    tmp_ptr, chunks = None, 1
+    if tmp is not None and num_chunks > 1:
+        _check("batch_decode_i4", [(tmp, "tmp"), (q, "q")], [torch.float32, None])
+        if tmp.numel() != B * Hq * num_chunks * (D + 4):
+            raise RuntimeError("batch_decode_i4: tmp must be [B, N, num_chunks, head_dim + 4]")
+        tmp_ptr, chunks = _ptr(tmp), int(num_chunks)
+    _call("srq_batch_decode_i4", _ptr(o), _ptr(q), _ptr(kv_data), _ptr(kv_param),
+          _ptr(kv_indptr), _ptr(kv_indices), _ptr(last_page_offset), B, Hq, H, L,
+          int(layer_idx), P, D, tmp_ptr, chunks, _stream(q))
+
+
+# ------------------------------------------------------- decode-layer glue
+
+def rmsnorm(x, eps, mean_dim):
+    """fp16 RMSNorm without gamma over the last dim (bindings.cpp:423-435)."""
+    _check("rmsnorm", [(x, "x")])
+    if x.dtype != torch.float16:
+        raise RuntimeError("rmsnorm expects fp16 input")
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    out = torch.empty_like(x)
+    _call("srq_rmsnorm", _ptr(x), rows, cols, float(eps), int(mean_dim), _ptr(out), _stream(x))
+    return out
+
+
+def rope_qk(q, k, cos, sin):
+    """In-place rotary embedding of q, k [B, T, H, D] (bindings.cpp:383-409)."""
+    _check("rope_qk", [(q, "q"), (k, "k"), (cos, "cos"), (sin, "sin")])
+    if q.dim() != 4 or k.dim() != 4:
+        raise RuntimeError("rope_qk expects [B, T, H, D] q/k")
+    if cos.dim() != 3:
+        raise RuntimeError("rope_qk expects [B or 1, T, D] cos/sin")
+    if cos.shape != sin.shape:
+        raise RuntimeError("cos and sin must have the same shape")
+    if q.dtype != torch.float16 or k.dtype != torch.float16:
+        raise RuntimeError("rope_qk expects fp16 q/k")
+    if cos.dtype != torch.float16 or sin.dtype != torch.float16:
+        raise RuntimeError("rope_qk expects fp16 cos/sin")
+    if k.shape[0] != q.shape[0] or k.shape[1] != q.shape[1] or k.shape[3] != q.shape[3]:
+        raise RuntimeError("q and k must agree on batch, sequence and head_dim")
+    if cos.shape[1] != q.shape[1] or cos.shape[2] != q.shape[3]:
+        raise RuntimeError("cos/sin must be [B or 1, T, head_dim]")
+    if cos.shape[0] not in (1, q.shape[0]):
+        raise RuntimeError("cos/sin batch must be 1 or match q")
+    if q.shape[3] % 2:
+        raise RuntimeError("rope_qk expects an even head_dim")
+    _call("srq_rope_qk", _ptr(q), _ptr(k), _ptr(cos), _ptr(sin), q.shape[0], q.shape[1],
+          cos.shape[0], q.shape[2], k.shape[2], q.shape[3], _stream(q))
+
+
+def swiglu(gate, up):
+    """fp16(fp16(silu(gate)) * up) (bindings.cpp:411-421)."""
+    _check("swiglu", [(gate, "gate"), (up, "up")])
+    if gate.shape != up.shape:
+        raise RuntimeError("gate and up must have the same shape")
+    if gate.dtype != torch.float16 or up.dtype != torch.float16:
+        raise RuntimeError("swiglu expects fp16 input")
+    out = torch.empty_like(gate)
+    _call("srq_swiglu", _ptr(gate), _ptr(up), gate.numel(), _ptr(out), _stream(gate))
+    return out

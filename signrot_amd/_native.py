@@ -25,6 +25,15 @@ SIGNATURES = {
     "srq_hadamard_transform": [_p, _p, _i64, _i64, _f32, _i32, _p],
     "srq_online_hadamard": [_p, _p, _i64, _i64, _i64, _p, _p, _i32, _p],
     "srq_had_sign_quant": [_p, _i64, _i64, _i64, _p, _p, _i32, _f32, _p, _p, _p],
+    "srq_append_kv_i4": [_p, _p, _p, _p, _p, _p, _p, _p, _p,
+                         _i64, _i64, _i64, _i64, _i64, _i64, _p],
+    "srq_init_kv_i4": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                       _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
+    "srq_batch_decode_i4": [_p, _p, _p, _p, _p, _p, _p,
+                            _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "srq_rmsnorm": [_p, _i64, _i64, _f32, _i64, _p, _p],
+    "srq_rope_qk": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p],
+    "srq_swiglu": [_p, _p, _i64, _p, _p],
 }
 
 

@@ -45,7 +45,7 @@ static inline bool srq_aligned(const void *p, size_t a) {
     return (reinterpret_cast<uintptr_t>(p) % a) == 0;
 }
 
-static inline int64_t srq_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ static inline int64_t srq_cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ------------------------------------------------------------ wave helpers
 SRQ_DEV float wave_max(float v) {

@@ -1,0 +1,172 @@
+// Element-wise and row-wise glue of the decode layer for gfx950: RMSNorm
+// without gamma (gamma is folded into the next linear offline), in-place
+// rotary embedding of q and k, and SwiGLU.
+//
+// Semantics follow signrot/kernels/fused.cu:278-390:
+//   rmsnorm: out = fp16(x * rsqrt(sum(x^2) / mean_dim + eps)), fp32 sum
+//   rope_qk: x' = fp16(fp16(x * cos) + fp16(rotate_half(x) * sin)), per op
+//            rounding as the three-op torch expression (HF rotate_half)
+//   swiglu : out = fp16(fp16(g / (1 + exp(-g))) * up)
+#include "common.h"
+
+namespace {
+
+// ------------------------------------------------------------------ RMSNorm
+// One row per 64-lane wave (rows <= 8192 values: 16-byte loads, the row in
+// registers, one wave reduction), 4 rows per block.
+template <int VPT>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const f16 *__restrict__ x, int64_t rows,
+                                                      int nvec, float eps, float mean_dim,
+                                                      f16 *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const v8h *xr = reinterpret_cast<const v8h *>(x) + row * nvec;
+    v8h v[VPT];
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = lane + 64 * i;
+        v[i] = idx < nvec ? xr[idx] : (v8h){};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = (float)v[i][e];
+            acc = __builtin_fmaf(f, f, acc);
+        }
+    }
+    acc = wave_sum(acc);
+    const float inv = 1.0f / __builtin_sqrtf(acc / mean_dim + eps);
+    v8h *orow = reinterpret_cast<v8h *>(out) + row * nvec;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = lane + 64 * i;
+        if (idx < nvec) {
+            v8h o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = f16_rn((float)v[i][e] * inv);
+            orow[idx] = o;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_generic_kernel(const f16 *__restrict__ x,
+                                                              int64_t rows, int64_t cols,
+                                                              float eps, float mean_dim,
+                                                              f16 *__restrict__ out) {
+    __shared__ float red[4];
+    const int64_t row = blockIdx.x;
+    const f16 *xr = x + row * cols;
+    float acc = 0.f;
+    for (int64_t i = threadIdx.x; i < cols; i += 256) {
+        const float f = (float)xr[i];
+        acc = __builtin_fmaf(f, f, acc);
+    }
+    acc = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    acc = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / __builtin_sqrtf(acc / mean_dim + eps);
+    for (int64_t i = threadIdx.x; i < cols; i += 256)
+        out[row * cols + i] = f16_rn((float)xr[i] * inv);
+}
+
+// ------------------------------------------------------------------ RoPE
+// One thread per rotate_half pair (i, i + D/2) of one (token, head).
+__global__ __launch_bounds__(256) void rope_qk_kernel(f16 *__restrict__ q, f16 *__restrict__ k,
+                                                      const f16 *__restrict__ cs,
+                                                      const f16 *__restrict__ sn, int64_t tokens,
+                                                      int64_t seq_len, int cos_batch, int hq,
+                                                      int hk, int half) {
+    const int64_t total = tokens * (hq + hk) * half;
+    for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * 256) {
+        const int i = (int)(idx % half);
+        const int64_t th = idx / half;
+        const int h = (int)(th % (hq + hk));
+        const int64_t tok = th / (hq + hk);
+        f16 *base = h < hq ? q + (tok * hq + h) * (2 * half) : k + (tok * hk + (h - hq)) * (2 * half);
+        const int64_t ct = cos_batch == 1 ? tok % seq_len : tok;
+        const f16 *c = cs + ct * (2 * half);
+        const f16 *s = sn + ct * (2 * half);
+        const float x0 = (float)base[i], x1 = (float)base[i + half];
+        // products of two fp16 values are exact in fp32, so each rounds once
+        const f16 a0 = (f16)(x0 * (float)c[i]);
+        const f16 b0 = (f16)(-x1 * (float)s[i]);
+        const f16 a1 = (f16)(x1 * (float)c[i + half]);
+        const f16 b1 = (f16)(x0 * (float)s[i + half]);
+        base[i] = (f16)((float)a0 + (float)b0);
+        base[i + half] = (f16)((float)a1 + (float)b1);
+    }
+}
+
+// ------------------------------------------------------------------ SwiGLU
+__global__ __launch_bounds__(256) void swiglu_kernel(const f16 *__restrict__ g,
+                                                     const f16 *__restrict__ u, int64_t n,
+                                                     f16 *__restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * 256) {
+        const float gv = (float)g[i];
+        const f16 sl = f16_rn(gv / (1.f + expf(-gv)));
+        out[i] = (f16)((float)sl * (float)u[i]);
+    }
+}
+
+}  // namespace
+
+extern "C" int srq_rmsnorm(const void *x, int64_t rows, int64_t cols, float eps, int64_t mean_dim,
+                           void *out, void *stream) {
+    SRQ_CHECK_ARG(rows >= 0 && cols >= 0 && mean_dim > 0, "rmsnorm: bad shape");
+    if (rows == 0 || cols == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(x && out, "rmsnorm: null pointer");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t nvec = cols / 8;
+    if (cols % 8 == 0 && nvec <= 64 * 16 && srq_aligned(x, 16) && srq_aligned(out, 16)) {
+        const dim3 grid((unsigned)srq_cdiv(rows, 4));
+        const int vpt = (int)srq_cdiv(nvec, 64);
+        if (vpt <= 1)
+            rmsnorm_kernel<1><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
+        else if (vpt <= 2)
+            rmsnorm_kernel<2><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
+        else if (vpt <= 4)
+            rmsnorm_kernel<4><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
+        else if (vpt <= 8)
+            rmsnorm_kernel<8><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
+        else
+            rmsnorm_kernel<16><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
+    } else {
+        rmsnorm_generic_kernel<<<dim3((unsigned)rows), 256, 0, st>>>(
+            (const f16 *)x, rows, cols, eps, (float)mean_dim, (f16 *)out);
+    }
+    SRQ_LAUNCH_CHECK("rmsnorm");
+    return SRQ_OK;
+}
+
+extern "C" int srq_rope_qk(void *q, void *k, const void *cos, const void *sin, int64_t n_seqs,
+                           int64_t seq_len, int64_t cos_batch, int64_t n_q_heads,
+                           int64_t n_k_heads, int64_t head_dim, void *stream) {
+    SRQ_CHECK_ARG(n_seqs >= 0 && seq_len >= 0 && n_q_heads >= 0 && n_k_heads >= 0,
+                  "rope_qk: bad shape");
+    SRQ_CHECK_ARG(head_dim > 0 && head_dim % 2 == 0, "rope_qk expects an even head_dim");
+    SRQ_CHECK_ARG(cos_batch == 1 || cos_batch == n_seqs, "rope_qk: cos/sin batch must be 1 or B");
+    const int64_t tokens = n_seqs * seq_len;
+    if (tokens == 0 || n_q_heads + n_k_heads == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(q && k && cos && sin, "rope_qk: null pointer");
+    const int64_t total = tokens * (n_q_heads + n_k_heads) * (head_dim / 2);
+    const int64_t blocks = std::min<int64_t>(srq_cdiv(total, 256), 65536);
+    rope_qk_kernel<<<dim3((unsigned)blocks), 256, 0, (hipStream_t)stream>>>(
+        (f16 *)q, (f16 *)k, (const f16 *)cos, (const f16 *)sin, tokens, seq_len, (int)cos_batch,
+        (int)n_q_heads, (int)n_k_heads, (int)(head_dim / 2));
+    SRQ_LAUNCH_CHECK("rope_qk");
+    return SRQ_OK;
+}
+
+extern "C" int srq_swiglu(const void *gate, const void *up, int64_t n, void *out, void *stream) {
+    SRQ_CHECK_ARG(n >= 0, "swiglu: bad size");
+    if (n == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(gate && up && out, "swiglu: null pointer");
+    const int64_t blocks = std::min<int64_t>(srq_cdiv(n, 256), 65536);
+    swiglu_kernel<<<dim3((unsigned)blocks), 256, 0, (hipStream_t)stream>>>(
+        (const f16 *)gate, (const f16 *)up, n, (f16 *)out);
+    SRQ_LAUNCH_CHECK("swiglu");
+    return SRQ_OK;
+}

@@ -13,6 +13,9 @@ __all__ = [
     "kv_quant_pack",
     "w4a4_linear",
     "had_sign_quant",
+    "rope_qk",
+    "swiglu",
+    "rmsnorm",
     "PackedQuantizedTensor",
 ]
 
@@ -112,6 +115,26 @@ def kv_quant_pack(x):
     (packed_q, param) with param[..., 0] the scale and param[..., 1] the zero."""
     assert x.dtype == torch.float16
     return _CUDA.kv_quant_pack(x.contiguous())
+
+
+def rope_qk(q, k, cos, sin):
+    """In-place rotary embedding of q [B, T, Hq, D] and k [B, T, Hk, D], as
+    HF apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim=2) with per-op fp16
+    rounding (signrot/functional/kernel.py:158-165)."""
+    _CUDA.rope_qk(q, k, cos.contiguous(), sin.contiguous())
+    return q, k
+
+
+def swiglu(gate, up):
+    """silu(gate) * up in one launch (signrot/functional/kernel.py:168-170)."""
+    return _CUDA.swiglu(gate.contiguous(), up.contiguous())
+
+
+def rmsnorm(x, eps, mean_dim):
+    """RMSNorm over the last dim, fp32 sum, fp16 in/out
+    (signrot/functional/kernel.py:173-176)."""
+    assert x.dtype == torch.float16
+    return _CUDA.rmsnorm(x.contiguous(), eps, mean_dim)
 
 
 def sym_dequant(q, scale_row, scale_col, bits=32):
