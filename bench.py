@@ -42,6 +42,9 @@ def parse():
     p.add_argument("--outlier-mag", type=float, default=50.0)
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run plain device copies of a known size (the reference "
+                        "kernel for scaling the FETCH_SIZE / WRITE_SIZE counters)")
     p.add_argument("--cpu-rows", type=int, default=256,
                    help="rows of the CPU baseline sample")
     p.add_argument("--min-bytes", type=float, default=640e6,
@@ -111,6 +114,30 @@ def time_cpu_baseline(args, x, hadk, k, sign, wfq):
                        f"{reps} reps, {t * 1e3:.1f} ms +- {1.96 * sd * 1e3:.1f} ms each")}
 
 
+COPY_BYTES = 1 << 30
+
+
+def gemm_kernel_name(M):
+    """Kernel srq_w4a4_linear launches for M rows (gemm.hip dispatch)."""
+    if M <= 64:
+        return "gemm_skinny_kernel (srq_w4a4_linear)"
+    if M >= 1024:
+        return "gemm_big_kernel (srq_w4a4_linear)"
+    return "gemm_tile_kernel (srq_w4a4_linear)"
+
+
+def calibrate_copy(dev, reps=3):
+    """`reps` launches of torch's device copy over COPY_BYTES bytes: each
+    reads and writes exactly COPY_BYTES, so FETCH_SIZE / WRITE_SIZE per
+    dispatch divided by COPY_BYTES is the counters' scale factor."""
+    src = torch.randint(0, 255, (COPY_BYTES // 4,), dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibrate_copy_bytes": COPY_BYTES, "reps": reps}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -122,6 +149,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        calibrate_copy(dev)
+        return
     from signrot_amd import _CUDA
 
     M, K, N = args.M, args.K, args.N
@@ -209,7 +239,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 1),
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": None,
-                     "kernel": "gemm_tile_kernel (srq_w4a4_linear)",
+                     "kernel": gemm_kernel_name(M),
                      "algorithmic_ops": ops, "avg_launch_us": round(gemm_ms * 1e3, 2)},
         "kernels": {
             "had_sign_quant": {"avg_us": round(had_ms * 1e3, 2), "bound": "hbm",

@@ -88,6 +88,28 @@ SRQ_DEV float group_sum(float v) {
     return v;
 }
 
+// ------------------------------------------------------------ buffer memory
+// Raw buffer resource over [p, p + bytes): a load at or past the byte size
+// returns zeros in hardware, so tile edges need no branches.
+SRQ_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t bytes) {
+    const uint32_t n = bytes > 0xFFFFFFF0LL ? 0xFFFFFFF0u : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)n, 0x00020000);
+}
+
+// Direct global -> LDS loads (no VGPR staging).  One instruction per wave:
+// lane l's 16 (dma16) or 4 (dma4) bytes from buffer offset voff land at LDS
+// byte address lds + 16 l (resp. + 4 l).  They count in vmcnt like any vector
+// load; the caller waits with an explicit s_waitcnt before reading the LDS.
+SRQ_DEV void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(lds), "v"(voff), "s"(r) : "memory");
+}
+
+SRQ_DEV void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :: "s"(lds), "v"(voff), "s"(r) : "memory");
+}
+
 // ------------------------------------------------------- fp16 rounding
 // Round an fp32 *result* to fp16 in two steps, as the reference does
 // (fp32 op, then __float2half).  The empty asm pins the fp32 value in a

@@ -42,13 +42,6 @@ SRQ_DEV v4i mfma16(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// Raw buffer loads: an offset at or past the resource's byte size returns
-// zeros in hardware, so tile edges and the K tail need no branches.
-SRQ_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t bytes) {
-    const uint32_t n = bytes > 0xFFFFFFF0LL ? 0xFFFFFFF0u : (uint32_t)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, (int)n, 0x00020000);
-}
-
 constexpr uint32_t kOob = 0xFFFFFFF0u;
 
 SRQ_DEV v4i bload16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -262,12 +255,6 @@ constexpr int kBigStage = kBigRows * kBKB;           // 48 KiB
 constexpr int kBigDma = kBigRows / 8;                 // 1 KiB DMA blocks per stage
 constexpr int kBigWaves = 8;                          // 4 (M) x 2 (N), 64 x 64 each
 constexpr int kBigDmaPerWave = kBigDma / kBigWaves;   // 6
-
-// One 1 KiB DMA block: lane l's 16 bytes land at lds + 16 l.
-SRQ_DEV void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :: "s"(lds), "v"(voff), "s"(r) : "memory");
-}
 
 template <int FM, int FN>
 SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {

@@ -104,23 +104,56 @@ SRQ_DEV v16f mfma32h(v8h a, v8h b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// 8 uint4 codes (one dword, code 2j in the low nibble of byte j) -> 8 exact
-// fp16 values in the order [0, 4, 1, 5, 2, 6, 3, 7]
-SRQ_DEV v8h codes8(u32 w) {
-    const u32 m = 0x000F000Fu, magic = 0x64006400u;
-    const v2h off = (v2h){(f16)-1024, (f16)-1024};
-    v2h p0 = __builtin_bit_cast(v2h, (w & m) | magic) + off;
-    v2h p1 = __builtin_bit_cast(v2h, ((w >> 4) & m) | magic) + off;
-    v2h p2 = __builtin_bit_cast(v2h, ((w >> 8) & m) | magic) + off;
-    v2h p3 = __builtin_bit_cast(v2h, ((w >> 12) & m) | magic) + off;
-    v8h r;
-    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
-    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
-    return r;
+// uint4 -> fp16 by masking alone: a nibble in the low mantissa bits of an
+// fp16 with a zero exponent is the subnormal c * 2^-24 (bits 0-3, even dims)
+// or 16 c * 2^-24 (bits 4-7, odd dims), both exact.  The MFMA and dot2
+// products with these are exact in fp32; the 2^24 (even) and 2^20 (odd)
+// factors are applied to the fp32 results (on the query side for K: the odd
+// dims of q are pre-divided by 16).  The masks live in VGPRs (opaque to the
+// compiler) so each pair is one v_and_b32.
+struct Nib {
+    u32 mlo, mhi;
+};
+
+SRQ_DEV Nib make_nib() {
+    Nib n{0x000F000Fu, 0x00F000F0u};
+    asm volatile("" : "+v"(n.mlo), "+v"(n.mhi));
+    return n;
+}
+
+// codes of the low (hi = false) or high nibbles of bytes 0 and 2, scaled by
+// 2^-24 (low) or 2^-20 (high)
+SRQ_DEV v2h nib_lo(const Nib &n, u32 w) { return __builtin_bit_cast(v2h, w & n.mlo); }
+SRQ_DEV v2h nib_hi(const Nib &n, u32 w) { return __builtin_bit_cast(v2h, w & n.mhi); }
+
+// 8 uint4 codes (one dword, code 2j in the low nibble of byte j) -> 8 fp16
+// values in the order [0, 4, 1, 5, 2, 6, 3, 7]: c * 2^-24 at even dims,
+// c * 2^-20 at odd dims
+SRQ_DEV v8h codes8(const Nib &n, u32 w) {
+    const u32 w8 = w >> 8;
+    const v2h p0 = nib_lo(n, w), p1 = nib_hi(n, w), p2 = nib_lo(n, w8), p3 = nib_hi(n, w8);
+    return (v8h){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
 }
 
 // dim order of codes8 slot e (within its 8-dim group)
 SRQ_DEV int codes8_dim(int e) { return (e >> 1) + 4 * (e & 1); }
+
+template <int CTRL>
+SRQ_DEV float dpp(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// max over each 32-lane half of the wave: quad permutes, half-row and row
+// mirrors (DPP), then a swizzle that swaps the 16-lane halves
+SRQ_DEV float max32(float x) {
+    x = fmaxf(x, dpp<0xB1>(x));   // quad_perm [1, 0, 3, 2]
+    x = fmaxf(x, dpp<0x4E>(x));   // quad_perm [2, 3, 0, 1]
+    x = fmaxf(x, dpp<0x141>(x));  // row_half_mirror
+    x = fmaxf(x, dpp<0x140>(x));  // row_mirror
+    return fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(
+                                                  __builtin_bit_cast(int, x), 0x401F)));
+}
 
 struct DecodeArgs {
     Paged p;
@@ -132,209 +165,389 @@ struct DecodeArgs {
     float sm_scale_log2;
 };
 
+// Row (token) index of the K row of `entry` in page `pg`; the V row is
+// H * page rows further.
+SRQ_DEV int64_t k_row(const Paged &p, int64_t pg, int64_t head, int64_t entry) {
+    return ((pg * p.L + p.layer) * 2 * p.H + head) * p.page + entry;
+}
+
+// ---------------------------------------------------------------------------
+// One 32-token tile lives in an LDS stage of the wave:
+//   [K codes 2 KiB][V codes 2 KiB][K params 128 B][V params 128 B]
+// rows of 64 bytes, token t's 16-byte chunk c stored at chunk
+// c ^ ((t >> 2) & 3) (conflict-free reads below).
+constexpr int kStageBytes = 2 * 2048 + 2 * 128;
+// per-wave fp16 weights P[16 heads][32 tokens] (the P.V MFMA's A operand)
+constexpr int kPvBytes = 16 * kTile * 2;
+// page-table slice of a chunk kept in LDS
+constexpr int kMaxChunkPages = 256;
+
+SRQ_DEV int swz(int t, int chunk) { return t * 64 + 16 * (chunk ^ ((t >> 2) & 3)); }
+
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+
+// ds_read_b64_tr_b4: within each 16-lane group, lane i receives nibble i of
+// the 8-byte chunks addressed by lanes 0..15 of the group (nibble e of the
+// result from lane e's chunk).
+SRQ_DEV v2i ds_tr4(const uint8_t *p) {
+    return __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_v2i *)(p));
+}
+
+SRQ_DEV v4f mfma16h(v8h a, v8h b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Online-softmax state of one wave.
 template <int GP>
-__global__ __launch_bounds__(256) void decode_kernel(DecodeArgs a) {
-    // per-wave scratch: p * v_scale (fp16) [tile token][8 heads] and the
-    // tile tokens' V code row offsets; cross-wave merge buffers
-    __shared__ __attribute__((aligned(16))) f16 pv_s[4][kTile][8];
-    __shared__ int64_t voff_s[4][kTile];
-    __shared__ float m_s[4][8], d_s[4][8], z_s[4][8];
-    __shared__ __attribute__((aligned(16))) float o_s[4][8][kD];
+struct DecodeState {
+    v8h qa[8];         // Q.K^T A operand (rows = heads of the group)
+    float qs[4];       // sm_scale log2(e) * sum of q, heads 4 h2 + r
+    float m_run[4], d_part[4], z_part[4];  // S layout: heads 4 h2 + r
+    v4f acc[8];        // P.V output, N-block nb: [head 4 g + r][dim 16 nb + i]
+};
+
+// Slot of token e (0..7) in its 8-token group of the P operand: the order
+// [0, 4, 1, 5, 2, 6, 3, 7] that codes8 produces from a transposed dword.
+SRQ_DEV int p_slot(int e) { return 2 * (e & 3) + (e >> 2); }
+
+// lazy running-max slack (log2 units)
+constexpr float kLazyMax = 8.f;
+
+// One tile starting at token tb (tokens >= t1 masked), from LDS stage `sg`.
+//   Q.K^T: v_mfma_f32_32x32x16_f16, A = q (heads), B = K codes of the lane's
+//   token (lane = token tl + 32 h2, dims 64 h2 .. 64 h2 + 63).
+//   P.V:   v_mfma_f32_16x16x32_f16 per 16-dim N-block, A = P[head][token],
+//   B = V codes transposed by ds_read_b64_tr_b4: lane (i, g) gets dim
+//   16 nb + i of tokens 8 g .. 8 g + 7.
+template <int GP>
+SRQ_DEV void tile_step(DecodeState<GP> &st, const uint8_t *sg, int64_t tb, int64_t t1, int lane,
+                       float sm_scale_log2, f16 *pvt, const Nib &nib) {
+    const int tl = lane & 31, h2 = lane >> 5;
+    // ---------------- scores: lane (token tl, half h2)
+    const int sw = (tl >> 2) & 3;
+    const v4i c0 = *reinterpret_cast<const v4i *>(sg + tl * 64 + 16 * ((2 * h2) ^ sw));
+    const v4i c1 = *reinterpret_cast<const v4i *>(sg + tl * 64 + 16 * ((2 * h2 + 1) ^ sw));
+    const v2h kp = *reinterpret_cast<const v2h *>(sg + 4096 + 4 * tl);
+    const v2h vp = *reinterpret_cast<const v2h *>(sg + 4096 + 128 + 4 * tl);
+    const bool valid = tb + tl < t1;
+    // logits in log2 units: sm_scale log2(e) (2^24 scale * sacc - zero * sum q)
+    const float ks2 = (float)kp[0] * (16777216.f * sm_scale_log2), kz = (float)kp[1];
+    // V scale of the P operand entry: odd tokens meet V codes scaled by 2^-20
+    // (high nibbles of the transposed dword), so they are divided by 16
+    const float vs = valid ? (float)vp[0] * ((tl & 1) ? 0.0625f : 1.f) : 0.f;
+    const float vz = valid ? (float)vp[1] : 0.f;
+    v16f sacc = {};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sacc = mfma32h(st.qa[ks], codes8(nib, (u32)c0[ks]), sacc);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sacc = mfma32h(st.qa[4 + ks], codes8(nib, (u32)c1[ks]), sacc);
+    // lane (tl, h2) holds 2^-24 S[head 4 h2 + r][token tl] in sacc[r]
+    float lg[4], mn[4];
+    bool grow = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        lg[i] = valid ? __builtin_fmaf(ks2, sacc[i], -kz * st.qs[i]) : -INFINITY;
+        // lazy running max: it moves only when a logit exceeds it by more
+        // than kLazyMax, so the weights stay below 2^kLazyMax and the
+        // accumulators are rarely rescaled
+        grow |= lg[i] > st.m_run[i] + kLazyMax;
+        mn[i] = st.m_run[i];
+    }
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float tmax = max32(lg[i]);  // finite: token tb is valid
+            mn[i] = tmax > st.m_run[i] + kLazyMax ? tmax : st.m_run[i];
+        }
+    }
+    float pr[4], ph[4];
+    bool big = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        pr[i] = __builtin_amdgcn_exp2f(lg[i] - mn[i]);  // 0 for masked tokens
+        ph[i] = pr[i] * vs;
+        big |= 4 * h2 + i < GP && ph[i] > 32768.f;
+    }
+    if (__builtin_amdgcn_ballot_w64(big)) {
+        // an fp16 weight would overflow: move the max to this tile's
+        // (weights <= 1, |p v_scale| <= 4368)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            mn[i] = fmaxf(mn[i], max32(lg[i]));
+            pr[i] = __builtin_amdgcn_exp2f(lg[i] - mn[i]);
+            ph[i] = pr[i] * vs;
+        }
+    }
+    const int pcol = 8 * (tl >> 3) + p_slot(tl & 7);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (4 * h2 + i < GP) pvt[(4 * h2 + i) * kTile + pcol] = (f16)ph[i];
+    // rescale when a real head's max moved (wave-uniform: heads 0-3 as seen
+    // by lane 0, heads 4-7 by lane 32)
+    bool moved = false;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const bool m0 = r < GP && __builtin_amdgcn_readlane(__builtin_bit_cast(int, mn[r]), 0) !=
+                                      __builtin_amdgcn_readlane(__builtin_bit_cast(int, st.m_run[r]), 0);
+        const bool m1 = GP > 4 && __builtin_amdgcn_readlane(__builtin_bit_cast(int, mn[r]), 32) !=
+                                      __builtin_amdgcn_readlane(__builtin_bit_cast(int, st.m_run[r]), 32);
+        moved |= m0 | m1;
+    }
+    const int g = lane >> 4;
+    float al[4] = {1.f, 1.f, 1.f, 1.f};
+    if (moved) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float alpha = __builtin_amdgcn_exp2f(st.m_run[i] - mn[i]);
+            st.d_part[i] *= alpha;
+            st.z_part[i] *= alpha;
+            // alpha of the P.V rows of this lane: heads 4 g + r (g = lane >> 4)
+            const float a0 = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 0));
+            const float a1 = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, alpha), 32));
+            al[i] = g == 1 ? a1 : a0;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        st.m_run[i] = mn[i];
+        st.d_part[i] += pr[i];
+        st.z_part[i] = __builtin_fmaf(pr[i], vz, st.z_part[i]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---------------- P.V
+    if (moved) {
+#pragma unroll
+        for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) st.acc[nb][r] *= al[r];
+    }
+    const int i = lane & 15;
+    const v8h pa = *reinterpret_cast<const v8h *>(pvt + i * kTile + 8 * g);
+    // lanes e = 0..7 of group g address token 8 g + e of N-block 2 nb2, lanes
+    // 8..15 the same tokens of N-block 2 nb2 + 1
+    const int trow = 8 * g + (i & 7);
+#pragma unroll
+    for (int nb2 = 0; nb2 < 4; ++nb2) {
+        const int nbk = 2 * nb2 + (i >> 3);  // 8-byte chunk = 16-dim block
+        const v2i w = ds_tr4(sg + 2048 + swz(trow, nbk >> 1) + 8 * (nbk & 1));
+        st.acc[2 * nb2] = mfma16h(pa, codes8(nib, (u32)w[0]), st.acc[2 * nb2]);
+        st.acc[2 * nb2 + 1] = mfma16h(pa, codes8(nib, (u32)w[1]), st.acc[2 * nb2 + 1]);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+template <int NW, int S>
+struct DecodeCfg {
+    static constexpr int wave_lds = S * kStageBytes + kPvBytes;
+    static constexpr int lds = NW * wave_lds + 4 * kMaxChunkPages;
+};
+
+// Start the direct-to-LDS loads of the tile at tb (page % 32 == 0, so the 32
+// rows are consecutive entries of physical page pg: 2 KiB of K codes, 2 KiB
+// of V codes, 128 B each of K and V params).  Rows past the request end are
+// still inside the page and are masked by the consumer.  5 loads per lane.
+SRQ_DEV void dma_tile(const Paged &p, int64_t kvh, int64_t tb, int pg, int lane, uint32_t lds) {
+    const int64_t krow = k_row(p, pg, kvh, (int)tb % (int)p.page);
+    const int64_t vshift = p.H * p.page;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.data + krow * (kD / 2), 2048);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.data + (krow + vshift) * (kD / 2), 2048);
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(p.param + 2 * krow, vshift * 4 + 128);
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const int slot = 64 * half + lane;           // LDS chunk slot (row slot / 4, slot % 4)
+        const int row = slot >> 2, cs = slot & 3;
+        const uint32_t off = row * 64 + 16 * (cs ^ ((row >> 2) & 3));
+        dma16(rk, off, lds + 1024 * half);
+        dma16(rv, off, lds + 2048 + 1024 * half);
+    }
+    const uint32_t poff = lane < 32 ? 4 * lane : (uint32_t)(vshift * 4) + 4 * (lane - 32);
+    dma4(rp, poff, lds + 4096);
+}
+
+// The same tile layout filled with ordinary loads and LDS stores (any page
+// size); tokens past t1 are clamped to t1 - 1 (masked by the consumer).
+SRQ_DEV void stage_tile(const Paged &p, int64_t np0, int64_t kvh, int64_t tb, int64_t t1, int lane,
+                        uint8_t *sg) {
+    const int lastc = (int)(t1 - 1 - tb);
+    const int64_t vshift = p.H * p.page;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        const int slot = 64 * half + lane;
+        const int row = slot >> 2, cs = slot & 3;
+        const int64_t t = tb + min(row, lastc);
+        const int64_t krow = k_row(p, p.indices[np0 + t / p.page], kvh, t % p.page);
+        const v4i kc = *reinterpret_cast<const v4i *>(p.data + krow * (kD / 2) + 16 * cs);
+        const v4i vc = *reinterpret_cast<const v4i *>(p.data + (krow + vshift) * (kD / 2) + 16 * cs);
+        *reinterpret_cast<v4i *>(sg + swz(row, cs)) = kc;
+        *reinterpret_cast<v4i *>(sg + 2048 + swz(row, cs)) = vc;
+        if (half == 0 && cs == 0) {
+            reinterpret_cast<u32 *>(sg + 4096)[row] = reinterpret_cast<const u32 *>(p.param)[krow];
+            reinterpret_cast<u32 *>(sg + 4096 + 128)[row] =
+                reinterpret_cast<const u32 *>(p.param)[krow + vshift];
+        }
+    }
+    // rows 16..31 of the params come from the second half's lanes
+    {
+        const int row = 16 + (lane >> 2);
+        if ((lane & 3) == 0) {
+            const int64_t t = tb + min(row, lastc);
+            const int64_t krow = k_row(p, p.indices[np0 + t / p.page], kvh, t % p.page);
+            reinterpret_cast<u32 *>(sg + 4096)[row] = reinterpret_cast<const u32 *>(p.param)[krow];
+            reinterpret_cast<u32 *>(sg + 4096 + 128)[row] =
+                reinterpret_cast<const u32 *>(p.param)[krow + vshift];
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Decode attention of one (request, KV head, chunk); NW waves take the
+// chunk's 32-token tiles round robin.  When the page size is a multiple of 32
+// and the chunk's page-table slice fits in LDS, each wave streams its tiles
+// through an S-deep direct-to-LDS ring; otherwise each tile is staged with
+// ordinary loads.
+template <int GP, int NW, int S>
+__global__ __launch_bounds__(NW * 64) void decode_kernel(DecodeArgs a) {
+    using Cfg = DecodeCfg<NW, S>;
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    __shared__ float m_s[NW][8], d_s[NW][8], z_s[NW][8];
 
     const Paged &p = a.p;
     const int64_t b = blockIdx.x;
     const int64_t kvh = blockIdx.y;
     const int chunk = blockIdx.z;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int G = (int)a.G;
 
     const int64_t len = seq_len_of(p, b);
     const int64_t per = srq_cdiv(srq_cdiv(len, a.chunks), kTile) * kTile;
     const int64_t t0 = per * chunk;
     const int64_t t1 = (t0 + per < len) ? t0 + per : len;
-
-    // ---- query operand: rows = heads (row m < G), k-slot (h2, e) of k-step
-    // ks = dim 64 h2 + 8 ks + codes8_dim(e)
-    const int m = lane & 31, h2 = lane >> 5;
-    const int64_t qrow = (b * a.Hq + kvh * G + m) * kD;
-    v8h qa[8];
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            qa[ks][e] = m < G ? a.q[qrow + 64 * h2 + 8 * ks + codes8_dim(e)] : (f16)0;
-    // sum of q per head, for the zero-point term (heads 4 h2 .. 4 h2 + 3)
-    float qsum[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int h = 4 * h2 + r;
-        float s = 0.f;
-        if (h < G) {
-            const f16 *qr = a.q + (b * a.Hq + kvh * G + h) * kD;
-            for (int d = 0; d < kD; ++d) s += (float)qr[d];
-        }
-        qsum[r] = s;
-    }
-
-    // running state.  Token lanes (S layout): heads 4 h2 + r, r < 4.
-    float m_run[4], d_part[4], z_part[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        m_run[r] = -INFINITY;
-        d_part[r] = 0.f;
-        z_part[r] = 0.f;
-    }
-    // PV layout: lane = (tq = lane >> 4, ds = lane & 15): 8 dims 8 ds .. 8 ds + 7
-    const int tq = lane >> 4, ds = lane & 15;
-    float acc[GP][8];
-#pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-        for (int d = 0; d < 8; ++d) acc[h][d] = 0.f;
-
     const int64_t np0 = p.indptr[b];
-    for (int64_t tb = t0 + (int64_t)wave * kTile; tb < t1; tb += 4 * kTile) {
-        // ---------------- S phase: lane (token tl = lane & 31, half h2)
-        const int tl = lane & 31;
-        const int64_t t = tb + tl;
-        const bool valid = t < t1;
-        int64_t kro = 0, vro = 0;
-        u32 kw[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        float ksc = 0.f, kz = 0.f, vsc = 0.f, vz = 0.f;
-        if (valid) {
-            const int64_t page = p.indices[np0 + t / p.page];
-            const int64_t entry = t % p.page;
-            kro = row_index(p, page, 0, kvh, entry);
-            vro = row_index(p, page, 1, kvh, entry);
-            const v4i c0 = *reinterpret_cast<const v4i *>(p.data + kro * (kD / 2) + 32 * h2);
-            const v4i c1 = *reinterpret_cast<const v4i *>(p.data + kro * (kD / 2) + 32 * h2 + 16);
-            kw[0] = c0[0]; kw[1] = c0[1]; kw[2] = c0[2]; kw[3] = c0[3];
-            kw[4] = c1[0]; kw[5] = c1[1]; kw[6] = c1[2]; kw[7] = c1[3];
-            const v2h kp = *reinterpret_cast<const v2h *>(p.param + 2 * kro);
-            const v2h vp = *reinterpret_cast<const v2h *>(p.param + 2 * vro);
-            ksc = (float)kp[0];
-            kz = (float)kp[1];
-            vsc = (float)vp[0];
-            vz = (float)vp[1];
-        }
-        if (h2 == 0) voff_s[wave][tl] = valid ? vro * (kD / 2) : -1;
-        v16f sacc = {};
-#pragma unroll
-        for (int ks = 0; ks < 8; ++ks) sacc = mfma32h(qa[ks], codes8(kw[ks]), sacc);
-        // lane (tl, h2) holds S[head 4 h2 + r][token tl] in sacc[r]
-        float lg[4], tmax[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float dot = ksc * sacc[r] - kz * qsum[r];
-            lg[r] = valid ? dot * a.sm_scale_log2 : -INFINITY;
-            tmax[r] = lg[r];
-        }
-#pragma unroll
-        for (int off = 1; off < 32; off <<= 1)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) tmax[r] = fmaxf(tmax[r], __shfl_xor(tmax[r], off, 64));
-        float alpha[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float mn = fmaxf(m_run[r], tmax[r]);
-            // mn == -inf only when every token so far is masked
-            alpha[r] = mn == -INFINITY ? 1.f : exp2f(m_run[r] - mn);
-            const float pr = valid ? exp2f(lg[r] - mn) : 0.f;
-            m_run[r] = mn;
-            d_part[r] = d_part[r] * alpha[r] + pr;
-            z_part[r] = z_part[r] * alpha[r] + pr * vz;
-            pv_s[wave][tl][4 * h2 + r] = (f16)(pr * vsc);
-        }
-        // the PV lanes need alpha of all 8 heads: heads 0-3 from lane 0,
-        // heads 4-7 from lane 32 (uniform within each half)
-        float al[8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            al[r] = __shfl(alpha[r], 0, 64);
-            al[4 + r] = __shfl(alpha[r], 32, 64);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-        // ---------------- PV phase: lane (tq, ds), tokens 8 tq .. 8 tq + 7
+    // page-table slice of the chunk into LDS
+    int *pt = reinterpret_cast<int *>(lds + NW * Cfg::wave_lds);
+    const int ipage = (int)p.page;
+    const int pfirst = t0 < t1 ? (int)(t0 / ipage) : 0;
+    const int pcount = t0 < t1 ? (int)((t1 - 1) / ipage) - pfirst + 1 : 0;
+    const bool pipe = ipage % kTile == 0 && pcount <= kMaxChunkPages;
+    if (pipe)
+        for (int i = threadIdx.x; i < pcount; i += NW * 64) pt[i] = p.indices[np0 + pfirst + i];
+
+    DecodeState<GP> st;
+    // ---- query operand: row m = head (zero for m >= G); k-step ks, half h2
+    // holds dims 64 h2 + 8 ks + [0, 4, 1, 5, 2, 6, 3, 7] (the codes8 order)
+    const int m = lane & 31, h2 = lane >> 5;
+    float qpart = 0.f;
+    {
+        const f16 *qrow = a.q + (b * a.Hq + kvh * G + min(m, G - 1)) * kD + 64 * h2;
 #pragma unroll
-        for (int h = 0; h < GP; ++h)
+        for (int ks = 0; ks < 8; ++ks) {
+            v8h raw = *reinterpret_cast<const v8h *>(qrow + 8 * ks);
+            if (m >= G) raw = (v8h){};
+            // odd dims meet K codes scaled by 2^-20: divide them by 16
+            const f16 s16 = (f16)0.0625f;
+            st.qa[ks] = (v8h){raw[0], raw[4], raw[1] * s16, raw[5] * s16,
+                              raw[2], raw[6], raw[3] * s16, raw[7] * s16};
 #pragma unroll
-            for (int d = 0; d < 8; ++d) acc[h][d] *= al[h];
-#pragma unroll
-        for (int pr2 = 0; pr2 < 4; ++pr2) {
-            const int ta = 8 * tq + 2 * pr2, tb2 = ta + 1;
-            const int64_t oa = voff_s[wave][ta], ob = voff_s[wave][tb2];
-            const u32 wa = oa >= 0 ? *reinterpret_cast<const u32 *>(p.data + oa + 4 * ds) : 0u;
-            const u32 wb = ob >= 0 ? *reinterpret_cast<const u32 *>(p.data + ob + 4 * ds) : 0u;
-            // (p_a v_scale_a, p_b v_scale_b) per head as an fp16 pair
-            const v8h pa = *reinterpret_cast<const v8h *>(&pv_s[wave][ta][0]);
-            const v8h pb = *reinterpret_cast<const v8h *>(&pv_s[wave][tb2][0]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                // byte j of both tokens -> (c_a, c_b) for dims 2j (low) and 2j + 1 (high)
-                const u32 pj = ((wa >> (8 * j)) & 0xFFu) | (((wb >> (8 * j)) & 0xFFu) << 16);
-                const v2h lo = __builtin_bit_cast(v2h, (pj & 0x000F000Fu) | 0x64006400u) +
-                               (v2h){(f16)-1024, (f16)-1024};
-                const v2h hi = __builtin_bit_cast(v2h, ((pj >> 4) & 0x000F000Fu) | 0x64006400u) +
-                               (v2h){(f16)-1024, (f16)-1024};
-#pragma unroll
-                for (int h = 0; h < GP; ++h) {
-                    const v2h ph = (v2h){pa[h], pb[h]};
-                    acc[h][2 * j] = __builtin_amdgcn_fdot2(ph, lo, acc[h][2 * j], false);
-                    acc[h][2 * j + 1] = __builtin_amdgcn_fdot2(ph, hi, acc[h][2 * j + 1], false);
-                }
-            }
+            for (int e = 0; e < 8; ++e) qpart += (float)raw[e];
         }
-        __builtin_amdgcn_wave_barrier();
+    }
+    qpart += __shfl_xor(qpart, 32, 64);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        st.qs[r] = __shfl(qpart, 4 * h2 + r, 64) * a.sm_scale_log2;
+        st.m_run[r] = -INFINITY;
+        st.d_part[r] = 0.f;
+        st.z_part[r] = 0.f;
+    }
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb) st.acc[nb] = (v4f){};
+
+    const Nib nib = make_nib();
+    uint8_t *wlds = lds + wave * Cfg::wave_lds;
+    f16 *pvt = reinterpret_cast<f16 *>(wlds + S * kStageBytes);
+    const uint32_t wlds_addr = (uint32_t)(uintptr_t)wlds;
+    const int64_t stride = NW * kTile;  // a wave's tiles are NW tiles apart
+    int64_t tb = t0 + (int64_t)wave * kTile;
+    __syncthreads();  // page-table slice
+
+    if (pipe) {
+        // iteration j issues tile j + S - 1 into stage (j + S - 1) % S, then
+        // waits until only the S - 1 newest tiles' 5 loads each may be
+        // outstanding: tile j has landed
+        const int ntiles = tb < t1 ? (int)srq_cdiv(t1 - tb, stride) : 0;
+        auto issue = [&](int j) {
+            // past the end: the last tile again, so every step issues 5 loads
+            const int tj = (int)tb + min(j, ntiles - 1) * (int)stride;
+            const int pg = __builtin_amdgcn_readfirstlane(pt[tj / ipage - pfirst]);
+            dma_tile(p, kvh, tj, pg, lane, wlds_addr + (j % S) * kStageBytes);
+        };
+        if (ntiles > 0) {
+#pragma unroll
+            for (int j = 0; j < S - 1; ++j) issue(j);
+            for (int j = 0; j < ntiles; ++j) {
+                issue(j + S - 1);
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * (S - 1)) : "memory");
+                tile_step<GP>(st, wlds + (j % S) * kStageBytes, tb + (int64_t)j * stride, t1, lane,
+                              a.sm_scale_log2, pvt, nib);
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+    } else {
+        for (; tb < t1; tb += stride) {
+            stage_tile(p, np0, kvh, tb, t1, lane, wlds);
+            tile_step<GP>(st, wlds, tb, t1, lane, a.sm_scale_log2, pvt, nib);
+        }
     }
 
-    // ---- reduce within the wave
-    // d, z: sum over the 32 token lanes of each half
+    // ---- reduce d, z within each 32-lane half
 #pragma unroll
     for (int off = 1; off < 32; off <<= 1)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            d_part[r] += __shfl_xor(d_part[r], off, 64);
-            z_part[r] += __shfl_xor(z_part[r], off, 64);
+            st.d_part[r] += __shfl_xor(st.d_part[r], off, 64);
+            st.z_part[r] += __shfl_xor(st.z_part[r], off, 64);
         }
-    // o: sum over the 4 token quarters (lanes with equal ds)
-#pragma unroll
-    for (int h = 0; h < GP; ++h)
-#pragma unroll
-        for (int d = 0; d < 8; ++d) {
-            float v = acc[h][d];
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            acc[h][d] = v;
-        }
+    // the stage buffers are reused for the cross-wave merge
+    __syncthreads();
+    float(*o_s)[GP][kD] = reinterpret_cast<float(*)[GP][kD]>(lds);
     if (lane == 0 || lane == 32) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            m_s[wave][4 * h2 + r] = m_run[r];
-            d_s[wave][4 * h2 + r] = d_part[r];
-            z_s[wave][4 * h2 + r] = z_part[r];
+            m_s[wave][4 * h2 + r] = st.m_run[r];
+            d_s[wave][4 * h2 + r] = st.d_part[r];
+            z_s[wave][4 * h2 + r] = st.z_part[r];
         }
     }
-    if (tq == 0) {
+    {
+        const int g = lane >> 4, i = lane & 15;
 #pragma unroll
-        for (int h = 0; h < GP; ++h)
+        for (int r = 0; r < 4; ++r)
+            if (4 * g + r < GP)
 #pragma unroll
-            for (int d = 0; d < 8; ++d) o_s[wave][h][8 * ds + d] = acc[h][d];
+                for (int nb = 0; nb < 8; ++nb)
+                    o_s[wave][4 * g + r][16 * nb + i] = st.acc[nb][r] * 16777216.f;
     }
     __syncthreads();
 
-    // ---- merge the four waves: thread (h, d) for h < G, d < 128
-    for (int idx = threadIdx.x; idx < G * kD; idx += 256) {
+    // ---- merge the waves: thread (h, d) for h < G, d < 128
+    for (int idx = threadIdx.x; idx < G * kD; idx += NW * 64) {
         const int h = idx / kD, d = idx - h * kD;
         float mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) mx = fmaxf(mx, m_s[w][h]);
+        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, m_s[w][h]);
         float ov = 0.f, dv = 0.f, zv = 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float sc = m_s[w][h] == -INFINITY ? 0.f : exp2f(m_s[w][h] - mx);
             ov += o_s[w][h][d] * sc;
             dv += d_s[w][h] * sc;
@@ -463,6 +676,37 @@ extern "C" int srq_init_kv_i4(void *kv_data, void *kv_param, const int32_t *kv_i
                          stream);
 }
 
+namespace {
+
+// waves per block and ring depth of the decode kernel, per padded group
+// size: as many waves as the registers allow (170 / 256 VGPRs for 12 / 8
+// waves per CU), 6 tiles of each SIMD in flight
+template <int GP> struct DecodeShape { static constexpr int nw = 4, s = 2; };
+
+template <int GP>
+int launch_decode_g(const DecodeArgs &a, dim3 grid, hipStream_t st) {
+    constexpr int NW = DecodeShape<GP>::nw, S = DecodeShape<GP>::s;
+    using Cfg = DecodeCfg<NW, S>;
+    auto kern = decode_kernel<GP, NW, S>;
+    static_assert(Cfg::lds <= 160 * 1024 - 4096, "decode LDS");
+    if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            Cfg::lds) != hipSuccess) {
+        srq_set_error("batch_decode_i4: cannot reserve %d bytes of LDS", Cfg::lds);
+        return SRQ_ELAUNCH;
+    }
+    kern<<<grid, NW * 64, Cfg::lds, st>>>(a);
+    return SRQ_OK;
+}
+
+int launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {
+    if (a.G == 1) return launch_decode_g<1>(a, grid, st);
+    if (a.G == 2) return launch_decode_g<2>(a, grid, st);
+    if (a.G <= 4) return launch_decode_g<4>(a, grid, st);
+    return launch_decode_g<8>(a, grid, st);
+}
+
+}  // namespace
+
 extern "C" int srq_batch_decode_i4(void *o, const void *q, const void *kv_data,
                                    const void *kv_param, const int32_t *kv_indptr,
                                    const int32_t *kv_indices, const int32_t *last_page_offset,
@@ -481,6 +725,7 @@ extern "C" int srq_batch_decode_i4(void *o, const void *q, const void *kv_data,
                   (long long)num_qo_heads, (long long)num_kv_heads);
     if (batch == 0) return SRQ_OK;
     SRQ_CHECK_ARG(o && q, "batch_decode_i4: null q/o");
+    SRQ_CHECK_ARG(srq_aligned(q, 16), "batch_decode_i4: q must be 16-byte aligned");
     if (num_chunks < 1 || tmp == nullptr) num_chunks = 1;
     SRQ_CHECK_ARG(num_chunks <= 1024, "batch_decode_i4: num_chunks > 1024");
     DecodeArgs a;
@@ -496,14 +741,8 @@ extern "C" int srq_batch_decode_i4(void *o, const void *q, const void *kv_data,
     a.sm_scale_log2 = (1.0f / sqrtf((float)head_dim)) * 1.44269504088896340736f;
     hipStream_t st = (hipStream_t)stream;
     const dim3 grid((unsigned)batch, (unsigned)num_kv_heads, (unsigned)num_chunks);
-    if (a.G == 1)
-        decode_kernel<1><<<grid, 256, 0, st>>>(a);
-    else if (a.G == 2)
-        decode_kernel<2><<<grid, 256, 0, st>>>(a);
-    else if (a.G <= 4)
-        decode_kernel<4><<<grid, 256, 0, st>>>(a);
-    else
-        decode_kernel<8><<<grid, 256, 0, st>>>(a);
+    rc = launch_decode(a, grid, st);
+    if (rc) return rc;
     SRQ_LAUNCH_CHECK("batch_decode_i4");
     if (num_chunks > 1) {
         merge_kernel<<<dim3((unsigned)(batch * num_qo_heads)), 128, 0, st>>>(tmp, (f16 *)o,
