@@ -42,6 +42,11 @@ def parse():
     p.add_argument("--outlier-mag", type=float, default=50.0)
     p.add_argument("--seed", type=int, default=1)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-decode", action="store_true",
+                   help="skip the config-3 decode-layer measurement")
+    p.add_argument("--decode-layers", type=int, default=4,
+                   help="distinct layers (weights + cache) replayed per decode step")
+    p.add_argument("--decode-steps", type=int, default=20)
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run plain device copies of a known size (the reference "
                         "kernel for scaling the FETCH_SIZE / WRITE_SIZE counters)")
@@ -58,7 +63,7 @@ def make_inputs(args, dev):
     the sign folded by column, RTN per-channel symmetric int4."""
     from signrot_amd import _CUDA
     from signrot_amd.functional.hadamard import get_hadK
-    from signrot_amd.functional.quantization import pack_i4
+    from signrot_amd.functional.quantization import rtn_weight_pack
 
     M, K, N = args.M, args.K, args.N
     g = torch.Generator().manual_seed(args.seed)
@@ -75,15 +80,8 @@ def make_inputs(args, dev):
     sign = ((rot[t] >= 0).to(torch.int8) * 2 - 1).contiguous()
     # weights: N(0, 0.02), fold sign, RTN on the symmetric grid (A18 rule)
     w = (torch.randn(N, K, generator=g) * 0.02).half().to(dev)
-    w = w * sign
-    wf = w.float()
-    xmax = torch.maximum(wf.min(1)[0].clamp(max=0).abs(), wf.max(1)[0].clamp(min=0))
-    s = (xmax.clamp(min=1e-5) / 7).unsqueeze(1)
-    wfq = (torch.clamp(torch.round(wf / s), -7, 7) * s).half()
-    s16 = s.half()
-    codes = (wfq / s16).round().to(torch.int8)
-    wq = pack_i4(codes).contiguous()
-    return x, hadk, k, sign, wq, s16.view(-1).contiguous(), wfq
+    wq, s16, wfq = rtn_weight_pack(w * sign, symmetric_grid=True)
+    return x, hadk, k, sign, wq, s16, wfq
 
 
 def time_cpu_baseline(args, x, hadk, k, sign, wfq):
@@ -115,6 +113,76 @@ def time_cpu_baseline(args, x, hadk, k, sign, wfq):
 
 
 COPY_BYTES = 1 << 30
+
+
+def bench_decode_layer(args, dev):
+    """Config 3: one Llama-3-8B-shape decoder layer in real-quant decode
+    (hidden 4096, 32 query / 8 KV heads of 128, FFN 14336, batch 32, 4096
+    cached tokens, one new token per sequence).  `decode_layers` distinct
+    layers (own weights, own cache layer) run back to back inside one HIP
+    graph, so weights and KV pages stream from HBM as in a full model;
+    returns microseconds per layer and the per-layer HBM floor."""
+    from signrot_amd.transformers import MultiLayerPagedKVCache4Bit
+    from signrot_amd.transformers.decode_layer import W4A4LlamaDecodeLayer, rope_cos_sin
+    B, T, hidden, Hq, Hkv, D, ffn, page = 32, 4096, 4096, 32, 8, 128, 14336, 256
+    NL = args.decode_layers
+    layers = [W4A4LlamaDecodeLayer.random(hidden, Hq, Hkv, D, ffn, layer_idx=i, seed=args.seed + i,
+                                          device=dev) for i in range(NL)]
+    cache = MultiLayerPagedKVCache4Bit(B, page, T + page, dev, NL, Hkv, D, group_size=Hq // Hkv)
+    # seeded random int4 context: codes and [scale, zero] pairs of T tokens
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    cache.pages.copy_(torch.randint(0, 256, cache.pages.shape, dtype=torch.uint8, device=dev,
+                                    generator=gen))
+    cache.scales[..., 0].uniform_(0.02, 0.3, generator=gen)
+    cache.scales[..., 1].uniform_(-2.0, 2.0, generator=gen)
+    cache.length = T
+    cache._needs_init = [False] * NL
+    h0 = (torch.randn(B, 1, hidden, device=dev, generator=gen) * 0.5).half()
+    cos, sin = rope_cos_sin([T], D, layers[0].rope_theta, dev)
+
+    def step():
+        cache.length = T
+        h = h0
+        for layer in layers:
+            h = layer(h, cache, cos, sin)
+        return h
+
+    eager = step()
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        out = step()
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager), "graph replay differs from the eager decode step"
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.decode_steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us_layer = e0.elapsed_time(e1) * 1e3 / args.decode_steps / NL
+    wbytes = sum(getattr(layers[0], f"w_{n}").numel() for n in ("qkv", "o", "gu", "down"))
+    kvbytes = B * T * Hkv * 2 * (D // 2 + 4)
+    hbm = wbytes + kvbytes
+    return {
+        "workload": ("cfg3 Llama-3-8B-shape W4A4 decoder layer, decode step: batch 32, "
+                     "4096-token int4 KV context (GQA 32/8), FFN 14336, HIP graph"),
+        "us_per_layer": round(us_layer, 2),
+        "layers_per_step": NL,
+        "hbm_bytes_per_layer": hbm,
+        "achieved_GBs": round(hbm / (us_layer * 1e-6) / 1e9, 1),
+        "frac_hbm": round(hbm / (us_layer * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+        "floor_us_at_peak": round(hbm / (PEAK_HBM_GBS * 1e9) * 1e6, 2),
+    }
 
 
 def gemm_kernel_name(M):
@@ -215,6 +283,12 @@ def main():
     had_gbs = had_bytes / (had_ms * 1e-3) / 1e9
     gemm_bytes = M * K // 2 + N * K // 2 + M * 2 + N * 2 + M * N * 2
 
+    decode = None
+    if not args.no_decode:
+        del xs, wqs, qbufs, outs
+        torch.cuda.empty_cache()
+        decode = bench_decode_layer(args, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = time_cpu_baseline(args, x0, hadk, k, sign, wfq)
@@ -251,6 +325,7 @@ def main():
                             "achieved_TOPS": round(gemm_tops, 1),
                             "frac_mfma": round(gemm_tops / PEAK_INT8_TOPS, 4)},
         },
+        "decode_layer": decode,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -88,7 +88,7 @@ int srq_w4a4_linear(const void *A, const void *a_scale, const void *B,
 /* --------------------------------------------------------------- Hadamard */
 
 /* Walsh-Hadamard transform (Sylvester order) over the last dim, times scale.
- * x, out [rows, n], n a power of two, 2 <= n <= 32768; dtype 0 = f16, 1 = f32
+ * x, out [rows, n], n a power of two, 8 <= n <= 32768; dtype 0 = f16, 1 = f32
  * (in and out share the dtype); accumulation in fp32.  out may equal x.
  * Replaces fast_hadamard_transform.hadamard_transform(x, scale) (called at
  * signrot/functional/hadamard.py:81,85; transformers/kv_cache.py:72). */

@@ -689,7 +689,8 @@ int launch_decode_g(const DecodeArgs &a, dim3 grid, hipStream_t st) {
     using Cfg = DecodeCfg<NW, S>;
     auto kern = decode_kernel<GP, NW, S>;
     static_assert(Cfg::lds <= 160 * 1024 - 4096, "decode LDS");
-    if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+    if (Cfg::lds > 64 * 1024 &&
+        hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                             Cfg::lds) != hipSuccess) {
         srq_set_error("batch_decode_i4: cannot reserve %d bytes of LDS", Cfg::lds);
         return SRQ_ELAUNCH;

@@ -80,3 +80,21 @@ def unpack_ui4(x: torch.Tensor):
     lo = (x & 0x0F).to(torch.int32)
     hi = (x >> 4).to(torch.int32)
     return torch.stack((lo, hi), dim=-1).reshape(*x.shape[:-1], x.shape[-1] * 2)
+
+
+def rtn_weight_pack(w: torch.Tensor, symmetric_grid: bool = False):
+    """Per-output-channel symmetric int4 RTN of an fp16 weight [N, K] and its
+    kernel form (fake_quant/quant_utils.py:453-529 WeightQuantizer
+    find_params/quantize, then nn/linear.py:52-73 Linear4bit.from_float):
+      s = max(|min(W, 0)|, max(W, 0)).clamp(1e-5) / 7      (fp32)
+      W_fq = fp16(clamp(round(W / s), qmin, 7) * s)         qmin = -8, or -7 on
+                                                            the symmetric grid
+      codes = round(W_fq / fp16(s)) in fp16, packed; scale = fp16(s).
+    Returns (packed u8 [N, K/2], scale f16 [N], W_fq f16 [N, K])."""
+    wf = w.float()
+    xmax = torch.maximum(wf.min(1)[0].clamp(max=0).abs(), wf.max(1)[0].clamp(min=0))
+    s = (xmax.clamp(min=1e-5) / 7).unsqueeze(1)
+    wfq = (torch.clamp(torch.round(wf / s), -7 if symmetric_grid else -8, 7) * s).half()
+    s16 = s.half()
+    codes = (wfq / s16).round().to(torch.int8)
+    return pack_i4(codes).contiguous(), s16.view(-1).contiguous(), wfq
