@@ -185,6 +185,23 @@ def bench_decode_layer(args, dev):
     }
 
 
+def measured_traffic(kernel, M, K, N):
+    """HBM bytes per launch of `kernel` at this shape from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_cfg2.json,
+    already scaled by the plain-copy calibration), or None."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "traffic_cfg2.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = rec.get("kernels", {}).get(kernel)
+    if not entry or [rec.get("M"), rec.get("K"), rec.get("N")] != [M, K, N]:
+        return None
+    return entry.get("hbm_bytes")
+
+
 def gemm_kernel_name(M):
     """Kernel srq_w4a4_linear launches for M rows (gemm.hip dispatch)."""
     if M <= 64:
@@ -236,20 +253,14 @@ def main():
 
     stream = torch.cuda.current_stream()
 
-    def step(i, evs=None):
+    def step(i):
         j = i % nsets
-        if evs is not None:
-            evs[0].record(stream)
         _native.call("srq_had_sign_quant", xs[j].data_ptr(), M, K, k,
                      hadk.data_ptr() if hadk is not None else None, sign.data_ptr(), 0, 1.0,
                      qbufs[j].data_ptr(), sbufs[j].data_ptr(), stream.cuda_stream)
-        if evs is not None:
-            evs[1].record(stream)
         _native.call("srq_w4a4_linear", qbufs[j].data_ptr(), sbufs[j].data_ptr(),
                      wqs[j].data_ptr(), ws.data_ptr(), None, M, N, K, outs[j].data_ptr(),
                      stream.cuda_stream)
-        if evs is not None:
-            evs[2].record(stream)
 
     # correctness guard on the measured buffers: fused path == module path
     from signrot_amd.functional import kernel
@@ -262,19 +273,36 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     t_start = torch.cuda.Event(enable_timing=True)
     t_stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
     for i in range(args.steps):
-        step(i, evs[i])
+        step(i)
     t_stop.record(stream)
     torch.cuda.synchronize()
     total_ms = t_start.elapsed_time(t_stop)
     ms_step = total_ms / args.steps
-    had_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
-    gemm_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+
+    # per-kernel averages: each kernel alone, back to back, over the same
+    # rotating buffers, HIP events on the launch stream around the loop
+    def time_kernel(launch):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for i in range(args.steps):
+            launch(i % nsets)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    had_ms = time_kernel(lambda j: _native.call(
+        "srq_had_sign_quant", xs[j].data_ptr(), M, K, k,
+        hadk.data_ptr() if hadk is not None else None, sign.data_ptr(), 0, 1.0,
+        qbufs[j].data_ptr(), sbufs[j].data_ptr(), stream.cuda_stream))
+    gemm_ms = time_kernel(lambda j: _native.call(
+        "srq_w4a4_linear", qbufs[j].data_ptr(), sbufs[j].data_ptr(), wqs[j].data_ptr(),
+        ws.data_ptr(), None, M, N, K, outs[j].data_ptr(), stream.cuda_stream))
 
     ops = 2.0 * M * N * K
     value = ops / (ms_step * 1e-3) / 1e12
@@ -312,14 +340,16 @@ def main():
                    "M": M, "K": K, "N": N, "input_sets": nsets},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 1),
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
+                     "traffic": measured_traffic(gemm_kernel_name(M).split()[0], M, K, N),
                      "kernel": gemm_kernel_name(M),
                      "algorithmic_ops": ops, "avg_launch_us": round(gemm_ms * 1e3, 2)},
         "kernels": {
             "had_sign_quant": {"avg_us": round(had_ms * 1e3, 2), "bound": "hbm",
                                "algorithmic_bytes": had_bytes,
                                "achieved_GBs": round(had_gbs, 1),
-                               "frac_hbm": round(had_gbs / PEAK_HBM_GBS, 4)},
+                               "frac_hbm": round(had_gbs / PEAK_HBM_GBS, 4),
+                               "traffic": measured_traffic("had512_mfma_kernel<4, 1>", M, K, N)},
             "w4a4_linear": {"avg_us": round(gemm_ms * 1e3, 2), "bound": "mfma",
                             "algorithmic_bytes": gemm_bytes,
                             "achieved_TOPS": round(gemm_tops, 1),
