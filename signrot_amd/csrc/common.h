@@ -66,6 +66,24 @@ SRQ_DEV float wave_sum(float v) {
     return v;
 }
 
+// Wave max by DPP moves inside each row of 16 lanes (no LDS round trips),
+// then the four row results read back as uniform values.
+#define SRQ_DPP(v, ctrl) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), \
+                                                           ctrl, 0xF, 0xF, false))
+SRQ_DEV float wave_max_dpp(float v) {
+    v = fmaxf(v, SRQ_DPP(v, 0xB1));   // quad_perm [1, 0, 3, 2]
+    v = fmaxf(v, SRQ_DPP(v, 0x4E));   // quad_perm [2, 3, 0, 1]
+    v = fmaxf(v, SRQ_DPP(v, 0x124));  // row_ror:4
+    v = fmaxf(v, SRQ_DPP(v, 0x128));  // row_ror:8
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // Reduction over a group of G consecutive lanes (G a power of two <= 64).
 template <int G>
 SRQ_DEV float group_max(float v) {

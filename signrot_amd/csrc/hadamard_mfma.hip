@@ -1,20 +1,21 @@
-// MFMA rotation kernel for n = K * 512 (2 <= K <= 32): the rotation of the
+// MFMA rotation kernel for n = K * 512 (9 <= K <= 32): the rotation of the
 // SignRot down_proj input (Llama-3 FFN 14336 = had_28 ⊗ H_512), optionally
 // fused with the SignRot sign and the per-token int4 quantizer.
 //
-// A block of 4 waves owns one token row at a time (persistent over rows):
-// the row is staged in LDS by direct global -> LDS loads (the next row's
-// transfer overlaps this row's K-mix and quantization), and wave w computes
+// A block of 4 waves owns one token row at a time (persistent over rows).
+// The row sits in LDS in the lane order of the stage-A A operand; the next
+// row is prefetched into registers (16 bytes per lane per slot) while this
+// one is transformed, and written to LDS after this row's LDS reads are
+// done, so its HBM latency overlaps a whole row of work.  Wave w computes
 // output columns i2 in [32 w, 32 w + 32) of every 128-element segment.
 //
-// Stage A (bits 0-6 of the 512-chunk, H_128): fp16 MFMA 32x32x16 straight
-// from the global loads.  A-operand row rr of a tile is the 128-element
-// segment (chunk 8T + ct, quarter i1) with i1 = rr & 3 and
-// ct = ((rr >> 3) & 3) | (((rr >> 2) & 1) << 2); with the MFMA output layout
-// (lane l, register v -> row 8(v/4) + 4(l/32) + v%4, column l%32) this puts
-// i1 = v % 4 and chunk 8T + 4(l/32) + v/4 in the registers of the lane that
-// owns column i2 = 32 nt + l%32.  B is H_128 = H_4 ⊗ H_32 (two ±1 fragments
-// and their negations).
+// Stage A (bits 0-6 of the 512-chunk, H_128): fp16 MFMA 32x32x16.  A-operand
+// row rr of a tile is the 128-element segment (chunk 8T + ct, quarter i1)
+// with i1 = rr & 3 and ct = ((rr >> 3) & 3) | (((rr >> 2) & 1) << 2); with
+// the MFMA output layout (lane l, register v -> row 8(v/4) + 4(l/32) + v%4,
+// column l%32) this puts i1 = v % 4 and chunk 8T + 4(l/32) + v/4 in the
+// registers of the lane that owns column i2 = 32 nt + l%32.  B is
+// H_128 = H_4 ⊗ H_32 (two ±1 fragments and their negations).
 // Stage B (bits 7-8, H_4 over i1): two butterfly stages in registers.
 // y = fp16(fp32 FWHT_512 * 1/sqrt(n))        -- first rounding point
 // Stage K (hadK over the K chunks): transposed MFMA out^T[i2][c] =
@@ -22,19 +23,25 @@
 // registers (k-slot (g, e) <-> chunk 8(2s + e/4) + 4g + e%4), so lane
 // (c = l%32, g) receives runs of 4 consecutive i2 of chunk c.
 // out = fp16(fp32 sum)                        -- second rounding point
-// Then sign (xor of the fp16 sign bit), row amax (a first pass over the
-// K-mix), scale, and the exact quantizer:
-//   t = x * r, e = fma(-s, t, x), t' = fma(e, r, t) with r = 1/s.
-// For fp16 x and s the exact quotient x/s is either an fp16 rounding
-// midpoint never (12 significant bits cannot be a product of 11-bit
-// numbers) or at relative distance >= 2^-22 from every midpoint, and t' is
-// within 2^-23 of x/s, so fp16(t') == fp16(x/s): the reference's correctly
-// rounded __hdiv.  Round half even and clamp to [-8, 7] via + 1536 in fp16.
+// The K-mix result stays in registers as packed fp16 (with the sign applied
+// as an xor of the fp16 sign bit) while the block reduces the row max.
+//
+// Quantizer: s = fp16(amax / 7) (then fp16(s * clip)), r = fl32(1 / s), and
+// per element fp16(x * r) by one v_fma_mix*_f16.  For fp16 x and s that is
+// the correctly rounded fp16(x / s) of the reference's __hdiv whenever the
+// quotient is >= 2^-14, and it yields the same int4 code for every pair
+// (exhaustively checked over all fp16 pairs by tests/c/quot_exact.c).
+// Round half even to an integer by + 1544 in fp16 (ulp 1 there): the low
+// nibble is then code + 8, turned into the two's-complement nibble by an
+// xor with 8 after packing.  The clamp to [-8, 7] is skipped for a row whose
+// quotients all lie within ±7.25 (amax <= 7.25 s), the usual case for
+// clip = 1; otherwise codes are clamped in fp16 first.
 #include "common.h"
 
 namespace {
 
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
 SRQ_DEV v16f mfma32(v8h a, v8h b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
@@ -42,8 +49,51 @@ SRQ_DEV v16f mfma32(v8h a, v8h b, v16f c) {
 
 SRQ_DEV int parity(int v) { return __builtin_popcount(v) & 1; }
 
+// two fp32 -> packed fp16 pair (v_cvt_pk_f16_f32, round to nearest even)
+SRQ_DEV u32 pk16(float a, float b) {
+    return __builtin_bit_cast(u32, __builtin_convertvector((v2f){a, b}, v2h));
+}
 
-typedef __attribute__((address_space(3))) void lds_void;
+// max(m, |a|, |b|): written as a left-leaning chain, which the backend
+// turns into one v_max3_f32 with abs modifiers (an inline-asm v_max3 would
+// read MFMA results without the hazard wait states the compiler inserts)
+SRQ_DEV float absmax3(float m, float a, float b) { return fmaxf(fmaxf(m, fabsf(a)), fabsf(b)); }
+
+// fp16(x * r) for both fp16 halves of w, each rounded once from the exact
+// product (see the header for why this is the fp16 quotient x / s)
+SRQ_DEV u32 quot2(u32 w, float r) {
+    u32 q;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=&v"(q)
+        : "v"(w), "v"(r));
+    return q;
+}
+
+// packed fp16 quotients -> fp16 (round_half_even(q) + 1544): low nibble of
+// each half = code + 8
+template <bool CLAMP>
+SRQ_DEV u32 offset_codes(u32 q) {
+    v2h h = __builtin_bit_cast(v2h, q);
+    if (CLAMP)
+        h = __builtin_elementwise_min(__builtin_elementwise_max(h, (v2h){-8, -8}),
+                                      (v2h){7, 7});
+    h = h + (v2h){1544, 1544};
+    return __builtin_bit_cast(u32, h);
+}
+
+// eight offset codes (pairs a = (e0, e1), b = (e2, e3), c = (e4, e5),
+// d = (e6, e7), nibble in bits 0-3 and 16-19 of each) -> 32 bits of packed
+// two's-complement nibbles, e0 in bits 0-3 ... e7 in bits 28-31
+SRQ_DEV u32 pack8(u32 a, u32 b, u32 c, u32 d) {
+    const u32 x = __builtin_amdgcn_perm(b, a, 0x06020400u);  // e0 e2 e1 e3
+    const u32 y = __builtin_amdgcn_perm(d, c, 0x06020400u);  // e4 e6 e5 e7
+    const u32 lo = __builtin_amdgcn_perm(y, x, 0x05040100u); // e0 e2 e4 e6
+    const u32 hi = __builtin_amdgcn_perm(y, x, 0x07060302u); // e1 e3 e5 e7
+    return (lo | (hi << 4)) ^ 0x88888888u;
+}
+
+constexpr uint32_t kOob = 0xFFFFFFF0u;
 
 struct MfmaRotArgs {
     const f16 *x;
@@ -53,20 +103,43 @@ struct MfmaRotArgs {
     const int8_t *sign;   // [n] or null
     float scale;          // fp32 1/sqrt(n)
     float clip;
-    uint16_t *q;          // quant mode: packed codes, rows of n/2 bytes
+    uint8_t *q;           // quant mode: packed codes, rows of n/2 bytes
     f16 *qscale;          // quant mode: [rows]
     f16 *out;             // rotation mode: fp16 rows of n
 };
 
+// Quantize one row's packed K-mix results w (this lane: chunk ln, i2 runs
+// 32 nt + 8u + 4g .. +3 for u = 0..3, per quarter i1) and write the codes
+// to the row's LDS staging area (qrow: this lane's first code byte there).
+template <bool CLAMP>
+SRQ_DEV void quant_store(const u32 (&w)[4][8], float rcp, uint8_t *qrow) {
+#pragma unroll
+    for (int i1 = 0; i1 < 4; ++i1)
+#pragma unroll
+        for (int u = 0; u < 4; u += 2) {
+            const u32 a = offset_codes<CLAMP>(quot2(w[i1][2 * u], rcp));
+            const u32 b = offset_codes<CLAMP>(quot2(w[i1][2 * u + 1], rcp));
+            const u32 c = offset_codes<CLAMP>(quot2(w[i1][2 * u + 2], rcp));
+            const u32 d = offset_codes<CLAMP>(quot2(w[i1][2 * u + 3], rcp));
+            const u32 r = pack8(a, b, c, d);
+            // runs u and u + 1 are 8 elements (4 bytes) apart
+            uint8_t *p = qrow + i1 * 64 + 4 * u;
+            *reinterpret_cast<uint16_t *>(p) = (uint16_t)r;
+            *reinterpret_cast<uint16_t *>(p + 4) = (uint16_t)(r >> 16);
+        }
+}
+
 template <int NT, int MODE>
 __global__ __launch_bounds__(256, 2) void had512_mfma_kernel(MfmaRotArgs a) {
-    // One block of 4 waves transforms one token row at a time (persistent
-    // over rows).  The row is staged in LDS by direct global -> LDS loads in
-    // the lane order of the stage-A A operand: slot (T, ks) holds each lane's
-    // 16-byte piece at rowbuf[((T * 8 + ks) * 64 + lane) * 4].  Wave w owns
-    // output n-tile nt = w (columns i2 = 32 w .. 32 w + 31 of every
-    // 128-segment): its stage A, H_4, K-mix and quantization.
-    __shared__ __attribute__((aligned(16))) uint32_t rowbuf[NT * 8 * 64 * 4];
+    // The staged row: 128-element segment (chunk c, quarter i1) at
+    // rowbuf + 256 (4c + i1) bytes, its 16-byte piece p at position
+    // p ^ 2h(c, i1), h = i1 | ((c >> 2) & 1) << 2.  The swizzle makes both
+    // the row writes (8 lanes: 8 pieces of one segment) and the stage-A
+    // reads (8 lanes: one piece of 8 segments with distinct h) hit distinct
+    // LDS banks.  Chunks K .. 8 NT - 1 stay zero.
+    __shared__ v4i rowbuf[NT * 8 * 64];
+    // codes of one row for coalesced stores: chunk c's 256 bytes at 272 c
+    __shared__ v4i cbuf[MODE == 1 ? NT * 8 * 17 : 1];
     __shared__ float red[2][4];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -76,91 +149,156 @@ __global__ __launch_bounds__(256, 2) void had512_mfma_kernel(MfmaRotArgs a) {
     const int n = a.KC * 512;
 
     // ---- constants
-    v8h Bk[8];  // H_128 B operand for this n-tile, k-steps 0..7
+    // H_128 B operand for this n-tile, k-steps 0..7: entry e of step ks is
+    // (-1)^(parity((16 (ks & 1) + 8 g + e) & ln) ^ parity((ks >> 1) & nt)).
+    // The low 3 bits of the row index are e alone, so the parity splits into
+    // an 8-entry pattern in e (shared by all steps) and one sign per step.
+    union BkU {
+        v8h h;
+        u32 w[4];
+    } Bk[8];
+    {
+        BkU pat;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-        const bool neg = parity((ks >> 1) & nt);
+        for (int e = 0; e < 8; ++e) pat.h[e] = parity(e & ln) ? (f16)-1 : (f16)1;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const bool m = parity((16 * (ks & 1) + 8 * g + e) & ln) ^ neg;
-            Bk[ks][e] = m ? (f16)-1 : (f16)1;
+        for (int ks = 0; ks < 8; ++ks) {
+            const u32 flip = (parity((16 * (ks & 1) + 8 * g) & ln) ^ parity((ks >> 1) & nt))
+                                 ? 0x80008000u : 0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Bk[ks].w[i] = pat.w[i] ^ flip;
         }
     }
+    // hadK B operand (k-slot (g, e) <-> chunk cp = 8 (2s + e/4) + 4g + e%4,
+    // column ln) and the sign xor masks of this lane's outputs (for each i1,
+    // the 16 values v' at i2 = 32 nt + 8 (v'/4) + 4 g + v'%4 of chunk ln, as
+    // 8 fp16 pairs), fetched by independent buffer loads (out-of-range
+    // offsets read zeros) so their latencies overlap.  K is a multiple of 4,
+    // so each run of 4 cp is wholly inside or outside the table.
     v8h HB[2];
+    {
+        const __amdgpu_buffer_rsrc_t hr = make_rsrc(a.hadK, (int64_t)a.KC * a.KC * 2);
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+        for (int s = 0; s < 2; ++s)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int cp = 8 * (2 * s + e / 4) + 4 * g + (e % 4);
-            HB[s][e] = (ln < a.KC && cp < a.KC) ? a.hadK[ln * a.KC + cp] : (f16)0;
-        }
-    // sign xor masks of this lane's outputs: for each i1, the 16 values
-    // v' (i2 = 32 nt + 8 (v'/4) + 4 g + v'%4 of chunk ln) as 8 fp16 pairs
-    uint32_t msk[4][8];
+            for (int h = 0; h < 2; ++h) {
+                const int cp = 8 * (2 * s + h) + 4 * g;
+                const uint32_t off =
+                    (ln < a.KC && cp < a.KC) ? (uint32_t)((ln * a.KC + cp) * 2) : kOob;
+                const v4h v = __builtin_bit_cast(
+                    v4h, __builtin_amdgcn_raw_buffer_load_b64(hr, off, 0, 0));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) HB[s][4 * h + e] = v[e];
+            }
+    }
+    u32 msk[4][8];
 #pragma unroll
     for (int i1 = 0; i1 < 4; ++i1)
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            uint32_t m = 0;
-            if (a.sign && ln < a.KC) {
+        for (int p = 0; p < 8; ++p) msk[i1][p] = 0;
+    if (a.sign) {
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sign, n);
 #pragma unroll
-                for (int b = 0; b < 2; ++b) {
-                    const int vp = 2 * p + b;
-                    const int i2 = 32 * nt + 8 * (vp / 4) + 4 * g + (vp % 4);
-                    if (a.sign[ln * 512 + i1 * 128 + i2] < 0) m |= 0x8000u << (16 * b);
-                }
+        for (int i1 = 0; i1 < 4; ++i1)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                // int8 signs of i2 = 32 nt + 8u + 4g .. +3: bit 7 of each byte
+                const uint32_t off =
+                    ln < a.KC ? (uint32_t)(ln * 512 + i1 * 128 + 32 * nt + 8 * u + 4 * g) : kOob;
+                const u32 sw = __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
+                msk[i1][2 * u] = ((sw & 0x80u) << 8) | ((sw & 0x8000u) << 16);
+                msk[i1][2 * u + 1] = ((sw & 0x800000u) >> 8) | (sw & 0x80000000u);
             }
-            msk[i1][p] = m;
-        }
+    }
 
-    // A-operand row of this lane: segment (chunk 8T + ct, quarter i1a)
+    // Settle the prologue loads here: the empty asm consumes HB and msk,
+    // so the wait for their loads is placed once, before the row loop.
+    // Otherwise the wait-count pass, unable to prove across the loop's back
+    // edge that these loads are done, waits for them inside every row --
+    // and, counting in order, for the next row's prefetch as well.
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+        BkU t;
+        t.h = HB[s2];
+        asm volatile("" : "+v"(t.w[0]), "+v"(t.w[1]), "+v"(t.w[2]), "+v"(t.w[3]));
+        HB[s2] = t.h;
+    }
+#pragma unroll
+    for (int i1 = 0; i1 < 4; ++i1)
+#pragma unroll
+        for (int p = 0; p < 8; ++p) asm volatile("" : "+v"(msk[i1][p]));
+
+    // A-operand row of this lane in stage A: segment (chunk 8T + cta,
+    // quarter i1a), piece 2 ks + g.
     const int i1a = ln & 3;
     const int cta = ((ln >> 3) & 3) | (((ln >> 2) & 1) << 2);
-    // wave w issues the loads of slots (T, ks) with (T * 8 + ks) % 4 == w
-    auto load_row = [&](int64_t r) {
+    const int ha = i1a | (((cta >> 2) & 1) << 2);
+    const uint8_t *rowb = reinterpret_cast<const uint8_t *>(rowbuf);
+    const int rdbase = (cta * 4 + i1a) * 256 + 16 * g;
+    // Row fetch: instruction j of wave w reads chunk c = 4j + w whole (1 KB,
+    // lane l: piece l % 16 of quarter l / 16), K / 4 instructions per wave.
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.rows * n * 2);
+    const int cpw = a.KC / 4;
+    const int wi1 = lane >> 4, wp = lane & 15;
+    v4i pre[NT * 2];
+    auto gload = [&](int64_t r) {
+        const uint32_t rb = (uint32_t)(r * n * 2) + (uint32_t)(wave * 1024 + lane * 16);
 #pragma unroll
-        for (int T = 0; T < NT; ++T) {
-            const int c = 8 * T + cta;
+        for (int j = 0; j < NT * 2; ++j)
+            if (j < cpw)
+                pre[j] = __builtin_bit_cast(
+                    v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, rb + j * 4096, 0, 0));
+    };
+    auto lstore = [&]() {
 #pragma unroll
-            for (int ks = wave & 3; ks < 8; ks += 4) {
-                if (c < a.KC)
-                    __builtin_amdgcn_global_load_lds(
-                        (const void *)(a.x + r * n + c * 512 + i1a * 128 + 8 * g + 16 * ks),
-                        (lds_void *)(rowbuf + (T * 8 + ks) * 64 * 4), 16, 0, 0);
-            }
+        for (int j = 0; j < NT * 2; ++j) {
+            if (j >= cpw) continue;
+            const int c = 4 * j + wave;
+            const int h = wi1 | (((c >> 2) & 1) << 2);
+            rowbuf[(c * 4 + wi1) * 16 + (wp ^ (2 * h))] = pre[j];
         }
     };
+    for (int i = threadIdx.x; i < (NT * 8 - a.KC) * 64; i += 256)
+        rowbuf[a.KC * 64 + i] = (v4i){0, 0, 0, 0};
 
+    const int64_t step = gridDim.x;
     int64_t row = blockIdx.x;
-    if (row < a.rows) load_row(row);
-    for (int it = 0; row < a.rows; row += gridDim.x, ++it) {
-        // this wave's transfers have landed; after the barrier, everyone's
-        // (a plain s_barrier: __syncthreads' release fence would also wait
-        // for the output stores still in flight)
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (row < a.rows) {
+        gload(row);
+        lstore();
+    }
+    for (int it = 0; row < a.rows; row += step, ++it) {
+        // every wave's LDS writes of this row are done
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
+        const bool more = row + step < a.rows;
+        if (more) gload(row + step);
 
         // ---- stage A (H_128 over i2, this wave's 32 output columns) and
         // stage B (H_4 over i1), y = fp16(FWHT * 1/sqrt(n)) into the K-mix
         // A operands ka[s][i1] (k-slot e <-> tile 2s + e/4, chunk 4g + e%4)
         constexpr int NS = (NT + 1) / 2;
-        v8h ka[NS][4];
+        union KA {
+            v8h h;
+            u32 w[4];
+        } ka[NS][4];
         if (NT % 2) {
 #pragma unroll
-            for (int i1 = 0; i1 < 4; ++i1) ka[NS - 1][i1] = (v8h){};
+            for (int i1 = 0; i1 < 4; ++i1) ka[NS - 1][i1].h = (v8h){};
         }
-#pragma unroll
-        for (int T = 0; T < NT; ++T) {
-            v16f d = {};
-            const bool live = 8 * T + cta < a.KC;
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                const v8h xk = live
-                    ? *reinterpret_cast<const v8h *>(rowbuf + ((T * 8 + ks) * 64 + lane) * 4)
-                    : (v8h){};
-                d = mfma32(xk, Bk[ks], d);
-            }
+        // (slots of chunks >= K hold zeros: their prefetch read zeros).
+        // The 8 LDS reads of tile T + 1 are issued before the MFMAs of tile
+        // T (left to itself the scheduler puts each read just before its
+        // MFMA and exposes every LDS round trip).
+        v8h xk[2][8];
+        auto rd = [&](int T, int ks) {
+            return *reinterpret_cast<const v8h *>(rowb + T * 8192 + rdbase + 32 * (ks ^ ha));
+        };
+        // Stage B + first rounding point for tile T's accumulators:
+        // register v -> ka[T/2][v%4] element 4 (T%2) + v/4; the pairs
+        // (v, v + 4) are adjacent elements.
+        auto finish = [&](v16f d, int T) {
 #pragma unroll
             for (int v = 0; v < 16; v += 4) {
                 const float a0 = d[v], a1 = d[v + 1], a2 = d[v + 2], a3 = d[v + 3];
@@ -171,25 +309,83 @@ __global__ __launch_bounds__(256, 2) void had512_mfma_kernel(MfmaRotArgs a) {
                 d[v + 3] = b1 - b3;
             }
 #pragma unroll
-            for (int v = 0; v < 16; ++v)
-                ka[T / 2][v % 4][4 * (T % 2) + v / 4] = f16_rn(d[v] * a.scale);
+            for (int v = 0; v < 16; ++v) {
+                if ((v / 4) % 2) continue;
+                float lo = d[v] * a.scale, hi = d[v + 4] * a.scale;
+                // pin the fp32 products: fp16(fp32(x * s)), two roundings
+                asm volatile("" : "+v"(lo), "+v"(hi));
+                ka[T / 2][v % 4].w[2 * (T % 2) + v / 8] = pk16(lo, hi);
+            }
+        };
+        // Software pipeline over the tiles: the LDS reads of tile T + 1 and
+        // the stage-B VALU work of tile T - 1 are interleaved with the 8
+        // MFMAs of tile T, so the matrix and vector pipes overlap.
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) xk[0][ks] = rd(0, ks);
+        v16f dprev = {};
+#pragma unroll
+        for (int T = 0; T < NT; ++T) {
+            if (T + 1 < NT) {
+#pragma unroll
+                for (int ks = 0; ks < 8; ++ks) xk[(T + 1) & 1][ks] = rd(T + 1, ks);
+            }
+            v16f d = {};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) d = mfma32(xk[T & 1][ks], Bk[ks].h, d);
+            if (T > 0) finish(dprev, T - 1);
+            if (T + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (T > 0) __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            dprev = d;
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();  // every wave is done with rowbuf
-        asm volatile("" ::: "memory");
-        if (row + gridDim.x < a.rows) load_row(row + gridDim.x);
+        finish(dprev, NT - 1);
 
-        // ---- K-mix pass 1: row max of |fp16(out)| = fp16(max |out|)
+        // ---- K-mix: round to fp16, apply the sign, keep; row max of |out|
+        u32 w[4][8];
         float amax = 0.f;
 #pragma unroll
         for (int i1 = 0; i1 < 4; ++i1) {
             v16f z = {};
-            z = mfma32(ka[0][i1], HB[0], z);
-            if (NS > 1) z = mfma32(ka[NS > 1 ? 1 : 0][i1], HB[1], z);
+            z = mfma32(ka[0][i1].h, HB[0], z);
+            if (NS > 1) z = mfma32(ka[NS > 1 ? 1 : 0][i1].h, HB[1], z);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) amax = fmaxf(amax, fabsf(z[v]));
+            for (int p = 0; p < 8; ++p) {
+                amax = absmax3(amax, z[2 * p], z[2 * p + 1]);
+                w[i1][p] = pk16(z[2 * p], z[2 * p + 1]) ^ msk[i1][p];
+            }
         }
-        amax = wave_max(amax);
+        if (MODE == 0) {
+            if (ln < a.KC) {
+#pragma unroll
+                for (int i1 = 0; i1 < 4; ++i1) {
+                    // runs of 4 fp16 (8 bytes) at i2 = 32 nt + 8u + 4g
+                    f16 *orow = a.out + row * n + ln * 512 + i1 * 128 + 32 * nt + 4 * g;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        uint2 pk;
+                        pk.x = w[i1][2 * u];
+                        pk.y = w[i1][2 * u + 1];
+                        *reinterpret_cast<uint2 *>(orow + 8 * u) = pk;
+                    }
+                }
+            }
+            if (more) {
+                // every wave is done reading this row from LDS
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                lstore();
+            }
+            continue;
+        }
+
+        // ---- block row max (this barrier also ends every wave's LDS reads
+        // of the row, so the prefetched row may be written afterwards)
+        amax = wave_max_dpp(amax);
         if (lane == 0) red[it & 1][wave] = amax;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
@@ -205,60 +401,37 @@ __global__ __launch_bounds__(256, 2) void had512_mfma_kernel(MfmaRotArgs a) {
         // (saturation, NaN -> 0)
         const float sq = fmaxf((float)s16, 0x1p-126f);
         const float rcp = 1.0f / sq;
-        if (MODE == 1 && threadIdx.x == 0) a.qscale[row] = s16;
+        if (threadIdx.x == 0) a.qscale[row] = s16;
+        // row-uniform: can any |x / s| round beyond ±7?
+        const bool clampit = __builtin_amdgcn_readfirstlane(!(amax <= 7.25f * sq));
 
-        // ---- K-mix pass 2: round, sign, then quantize (or store)
+        if (ln < a.KC) {
+            uint8_t *qrow = reinterpret_cast<uint8_t *>(cbuf) + ln * 272 + 16 * nt + 2 * g;
+            if (clampit) quant_store<true>(w, rcp, qrow);
+            else quant_store<false>(w, rcp, qrow);
+        }
+        // the row's codes are staged; write them out 16 bytes per lane
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        {
+            // LDS reads of the codes, then the prefetched row into LDS, then
+            // the global stores: the wait for the prefetch (vmcnt counts in
+            // order) then does not also wait for this row's code stores
+            constexpr int R = (NT * 8 * 16 + 255) / 256;
+            const int pieces = a.KC * 16;
+            v4i cv[R];
 #pragma unroll
-        for (int i1 = 0; i1 < 4; ++i1) {
-            v16f z = {};
-            z = mfma32(ka[0][i1], HB[0], z);
-            if (NS > 1) z = mfma32(ka[NS > 1 ? 1 : 0][i1], HB[1], z);
-            uint32_t w[8];
-#pragma unroll
-            for (int p = 0; p < 8; ++p) {
-                v2h h2;
-                h2[0] = (f16)z[2 * p];
-                h2[1] = (f16)z[2 * p + 1];
-                w[p] = __builtin_bit_cast(uint32_t, h2) ^ msk[i1][p];
+            for (int r = 0; r < R; ++r) {
+                const int pc = threadIdx.x + 256 * r;
+                cv[r] = pc < pieces ? cbuf[(pc >> 4) * 17 + (pc & 15)] : (v4i){};
             }
-            if (ln >= a.KC) continue;
-            const int64_t base = (int64_t)ln * 512 + i1 * 128 + 32 * nt + 4 * g;
-            if constexpr (MODE == 0) {
-                // rotation output: runs of 4 fp16 (8 bytes) at i2 = 8u + 4g
-                f16 *orow = a.out + row * n + base;
+            if (more) lstore();
+            uint8_t *qout = a.q + row * (n / 2);
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    uint2 pk;
-                    pk.x = w[2 * u];
-                    pk.y = w[2 * u + 1];
-                    *reinterpret_cast<uint2 *>(orow + 8 * u) = pk;
-                }
-            } else {
-                uint16_t *qrow = a.q + (row * n + base) / 4;
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    uint32_t nib[2];
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        const v2h xv = __builtin_bit_cast(v2h, w[2 * u + hh]);
-                        v2h qv;
-#pragma unroll
-                        for (int b = 0; b < 2; ++b) {
-                            const float xf = (float)xv[b];
-                            const float t = xf * rcp;
-                            const float er = __builtin_fmaf(-sq, t, xf);
-                            qv[b] = (f16)__builtin_fmaf(er, rcp, t);
-                        }
-                        // clamp to [-8, 7] then + 1536: round half even to an
-                        // integer whose low nibble is the two's-complement code
-                        qv = __builtin_elementwise_min(
-                            __builtin_elementwise_max(qv, (v2h){-8, -8}), (v2h){7, 7});
-                        qv = qv + (v2h){1536, 1536};
-                        const uint32_t bits = __builtin_bit_cast(uint32_t, qv) & 0x000F000Fu;
-                        nib[hh] = (bits | (bits >> 12)) & 0xFFu;
-                    }
-                    qrow[2 * u] = (uint16_t)(nib[0] | (nib[1] << 8));
-                }
+            for (int r = 0; r < R; ++r) {
+                const int pc = threadIdx.x + 256 * r;
+                if (pc < pieces) *reinterpret_cast<v4i *>(qout + pc * 16) = cv[r];
             }
         }
     }
@@ -272,8 +445,9 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
                     hipStream_t st) {
     if (K < 9 || K > 32 || n != K * 512) return 0;
+    if (rows * n * 2 >= (int64_t)kOob) return 0;  // 32-bit buffer offsets
     if (!srq_aligned(x, 16)) return 0;
-    if (q && !srq_aligned(q, 2)) return 0;
+    if (q && !srq_aligned(q, 16)) return 0;  // 16-byte code stores
     if (out && !srq_aligned(out, 8)) return 0;
     MfmaRotArgs a{};
     a.x = (const f16 *)x;
@@ -283,7 +457,7 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     a.sign = sign;
     a.scale = 1.0f / sqrtf((float)n);
     a.clip = clip;
-    a.q = (uint16_t *)q;
+    a.q = (uint8_t *)q;
     a.qscale = (f16 *)qscale;
     a.out = (f16 *)out;
     // persistent blocks of 4 waves, up to 2 per CU (256 CUs), one row each

@@ -84,6 +84,7 @@ def test_online_hadamard_fp32_mode(C):
 
 @pytest.mark.parametrize("n,rows", [(4096, 16), (14336, 64), (28672, 5), (128, 33),
                                     (11008, 3), (32, 10), (14336, 7), (14336, 3001),
+                                    (14336, 1), (14336, 513), (14336, 1024),
                                     (6144, 9), (10240, 13)])
 @pytest.mark.parametrize("use_sign", [False, True])
 def test_had_sign_quant_bitexact(C, n, rows, use_sign):
@@ -134,6 +135,32 @@ def test_had_sign_quant_edge_cases(C, case):
         clip = 0.8
     else:
         x = (x.astype(np.float32) * 300).astype(np.float16)
+    hk = _hadk(28)
+    sign = to_dev(rng.choice([-1, 1], n).astype(np.int8))
+    xd = to_dev(x)
+    rot = C.online_hadamard(xd, hk, 28, sign)
+    q, s = C.had_sign_quant(xd, hk, 28, sign, clip)
+    qw, sw = oq.sym_quant_dynamic(to_np(rot), clip)
+    assert_bitexact(to_np(s), sw, "scale")
+    assert_bitexact(to_np(q), qw, "codes")
+
+
+@pytest.mark.parametrize("clip", [1.0, 0.8])
+def test_had_sign_quant_mixed_rows(C, clip):
+    """One launch whose persistent blocks meet rows of every kind in turn:
+    ordinary rows, all-zero rows, rows whose fp16 scale is subnormal or
+    underflows (the clamped path) and large rows -- each row's codes and
+    scale must not depend on its neighbours."""
+    n, rows = 14336, 1100
+    rng = np.random.default_rng(7)
+    x = outlier_input(rng, rows, n, n_out=8, mag=50.0).astype(np.float32)
+    kind = rng.integers(0, 5, rows)
+    x[kind == 1] = 0
+    x[kind == 2] *= 1e-6
+    x[kind == 3] = 0
+    x[np.nonzero(kind == 3)[0], 11] = 2.0 ** -24
+    x[kind == 4] *= 200
+    x = x.astype(np.float16)
     hk = _hadk(28)
     sign = to_dev(rng.choice([-1, 1], n).astype(np.int8))
     xd = to_dev(x)
