@@ -20,6 +20,8 @@
 // fp16(out + bias[n]) as torch's fp16 add (nn/linear.py:47-48).
 #include "common.h"
 
+#include <type_traits>
+
 namespace {
 
 SRQ_DEV u32 lo4(u32 w) { return (w << 4) & 0xF0F0F0F0u; }
@@ -228,22 +230,27 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t *__restric
 }
 
 // ---------------------------------------------------------------------------
-// Large-M kernel: 256 x 128 block per workgroup of 8 waves (4 x 2), each
-// wave 64 x 64 as 2 x 2 blocks of v_mfma_i32_32x32x32_i8 (the gfx950 int8
-// MFMA with the highest sustained rate); two waves per SIMD, so one wave's
-// nibble unpacking and LDS reads overlap the other's MFMAs.  K advances 256 codes (128 bytes)
-// per step through a 3-stage LDS ring filled by buffer -> LDS DMA
-// (buffer_load_dwordx4 ... lds): two steps of loads are in flight while one
-// is multiplied, without spending VGPRs, and out-of-range chunks (tile
-// edges, K tail) arrive as zeros.  The DMA is issued from inline asm and
-// its completion tracked explicitly with vmcnt, so the compiler does not
-// serialise the ring by waiting for every outstanding DMA before each LDS
-// read.  A stage holds the 256 A rows then the 128 B rows, 128 bytes each,
-// with 16-byte chunk j of row r at position j ^ (r & 7): the 16-byte
-// fragment reads (rows r .. r+15 of one chunk column) hit distinct banks.
-// A lane reads 16 bytes (32 codes) per fragment and feeds two MFMA K-slices
-// from it (half-wave g takes chunk 2p + g, bytes 0-7 then 8-15); A and B use
-// the same K mapping, so the dot products are exact.
+// Large-M kernel: 256 x 128 block per workgroup, split into two kinds of
+// waves.  Producer waves (NPROD) only move data: K advances KBB bytes
+// (2 KBB codes) per step through an NSTG-stage LDS ring filled by buffer ->
+// LDS DMA (buffer_load_dwordx4 ... lds), NSTG - 1 steps in flight, with
+// out-of-range chunks (tile edges, K tail) arriving as zeros.  Compute waves
+// (WGM x WGN, each FM x FN blocks of v_mfma_i32_32x32x32_i8, the gfx950 int8
+// MFMA with the highest sustained rate) only read LDS, unpack nibbles and
+// multiply.  Keeping the DMA issue off the compute waves matters: a burst of
+// LDS-DMA instructions stalls the issuing wave until the address unit takes
+// them, which, on the compute waves, serialised data movement with the
+// MFMAs.  One workgroup barrier per step separates "step s landed / step
+// s - 1 consumed" from "step s + NSTG - 1 may be issued".  The DMA is issued
+// from inline asm and its completion tracked explicitly with vmcnt.
+// A stage holds the 256 A rows then the 128 B rows, KBB bytes each,
+// with 16-byte chunk j of row r at position j ^ f(r), f(r) = (r / R) % C
+// for R = 256 / KBB rows per 256-byte LDS bank cycle and C = KBB / 16
+// chunks per row: the 16 rows that a 16-lane group of a fragment read
+// touches (rows r .. r+15 of one chunk column) land in 16 distinct 16-byte
+// bank groups.  A lane reads 16 bytes (32 codes) per fragment and feeds two
+// MFMA K-slices from it (half-wave g takes chunk 2p + g, bytes 0-7 then
+// 8-15); A and B use the same K mapping, so the dot products are exact.
 
 SRQ_DEV v16i mfma32i8(v4i a, v4i b, v16i c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
@@ -251,13 +258,15 @@ SRQ_DEV v16i mfma32i8(v4i a, v4i b, v16i c) {
 
 constexpr int kBigBM = 256, kBigBN = 128;
 constexpr int kBigRows = kBigBM + kBigBN;
-constexpr int kBigStage = kBigRows * kBKB;           // 48 KiB
-constexpr int kBigDma = kBigRows / 8;                 // 1 KiB DMA blocks per stage
-constexpr int kBigWaves = 8;                          // 4 (M) x 2 (N), 64 x 64 each
-constexpr int kBigDmaPerWave = kBigDma / kBigWaves;   // 6
 
-template <int FM, int FN>
+template <int KBB>
+SRQ_DEV int swz(int r) {
+    return (r / (256 / KBB)) % (KBB / 16);
+}
+
+template <int FM, int FN, int KBB>
 SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {
+    constexpr int NPP = KBB / 32;  // 16-byte fragment fetches per step
     const int rr = lane & 31;
     const int g = lane >> 5;
     v4i fa[2][FM], fb[2][FN];
@@ -266,46 +275,75 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const int r = wm * (FM * 32) + i * 32 + rr;
-            fa[slot][i] = *reinterpret_cast<const v4i *>(stage + r * kBKB + ((j ^ (r & 7)) << 4));
+            fa[slot][i] = *reinterpret_cast<const v4i *>(stage + r * KBB + ((j ^ swz<KBB>(r)) << 4));
         }
 #pragma unroll
         for (int jn = 0; jn < FN; ++jn) {
             const int r = kBigBM + wn * (FN * 32) + jn * 32 + rr;
-            fb[slot][jn] = *reinterpret_cast<const v4i *>(stage + r * kBKB + ((j ^ (r & 7)) << 4));
+            fb[slot][jn] = *reinterpret_cast<const v4i *>(stage + r * KBB + ((j ^ swz<KBB>(r)) << 4));
         }
     };
+    // K slice s = 2 pp + h: bytes 8h .. 8h + 7 of the 16-byte fragments of
+    // fetch pp.  Software pipeline: the nibble unpacking of slice s + 1 is
+    // interleaved with the MFMAs of slice s (one MFMA, then its share of
+    // the unpacking VALU work), so the vector and matrix pipes overlap.
+    v4i ua[2][FM], ub[2][FN];
+    auto unpack = [&](int sl, int buf) {
+        const int pp = sl >> 1, h = sl & 1;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+            ua[buf][i] = unpack8((u32)fa[pp & 1][i][2 * h], (u32)fa[pp & 1][i][2 * h + 1]);
+#pragma unroll
+        for (int jn = 0; jn < FN; ++jn)
+            ub[buf][jn] = unpack8((u32)fb[pp & 1][jn][2 * h], (u32)fb[pp & 1][jn][2 * h + 1]);
+    };
     fetch(0, 0);
+    unpack(0, 0);
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-        if (pp + 1 < 4) fetch(pp + 1, (pp + 1) & 1);
+    for (int sl = 0; sl < 2 * NPP; ++sl) {
+        const int pp = sl >> 1;
+        if ((sl & 1) == 0 && pp + 1 < NPP) fetch(pp + 1, (pp + 1) & 1);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            v4i ua[FM], ub[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-                ua[i] = unpack8((u32)fa[pp & 1][i][2 * h], (u32)fa[pp & 1][i][2 * h + 1]);
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int jn = 0; jn < FN; ++jn)
-                ub[jn] = unpack8((u32)fb[pp & 1][jn][2 * h], (u32)fb[pp & 1][jn][2 * h + 1]);
+                acc[i][jn] = mfma32i8(ua[sl & 1][i], ub[sl & 1][jn], acc[i][jn]);
+        if (sl + 1 < 2 * NPP) unpack(sl + 1, (sl + 1) & 1);
+        if ((sl & 1) == 0 && pp + 1 < NPP)
+            __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
+        // unpack8 is 6 VALU; spread a slice's (FM + FN) of them over its
+        // FM * FN MFMAs
+        constexpr int kValuPerMfma = (6 * (FM + FN) + FM * FN - 1) / (FM * FN);
 #pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int jn = 0; jn < FN; ++jn) acc[i][jn] = mfma32i8(ua[i], ub[jn], acc[i][jn]);
+        for (int m = 0; m < FM * FN; ++m) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (sl + 1 < 2 * NPP) __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
-__global__ __launch_bounds__(512, 1) void gemm_big_kernel(const uint8_t *__restrict__ A,
-                                                         const uint8_t *__restrict__ B,
-                                                         int64_t M, int64_t N, int64_t K,
-                                                         Epi e) {
-    constexpr int FM = 2, FN = 2;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[3 * kBigStage];
+// WGM x WGN compute waves, each FM x FN blocks of 32 x 32 (a (32 FM) x
+// (32 FN) wave tile), plus NPROD producer waves; the block tile is always
+// kBigBM x kBigBN.
+template <int NPROD, int WGM, int WGN, int FM, int FN, int KBB, int NSTG>
+__global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
+    const uint8_t *__restrict__ A, const uint8_t *__restrict__ B, int64_t M, int64_t N,
+    int64_t K, Epi e) {
+    static_assert(WGM * FM * 32 == kBigBM && WGN * FN * 32 == kBigBN, "block tile");
+    static_assert(NSTG == 3, "the producers' vmcnt waits assume one step in flight beyond the next");
+    constexpr int kCompute = WGM * WGN;
+    constexpr int kStage = kBigRows * KBB;
+    constexpr int kRowsPerDma = 1024 / KBB;               // rows per 1 KiB DMA block
+    constexpr int kDma = kBigRows / kRowsPerDma;          // DMA blocks per stage
+    constexpr int kDmaPerWave = kDma / NPROD;
+    static_assert(kDmaPerWave * NPROD == kDma, "DMA split");
+    static_assert(kDmaPerWave <= 31, "vmcnt range");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTG * kStage];
 
     const int lane = threadIdx.x & 63;
     // wave-uniform: keeps the DMA addressing in scalar registers
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave >> 1, wn = wave & 1;  // 4 x 2 waves, 64 x 64 each
     const int64_t tiles_n = (N + kBigBN - 1) / kBigBN;
     const int64_t tiles = ((M + kBigBM - 1) / kBigBM) * tiles_n;
     int64_t t = blockIdx.x;
@@ -313,62 +351,80 @@ __global__ __launch_bounds__(512, 1) void gemm_big_kernel(const uint8_t *__restr
     const int64_t m0 = (t / tiles_n) * kBigBM;
     const int64_t n0 = (t % tiles_n) * kBigBN;
     const int64_t KB = K / 2;
-    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
-    const int steps = (int)((K + kBK - 1) / kBK);
-    const uint32_t lds0 =
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)smem;
+    const int steps = (int)((KB + KBB - 1) / KBB);
 
-    // DMA of K-step st into stage sl: block i = 6 wave + q covers stage rows
-    // 8i .. 8i+7; lane l fetches chunk (l % 8) ^ (r & 7) of row r = 8i + l/8.
-    // Per-lane row offsets are fixed for the whole K loop: rows outside the
-    // matrix get kOob (then every chunk reads as zero); a chunk past the K
-    // tail is redirected out of range the same way.
-    uint32_t roff[kBigDmaPerWave];
-    int jc[kBigDmaPerWave];
+    if (wave >= kCompute) {
+        // ---- producer: DMA block i = kDmaPerWave * pw + q covers stage rows
+        // R i .. R i + R - 1 (R = kRowsPerDma); lane l fetches chunk
+        // (l % C) ^ f(r) of row r = R i + l / C.  Per-lane row offsets are
+        // fixed for the whole K loop: rows outside the matrix get kOob (then
+        // every chunk reads as zero); a chunk past the K tail is redirected
+        // out of range the same way.
+        const int pw = wave - kCompute;
+        const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
+        const uint32_t lds0 =
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)smem;
+        constexpr int C = KBB / 16;
+        uint32_t roff[kDmaPerWave];
+        int jc[kDmaPerWave];
 #pragma unroll
-    for (int q = 0; q < kBigDmaPerWave; ++q) {
-        const int i = wave * kBigDmaPerWave + q;
-        const int r = 8 * i + (lane >> 3);
-        jc[q] = ((lane & 7) ^ (r & 7)) * 16;
-        const int64_t row = 8 * i < kBigBM ? m0 + r : n0 + r - kBigBM;
-        const int64_t rows = 8 * i < kBigBM ? M : N;
-        roff[q] = row < rows ? (uint32_t)(row * KB) : kOob;
-    }
-    auto issue = [&](int st, int sl) {
-        const int64_t kb0 = (int64_t)st * kBKB;
-        const bool tail = kb0 + kBKB > KB;
-#pragma unroll
-        for (int q = 0; q < kBigDmaPerWave; ++q) {
-            const int i = wave * kBigDmaPerWave + q;
-            const uint32_t dst = lds0 + sl * kBigStage + i * 1024;
-            uint32_t off = roff[q] == kOob ? kOob : roff[q] + (uint32_t)kb0 + jc[q];
-            if (tail && kb0 + jc[q] >= KB) off = kOob;
-            dma16(8 * i < kBigBM ? ar : br, off, dst);
+        for (int q = 0; q < kDmaPerWave; ++q) {
+            const int i = pw * kDmaPerWave + q;
+            const int r = kRowsPerDma * i + lane / C;
+            jc[q] = ((lane % C) ^ swz<KBB>(r)) * 16;
+            const bool isa = kRowsPerDma * i < kBigBM;
+            const int64_t row = isa ? m0 + r : n0 + r - kBigBM;
+            roff[q] = row < (isa ? M : N) ? (uint32_t)(row * KB) : kOob;
         }
-    };
+        auto issue = [&](int st, int sl) {
+            const int64_t kb0 = (int64_t)st * KBB;
+            const bool tail = kb0 + KBB > KB;
+#pragma unroll
+            for (int q = 0; q < kDmaPerWave; ++q) {
+                const int i = pw * kDmaPerWave + q;
+                const uint32_t dst = lds0 + sl * kStage + i * 1024;
+                uint32_t off = roff[q] == kOob ? kOob : roff[q] + (uint32_t)kb0 + jc[q];
+                if (tail && kb0 + jc[q] >= KB) off = kOob;
+                dma16(kRowsPerDma * i < kBigBM ? ar : br, off, dst);
+            }
+        };
+        issue(0, 0);
+        if (steps > 1) issue(1, 1);
+        int sl = 0;
+        for (int s = 0; s < steps; ++s) {
+            // this wave's DMA of step s is done (step s + 1's may stay in
+            // flight: vmcnt counts this wave's outstanding DMA in issue order)
+            if (s + 1 < steps) {
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave) : "memory");
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            // every producer's DMA of step s has landed, and every compute
+            // wave is done with the stage that step s + 2 now overwrites
+            // (read in step s - 1)
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (s + 2 < steps) issue(s + 2, sl == 0 ? 2 : sl - 1);
+            sl = sl == 2 ? 0 : sl + 1;
+        }
+        // the compute waves meet no barrier after their K loop, so the
+        // producers end here
+        return;
+    }
 
+    // ---- compute
+    const int wm = wave / WGN, wn = wave % WGN;
     v16i acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){};
-
-    issue(0, 0);
-    if (steps > 1) issue(1, 1);
     int sl = 0;
     for (int s = 0; s < steps; ++s) {
-        // this wave's DMA of step s is done (step s + 1's may stay in flight)
-        if (s + 1 < steps) {
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kBigDmaPerWave) : "memory");
-        } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        // all waves' DMA of step s has landed, and all waves are done with
-        // the stage that step s + 2 now overwrites (read in step s - 1)
+        // step s has landed; every wave is done with step s - 1
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        if (s + 2 < steps) issue(s + 2, sl == 0 ? 2 : sl - 1);
-        big_compute<FM, FN>(smem + sl * kBigStage, wm, wn, lane, acc);
+        big_compute<FM, FN, KBB>(smem + sl * kStage, wm, wn, lane, acc);
         sl = sl == 2 ? 0 : sl + 1;
     }
 
@@ -524,11 +580,21 @@ int run_gemm(const char *name, const void *A, const void *B, int64_t M, int64_t 
             a, b, M, N, K, e);
     } else if (M >= 1024) {
         const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
-        gemm_big_kernel<<<dim3((unsigned)tiles), dim3(64 * kBigWaves), 0, st>>>(a, b, M, N, K, e);
+        // 4 compute waves (128 x 64 each) + 4 producer waves
+        gemm_big_kernel<4, 2, 2, 4, 2, 128, 3><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(
+            a, b, M, N, K, e);
     } else {
-        constexpr int BM = 128, BN = 128;
-        const int64_t tiles = srq_cdiv(M, BM) * srq_cdiv(N, BN);
-        gemm_tile_kernel<BM, BN><<<dim3((unsigned)tiles), dim3(256), 0, st>>>(a, b, M, N, K, e);
+        // mid-size M: the tile shrinks with M so the grid still covers the
+        // 256 CUs (at N = 4096: 256 workgroups for M = 128, 256, 512)
+        auto tile = [&](auto bm, auto bn) {
+            constexpr int BM = decltype(bm)::value, BN = decltype(bn)::value;
+            const int64_t tiles = srq_cdiv(M, BM) * srq_cdiv(N, BN);
+            gemm_tile_kernel<BM, BN><<<dim3((unsigned)tiles), dim3(256), 0, st>>>(a, b, M, N, K, e);
+        };
+        if (M <= 128) tile(std::integral_constant<int, 64>{}, std::integral_constant<int, 32>{});
+        else if (M <= 256) tile(std::integral_constant<int, 64>{}, std::integral_constant<int, 64>{});
+        else if (M <= 512) tile(std::integral_constant<int, 128>{}, std::integral_constant<int, 64>{});
+        else tile(std::integral_constant<int, 128>{}, std::integral_constant<int, 128>{});
     }
     SRQ_LAUNCH_CHECK(name);
     return SRQ_OK;
