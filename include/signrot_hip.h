@@ -183,6 +183,60 @@ int srq_rope_qk(void *q, void *k, const void *cos, const void *sin, int64_t n_se
  * Replaces _CUDA.swiglu (bindings.cpp:411-421, fused.cu:367-390). */
 int srq_swiglu(const void *gate, const void *up, int64_t n, void *out, void *stream);
 
+/* --------------------------------------------------------------- MoE */
+
+/* Grouped int4 x int4 -> int32 GEMM over `problem_count` problems whose
+ * descriptors live in device memory (nothing is read on the host, so the call
+ * is graph-capturable with data-dependent sizes): problem p has
+ * (m, n, k) = problem_sizes[3p .. 3p+2] (int32), A at ptr_A[p] (packed int4,
+ * row stride lda[p] codes), B at ptr_B[p] (packed int4 [n, k/2], row stride
+ * ldb[p] codes), and writes C_p[i * ldc[p] + j] = sum_k A_p[i,k] B_p[j,k]
+ * (int32) at ptr_C[p].  Each k must be a multiple of 32 and <= 131072 (not
+ * checkable on the host).  signed_a == 0 (unsigned asymmetric activations)
+ * returns SRQ_EUNSUPPORTED.  Per element identical to srq_matmul_s4s4 on
+ * each problem.
+ * Replaces _CUDA.matmul_grouped (signrot/kernels/bindings.cpp:49-91,
+ * gemm_grouped.cu:54-107). */
+int srq_matmul_grouped(const int32_t *problem_sizes, const int64_t *ptr_A,
+                       const int64_t *ptr_B, const int64_t *ptr_C, const int64_t *lda,
+                       const int64_t *ldb, const int64_t *ldc, int64_t problem_count,
+                       int signed_a, void *stream);
+
+/* Fused grouped W4A4 linear of the MoE block: expert e owns rows
+ * expert_offsets[e] .. expert_offsets[e+1] (device int32 [num_experts + 1],
+ * non-decreasing, last <= rows) of A u8 [rows, K/2]; B u8 [num_experts, N,
+ * K/2]; out f16 [rows, N] = fp16((float(A_e · B_eᵀ) * float(a_scale[row]))
+ * * float(b_scale[e, N])).  Rows outside every expert's range are not
+ * written.  Bit-identical to srq_matmul_grouped followed by
+ * srq_sym_dequant_moe.  Replaces the matmul_grouped + sym_dequant_moe pair
+ * of SignRotMoEBlock._gemm_dequant_grouped (signrot/nn/moe.py:126-136). */
+int srq_w4a4_linear_moe(const void *A, const void *a_scale, const void *B, const void *b_scale,
+                        const int32_t *expert_offsets, int64_t num_experts, int64_t rows,
+                        int64_t N, int64_t K, void *out, void *stream);
+
+/* Per-row symmetric int4 quantization of expert-sorted rows with the
+ * per-expert SignRot sign fused in: row r is multiplied by
+ * sign[expert_ids[r]] (int8 ±1 [num_experts, cols], or NULL) and quantized
+ * as srq_sym_quant_dynamic.  q u8 [rows, ceil(cols/2)], scale f16 [rows].
+ * An expert id outside [0, num_experts) uses sign +1.
+ * Replaces _CUDA.sym_quant_dynamic_moe (signrot/kernels/bindings.cpp:108-132,
+ * moe.cu:60-101, 181-188). */
+int srq_sym_quant_dynamic_moe(const void *x, const int8_t *sign, const int32_t *expert_ids,
+                              int64_t num_experts, int64_t rows, int64_t cols, float clip_ratio,
+                              void *q, void *scale, void *stream);
+
+/* Expert-indexed dequant: out f16 [rows, cols] = fp16((float(q[r,c] -
+ * zero_row[r] * w_sum[e,c]) * float(scale_row[r])) * float(w_scales[e,c])),
+ * e = expert_ids[r]; the int32 correction (two's-complement arithmetic) only
+ * when zero_row (int8 [rows]) and w_sum (int32 [num_experts, cols]) are both
+ * given.  An expert id outside [0, num_experts) reads scale 0.
+ * Replaces _CUDA.sym_dequant_moe (signrot/kernels/bindings.cpp:161-206,
+ * moe.cu:202-238). */
+int srq_sym_dequant_moe(const int32_t *q, const void *scale_row, const void *w_scales,
+                        const int32_t *expert_ids, const int8_t *zero_row, const int32_t *w_sum,
+                        int64_t num_experts, int64_t rows, int64_t cols, void *out,
+                        void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,7 @@ Added ops (no reference counterpart, fused forms of reference chains):
   w4a4_linear     = matmul + sym_dequant (+ bias)            nn/linear.py:45-50
   online_hadamard = matmul_hadU_cuda + sign multiply          nn/hadamard.py:26-42
   had_sign_quant  = online_hadamard + sym_quant_dynamic       modeling_llama.py:134-138
+  w4a4_linear_moe = matmul_grouped + sym_dequant_moe          nn/moe.py:126-136
 """
 import torch
 
@@ -343,4 +344,118 @@ def swiglu(gate, up):
         raise RuntimeError("swiglu expects fp16 input")
     out = torch.empty_like(gate)
     _call("srq_swiglu", _ptr(gate), _ptr(up), gate.numel(), _ptr(out), _stream(gate))
+    return out
+
+
+# -------------------------------------------------------------------- MoE
+
+def matmul_grouped(problem_sizes, ptr_A, ptr_B, ptr_C, lda, ldb, ldc, signed_a=True):
+    """Grouped int4 GEMM, C_p = A_p · B_pᵀ (int32) per problem, all problem
+    descriptors in device memory (bindings.cpp:49-91): problem_sizes int32
+    [P, 3] rows (m, n, k); ptr_* int64 [P] device addresses; ld* int64 [P]
+    row strides (codes for A/B, int32 elements for C).  Writes through ptr_C;
+    returns None.  signed_a=False (unsigned asymmetric A) is not part of this
+    build's W4A4 path."""
+    name = "matmul_grouped"
+    _check(name, [(problem_sizes, "problem_sizes"), (ptr_A, "ptr_A"), (ptr_B, "ptr_B"),
+                  (ptr_C, "ptr_C"), (lda, "lda"), (ldb, "ldb"), (ldc, "ldc")])
+    if problem_sizes.dtype != torch.int32 or problem_sizes.dim() != 2 or \
+            problem_sizes.shape[1] != 3:
+        raise RuntimeError("problem_sizes must be int32 [problem_count, 3] (m, n, k) rows")
+    P = problem_sizes.shape[0]
+    for t in (ptr_A, ptr_B, ptr_C, lda, ldb, ldc):
+        if t.dtype != torch.int64 or t.numel() != P:
+            raise RuntimeError("pointer/ld arrays must be int64 with one entry per problem")
+    _call("srq_matmul_grouped", _ptr(problem_sizes), _ptr(ptr_A), _ptr(ptr_B), _ptr(ptr_C),
+          _ptr(lda), _ptr(ldb), _ptr(ldc), P, 1 if signed_a else 0, _stream(problem_sizes))
+
+
+def _moe_sign(name, sign, cols):
+    if sign is None:
+        return None
+    _check(name, [(sign, "sign")])
+    if sign.dtype != torch.int8 or sign.dim() != 2 or sign.shape[1] != cols:
+        raise RuntimeError(f"{name}: sign must be int8 [num_experts, cols]")
+    return sign
+
+
+def sym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio=1.0):
+    """sym_quant_dynamic of expert-sorted rows with the per-expert sign fused:
+    row r is multiplied by sign[expert_ids[r]] first (bindings.cpp:108-132).
+    Returns (q u8 [rows, ceil(cols/2)], scale f16 [rows, 1])."""
+    name = "sym_quant_dynamic_moe"
+    _check(name, [(x, "x"), (expert_ids, "expert_ids")])
+    if x.dim() != 2 or x.dtype != torch.float16:
+        raise RuntimeError("sym_quant_dynamic_moe expects a 2D fp16 [rows, cols] tensor")
+    if expert_ids.dtype != torch.int32 or expert_ids.numel() != x.shape[0]:
+        raise RuntimeError("expert_ids must be int32 with one entry per row")
+    rows, cols = x.shape
+    sign = _moe_sign(name, sign, cols)
+    if sign is not None:
+        _check(name, [(x, "x"), (sign, "sign")])
+    E = sign.shape[0] if sign is not None else 0
+    q = torch.empty((rows, (cols + 1) // 2), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((rows, 1), dtype=torch.float16, device=x.device)
+    _call("srq_sym_quant_dynamic_moe", _ptr(x), _ptr(sign), _ptr(expert_ids), E, rows, cols,
+          float(clip_ratio), _ptr(q), _ptr(scale), _stream(x))
+    return q, scale
+
+
+def asym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio=1.0):
+    """The asymmetric activation path (bindings.cpp:134-159) is not part of
+    this build's W4A4 path."""
+    raise RuntimeError("asym_quant_dynamic_moe: asymmetric activations are not part of this "
+                       "build's W4A4 path")
+
+
+def sym_dequant_moe(q, scale_row, w_scales, expert_ids, zero_row=None, w_sum=None):
+    """Expert-indexed dequant (bindings.cpp:161-206): out f16 [rows, cols] =
+    fp16((float(q - zero_row * w_sum[e]) * float(scale_row)) * float(w_scales[e]))
+    with e = expert_ids[row]; the zero term only when zero_row/w_sum given."""
+    name = "sym_dequant_moe"
+    _check(name, [(q, "q"), (scale_row, "scale_row"), (w_scales, "w_scales"),
+                  (expert_ids, "expert_ids"), (zero_row, "zero_row"), (w_sum, "w_sum")])
+    if q.dim() != 2 or q.dtype != torch.int32:
+        raise RuntimeError("q must be int32 [rows, cols]")
+    rows, cols = q.shape
+    if scale_row.dtype != torch.float16 or scale_row.numel() != rows:
+        raise RuntimeError("scale_row must be fp16 with one entry per row")
+    if w_scales.dtype != torch.float16 or w_scales.dim() != 2 or w_scales.shape[1] != cols:
+        raise RuntimeError("w_scales must be fp16 [num_experts, cols]")
+    if expert_ids.dtype != torch.int32 or expert_ids.numel() != rows:
+        raise RuntimeError("expert_ids must be int32 with one entry per row")
+    if (zero_row is None) != (w_sum is None):
+        raise RuntimeError("zero_row and w_sum must be given together")
+    if zero_row is not None:
+        if zero_row.dtype != torch.int8 or zero_row.numel() != rows:
+            raise RuntimeError("zero_row must be int8 with one entry per row")
+        if w_sum.dtype != torch.int32 or w_sum.dim() != 2 or w_sum.shape[1] != cols or \
+                w_sum.shape[0] != w_scales.shape[0]:
+            raise RuntimeError("w_sum must be int32 [num_experts, cols]")
+    out = torch.empty((rows, cols), dtype=torch.float16, device=q.device)
+    _call("srq_sym_dequant_moe", _ptr(q), _ptr(scale_row), _ptr(w_scales), _ptr(expert_ids),
+          _ptr(zero_row), _ptr(w_sum), w_scales.shape[0], rows, cols, _ptr(out), _stream(q))
+    return out
+
+
+def w4a4_linear_moe(A, a_scale, B, b_scale, expert_offsets):
+    """Fused grouped GEMM + expert-indexed dequant over expert-sorted rows:
+    expert e owns rows expert_offsets[e] .. expert_offsets[e + 1] (int32
+    [E + 1], device) of A u8 [R, K/2]; B u8 [E, N, K/2]; b_scale f16 [E, N];
+    returns fp16 [R, N] (rows owned by no expert are left uninitialised)."""
+    name = "w4a4_linear_moe"
+    _check(name, [(A, "A"), (a_scale, "a_scale"), (B, "B"), (b_scale, "b_scale"),
+                  (expert_offsets, "expert_offsets")],
+           [torch.uint8, torch.float16, torch.uint8, torch.float16, torch.int32])
+    if A.dim() != 2 or B.dim() != 3 or B.shape[2] != A.shape[1]:
+        raise RuntimeError(f"{name}: expected A [R, K/2] and B [E, N, K/2], got "
+                           f"{tuple(A.shape)} and {tuple(B.shape)}")
+    R, E, N, K = A.shape[0], B.shape[0], B.shape[1], A.shape[1] * 2
+    if a_scale.numel() != R or tuple(b_scale.shape) != (E, N):
+        raise RuntimeError(f"{name}: a_scale must have R entries and b_scale be [E, N]")
+    if expert_offsets.numel() != E + 1:
+        raise RuntimeError(f"{name}: expert_offsets must have num_experts + 1 entries")
+    out = torch.empty((R, N), dtype=torch.float16, device=A.device)
+    _call("srq_w4a4_linear_moe", _ptr(A), _ptr(a_scale), _ptr(B), _ptr(b_scale),
+          _ptr(expert_offsets), E, R, N, K, _ptr(out), _stream(A))
     return out

@@ -264,7 +264,8 @@ SRQ_DEV int swz(int r) {
     return (r / (256 / KBB)) % (KBB / 16);
 }
 
-template <int FM, int FN, int KBB>
+// One K step of a compute wave: the stage holds BM A rows then the B rows.
+template <int FM, int FN, int KBB, int BM = kBigBM>
 SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {
     constexpr int NPP = KBB / 32;  // 16-byte fragment fetches per step
     const int rr = lane & 31;
@@ -279,7 +280,7 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
         }
 #pragma unroll
         for (int jn = 0; jn < FN; ++jn) {
-            const int r = kBigBM + wn * (FN * 32) + jn * 32 + rr;
+            const int r = BM + wn * (FN * 32) + jn * 32 + rr;
             fb[slot][jn] = *reinterpret_cast<const v4i *>(stage + r * KBB + ((j ^ swz<KBB>(r)) << 4));
         }
     };
@@ -533,6 +534,215 @@ __global__ __launch_bounds__(KW * 64) void gemm_skinny_kernel(const uint8_t *__r
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Grouped GEMM (MoE experts): the producer/consumer structure of the large-M
+// kernel with 128 x 128 tiles, made persistent.  The problem list lives in
+// device memory only, so the launch needs no host read and is
+// graph-capturable: every workgroup walks tiles t = blockIdx.x, +gridDim.x,
+// ... of the concatenated per-problem tile lists (tiles of problem p follow
+// those of p - 1, row-major within a problem), locating each tile's problem
+// with a running prefix sum.  Producers and compute waves walk the same
+// sequence, so their barrier counts agree: K steps plus one end-of-tile
+// barrier per tile (after it the stages are free for the next tile's
+// prologue).  Rows past a problem's m and chunks past its k read as zeros.
+
+constexpr int kGrpBM = 128, kGrpBN = 128;
+constexpr int kGrpRows = kGrpBM + kGrpBN;
+
+struct GroupedArgs {
+    int P;
+    // pointer-array form (srq_matmul_grouped): problem p has sizes
+    // (m, n, k) = sizes[3p .. 3p+2], operands at ptr_a[p] / ptr_b[p] with
+    // row strides lda[p] / ldb[p] codes, int32 output at ptr_c[p] with row
+    // stride ldc[p]
+    const int32_t *sizes;
+    const int64_t *pa, *pb, *pc, *lda, *ldb, *ldc;
+    // expert-offset form (srq_w4a4_linear_moe): expert p owns rows
+    // offsets[p] .. offsets[p + 1] of A [R, K/2]; B [P, N, K/2]; fp16 output
+    // [R, N] = fp16((float(acc) * float(sa[row])) * float(sb[p, col]))
+    const int32_t *offsets;
+    const uint8_t *A, *B;
+    int64_t N, K;
+    const f16 *sa, *sb;
+    f16 *out;
+};
+
+struct GroupedProb {
+    const uint8_t *a, *b;
+    int32_t *c;
+    int64_t m, n, k, lda_b, ldb_b, ldc, row0;
+};
+
+SRQ_DEV int64_t uni(int64_t v) {
+    return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(v >> 32)) << 32) |
+                     (uint32_t)__builtin_amdgcn_readfirstlane((int)v));
+}
+
+SRQ_DEV GroupedProb grouped_prob(const GroupedArgs &g, int p) {
+    GroupedProb r;
+    if (g.sizes) {
+        r.m = uni(g.sizes[3 * p]);
+        r.n = uni(g.sizes[3 * p + 1]);
+        r.k = uni(g.sizes[3 * p + 2]);
+        r.a = (const uint8_t *)uni(g.pa[p]);
+        r.b = (const uint8_t *)uni(g.pb[p]);
+        r.c = (int32_t *)uni(g.pc[p]);
+        r.lda_b = uni(g.lda[p]) / 2;
+        r.ldb_b = uni(g.ldb[p]) / 2;
+        r.ldc = uni(g.ldc[p]);
+        r.row0 = 0;
+    } else {
+        r.row0 = uni(g.offsets[p]);
+        r.m = uni(g.offsets[p + 1]) - r.row0;
+        r.n = g.N;
+        r.k = g.K;
+        r.lda_b = r.ldb_b = g.K / 2;
+        r.a = g.A + r.row0 * r.lda_b;
+        r.b = g.B + (int64_t)p * g.N * r.ldb_b;
+        r.c = nullptr;
+        r.ldc = g.N;
+    }
+    return r;
+}
+
+SRQ_DEV int64_t grouped_tiles(const GroupedProb &r) {
+    if (r.m <= 0 || r.n <= 0) return 0;
+    return ((r.m + kGrpBM - 1) / kGrpBM) * ((r.n + kGrpBN - 1) / kGrpBN);
+}
+
+template <int NPROD>
+__global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(GroupedArgs g) {
+    constexpr int WGN = 2, FM = 2, FN = 2, KBB = 128, NSTG = 3;
+    constexpr int kCompute = 4;
+    constexpr int kStage = kGrpRows * KBB;
+    constexpr int kDma = kGrpRows / 8;
+    constexpr int kDmaPerWave = kDma / NPROD;
+    static_assert(kDmaPerWave * NPROD == kDma, "DMA split");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTG * kStage];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool producer = wave >= kCompute;
+    const int pw = wave - kCompute;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)smem;
+
+    int p = 0;
+    int64_t pstart = 0;
+    GroupedProb pr = grouped_prob(g, 0);
+    int64_t ptiles = grouped_tiles(pr);
+    for (int64_t t = blockIdx.x;; t += gridDim.x) {
+        while (p < g.P && t >= pstart + ptiles) {
+            pstart += ptiles;
+            ++p;
+            if (p < g.P) {
+                pr = grouped_prob(g, p);
+                ptiles = grouped_tiles(pr);
+            }
+        }
+        if (p >= g.P) break;
+        const int64_t tiles_n = (pr.n + kGrpBN - 1) / kGrpBN;
+        const int64_t local = t - pstart;
+        const int64_t m0 = (local / tiles_n) * kGrpBM, n0 = (local % tiles_n) * kGrpBN;
+        const int64_t KB = pr.k / 2;
+        const int steps = (int)((KB + KBB - 1) / KBB);
+
+        if (producer) {
+            const __amdgpu_buffer_rsrc_t ar = make_rsrc(pr.a, pr.m * pr.lda_b);
+            const __amdgpu_buffer_rsrc_t br = make_rsrc(pr.b, pr.n * pr.ldb_b);
+            uint32_t roff[kDmaPerWave];
+            int jc[kDmaPerWave];
+#pragma unroll
+            for (int q = 0; q < kDmaPerWave; ++q) {
+                const int i = pw * kDmaPerWave + q;
+                const int r = 8 * i + lane / 8;
+                jc[q] = ((lane % 8) ^ swz<KBB>(r)) * 16;
+                const bool isa = 8 * i < kGrpBM;
+                const int64_t row = isa ? m0 + r : n0 + r - kGrpBM;
+                roff[q] = row < (isa ? pr.m : pr.n)
+                              ? (uint32_t)(row * (isa ? pr.lda_b : pr.ldb_b)) : kOob;
+            }
+            auto issue = [&](int st, int sl) {
+                const int64_t kb0 = (int64_t)st * KBB;
+                const bool tail = kb0 + KBB > KB;
+#pragma unroll
+                for (int q = 0; q < kDmaPerWave; ++q) {
+                    const int i = pw * kDmaPerWave + q;
+                    const uint32_t dst = lds0 + sl * kStage + i * 1024;
+                    uint32_t off = roff[q] == kOob ? kOob : roff[q] + (uint32_t)kb0 + jc[q];
+                    if (tail && kb0 + jc[q] >= KB) off = kOob;
+                    dma16(8 * i < kGrpBM ? ar : br, off, dst);
+                }
+            };
+            if (steps > 0) issue(0, 0);
+            if (steps > 1) issue(1, 1);
+            int sl = 0;
+            for (int s = 0; s < steps; ++s) {
+                if (s + 1 < steps) {
+                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave) : "memory");
+                } else {
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                }
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                if (s + 2 < steps) issue(s + 2, sl == 0 ? 2 : sl - 1);
+                sl = sl == 2 ? 0 : sl + 1;
+            }
+            // end of tile: every compute wave is done with every stage
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            continue;
+        }
+
+        v16i acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){};
+        int sl = 0;
+        for (int s = 0; s < steps; ++s) {
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            big_compute<FM, FN, KBB, kGrpBM>(smem + sl * kStage, wm, wn, lane, acc);
+            sl = sl == 2 ? 0 : sl + 1;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+
+        // 32x32 accumulator layout: lane holds column lane & 31, rows
+        // 8 (v / 4) + 4 (lane / 32) + v % 4
+        float sbv[FN];
+        int64_t gnv[FN];
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            gnv[j] = n0 + wn * (FN * 32) + j * 32 + (lane & 31);
+            sbv[j] = (g.out && gnv[j] < pr.n) ? (float)g.sb[(int64_t)p * g.N + gnv[j]] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t gm =
+                    m0 + wm * (FM * 32) + i * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+                if (gm >= pr.m) continue;
+                const float sa = g.out ? (float)g.sa[pr.row0 + gm] : 0.f;
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    if (gnv[j] >= pr.n) continue;
+                    const int val = acc[i][j][v] >> 8;
+                    if (g.out) {
+                        const float a = (float)val * sa;
+                        g.out[(pr.row0 + gm) * g.N + gnv[j]] = f16_rn(a * sbv[j]);
+                    } else {
+                        pr.c[gm * pr.ldc + gnv[j]] = val;
+                    }
+                }
+            }
+    }
+}
+
 int check_gemm(const char *name, const void *A, const void *B, int64_t M, int64_t N,
                int64_t K) {
     SRQ_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", name);
@@ -624,4 +834,67 @@ extern "C" int srq_w4a4_linear(const void *A, const void *a_scale, const void *B
     e.sb = (const f16 *)b_scale;
     e.bias = (const f16 *)bias;
     return run_gemm("w4a4_linear", A, B, M, N, K, e, (hipStream_t)stream);
+}
+
+// Persistent grid of the grouped kernel: one workgroup per CU (256 CUs).
+static constexpr int kGroupedGrid = 256;
+
+extern "C" int srq_matmul_grouped(const int32_t *problem_sizes, const int64_t *ptr_A,
+                                  const int64_t *ptr_B, const int64_t *ptr_C,
+                                  const int64_t *lda, const int64_t *ldb, const int64_t *ldc,
+                                  int64_t problem_count, int signed_a, void *stream) {
+    SRQ_CHECK_ARG(problem_count >= 0 && problem_count <= 0x7fffffffLL,
+                  "matmul_grouped: bad problem_count");
+    if (problem_count == 0) return SRQ_OK;
+    if (!signed_a) {
+        srq_set_error("matmul_grouped: unsigned (asymmetric) A operands are not part of this "
+                      "build's W4A4 path");
+        return SRQ_EUNSUPPORTED;
+    }
+    SRQ_CHECK_ARG(problem_sizes && ptr_A && ptr_B && ptr_C && lda && ldb && ldc,
+                  "matmul_grouped: null pointer");
+    GroupedArgs g{};
+    g.P = (int)problem_count;
+    g.sizes = problem_sizes;
+    g.pa = ptr_A;
+    g.pb = ptr_B;
+    g.pc = ptr_C;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.ldc = ldc;
+    gemm_grouped_kernel<4><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
+    SRQ_LAUNCH_CHECK("matmul_grouped");
+    return SRQ_OK;
+}
+
+extern "C" int srq_w4a4_linear_moe(const void *A, const void *a_scale, const void *B,
+                                   const void *b_scale, const int32_t *expert_offsets,
+                                   int64_t num_experts, int64_t rows, int64_t N, int64_t K,
+                                   void *out, void *stream) {
+    SRQ_CHECK_ARG(num_experts >= 0 && num_experts <= 0x7fffffffLL && rows >= 0 && N >= 0 &&
+                      K >= 0, "w4a4_linear_moe: bad shape");
+    SRQ_CHECK_ARG(K % 32 == 0 && K <= 131072, "w4a4_linear_moe: K=%lld must be a multiple of "
+                  "32 and <= 131072", (long long)K);
+    if (num_experts == 0 || rows == 0 || N == 0) return SRQ_OK;
+    if (rows * (K / 2) >= 0xFFFFFFF0LL || N * (K / 2) >= 0xFFFFFFF0LL) {
+        srq_set_error("w4a4_linear_moe: operand larger than 4 GiB");
+        return SRQ_EUNSUPPORTED;
+    }
+    SRQ_CHECK_ARG(A && a_scale && B && b_scale && expert_offsets && out,
+                  "w4a4_linear_moe: null pointer");
+    SRQ_CHECK_ARG(srq_aligned(A, 16) && srq_aligned(B, 16),
+                  "w4a4_linear_moe: A and B must be 16-byte aligned");
+    GroupedArgs g{};
+    g.P = (int)num_experts;
+    g.offsets = expert_offsets;
+    g.A = (const uint8_t *)A;
+    g.B = (const uint8_t *)B;
+    g.N = N;
+    g.K = K;
+    g.sa = (const f16 *)a_scale;
+    g.sb = (const f16 *)b_scale;
+    g.out = (f16 *)out;
+    gemm_grouped_kernel<4><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
+    SRQ_LAUNCH_CHECK("w4a4_linear_moe");
+    return SRQ_OK;
 }

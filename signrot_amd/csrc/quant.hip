@@ -23,7 +23,7 @@ void srq_set_error(const char *fmt, ...) {
 }
 
 extern "C" const char *srq_last_error(void) { return g_err; }
-extern "C" int srq_abi_version(void) { return 1; }
+extern "C" int srq_abi_version(void) { return 2; }
 
 // --------------------------------------------------------------------------
 // helpers

@@ -16,6 +16,11 @@ __all__ = [
     "rope_qk",
     "swiglu",
     "rmsnorm",
+    "matmul_grouped",
+    "sym_quant_dynamic_moe",
+    "asym_quant_dynamic_moe",
+    "sym_dequant_moe",
+    "w4a4_linear_moe",
     "PackedQuantizedTensor",
 ]
 
@@ -144,3 +149,41 @@ def sym_dequant(q, scale_row, scale_col, bits=32):
     q, q_shape_excl_last = flatten_last_dim_and_return_shape(q)
     return _CUDA.sym_dequant(q, scale_row.view(-1), scale_col.view(-1), bits).view(
         *q_shape_excl_last, -1)
+
+
+def matmul_grouped(problem_sizes, ptr_a, ptr_b, ptr_c, lda, ldb, ldc, signed_a=True):
+    """Grouped 4-bit GEMM, C_i = A_i @ B_i^T per problem in one launch
+    (signrot/functional/kernel.py:83-92).  All arguments are device tensors:
+    problem_sizes int32 [P, 3] rows (m, n, k), the rest int64 [P] device
+    addresses / leading dims; per-element output identical to matmul_si4_si4
+    on each problem; nothing is read on the host (graph-capturable)."""
+    _CUDA.matmul_grouped(problem_sizes, ptr_a, ptr_b, ptr_c, lda, ldb, ldc, signed_a)
+
+
+def sym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio=1.0):
+    """sym_quant_dynamic over expert-sorted rows with the per-expert had_adj
+    sign fused: row r is multiplied by sign[expert_ids[r]] (exact for +-1)
+    before quantization; sign may be None (kernel.py:123-128)."""
+    assert x.dtype == torch.float16
+    return _CUDA.sym_quant_dynamic_moe(x.contiguous(), sign, expert_ids, clip_ratio)
+
+
+def asym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio=1.0):
+    """(kernel.py:131-134) -- the asymmetric activation path is not part of
+    this build; raises RuntimeError."""
+    return _CUDA.asym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio)
+
+
+def sym_dequant_moe(q, scale_row, w_scales, expert_ids, zero_row=None, w_sum=None):
+    """Expert-indexed dequant with the asym zero correction fused in
+    (kernel.py:137-145): out[r, c] = (q[r, c] - zero_row[r] * w_sum[e, c]) *
+    scale_row[r] * w_scales[e, c], e = expert_ids[r]."""
+    assert q.dtype == torch.int32
+    return _CUDA.sym_dequant_moe(q, scale_row.contiguous(), w_scales, expert_ids, zero_row,
+                                 w_sum)
+
+
+def w4a4_linear_moe(A, a_scale, B, b_scale, expert_offsets):
+    """Fused grouped int4 GEMM + expert-indexed dequant over expert-sorted
+    rows (one launch; bit-identical to matmul_grouped + sym_dequant_moe)."""
+    return _CUDA.w4a4_linear_moe(A, a_scale.reshape(-1), B, b_scale, expert_offsets)

@@ -50,6 +50,14 @@ def test_abi_version(lib):
                                     None), "power of two"),
     (lambda L: L.srq_w4a4_linear(ctypes.c_void_p(8), None, ctypes.c_void_p(16), None, None, 4,
                                  4, 64, None, None), "aligned"),
+    (lambda L: L.srq_matmul_grouped(None, None, None, None, None, None, None, 3, 1, None),
+     "null"),
+    (lambda L: L.srq_w4a4_linear_moe(None, None, None, None, None, 8, 16, 64, 48, None, None),
+     "multiple of 32"),
+    (lambda L: L.srq_sym_quant_dynamic_moe(None, None, None, 4, -1, 8, 1.0, None, None, None),
+     "negative"),
+    (lambda L: L.srq_sym_dequant_moe(None, None, None, None, ctypes.c_void_p(8), None, 4, 4, 4,
+                                     None, None), "together"),
 ])
 def test_argument_errors(lib, call, msg):
     rc = call(lib)
@@ -61,3 +69,11 @@ def test_empty_inputs_are_noops(lib):
     assert lib.srq_sym_quant_dynamic(None, 0, 4096, 1.0, None, None, None) == 0
     assert lib.srq_matmul_s4s4(None, None, 0, 16, 64, None, None) == 0
     assert lib.srq_kv_quant_pack(None, 0, 128, None, None, None) == 0
+    assert lib.srq_matmul_grouped(None, None, None, None, None, None, None, 0, 1, None) == 0
+    assert lib.srq_sym_dequant_moe(None, None, None, None, None, None, 8, 0, 16, None, None) == 0
+
+
+def test_grouped_unsigned_is_unsupported(lib):
+    z = ctypes.c_void_p(16)
+    assert lib.srq_matmul_grouped(z, z, z, z, z, z, z, 2, 0, None) == -2
+    assert "asymmetric" in lib.srq_last_error().decode()

@@ -1,0 +1,291 @@
+"""GPU parity of the MoE path (the reference's benchmarks/test_moe_kernels.py,
+test_grouped_gemm.py and test_moe_equivalence.py cases, restated):
+
+* sym_quant_dynamic_moe == x * sign[eid] then quant: bit-exact vs the oracle
+  and vs the unfused GPU composition;
+* sym_dequant_moe (with and without the zero correction): bit-exact;
+* matmul_grouped == the dense GEMM per problem, bit-exact, over decode
+  (M = 1 per expert), ragged prefill with never-routed experts, heavy skew
+  and a single problem; w4a4_linear_moe == matmul_grouped + sym_dequant_moe;
+* SignRotMoEBlock: grouped path == per-expert loop bit for bit, stage-wise
+  parity with the oracle, and a captured HIP graph replayed on inputs it
+  never saw (routing is data-dependent) == eager.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe as om
+from oracle import quant as oq
+from tests.gpu_util import assert_bitexact, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def C():
+    from signrot_amd import _CUDA
+    return _CUDA
+
+
+def _rows(rng, rows, cols, experts):
+    x = rng.standard_normal((rows, cols)).astype(np.float16)
+    eid = rng.integers(0, experts, rows).astype(np.int32)
+    sign = (rng.integers(0, 2, (experts, cols)) * 2 - 1).astype(np.int8)
+    sign[-1] = 1  # an identity (never-calibrated) expert
+    return x, eid, sign
+
+
+QUANT_CASES = [  # rows, cols, experts, clip, with_sign
+    (8, 2048, 128, 1.0, True), (8, 768, 128, 1.0, True), (4096, 768, 128, 1.0, True),
+    (33, 768, 128, 1.0, False), (128, 768, 128, 0.9, True), (5, 192, 16, 1.0, True),
+    (1024, 14336, 8, 1.0, True), (7, 100, 3, 1.0, True), (3, 4104, 2, 1.0, True),
+]
+
+
+@pytest.mark.parametrize("rows,cols,experts,clip,with_sign", QUANT_CASES)
+def test_sym_quant_dynamic_moe(C, rows, cols, experts, clip, with_sign):
+    rng = np.random.default_rng(rows + cols + experts)
+    x, eid, sign = _rows(rng, rows, cols, experts)
+    s_arg = to_dev(sign) if with_sign else None
+    q, s = C.sym_quant_dynamic_moe(to_dev(x), s_arg, to_dev(eid), clip)
+    qw, sw = om.sym_quant_dynamic_moe(x, sign if with_sign else None, eid, clip)
+    assert_bitexact(to_np(s), sw, "scale")
+    assert_bitexact(to_np(q), qw, "codes")
+    # the eager composition it replaces: x * sign[eid], then the plain kernel
+    xd = to_dev(x)
+    x_ref = xd * to_dev(sign)[to_dev(eid).long()] if with_sign else xd
+    q2, s2 = C.sym_quant_dynamic(x_ref.contiguous(), clip)
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+
+
+@pytest.mark.parametrize("rows,cols,experts", [(8, 768, 128), (8, 2048, 128), (200, 2048, 128),
+                                               (37, 14336, 8)])
+@pytest.mark.parametrize("asym", [False, True])
+def test_sym_dequant_moe(C, rows, cols, experts, asym):
+    rng = np.random.default_rng(rows * 3 + cols + asym)
+    q = rng.integers(-(2 ** 20), 2 ** 20, (rows, cols)).astype(np.int32)
+    s_row = ((rng.random(rows) + 0.1) / 64).astype(np.float16)
+    w_scales = ((rng.random((experts, cols)) + 0.1) / 64).astype(np.float16)
+    eid = rng.integers(0, experts, rows).astype(np.int32)
+    z = ws = None
+    if asym:
+        z = rng.integers(0, 16, rows).astype(np.int8)
+        ws = rng.integers(-8 * cols, 7 * cols, (experts, cols)).astype(np.int32)
+    out = C.sym_dequant_moe(to_dev(q), to_dev(s_row), to_dev(w_scales), to_dev(eid),
+                            None if z is None else to_dev(z), None if ws is None else to_dev(ws))
+    assert_bitexact(to_np(out), om.sym_dequant_moe(q, s_row, w_scales, eid, z, ws), "dequant")
+
+
+def _grouped_inputs(rng, counts, n, k):
+    e = len(counts)
+    m_total = int(sum(counts))
+    a = torch.randint(0, 256, (max(m_total, 1), k // 2), dtype=torch.uint8, device=DEV)[:m_total]
+    b = torch.randint(0, 256, (e, n, k // 2), dtype=torch.uint8, device=DEV)
+    return a.contiguous(), b
+
+
+def _run_grouped(C, a, b, counts, n, k):
+    e = len(counts)
+    c = torch.full((a.shape[0], n), -7, dtype=torch.int32, device=DEV)
+    counts_t = torch.tensor(counts, dtype=torch.int32, device=DEV)
+    offsets = torch.zeros(e, dtype=torch.int64, device=DEV)
+    if e > 1:
+        offsets[1:] = torch.cumsum(counts_t[:-1], 0)
+    ps = torch.empty((e, 3), dtype=torch.int32, device=DEV)
+    ps[:, 0] = counts_t
+    ps[:, 1] = n
+    ps[:, 2] = k
+    ptr_a = a.data_ptr() + offsets * (k // 2)
+    ptr_b = b.data_ptr() + torch.arange(e, dtype=torch.int64, device=DEV) * (n * k // 2)
+    ptr_c = c.data_ptr() + offsets * (n * 4)
+    lda = torch.full((e,), k, dtype=torch.int64, device=DEV)
+    ldc = torch.full((e,), n, dtype=torch.int64, device=DEV)
+    C.matmul_grouped(ps, ptr_a, ptr_b, ptr_c, lda, lda, ldc, True)
+    return c
+
+
+def _prefill_counts():
+    g = np.random.default_rng(0)
+    counts = g.integers(0, 40, 128).tolist()
+    counts[::7] = [0] * len(counts[::7])
+    return counts
+
+
+GROUPED_CASES = [  # name, counts, n, k
+    ("decode 8x(M=1)/128 gateup", [1] * 8 + [0] * 120, 768, 2048),
+    ("decode 8x(M=1)/128 down", [1] * 8 + [0] * 120, 2048, 768),
+    ("prefill random/128 gateup", _prefill_counts(), 768, 2048),
+    ("prefill random/128 down", _prefill_counts(), 2048, 768),
+    ("skew [4096,3,0,1]", [4096, 3, 0, 1], 768, 2048),
+    ("single problem M=513", [513], 2048, 768),
+    ("mixtral 8 experts", [130, 125, 140, 111, 128, 119, 135, 136], 1024, 4096),
+    ("all empty", [0, 0, 0], 64, 64),
+]
+
+
+@pytest.mark.parametrize("name,counts,n,k", GROUPED_CASES, ids=[c[0] for c in GROUPED_CASES])
+def test_matmul_grouped_vs_dense(C, name, counts, n, k):
+    torch.manual_seed(len(counts) + n + k)
+    a, b = _grouped_inputs(None, counts, n, k)
+    c = _run_grouped(C, a, b, counts, n, k)
+    row = 0
+    for i, m in enumerate(counts):
+        if m == 0:
+            continue
+        ref = C.matmul(a[row:row + m].contiguous(), b[i].contiguous())
+        assert torch.equal(c[row:row + m], ref), f"problem {i} (m={m}) differs"
+        row += m
+
+
+def test_matmul_grouped_vs_oracle(C):
+    counts, n, k = [3, 0, 17, 1], 40, 96
+    torch.manual_seed(1)
+    a, b = _grouped_inputs(None, counts, n, k)
+    c = to_np(_run_grouped(C, a, b, counts, n, k))
+    an, bn = to_np(a), to_np(b)
+    off = om.expert_offsets(counts)
+    want = om.matmul_grouped([(an[off[e]:off[e + 1]], bn[e]) for e in range(len(counts))])
+    for e in range(len(counts)):
+        assert_bitexact(c[off[e]:off[e + 1]], want[e], f"problem {e}")
+
+
+def test_matmul_grouped_unsigned_is_unsupported(C):
+    ps = torch.zeros((1, 3), dtype=torch.int32, device=DEV)
+    z = torch.zeros(1, dtype=torch.int64, device=DEV)
+    with pytest.raises(RuntimeError):
+        C.matmul_grouped(ps, z, z, z, z, z, z, False)
+
+
+@pytest.mark.parametrize("counts,n,k", [([3, 0, 5, 1], 300, 768),
+                                        ([130, 125, 140, 111, 128, 119, 135, 136], 14336, 4096),
+                                        ([0, 0], 128, 128), ([1], 4096, 14336)])
+def test_w4a4_linear_moe(C, counts, n, k):
+    torch.manual_seed(sum(counts) + n)
+    a, b = _grouped_inputs(None, counts, n, k)
+    e, rows = len(counts), a.shape[0]
+    sa = (torch.rand(rows, device=DEV) * 0.05 + 1e-3).half()
+    sb = (torch.rand(e, n, device=DEV) * 0.01 + 1e-4).half()
+    off = torch.tensor(om.expert_offsets(counts), dtype=torch.int32, device=DEV)
+    out = C.w4a4_linear_moe(a, sa, b, sb, off)
+    eid = torch.repeat_interleave(torch.arange(e, device=DEV, dtype=torch.int32),
+                                  torch.tensor(counts, device=DEV))
+    c = _run_grouped(C, a, b, counts, n, k)
+    ref = C.sym_dequant_moe(c, sa, sb, eid)
+    assert torch.equal(out, ref)
+    if rows and rows * n * k <= 64 * 1024 * 1024:
+        want = om.w4a4_linear_moe(to_np(a), to_np(sa), to_np(b), to_np(sb), to_np(off))
+        assert_bitexact(to_np(out), want, "fp16 out")
+
+
+# ------------------------------------------------------------------ block
+
+def _block(hidden, inter, experts, top_k, norm, seed, with_sign=True):
+    from signrot_amd.nn import SignRotMoEBlock
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    gate = torch.nn.Linear(hidden, experts, bias=False, dtype=torch.float16, device=DEV)
+    with torch.no_grad():
+        gate.weight.normal_(0, 0.1, generator=g)
+
+    def w(n, k):
+        return torch.randint(0, 256, (experts, n, k // 2), dtype=torch.uint8, device=DEV,
+                             generator=g)
+
+    def s(n, k):
+        # keep each stage's gain near one so activations stay finite in fp16
+        return torch.full((experts, n), 1.0 / k, dtype=torch.float16, device=DEV)
+
+    sign = None
+    if with_sign:
+        sign = (torch.randint(0, 2, (experts, inter), dtype=torch.int8, device=DEV,
+                              generator=g) * 2 - 1)
+    return SignRotMoEBlock(gate, top_k=top_k, norm_topk_prob=norm,
+                           w_gate=w(inter, hidden), s_gate=s(inter, hidden),
+                           w_up=w(inter, hidden), s_up=s(inter, hidden),
+                           w_down=w(hidden, inter), s_down=s(hidden, inter),
+                           sign_down=sign).eval()
+
+
+BLOCKS = [  # hidden, inter, experts, top_k, norm, tokens
+    (256, 768, 16, 4, True, 37),
+    (512, 1536, 8, 2, False, 5),
+    (4096, 14336, 8, 2, True, 64),
+]
+
+
+@pytest.mark.parametrize("hidden,inter,experts,top_k,norm,tokens", BLOCKS)
+@torch.no_grad()
+def test_block_grouped_equals_loop(hidden, inter, experts, top_k, norm, tokens):
+    blk = _block(hidden, inter, experts, top_k, norm, seed=hidden + tokens)
+    x = torch.randn(1, tokens, hidden, device=DEV, dtype=torch.float16)
+    blk.use_grouped = True
+    out, logits = blk(x)
+    blk.use_grouped = False
+    out_loop, logits_loop = blk(x)
+    assert torch.equal(logits, logits_loop)
+    assert torch.equal(out, out_loop)
+    assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("hidden,inter,experts,top_k,norm,tokens", BLOCKS[:2])
+@torch.no_grad()
+def test_block_stagewise_vs_oracle(C, hidden, inter, experts, top_k, norm, tokens):
+    """Each stage of the grouped forward against the oracle on the previous
+    stage's GPU output (the rotation's fp16 bits are tolerance-pinned, so it
+    is checked against its own oracle separately)."""
+    from signrot_amd.functional.hadamard import matmul_hadU_cuda
+    from oracle import glue as og
+    blk = _block(hidden, inter, experts, top_k, norm, seed=7 + tokens)
+    x = torch.randn(tokens, hidden, device=DEV, dtype=torch.float16)
+    _, _, perm, counts, flat_e = blk.route(x)
+    tok = perm // top_k
+    eid = flat_e[perm].to(torch.int32)
+    off = torch.zeros(experts + 1, dtype=torch.int32, device=DEV)
+    off[1:] = torch.cumsum(counts, 0)
+    q_tok, s_tok = C.sym_quant_dynamic(x, 1.0)
+    qw, sw = oq.sym_quant_dynamic(to_np(x))
+    assert_bitexact(to_np(q_tok), qw, "token codes")
+    q_a, s_a = q_tok[tok], s_tok[tok]
+    gate_h = C.w4a4_linear_moe(q_a, s_a.view(-1), blk.w_gate, blk.s_gate, off)
+    up_h = C.w4a4_linear_moe(q_a, s_a.view(-1), blk.w_up, blk.s_up, off)
+    offn = to_np(off)
+    assert_bitexact(to_np(gate_h), om.w4a4_linear_moe(to_np(q_a), to_np(s_a), to_np(blk.w_gate),
+                                                       to_np(blk.s_gate), offn), "gate")
+    assert_bitexact(to_np(up_h), om.w4a4_linear_moe(to_np(q_a), to_np(s_a), to_np(blk.w_up),
+                                                     to_np(blk.s_up), offn), "up")
+    inter_h = C.swiglu(gate_h, up_h)
+    np.testing.assert_allclose(to_np(inter_h).astype(np.float32),
+                               og.swiglu(to_np(gate_h), to_np(up_h)).astype(np.float32),
+                               rtol=2e-3, atol=2e-3)
+    h = matmul_hadU_cuda(inter_h, blk.had_K, blk.K)
+    q_d, s_d = C.sym_quant_dynamic_moe(h, blk.sign_down, eid, 1.0)
+    qdw, sdw = om.sym_quant_dynamic_moe(to_np(h), to_np(blk.sign_down), to_np(eid))
+    assert_bitexact(to_np(s_d), sdw, "down scale")
+    assert_bitexact(to_np(q_d), qdw, "down codes")
+    y = C.w4a4_linear_moe(q_d, s_d.view(-1), blk.w_down, blk.s_down, off)
+    assert_bitexact(to_np(y), om.w4a4_linear_moe(qdw, sdw, to_np(blk.w_down), to_np(blk.s_down),
+                                                  offn), "down")
+
+
+@torch.no_grad()
+def test_block_graph_replay_on_new_inputs():
+    blk = _block(256, 768, 16, 4, True, seed=99)
+    x_static = torch.randn(1, 24, 256, device=DEV, dtype=torch.float16)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            blk(x_static)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_static, _ = blk(x_static)
+    for i in range(4):
+        x_new = torch.randn(1, 24, 256, device=DEV, dtype=torch.float16) * (1 + i)
+        x_static.copy_(x_new)
+        graph.replay()
+        torch.cuda.synchronize()
+        want, _ = blk(x_new)
+        torch.cuda.synchronize()
+        assert torch.equal(out_static, want), f"replay {i} differs from eager"
