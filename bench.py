@@ -47,6 +47,8 @@ def parse():
     p.add_argument("--decode-layers", type=int, default=4,
                    help="distinct layers (weights + cache) replayed per decode step")
     p.add_argument("--decode-steps", type=int, default=20)
+    p.add_argument("--no-configs", action="store_true",
+                   help="skip the per-config measurements (cfg1, cfg2 sweep, cfg4, cfg5)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run plain device copies of a known size (the reference "
                         "kernel for scaling the FETCH_SIZE / WRITE_SIZE counters)")
@@ -185,6 +187,178 @@ def bench_decode_layer(args, dev):
     }
 
 
+def _time_launches(launch, n, stream):
+    """Average ms of `launch(i)`, i = 0 .. n-1, back to back, HIP events on
+    the launch stream."""
+    for i in range(2):
+        launch(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(n):
+        launch(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def _roof(us, ops, nbytes):
+    tops = ops / (us * 1e-6) / 1e12
+    gbs = nbytes / (us * 1e-6) / 1e9
+    bound = "mfma" if ops / (PEAK_INT8_TOPS * 1e12) > nbytes / (PEAK_HBM_GBS * 1e9) else "hbm"
+    return {"us": round(us, 2), "TOPS": round(tops, 1), "GBs": round(gbs, 1),
+            "frac_mfma": round(tops / PEAK_INT8_TOPS, 4), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+            "bound": bound, "algorithmic_ops": ops, "algorithmic_bytes": nbytes}
+
+
+def _rand_w(n, k, dev, g):
+    return torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=g)
+
+
+def bench_qlinear(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9, reps=20):
+    """One W4A4 QLinear (had_sign_quant + w4a4_linear) at [M, K] x [N, K]:
+    whole-QLinear and per-kernel averages over distinct input/weight sets
+    (> min_bytes in total, so weights stream from HBM, not the MALL)."""
+    from signrot_amd import _native
+    from signrot_amd.functional.hadamard import get_hadK
+    st = torch.cuda.current_stream()
+    g = torch.Generator(device=dev).manual_seed(seed)
+    had, k = get_hadK(K)
+    hadk = had.half().to(dev).contiguous() if k > 1 else None
+    sign = (torch.randint(0, 2, (K,), device=dev, generator=g).to(torch.int8) * 2 - 1)
+    set_bytes = M * K * 2 + N * K // 2 + M * K // 2 + M * N * 2
+    nsets = max(1, min(256, math.ceil(min_bytes / set_bytes)))
+    x0 = torch.randn(M, K, device=dev, generator=g)
+    ch = torch.randperm(K, device=dev, generator=g)[:n_out]
+    x0[:, ch] *= mag
+    x0 = x0.half()
+    xs = [x0] + [x0.clone() for _ in range(min(nsets, 8) - 1)]
+    ws = [_rand_w(N, K, dev, g) for _ in range(nsets)]
+    wsc = (torch.rand(N, device=dev, generator=g) * 1e-3 + 1e-4).half()
+    qb = [torch.empty(M, K // 2, dtype=torch.uint8, device=dev) for _ in range(len(xs))]
+    sb = [torch.empty(M, dtype=torch.float16, device=dev) for _ in range(len(xs))]
+    ob = [torch.empty(M, N, dtype=torch.float16, device=dev) for _ in range(len(xs))]
+    hp = hadk.data_ptr() if hadk is not None else None
+
+    def had(i):
+        j = i % len(xs)
+        _native.call("srq_had_sign_quant", xs[j].data_ptr(), M, K, k, hp, sign.data_ptr(), 0,
+                     1.0, qb[j].data_ptr(), sb[j].data_ptr(), st.cuda_stream)
+
+    def gemm(i):
+        j = i % len(xs)
+        _native.call("srq_w4a4_linear", qb[j].data_ptr(), sb[j].data_ptr(),
+                     ws[i % nsets].data_ptr(), wsc.data_ptr(), None, M, N, K, ob[j].data_ptr(),
+                     st.cuda_stream)
+
+    def both(i):
+        had(i)
+        gemm(i)
+
+    n = max(reps, min(nsets, 64))
+    t_all = _time_launches(both, n, st) * 1e3
+    t_had = _time_launches(had, n, st) * 1e3
+    t_gemm = _time_launches(gemm, n, st) * 1e3
+    ops = 2.0 * M * N * K
+    res = {"M": M, "K": K, "N": N, "hadamard": f"had_{k} x H_{K // k}", "weight_sets": nsets,
+           "qlinear": _roof(t_all, ops, M * K * 2 + N * K // 2 + M * N * 2 + M * 2 + N * 2),
+           "had_sign_quant": _roof(t_had, 0.0, M * K * 2 + M * K // 2 + M * 2),
+           "w4a4_linear": _roof(t_gemm, ops, M * K // 2 + N * K // 2 + M * N * 2 + M * 2 + N * 2)}
+    del xs, ws, qb, sb, ob
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_mlp70b(dev, M, seed, hidden=8192, ffn=28672, reps=10, min_bytes=2.2e9):
+    """Config 4: Llama-3-70B-shape W4A4 MLP block: per-token int4 quant of x,
+    gate and up W4A4 linears, SwiGLU, had_28 x H_1024 rotation + sign +
+    quant, down W4A4 linear."""
+    from signrot_amd import _CUDA
+    from signrot_amd.functional.hadamard import get_hadK
+    g = torch.Generator(device=dev).manual_seed(seed)
+    had, k = get_hadK(ffn)
+    hadk = had.half().to(dev).contiguous()
+    sign = (torch.randint(0, 2, (ffn,), device=dev, generator=g).to(torch.int8) * 2 - 1)
+    wbytes = 3 * ffn * hidden // 2
+    nsets = max(1, math.ceil(min_bytes / wbytes))
+    Wg = [_rand_w(ffn, hidden, dev, g) for _ in range(nsets)]
+    Wu = [_rand_w(ffn, hidden, dev, g) for _ in range(nsets)]
+    Wd = [_rand_w(hidden, ffn, dev, g) for _ in range(nsets)]
+    sgu = torch.full((ffn,), 1.0 / hidden, dtype=torch.float16, device=dev)
+    sd = torch.full((hidden,), 1.0 / ffn, dtype=torch.float16, device=dev)
+    x = torch.randn(M, hidden, device=dev, generator=g)
+    ch = torch.randperm(hidden, device=dev, generator=g)[:8]
+    x[:, ch] *= 100.0
+    x = x.half()
+
+    def mlp(i):
+        j = i % nsets
+        q, s = _CUDA.sym_quant_dynamic(x)
+        gate = _CUDA.w4a4_linear(q, s.view(-1), Wg[j], sgu)
+        up = _CUDA.w4a4_linear(q, s.view(-1), Wu[j], sgu)
+        inter = _CUDA.swiglu(gate, up)
+        qd, sdn = _CUDA.had_sign_quant(inter, hadk, k, sign)
+        return _CUDA.w4a4_linear(qd, sdn.view(-1), Wd[j], sd)
+
+    st = torch.cuda.current_stream()
+    t = _time_launches(mlp, max(reps, nsets), st) * 1e3
+    ops = 2.0 * M * 3 * hidden * ffn
+    nbytes = wbytes + M * hidden * 2 * 2
+    del Wg, Wu, Wd
+    torch.cuda.empty_cache()
+    return {"M": M, "hidden": hidden, "ffn": ffn, "hadamard": f"had_{k} x H_{ffn // k}",
+            "weight_sets": nsets, "mlp": _roof(t, ops, nbytes)}
+
+
+def bench_moe(dev, seed, tokens=512, hidden=4096, ffn=14336, experts=8, top_k=2, reps=10):
+    """Config 5: Mixtral-8x7B-shape W4A4 MoE FFN (SignRotMoEBlock, grouped
+    path): 8 experts, top-2 routing of 512 tokens (router logits N(0,1)
+    seeded through a random router), hidden 4096, FFN 14336, SwiGLU,
+    had_28 x H_512 + per-expert sign on the down-proj input."""
+    from signrot_amd.nn import SignRotMoEBlock
+    g = torch.Generator(device=dev).manual_seed(seed)
+    gate = torch.nn.Linear(hidden, experts, bias=False, dtype=torch.float16, device=dev)
+    with torch.no_grad():
+        gate.weight.normal_(0, 1.0 / math.sqrt(hidden), generator=g)
+
+    def w(n, k):
+        return torch.randint(0, 256, (experts, n, k // 2), dtype=torch.uint8, device=dev,
+                             generator=g)
+
+    def sc(n, k):
+        return torch.full((experts, n), 1.0 / k, dtype=torch.float16, device=dev)
+
+    sign = torch.randint(0, 2, (experts, ffn), dtype=torch.int8, device=dev, generator=g) * 2 - 1
+    blk = SignRotMoEBlock(gate, top_k=top_k, norm_topk_prob=True, w_gate=w(ffn, hidden),
+                          s_gate=sc(ffn, hidden), w_up=w(ffn, hidden), s_up=sc(ffn, hidden),
+                          w_down=w(hidden, ffn), s_down=sc(hidden, ffn), sign_down=sign).eval()
+    xs = [torch.randn(1, tokens, hidden, device=dev, generator=g).half() for _ in range(4)]
+    st = torch.cuda.current_stream()
+    with torch.no_grad():
+        t = _time_launches(lambda i: blk(xs[i % len(xs)]), reps, st) * 1e3
+        _, _, perm, counts, _ = blk.route(xs[0].view(-1, hidden))
+    rows = tokens * top_k
+    ops = 2.0 * rows * 3 * hidden * ffn
+    nbytes = 3 * experts * ffn * hidden // 2
+    res = {"tokens": tokens, "experts": experts, "top_k": top_k, "hidden": hidden, "ffn": ffn,
+           "rows_per_expert": counts.tolist(), "block": _roof(t, ops, nbytes)}
+    del blk, xs
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_configs(args, dev):
+    """The BASELINE.json configs other than the headline one, each at its
+    own shape (configs[0], the cfg2 M sweep, configs[3], configs[4])."""
+    out = {"cfg1_qproj_M16": bench_qlinear(dev, 16, 4096, 4096, args.seed + 10, n_out=4,
+                                           mag=100.0),
+           "cfg2_sweep": [bench_qlinear(dev, m, 14336, 4096, args.seed + 20 + m)
+                          for m in (1, 16, 128, 2048, 8192)],
+           "cfg4_mlp70b": [bench_mlp70b(dev, m, args.seed + 30 + m) for m in (1, 32, 512, 4096)],
+           "cfg5_moe": bench_moe(dev, args.seed + 40)}
+    return out
+
+
 def measured_traffic(kernel, M, K, N):
     """HBM bytes per launch of `kernel` at this shape from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE passes (profiles/traffic_cfg2.json,
@@ -317,6 +491,10 @@ def main():
         torch.cuda.empty_cache()
         decode = bench_decode_layer(args, dev)
 
+    configs = None
+    if not args.no_configs:
+        configs = bench_configs(args, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = time_cpu_baseline(args, x0, hadk, k, sign, wfq)
@@ -356,6 +534,7 @@ def main():
                             "frac_mfma": round(gemm_tops / PEAK_INT8_TOPS, 4)},
         },
         "decode_layer": decode,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
