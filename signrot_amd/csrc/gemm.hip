@@ -536,6 +536,245 @@ __global__ __launch_bounds__(KW * 64) void gemm_skinny_kernel(const uint8_t *__r
 
 
 // ---------------------------------------------------------------------------
+// Stream kernel for M <= 32 (decode): weight streaming at the HBM roofline's
+// access pattern, with the activation loaded once per workgroup.
+//
+// Persistent grid of G <= 256 workgroups of KW = 8 waves; workgroup b owns
+// column blocks (16 output columns each) b, b + G, ...  The K dimension is
+// cut into units of 128 bytes (256 codes) per row; wave w owns units
+// [w*per, (w+1)*per) of every column block.
+//
+// * A (M rows x the wave's units) is loaded once into registers in the MFMA
+//   operand layout: read line-friendly (8 rows x 128 B per instruction) and
+//   transposed through LDS.  Re-reading it per column block from L2 in the
+//   operand layout (16 rows x 16 B per quarter-wave) costs more L1 tag
+//   lookups than the weight stream itself.
+// * B streams through a per-wave ring of S LDS stages of 16 rows x 128 B by
+//   direct-to-LDS loads (no VGPR staging), S-1 items in flight.  Each
+//   16-lane quarter-wave fetches two whole 128-byte lines; lane p of a row
+//   fetches logical 16-byte chunk p ^ (row & 7), which makes the MFMA-layout
+//   reads (lane l: row l & 15, chunk 4t + (l >> 4)) bank-conflict-free.
+// * Per column block, each wave's partial sums go into an LDS int32 buffer
+//   with integer atomic adds (exact and order-independent), then one barrier,
+//   then wave (j mod KW) reads, clears and stores the block.  The buffer is
+//   double-buffered on j, so one barrier per block suffices.
+constexpr int kStreamKW = 8;
+constexpr int kStreamS = 4;
+constexpr int kStreamMaxCb = 16;   // column blocks per workgroup
+
+template <int MB, int NSUB, bool AUNP>
+__global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
+    const uint8_t *__restrict__ A, const uint8_t *__restrict__ B, int64_t M, int64_t N,
+    int64_t K, Epi e) {
+    constexpr int KW = kStreamKW, S = kStreamS;
+    __shared__ __attribute__((aligned(1024))) uint8_t ring[KW * S * 2048];
+    __shared__ int sum[2][MB * 256];
+    __shared__ float sbl[kStreamMaxCb * 16];
+    __shared__ float sal[MB * 16];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t KB = K / 2;
+    const int units = (int)((KB + 127) / 128);
+    const int per = (units + KW - 1) / KW;
+    const int u0 = wave * per;
+    const int nsub = max(0, min(per, units - u0));
+    const int ncb = (int)((N + 15) / 16);
+    const int G = gridDim.x;
+    const int ncb_mine = (ncb - (int)blockIdx.x + G - 1) / G;
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
+
+    for (int t = threadIdx.x; t < 2 * MB * 256; t += KW * 64) (&sum[0][0])[t] = 0;
+    if (!e.C) {
+        for (int t = threadIdx.x; t < MB * 16; t += KW * 64) sal[t] = t < M ? (float)e.sa[t] : 0.f;
+        for (int t = threadIdx.x; t < ncb_mine * 16; t += KW * 64) {
+            const int64_t n = (int64_t)(blockIdx.x + (t >> 4) * G) * 16 + (t & 15);
+            sbl[t] = n < N ? (float)e.sb[n] : 0.f;
+        }
+    }
+
+    // A: unit s of this wave, row block i, chunk pair t; lane holds row
+    // 16 i + (lane & 15), logical chunk 4 t + (lane >> 4) of the unit
+    v4i areg[NSUB][MB][2];
+    {
+        v4i raw[NSUB][MB][2];
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+            for (int h = 0; h < 2 * MB; ++h) {
+                const int64_t row = 8 * h + (lane >> 3);
+                const int64_t kb = (int64_t)(u0 + s) * 128 + 16 * (lane & 7);
+                const bool ok = s < nsub && row < M && kb < KB;
+                raw[s][h >> 1][h & 1] = bload16(ar, ok ? (uint32_t)(row * KB + kb) : kOob);
+            }
+        uint8_t *tb = ring + wave * (S * 2048);
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+            for (int h = 0; h < 2 * MB; ++h) {
+                const int row = 8 * h + (lane >> 3);
+                *(v4i *)(tb + row * 128 + 16 * ((lane & 7) ^ (row & 7))) = raw[s][h >> 1][h & 1];
+            }
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int row = 16 * i + (lane & 15);
+                    areg[s][i][t] =
+                        *(const v4i *)(tb + row * 128 + 16 * ((4 * t + (lane >> 4)) ^ (row & 7)));
+                }
+            // this wave's reads of unit s land before unit s + 1 overwrites the slot
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(areg[s][i][t]));
+    v4i aun[AUNP ? NSUB : 1][MB][2][2];
+    if (AUNP) {
+#pragma unroll
+        for (int s = 0; s < (AUNP ? NSUB : 1); ++s)
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    aun[s][i][t][0] = unpack8((u32)areg[s][i][t][0], (u32)areg[s][i][t][1]);
+                    aun[s][i][t][1] = unpack8((u32)areg[s][i][t][2], (u32)areg[s][i][t][3]);
+                }
+    }
+    __syncthreads();
+
+    // item = (column block j, unit s); DMA instruction h covers rows 8 h + (lane >> 3)
+    const uint32_t ring_w = (uint32_t)(uintptr_t)ring + (uint32_t)wave * (S * 2048);
+    const int total = ncb_mine * nsub;
+    auto issue = [&](int item) {
+        const uint32_t lds = ring_w + (item % S) * 2048;
+        int64_t nrow0 = 0, kb0 = 0;
+        const bool live = item < total;
+        if (live) {
+            const int j = item / nsub, s = item - j * nsub;
+            nrow0 = (int64_t)(blockIdx.x + j * G) * 16;
+            kb0 = (int64_t)(u0 + s) * 128;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = 8 * h + (lane >> 3);
+            const int64_t row = nrow0 + r;
+            const int64_t kb = kb0 + 16 * ((lane & 7) ^ (r & 7));
+            const uint32_t off = (live && row < N && kb < KB) ? (uint32_t)(row * KB + kb) : kOob;
+            dma16(br, off, __builtin_amdgcn_readfirstlane(lds + h * 1024));
+        }
+    };
+
+    v4i acc[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
+#pragma unroll
+    for (int it = 0; it < S - 1; ++it) issue(it);
+
+    const int rr = lane & 15;
+    for (int j = 0; j < ncb_mine; ++j) {
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+            if (s >= nsub) break;
+            const int it = j * nsub + s;
+            issue(it + S - 1);  // items past the end load zeros into a free stage
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (S - 1)) : "memory");
+            const uint8_t *st = ring + wave * (S * 2048) + (it % S) * 2048 + 128 * rr;
+            v4i bw[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                bw[t] = *(const v4i *)(st + 16 * ((4 * t + (lane >> 4)) ^ (rr & 7)));
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const v4i b0 = unpack8((u32)bw[t][0], (u32)bw[t][1]);
+                const v4i b1 = unpack8((u32)bw[t][2], (u32)bw[t][3]);
+#pragma unroll
+                for (int i = 0; i < MB; ++i) {
+                    v4i a0, a1;
+                    if (AUNP) {
+                        a0 = aun[AUNP ? s : 0][i][t][0];
+                        a1 = aun[AUNP ? s : 0][i][t][1];
+                    } else {
+                        v4i w = areg[s][i][t];
+                        asm volatile("" : "+v"(w));  // unpack per use, not hoisted out of j
+                        a0 = unpack8((u32)w[0], (u32)w[1]);
+                        a1 = unpack8((u32)w[2], (u32)w[3]);
+                    }
+                    acc[i] = mfma16(a0, b0, acc[i]);
+                    acc[i] = mfma16(a1, b1, acc[i]);
+                }
+            }
+        }
+        int *sm = sum[j & 1];
+        if (nsub > 0) {
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    __hip_atomic_fetch_add(&sm[i * 256 + (4 * (lane >> 4) + r) * 16 + rr], acc[i][r],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+#pragma unroll
+        for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
+        __syncthreads();
+        if (wave == j % KW) {
+            const int64_t gn = (int64_t)(blockIdx.x + j * G) * 16 + rr;
+            const float sbv = e.C ? 0.f : sbl[j * 16 + rr];
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = i * 16 + 4 * (lane >> 4) + r;
+                    const int idx = i * 256 + (4 * (lane >> 4) + r) * 16 + rr;
+                    const int v = sm[idx] >> 8;
+                    sm[idx] = 0;
+                    if (m < M && gn < N) {
+                        if (e.C) {
+                            e.C[m * N + gn] = v;
+                        } else {
+                            f16 o = f16_rn(((float)v * sal[m]) * sbv);
+                            if (e.bias) o = f16_rn((float)o + (float)e.bias[gn]);
+                            e.out[m * N + gn] = o;
+                        }
+                    }
+                }
+        }
+    }
+}
+
+// Launch the stream kernel if the shape fits its register and LDS budget;
+// returns false otherwise.
+bool launch_stream(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64_t K,
+                   const Epi &e, hipStream_t st) {
+    if (M > 32) return false;
+    const int64_t units = (K / 2 + 127) / 128;
+    const int64_t per = (units + kStreamKW - 1) / kStreamKW;
+    const int64_t ncb = (N + 15) / 16;
+    const int64_t cb_per = (ncb + 255) / 256;
+    if (cb_per > kStreamMaxCb) return false;
+    const dim3 grid((unsigned)((ncb + cb_per - 1) / cb_per)), block(kStreamKW * 64);
+#define SRQ_STREAM(MB, NSUB, AUNP) \
+    gemm_stream_kernel<MB, NSUB, AUNP><<<grid, block, 0, st>>>(a, b, M, N, K, e)
+    if (M <= 16) {
+        if (per <= 2) SRQ_STREAM(1, 2, true);
+        else if (per <= 4) SRQ_STREAM(1, 4, true);
+        else if (per <= 8) SRQ_STREAM(1, 8, false);
+        else return false;
+    } else {
+        if (per <= 2) SRQ_STREAM(2, 2, true);
+        else if (per <= 4) SRQ_STREAM(2, 4, false);
+        else if (per <= 7) SRQ_STREAM(2, 7, false);
+        else if (per <= 8) SRQ_STREAM(2, 8, false);
+        else return false;
+    }
+#undef SRQ_STREAM
+    return true;
+}
+
+// ---------------------------------------------------------------------------
 // Grouped GEMM (MoE experts): the producer/consumer structure of the large-M
 // kernel with 128 x 128 tiles, made persistent.  The problem list lives in
 // device memory only, so the launch needs no host read and is
@@ -779,6 +1018,8 @@ int run_gemm(const char *name, const void *A, const void *B, int64_t M, int64_t 
     if (K == 0) {
         const int64_t blocks = std::min<int64_t>(srq_cdiv(M * N, 256), 4096);
         fill_zero_epilogue<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(M, N, e);
+    } else if (launch_stream(a, b, M, N, K, e, st)) {
+        // M <= 32: persistent weight-streaming kernel
     } else if (M <= 16) {
         gemm_skinny_kernel<1, 8, 4><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
             a, b, M, N, K, e);

@@ -21,6 +21,12 @@ GEMM_SHAPES = [
     (17, 100, 768), (32, 768, 2048), (33, 64, 32), (64, 2048, 768), (65, 130, 4096),
     (128, 4096, 14336), (300, 513, 800), (513, 2048, 768), (2048, 4096, 14336),
     (2, 16, 32), (5, 3, 64), (1100, 300, 4128), (1024, 128, 256), (4096, 256, 1024),
+    # M <= 32 weight-streaming kernel: decode shapes, several column blocks per
+    # workgroup, ragged N and K, every A-register depth, and the fallback
+    # past its limits (K > 16384, > 16 column blocks per workgroup)
+    (32, 6144, 4096), (32, 28672, 4096), (32, 4096, 14336), (24, 4112, 16384),
+    (16, 1000, 8192), (1, 57344, 8192), (3, 17, 4128), (20, 50, 96), (32, 16, 32),
+    (9, 4096, 2048), (32, 300, 8320), (2, 70000, 256), (32, 64, 28672),
 ]
 
 
@@ -45,10 +51,17 @@ def test_matmul_extreme_values(C):
     b2 = np.full((17, K // 2), 0x77, np.uint8)
     c2 = to_np(C.matmul(to_dev(a), to_dev(b2)))
     assert np.all(c2 == -56 * K)
+    # the streaming kernel's deepest configuration (M = 32, K = 16384)
+    K = 16384
+    a = np.full((32, K // 2), 0x88, np.uint8)
+    b = np.full((40, K // 2), 0x88, np.uint8)
+    assert np.all(to_np(C.matmul(to_dev(a), to_dev(b))) == 64 * K)
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 4096, 4096), (33, 300, 768),
-                                   (128, 4096, 14336), (2048, 4096, 14336), (7, 5, 64)])
+                                   (128, 4096, 14336), (2048, 4096, 14336), (7, 5, 64),
+                                   (32, 6144, 4096), (32, 28672, 4096), (32, 4096, 14336),
+                                   (13, 4100, 8192)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_w4a4_linear_bitexact(C, M, N, K, bias):
     rng = np.random.default_rng(M + N + K + bias)
