@@ -141,6 +141,10 @@ def bench_decode_layer(args, dev):
     cache._needs_init = [False] * NL
     h0 = (torch.randn(B, 1, hidden, device=dev, generator=gen) * 0.5).half()
     cos, sin = rope_cos_sin([T], D, layers[0].rope_theta, dev)
+    # the reference's graph protocol (kv_cache.py:435-460): index buffers are
+    # refreshed outside the graph and frozen inside it
+    cache.refresh_specs(T + 1)
+    cache.freeze_specs(True)
 
     def step():
         cache.length = T

@@ -85,6 +85,17 @@ int srq_w4a4_linear(const void *A, const void *a_scale, const void *B,
                     const void *b_scale, const void *bias, int64_t M, int64_t N,
                     int64_t K, void *out, void *stream);
 
+/* srq_w4a4_linear with the decoder's residual add fused into the epilogue:
+ * out = fp16(lin + residual[m, n]) after the dequant (and bias), as torch's
+ * fp16 `residual + linear(x)` rounds it.  residual f16 [M, N]; out may be the
+ * residual buffer itself (each element is read before it is written by the
+ * same thread).  Replaces Linear4bit.forward followed by the residual add of
+ * the decoder layer (e2e/quantized_llama/modeling_llama.py:19-137, HF
+ * LlamaDecoderLayer residual structure). */
+int srq_w4a4_linear_residual(const void *A, const void *a_scale, const void *B,
+                             const void *b_scale, const void *bias, const void *residual,
+                             int64_t M, int64_t N, int64_t K, void *out, void *stream);
+
 /* --------------------------------------------------------------- Hadamard */
 
 /* Walsh-Hadamard transform (Sylvester order) over the last dim, times scale.
@@ -116,6 +127,18 @@ int srq_online_hadamard(const void *x, void *out, int64_t rows, int64_t n, int64
 int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_t K,
                        const void *hadK, const int8_t *sign, int fp32_had,
                        float clip_ratio, void *q, void *scale, void *stream);
+
+/* srq_had_sign_quant whose input row is SwiGLU of two strided rows:
+ * x[r, i] = fp16(fp16(silu(gate[r*ld + i])) * up[r*ld + i]) (the srq_swiglu
+ * arithmetic), then the rotation, sign and quantizer of srq_had_sign_quant.
+ * Bit-identical to srq_swiglu followed by srq_had_sign_quant.  gate, up f16
+ * with row stride ld >= n (e.g. the two halves of one [rows, 2n] gate/up
+ * projection); needs n = K * 512 with 9 <= K <= 32, else SRQ_EUNSUPPORTED.
+ * Replaces swiglu -> OnlineHadamard -> Quantizer of the decoder MLP
+ * (e2e/quantized_llama/modeling_llama.py:125-137; fused.cu:367-390). */
+int srq_swiglu_had_sign_quant(const void *gate, const void *up, int64_t ld, int64_t rows,
+                              int64_t n, int64_t K, const void *hadK, const int8_t *sign,
+                              float clip_ratio, void *q, void *scale, void *stream);
 
 /* ----------------------------------------------------- paged int4 KV cache */
 /* Cache layout (signrot/kernels/include/flashinfer/page.cuh:18-112):
@@ -161,6 +184,28 @@ int srq_batch_decode_i4(void *o, const void *q, const void *kv_data, const void 
                         int64_t page_size, int64_t head_dim, float *tmp, int64_t num_chunks,
                         void *stream);
 
+/* Decode-step q/k/v post-processing in one launch.  qkv f16 [batch,
+ * (n_q_heads + 2 n_kv_heads) * head_dim] is the q/k/v projection output of
+ * one new token per request (q heads, then k heads, then v heads); cos, sin
+ * f16 [cos_batch, head_dim] (cos_batch 1 or batch).  q and k rows get the
+ * rotary embedding (srq_rope_qk arithmetic); with rotate != 0 they are then
+ * rotated, fp16(FWHT_D(row) * had_scale) (srq_hadamard_transform
+ * arithmetic).  q rows go to q_out f16 [batch, n_q_heads, head_dim]; k and v
+ * rows are quantized (srq_kv_quant_pack) into the token's cache slot, as
+ * srq_append_kv_i4 places it (request b's last position).  head_dim == 128.
+ * Bit-identical to rope_qk -> hadamard_transform(k) -> kv_quant_pack(k, v) ->
+ * append_kv_i4 -> hadamard_transform(q).  Replaces that chain in the
+ * decoder's attention and MultiLayerPagedKVCache4Bit.update / the decode stub
+ * (e2e/quantized_llama/modeling_llama.py:62-79; signrot/transformers/
+ * kv_cache.py:144-170, 295-415). */
+int srq_qkv_rope_had_append(const void *qkv, const void *cos, const void *sin,
+                            int64_t cos_batch, int64_t batch, int64_t n_q_heads,
+                            int64_t n_kv_heads, int64_t head_dim, float had_scale, int rotate,
+                            void *q_out, void *kv_data, void *kv_param,
+                            const int32_t *kv_indptr, const int32_t *kv_indices,
+                            const int32_t *last_page_offset, int64_t num_layers,
+                            int64_t layer_idx, int64_t page_size, void *stream);
+
 /* ------------------------------------------------------ decode-layer glue */
 
 /* out f16 [rows, cols] = fp16(x * 1/sqrt(Σ x² / mean_dim + eps)), the sum in
@@ -169,6 +214,29 @@ int srq_batch_decode_i4(void *o, const void *q, const void *kv_data, const void 
  * signrot/nn/normalization.py:19-30). */
 int srq_rmsnorm(const void *x, int64_t rows, int64_t cols, float eps, int64_t mean_dim,
                 void *out, void *stream);
+
+/* RMSNorm followed by the per-token symmetric int4 quantizer in one launch:
+ * h = srq_rmsnorm(x) (written to out unless out is NULL), then q u8
+ * [rows, cols/2], scale f16 [rows] = srq_sym_quant_dynamic(h, clip_ratio).
+ * cols % 8 == 0, cols <= 8192.  Bit-identical to the two-step composition.
+ * Replaces RMSNorm -> Quantizer at the decoder's q/k/v and gate/up inputs
+ * (e2e/quantized_llama/modeling_llama.py; fused.cu:68-138, 278-309). */
+int srq_rmsnorm_quant(const void *x, int64_t rows, int64_t cols, float eps, int64_t mean_dim,
+                      float clip_ratio, void *out, void *q, void *scale, void *stream);
+
+/* Head-axis Hadamard of the attention output followed by the per-token
+ * quantizer (the o_proj input): x f16 [batch, n_heads, head_dim];
+ * y[b, h, d] = fp16(FWHT_H(x[b, :, d])[h] * scale) (srq_hadamard_transform
+ * arithmetic over the head axis); q u8 [batch, n_heads * head_dim / 2],
+ * qscale f16 [batch] = srq_sym_quant_dynamic of row y[b] (element
+ * h * head_dim + d).  rot (optional, f16 [batch, n_heads * head_dim])
+ * receives y.  n_heads a power of two <= 64, head_dim % 8 == 0, <= 256.
+ * Bit-identical to transpose -> hadamard_transform -> transpose ->
+ * sym_quant_dynamic.  Replaces that chain before o_proj
+ * (e2e/quantized_llama/modeling_llama.py:94, 117). */
+int srq_head_had_quant(const void *x, int64_t batch, int64_t n_heads, int64_t head_dim,
+                       float scale, float clip_ratio, void *q, void *qscale, void *rot,
+                       void *stream);
 
 /* In-place rotary embedding of q f16 [n_seqs, seq_len, n_q_heads, head_dim]
  * and k f16 [n_seqs, seq_len, n_k_heads, head_dim] with cos, sin f16

@@ -16,6 +16,12 @@ Added ops (no reference counterpart, fused forms of reference chains):
   online_hadamard = matmul_hadU_cuda + sign multiply          nn/hadamard.py:26-42
   had_sign_quant  = online_hadamard + sym_quant_dynamic       modeling_llama.py:134-138
   w4a4_linear_moe = matmul_grouped + sym_dequant_moe          nn/moe.py:126-136
+  w4a4_linear_residual  = w4a4_linear + residual add          modeling_llama.py:19-137
+  rmsnorm_quant         = rmsnorm + sym_quant_dynamic          fused.cu:68-138, 278-309
+  head_had_quant        = head-axis Hadamard + sym_quant_dynamic  modeling_llama.py:94, 117
+  swiglu_had_sign_quant = swiglu + had_sign_quant              modeling_llama.py:125-137
+  qkv_rope_had_append   = rope_qk + K/q Hadamard + kv_quant_pack + append_kv_i4
+                                                              kv_cache.py:144-170, 295-415
 """
 import torch
 
@@ -89,6 +95,33 @@ def w4a4_linear(A, a_scale, B, b_scale, bias=None):
 
 
 # ------------------------------------------------------------------ quant
+
+def w4a4_linear_residual(A, a_scale, B, b_scale, residual, bias=None, out=None):
+    """w4a4_linear with `+ residual` fused into the epilogue: out f16 [M, N] =
+    fp16(linear + residual).  `out` may be `residual` itself (in place)."""
+    _check("w4a4_linear_residual", [(A, "A"), (a_scale, "a_scale"), (B, "B"),
+                                    (b_scale, "b_scale"), (residual, "residual"), (bias, "bias"),
+                                    (out, "out")],
+           [torch.uint8, torch.float16, torch.uint8, torch.float16, torch.float16, torch.float16,
+            torch.float16])
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[1]:
+        raise RuntimeError(f"w4a4_linear_residual: expected A [M, K/2] and B [N, K/2], got "
+                           f"{tuple(A.shape)} and {tuple(B.shape)}")
+    M, N, K = A.shape[0], B.shape[0], A.shape[1] * 2
+    if a_scale.numel() != M or b_scale.numel() != N:
+        raise RuntimeError("w4a4_linear_residual: scale sizes do not match M / N")
+    if residual.numel() != M * N:
+        raise RuntimeError(f"w4a4_linear_residual: residual must have {M} x {N} elements")
+    if bias is not None and bias.numel() != N:
+        raise RuntimeError("w4a4_linear_residual: bias must have N elements")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    elif out.numel() != M * N:
+        raise RuntimeError(f"w4a4_linear_residual: out must have {M} x {N} elements")
+    _call("srq_w4a4_linear_residual", _ptr(A), _ptr(a_scale), _ptr(B), _ptr(b_scale), _ptr(bias),
+          _ptr(residual), M, N, K, _ptr(out), _stream(A))
+    return out
+
 
 def sym_quant(x, scale):
     """Packed int4 codes of fp16 x [M, N] with given fp16 scale [M]
@@ -270,6 +303,35 @@ def append_kv_i4(kv_data, kv_param, kv_indptr, kv_indices, last_page_offset, k, 
           int(layer_idx), H, P, D, _stream(kv_data))
 
 
+def qkv_rope_had_append(qkv, cos, sin, n_q_heads, n_kv_heads, kv_data, kv_param, kv_indptr,
+                        kv_indices, last_page_offset, layer_idx, had_scale, rotate=True):
+    """Decode-step q/k/v post-processing of qkv f16 [B, (Hq + 2 Hk) * 128]:
+    RoPE of q and k, head-dim Hadamard (times had_scale) of q and k when
+    `rotate`, int4 quantize-and-append of k and v into the cache slot of the
+    new token; returns q f16 [B, Hq, 128] (ready for batch_decode_i4)."""
+    L, H, P, D = _check_cache("qkv_rope_had_append", kv_data, kv_param, kv_indptr, kv_indices,
+                              last_page_offset)
+    _check("qkv_rope_had_append", [(qkv, "qkv"), (cos, "cos"), (sin, "sin"),
+                                   (kv_data, "kv_data")],
+           [torch.float16, torch.float16, torch.float16, None])
+    if H != n_kv_heads:
+        raise RuntimeError(f"qkv_rope_had_append: the cache holds {H} KV heads, not {n_kv_heads}")
+    B = qkv.shape[0]
+    if qkv.numel() != B * (n_q_heads + 2 * n_kv_heads) * D:
+        raise RuntimeError(f"qkv_rope_had_append: qkv must be [B, {(n_q_heads + 2 * n_kv_heads) * D}]")
+    if kv_indptr.shape[0] != B + 1 or last_page_offset.shape[0] != B:
+        raise RuntimeError("qkv_rope_had_append: index tensors do not match the batch")
+    cb = cos.numel() // D
+    if cos.numel() != sin.numel() or cos.numel() % D or cb not in (1, B):
+        raise RuntimeError(f"qkv_rope_had_append: cos/sin must be [1 or {B}, {D}]")
+    q = torch.empty((B, n_q_heads, D), dtype=torch.float16, device=qkv.device)
+    _call("srq_qkv_rope_had_append", _ptr(qkv), _ptr(cos), _ptr(sin), cb, B, int(n_q_heads),
+          int(n_kv_heads), D, float(had_scale), 1 if rotate else 0, _ptr(q), _ptr(kv_data),
+          _ptr(kv_param), _ptr(kv_indptr), _ptr(kv_indices), _ptr(last_page_offset), L,
+          int(layer_idx), P, _stream(qkv))
+    return q
+
+
 def batch_decode_i4(o, q, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset,
                     layer_idx, tmp=None, num_chunks=1):
     """Single-query attention over the int4 cache into o [B, Hq, 128]
@@ -310,6 +372,36 @@ def rmsnorm(x, eps, mean_dim):
     return out
 
 
+def rmsnorm_quant(x, eps, mean_dim, clip_ratio=1.0, return_norm=False):
+    """rmsnorm followed by sym_quant_dynamic in one launch: (q u8 [..., cols/2],
+    scale f16 [..., 1]) and, with return_norm, the fp16 normalized x."""
+    _check("rmsnorm_quant", [(x, "x")], [torch.float16])
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    q = torch.empty((*x.shape[:-1], cols // 2), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((*x.shape[:-1], 1), dtype=torch.float16, device=x.device)
+    h = torch.empty_like(x) if return_norm else None
+    _call("srq_rmsnorm_quant", _ptr(x), rows, cols, float(eps), int(mean_dim), float(clip_ratio),
+          _ptr(h), _ptr(q), _ptr(scale), _stream(x))
+    return (q, scale, h) if return_norm else (q, scale)
+
+
+def head_had_quant(x, scale, clip_ratio=1.0, return_rot=False):
+    """Head-axis Hadamard of x f16 [B, H, D] (times `scale`) then per-row
+    sym_quant_dynamic of the [B, H * D] result: (q u8 [B, H*D/2], scale f16
+    [B, 1]) and, with return_rot, the rotated fp16 rows."""
+    _check("head_had_quant", [(x, "x")], [torch.float16])
+    if x.dim() != 3:
+        raise RuntimeError("head_had_quant expects x [B, H, D]")
+    B, H, D = x.shape
+    q = torch.empty((B, H * D // 2), dtype=torch.uint8, device=x.device)
+    qs = torch.empty((B, 1), dtype=torch.float16, device=x.device)
+    rot = torch.empty((B, H * D), dtype=torch.float16, device=x.device) if return_rot else None
+    _call("srq_head_had_quant", _ptr(x), B, H, D, float(scale), float(clip_ratio), _ptr(q),
+          _ptr(qs), _ptr(rot), _stream(x))
+    return (q, qs, rot) if return_rot else (q, qs)
+
+
 def rope_qk(q, k, cos, sin):
     """In-place rotary embedding of q, k [B, T, H, D] (bindings.cpp:383-409)."""
     _check("rope_qk", [(q, "q"), (k, "k"), (cos, "cos"), (sin, "sin")])
@@ -348,6 +440,27 @@ def swiglu(gate, up):
 
 
 # -------------------------------------------------------------------- MoE
+
+def swiglu_had_sign_quant(gu, hadK, K, sign=None, clip_ratio=1.0):
+    """swiglu(gu[..., :n], gu[..., n:]) followed by had_sign_quant, one launch,
+    for a gate/up projection output gu f16 [..., 2n]: (q u8 [..., n/2], scale
+    f16 [..., 1])."""
+    _check("swiglu_had_sign_quant", [(gu, "gu"), (hadK, "hadK"), (sign, "sign")],
+           [torch.float16, torch.float16, torch.int8])
+    if gu.shape[-1] % 2:
+        raise RuntimeError("swiglu_had_sign_quant: the last dim must be 2n")
+    n = gu.shape[-1] // 2
+    _check_had("swiglu_had_sign_quant", n, hadK, K, sign, False)
+    rows = gu.numel() // (2 * n) if n else 0
+    q = torch.empty((*gu.shape[:-1], n // 2), dtype=torch.uint8, device=gu.device)
+    scale = torch.empty((*gu.shape[:-1], 1), dtype=torch.float16, device=gu.device)
+    if rows:
+        gate = gu.view(rows, 2 * n)
+        _call("srq_swiglu_had_sign_quant", _ptr(gate), gate[:, n:].data_ptr(), 2 * n, rows, n,
+              int(K), _ptr(hadK), _ptr(sign), float(clip_ratio), _ptr(q), _ptr(scale),
+              _stream(gu))
+    return q, scale
+
 
 def matmul_grouped(problem_sizes, ptr_A, ptr_B, ptr_C, lda, ldb, ldc, signed_a=True):
     """Grouped int4 GEMM, C_p = A_p · B_pᵀ (int32) per problem, all problem

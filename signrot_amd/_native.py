@@ -22,9 +22,11 @@ SIGNATURES = {
     "srq_kv_quant_pack": [_p, _i64, _i64, _p, _p, _p],
     "srq_matmul_s4s4": [_p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
+    "srq_w4a4_linear_residual": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_hadamard_transform": [_p, _p, _i64, _i64, _f32, _i32, _p],
     "srq_online_hadamard": [_p, _p, _i64, _i64, _i64, _p, _p, _i32, _p],
     "srq_had_sign_quant": [_p, _i64, _i64, _i64, _p, _p, _i32, _f32, _p, _p, _p],
+    "srq_swiglu_had_sign_quant": [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _f32, _p, _p, _p],
     "srq_append_kv_i4": [_p, _p, _p, _p, _p, _p, _p, _p, _p,
                          _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "srq_init_kv_i4": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
@@ -32,6 +34,10 @@ SIGNATURES = {
     "srq_batch_decode_i4": [_p, _p, _p, _p, _p, _p, _p,
                             _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "srq_rmsnorm": [_p, _i64, _i64, _f32, _i64, _p, _p],
+    "srq_rmsnorm_quant": [_p, _i64, _i64, _f32, _i64, _f32, _p, _p, _p, _p],
+    "srq_head_had_quant": [_p, _i64, _i64, _i64, _f32, _f32, _p, _p, _p, _p],
+    "srq_qkv_rope_had_append": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
+                                _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "srq_rope_qk": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "srq_swiglu": [_p, _p, _i64, _p, _p],
     "srq_matmul_grouped": [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p],

@@ -165,3 +165,78 @@ SRQ_DEV int kv_code(float x, float zero, float scale) {
     r = fminf(fmaxf(r, 0.f), 15.f);
     return (int)r;
 }
+
+// Eight symmetric codes packed into one 32-bit word, element i in bits
+// 4i .. 4i + 3 (the reference's nibble order).
+SRQ_DEV u32 pack8_sym(const v8h &v, float s) {
+    u32 w = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w |= (u32)(sym_code((float)v[i], s) & 0xF) << (4 * i);
+    return w;
+}
+
+SRQ_DEV float absmax8(const v8h &v, float m) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf((float)v[i]));
+    return m;
+}
+
+// Row scale from the exact fp32 max (fused.cu:93-95 order: divide, round to
+// fp16, then the clip multiply rounds again).
+SRQ_DEV f16 sym_row_scale(float amax, float clip) {
+    f16 s = f16_rn(amax / 7.f);
+    if (clip != 1.f) s = f16_rn((float)s * clip);
+    return s;
+}
+
+// SwiGLU of one element: fp16(fp16(g / (1 + exp(-g))) * u)
+// (signrot/kernels/fused.cu:367-390); every kernel that applies it calls
+// this one function, so fused and unfused forms round identically.
+SRQ_DEV f16 swiglu1(float g, float u) {
+    const f16 sl = f16_rn(g / (1.f + expf(-g)));
+    return (f16)((float)sl * u);
+}
+
+// In-register Walsh-Hadamard butterflies over R values (Sylvester order),
+// stages in ascending index bit: every FWHT kernel here runs its stages in
+// this order, so a fused kernel reproduces the unfused fp32 result exactly.
+template <int R>
+SRQ_DEV void fwht_regs(float (&v)[R]) {
+#pragma unroll
+    for (int h = 1; h < R; h <<= 1) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            if (!(i & h)) {
+                const float a = v[i], b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+        }
+    }
+}
+
+// KV-cache row parameters from the exact row max/min (fused.cu:246-252):
+// diff rounds to fp16, the clamp(min=1e-5) rounds to fp16, the / 15 rounds
+// again; zero = -min exactly.
+SRQ_DEV void kv_row_params(float vmax, float vmin, f16 &scale, f16 &zero) {
+    f16 diff = f16_rn((float)(f16)vmax - (float)(f16)vmin);
+    diff = f16_rn(fmaxf((float)diff, 1e-5f));
+    scale = f16_rn((float)diff / 15.f);
+    zero = -(f16)vmin;
+}
+
+// Rotary embedding of one rotate_half pair (x0 at i, x1 at i + D/2) with
+// per-op fp16 rounding, as the three-op torch expression
+// x * cos + rotate_half(x) * sin evaluates it in fp16 (fused.cu:316-362).
+// Products of two fp16 values are exact in fp32, so each rounds once.
+SRQ_DEV f16 rope_lo(float x0, float x1, float c, float s) {
+    const f16 a = (f16)(x0 * c);
+    const f16 b = (f16)(-x1 * s);
+    return (f16)((float)a + (float)b);
+}
+
+SRQ_DEV f16 rope_hi(float x0, float x1, float c, float s) {
+    const f16 a = (f16)(x1 * c);
+    const f16 b = (f16)(x0 * s);
+    return (f16)((float)a + (float)b);
+}

@@ -62,6 +62,7 @@ struct Epi {
     const f16 *sa;     // [M]
     const f16 *sb;     // [N]
     const f16 *bias;   // [N] or null
+    const f16 *res;    // [M, N] residual added last (may alias out) or null
 };
 
 SRQ_DEV void store_one(const Epi &e, int64_t N, int64_t m, int64_t n, int acc256) {
@@ -72,6 +73,7 @@ SRQ_DEV void store_one(const Epi &e, int64_t N, int64_t m, int64_t n, int acc256
         const float a = (float)v * (float)e.sa[m];
         f16 o = f16_rn(a * (float)e.sb[n]);
         if (e.bias) o = f16_rn((float)o + (float)e.bias[n]);
+        if (e.res) o = f16_rn((float)o + (float)e.res[m * N + n]);
         e.out[m * N + n] = o;
     }
 }
@@ -106,6 +108,7 @@ SRQ_DEV void store_block(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t
                     const float a = (float)v * sa;
                     f16 o = f16_rn(a * sbv[j]);
                     if (e.bias) o = f16_rn((float)o + (float)e.bias[gnv[j]]);
+                    if (e.res) o = f16_rn((float)o + (float)e.res[gm * N + gnv[j]]);
                     e.out[gm * N + gnv[j]] = o;
                 }
             }
@@ -455,6 +458,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
                     const float a = (float)val * sa;
                     f16 o = f16_rn(a * sbv[j]);
                     if (e.bias) o = f16_rn((float)o + (float)e.bias[gnv[j]]);
+                    if (e.res) o = f16_rn((float)o + (float)e.res[gm * N + gnv[j]]);
                     e.out[gm * N + gnv[j]] = o;
                 }
             }
@@ -737,6 +741,7 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
                         } else {
                             f16 o = f16_rn(((float)v * sal[m]) * sbv);
                             if (e.bias) o = f16_rn((float)o + (float)e.bias[gn]);
+                            if (e.res) o = f16_rn((float)o + (float)e.res[m * N + gn]);
                             e.out[m * N + gn] = o;
                         }
                     }
@@ -1075,6 +1080,24 @@ extern "C" int srq_w4a4_linear(const void *A, const void *a_scale, const void *B
     e.sb = (const f16 *)b_scale;
     e.bias = (const f16 *)bias;
     return run_gemm("w4a4_linear", A, B, M, N, K, e, (hipStream_t)stream);
+}
+
+extern "C" int srq_w4a4_linear_residual(const void *A, const void *a_scale, const void *B,
+                                        const void *b_scale, const void *bias,
+                                        const void *residual, int64_t M, int64_t N, int64_t K,
+                                        void *out, void *stream) {
+    int rc = check_gemm("w4a4_linear_residual", A, B, M, N, K);
+    if (rc) return rc;
+    if (M && N)
+        SRQ_CHECK_ARG(out && a_scale && b_scale && residual,
+                      "w4a4_linear_residual: null pointer");
+    Epi e{};
+    e.out = (f16 *)out;
+    e.sa = (const f16 *)a_scale;
+    e.sb = (const f16 *)b_scale;
+    e.bias = (const f16 *)bias;
+    e.res = (const f16 *)residual;
+    return run_gemm("w4a4_linear_residual", A, B, M, N, K, e, (hipStream_t)stream);
 }
 
 // Persistent grid of the grouped kernel: one workgroup per CU (256 CUs).

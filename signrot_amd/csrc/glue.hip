@@ -9,15 +9,22 @@
 //   swiglu : out = fp16(fp16(g / (1 + exp(-g))) * up)
 #include "common.h"
 
+#include <type_traits>
+
 namespace {
 
 // ------------------------------------------------------------------ RMSNorm
 // One row per 64-lane wave (rows <= 8192 values: 16-byte loads, the row in
-// registers, one wave reduction), 4 rows per block.
-template <int VPT>
+// registers, one wave reduction), 4 rows per block.  QUANT additionally
+// quantizes the normalized fp16 row (per-token symmetric int4, the
+// sym_quant_dynamic arithmetic) while it is still in registers; `out` may
+// then be null.
+template <int VPT, bool QUANT>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const f16 *__restrict__ x, int64_t rows,
                                                       int nvec, float eps, float mean_dim,
-                                                      f16 *__restrict__ out) {
+                                                      f16 *__restrict__ out, float clip,
+                                                      u32 *__restrict__ q,
+                                                      f16 *__restrict__ qscale) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -36,15 +43,28 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const f16 *__restrict__ x,
     }
     acc = wave_sum(acc);
     const float inv = 1.0f / __builtin_sqrtf(acc / mean_dim + eps);
-    v8h *orow = reinterpret_cast<v8h *>(out) + row * nvec;
+    float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = lane + 64 * i;
-        if (idx < nvec) {
-            v8h o;
+        v8h o;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = f16_rn((float)v[i][e] * inv);
-            orow[idx] = o;
+        for (int e = 0; e < 8; ++e) o[e] = f16_rn((float)v[i][e] * inv);
+        v[i] = o;
+        if (idx < nvec) {
+            if (out) reinterpret_cast<v8h *>(out)[row * nvec + idx] = o;
+            if (QUANT) amax = absmax8(o, amax);
+        }
+    }
+    if (QUANT) {
+        amax = wave_max(amax);
+        const f16 s = sym_row_scale(amax, clip);
+        if (lane == 0) qscale[row] = s;
+        const float sf = (float)s;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = lane + 64 * i;
+            if (idx < nvec) q[row * nvec + idx] = pack8_sym(v[i], sf);
         }
     }
 }
@@ -89,13 +109,8 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(f16 *__restrict__ q, f16 *
         const f16 *c = cs + ct * (2 * half);
         const f16 *s = sn + ct * (2 * half);
         const float x0 = (float)base[i], x1 = (float)base[i + half];
-        // products of two fp16 values are exact in fp32, so each rounds once
-        const f16 a0 = (f16)(x0 * (float)c[i]);
-        const f16 b0 = (f16)(-x1 * (float)s[i]);
-        const f16 a1 = (f16)(x1 * (float)c[i + half]);
-        const f16 b1 = (f16)(x0 * (float)s[i + half]);
-        base[i] = (f16)((float)a0 + (float)b0);
-        base[i + half] = (f16)((float)a1 + (float)b1);
+        base[i] = rope_lo(x0, x1, (float)c[i], (float)s[i]);
+        base[i + half] = rope_hi(x0, x1, (float)c[i + half], (float)s[i + half]);
     }
 }
 
@@ -105,13 +120,78 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const f16 *__restrict__ g,
                                                      f16 *__restrict__ out) {
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * 256) {
-        const float gv = (float)g[i];
-        const f16 sl = f16_rn(gv / (1.f + expf(-gv)));
-        out[i] = (f16)((float)sl * (float)u[i]);
+        out[i] = swiglu1((float)g[i], (float)u[i]);
+    }
+}
+
+// ------------------------------------------------- head Hadamard + quant
+// Input of the o_proj of a decode step (modeling_llama.py:94, 117): the
+// attention output x [B, H, D] is rotated over the head axis,
+//   y[b, h, d] = fp16(FWHT_H(x[b, :, d])[h] * scale),
+// and the row y[b] (element h * D + d) is quantized per token (symmetric
+// int4, sym_quant_dynamic arithmetic).  One block per b: thread d holds the
+// H values of column d in registers (stages in ascending bit, as the FWHT
+// kernel), the rotated row is staged in LDS as fp16, then packed eight
+// codes per 32-bit word.
+template <int H>
+__global__ __launch_bounds__(256) void head_had_quant_kernel(const f16 *__restrict__ x, int D,
+                                                             float scale, float clip,
+                                                             u32 *__restrict__ q,
+                                                             f16 *__restrict__ qscale,
+                                                             f16 *__restrict__ rot) {
+    __shared__ __attribute__((aligned(16))) f16 buf[H * 256];
+    __shared__ float red[4];
+    const int64_t b = blockIdx.x;
+    const f16 *xb = x + b * H * D;
+    float amax = 0.f;
+    const int d = threadIdx.x;
+    if (d < D) {
+        float v[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) v[h] = (float)xb[h * D + d];
+        fwht_regs<H>(v);
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const f16 y = f16_rn(v[h] * scale);
+            buf[h * D + d] = y;
+            amax = fmaxf(amax, fabsf((float)y));
+        }
+    }
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const f16 s = sym_row_scale(amax, clip);
+    if (threadIdx.x == 0) qscale[b] = s;
+    const float sf = (float)s;
+    const int nw = H * D / 8;
+    for (int w = threadIdx.x; w < nw; w += 256) {
+        const v8h v = *reinterpret_cast<const v8h *>(buf + 8 * w);
+        q[b * nw + w] = pack8_sym(v, sf);
+        if (rot) reinterpret_cast<v8h *>(rot)[b * nw + w] = v;
     }
 }
 
 }  // namespace
+
+template <bool QUANT>
+static void launch_rmsnorm_vec(const void *x, int64_t rows, int64_t nvec, float eps,
+                               float mean_dim, void *out, float clip, void *q, void *qs,
+                               hipStream_t st) {
+    const dim3 grid((unsigned)srq_cdiv(rows, 4));
+    const int vpt = (int)srq_cdiv(nvec, 64);
+    auto go = [&](auto vt) {
+        constexpr int V = decltype(vt)::value;
+        rmsnorm_kernel<V, QUANT><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps,
+                                                       mean_dim, (f16 *)out, clip, (u32 *)q,
+                                                       (f16 *)qs);
+    };
+    if (vpt <= 1) go(std::integral_constant<int, 1>{});
+    else if (vpt <= 2) go(std::integral_constant<int, 2>{});
+    else if (vpt <= 4) go(std::integral_constant<int, 4>{});
+    else if (vpt <= 8) go(std::integral_constant<int, 8>{});
+    else go(std::integral_constant<int, 16>{});
+}
 
 extern "C" int srq_rmsnorm(const void *x, int64_t rows, int64_t cols, float eps, int64_t mean_dim,
                            void *out, void *stream) {
@@ -121,23 +201,30 @@ extern "C" int srq_rmsnorm(const void *x, int64_t rows, int64_t cols, float eps,
     hipStream_t st = (hipStream_t)stream;
     const int64_t nvec = cols / 8;
     if (cols % 8 == 0 && nvec <= 64 * 16 && srq_aligned(x, 16) && srq_aligned(out, 16)) {
-        const dim3 grid((unsigned)srq_cdiv(rows, 4));
-        const int vpt = (int)srq_cdiv(nvec, 64);
-        if (vpt <= 1)
-            rmsnorm_kernel<1><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
-        else if (vpt <= 2)
-            rmsnorm_kernel<2><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
-        else if (vpt <= 4)
-            rmsnorm_kernel<4><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
-        else if (vpt <= 8)
-            rmsnorm_kernel<8><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
-        else
-            rmsnorm_kernel<16><<<grid, 256, 0, st>>>((const f16 *)x, rows, (int)nvec, eps, (float)mean_dim, (f16 *)out);
+        launch_rmsnorm_vec<false>(x, rows, nvec, eps, (float)mean_dim, out, 1.f, nullptr,
+                                  nullptr, st);
     } else {
         rmsnorm_generic_kernel<<<dim3((unsigned)rows), 256, 0, st>>>(
             (const f16 *)x, rows, cols, eps, (float)mean_dim, (f16 *)out);
     }
     SRQ_LAUNCH_CHECK("rmsnorm");
+    return SRQ_OK;
+}
+
+extern "C" int srq_rmsnorm_quant(const void *x, int64_t rows, int64_t cols, float eps,
+                                 int64_t mean_dim, float clip_ratio, void *out, void *q,
+                                 void *scale, void *stream) {
+    SRQ_CHECK_ARG(rows >= 0 && cols >= 0 && mean_dim > 0, "rmsnorm_quant: bad shape");
+    if (rows == 0 || cols == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(x && q && scale, "rmsnorm_quant: null pointer");
+    SRQ_CHECK_ARG(cols % 8 == 0 && cols <= 8192,
+                  "rmsnorm_quant: cols=%lld must be a multiple of 8 and <= 8192",
+                  (long long)cols);
+    SRQ_CHECK_ARG(srq_aligned(x, 16) && srq_aligned(q, 4) && (!out || srq_aligned(out, 16)),
+                  "rmsnorm_quant: x and out must be 16-byte aligned, q 4-byte aligned");
+    launch_rmsnorm_vec<true>(x, rows, cols / 8, eps, (float)mean_dim, out, clip_ratio, q, scale,
+                             (hipStream_t)stream);
+    SRQ_LAUNCH_CHECK("rmsnorm_quant");
     return SRQ_OK;
 }
 
@@ -168,5 +255,42 @@ extern "C" int srq_swiglu(const void *gate, const void *up, int64_t n, void *out
     swiglu_kernel<<<dim3((unsigned)blocks), 256, 0, (hipStream_t)stream>>>(
         (const f16 *)gate, (const f16 *)up, n, (f16 *)out);
     SRQ_LAUNCH_CHECK("swiglu");
+    return SRQ_OK;
+}
+
+extern "C" int srq_head_had_quant(const void *x, int64_t batch, int64_t n_heads, int64_t head_dim,
+                                  float scale, float clip_ratio, void *q, void *qscale, void *rot,
+                                  void *stream) {
+    SRQ_CHECK_ARG(batch >= 0 && n_heads > 0 && head_dim > 0, "head_had_quant: bad shape");
+    SRQ_CHECK_ARG(n_heads <= 64 && (n_heads & (n_heads - 1)) == 0,
+                  "head_had_quant: n_heads=%lld must be a power of two <= 64",
+                  (long long)n_heads);
+    SRQ_CHECK_ARG(head_dim <= 256 && head_dim % 8 == 0,
+                  "head_had_quant: head_dim=%lld must be a multiple of 8 and <= 256",
+                  (long long)head_dim);
+    SRQ_CHECK_ARG(batch <= 0x7fffffffLL, "head_had_quant: batch > 2^31-1");
+    if (batch == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(x && q && qscale, "head_had_quant: null pointer");
+    SRQ_CHECK_ARG(srq_aligned(q, 4) && (!rot || srq_aligned(rot, 16)),
+                  "head_had_quant: q must be 4-byte and rot 16-byte aligned");
+    const dim3 grid((unsigned)batch);
+    hipStream_t st = (hipStream_t)stream;
+    const int D = (int)head_dim;
+    switch (n_heads) {
+#define SRQ_HHQ(HH)                                                                         \
+    case HH:                                                                                \
+        head_had_quant_kernel<HH><<<grid, 256, 0, st>>>((const f16 *)x, D, scale, clip_ratio, \
+                                                        (u32 *)q, (f16 *)qscale, (f16 *)rot); \
+        break;
+        SRQ_HHQ(1)
+        SRQ_HHQ(2)
+        SRQ_HHQ(4)
+        SRQ_HHQ(8)
+        SRQ_HHQ(16)
+        SRQ_HHQ(32)
+        SRQ_HHQ(64)
+#undef SRQ_HHQ
+    }
+    SRQ_LAUNCH_CHECK("head_had_quant");
     return SRQ_OK;
 }

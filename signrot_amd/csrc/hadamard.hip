@@ -41,21 +41,6 @@ struct RotArgs {
     int rpb;            // rows per block
 };
 
-template <int R>
-SRQ_DEV void fwht_regs(float (&v)[R]) {
-#pragma unroll
-    for (int h = 1; h < R; h <<= 1) {
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-            if (!(i & h)) {
-                const float a = v[i], b = v[i + h];
-                v[i] = a + b;
-                v[i + h] = a - b;
-            }
-        }
-    }
-}
-
 // One radix-R pass over `total` LDS floats: butterflies on the index bits
 // [log2(s), log2(s) + log2(R)).  Group g covers base + j*s, j < R.
 template <int R>
@@ -371,7 +356,7 @@ int check_rotation(const char *name, const void *x, int64_t rows, int64_t n, int
 
 int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
-                    hipStream_t st);
+                    hipStream_t st, const void *up = nullptr, int64_t ld = 0);
 
 extern "C" int srq_hadamard_transform(const void *x, void *out, int64_t rows, int64_t n,
                                       float scale, int dtype, void *stream) {
@@ -455,4 +440,26 @@ extern "C" int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_
         return SRQ_OK;
     }
     return launch_rotate(a, 1, (hipStream_t)stream, "had_sign_quant");
+}
+
+extern "C" int srq_swiglu_had_sign_quant(const void *gate, const void *up, int64_t ld,
+                                         int64_t rows, int64_t n, int64_t K, const void *hadK,
+                                         const int8_t *sign, float clip_ratio, void *q,
+                                         void *scale, void *stream) {
+    int rc = check_rotation("swiglu_had_sign_quant", gate, rows, n, K, hadK);
+    if (rc) return rc;
+    if (rows == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(up && q && scale, "swiglu_had_sign_quant: null pointer");
+    SRQ_CHECK_ARG(ld >= n && ld % 8 == 0, "swiglu_had_sign_quant: ld=%lld must be >= n and a "
+                  "multiple of 8", (long long)ld);
+    SRQ_CHECK_ARG(srq_aligned(gate, 16) && srq_aligned(up, 16) && srq_aligned(q, 16),
+                  "swiglu_had_sign_quant: gate, up and q must be 16-byte aligned");
+    if (srq_had512_mfma(gate, rows, n, K, hadK, sign, clip_ratio, q, scale, nullptr,
+                        (hipStream_t)stream, up, ld)) {
+        SRQ_LAUNCH_CHECK("swiglu_had_sign_quant");
+        return SRQ_OK;
+    }
+    srq_set_error("swiglu_had_sign_quant: needs n = K * 512 with 9 <= K <= 32 (n=%lld, K=%lld)",
+                  (long long)n, (long long)K);
+    return SRQ_EUNSUPPORTED;
 }

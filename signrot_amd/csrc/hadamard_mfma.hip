@@ -38,6 +38,8 @@
 // clip = 1; otherwise codes are clamped in fp16 first.
 #include "common.h"
 
+#include <type_traits>
+
 namespace {
 
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
@@ -106,6 +108,8 @@ struct MfmaRotArgs {
     uint8_t *q;           // quant mode: packed codes, rows of n/2 bytes
     f16 *qscale;          // quant mode: [rows]
     f16 *out;             // rotation mode: fp16 rows of n
+    const f16 *up;        // SwiGLU input: x is the gate, this the up projection
+    int64_t ld;           // row stride of x (and up), elements
 };
 
 // Quantize one row's packed K-mix results w (this lane: chunk ln, i2 runs
@@ -129,8 +133,10 @@ SRQ_DEV void quant_store(const u32 (&w)[4][8], float rcp, uint8_t *qrow) {
         }
 }
 
-template <int NT, int MODE>
-__global__ __launch_bounds__(256, 2) void had512_mfma_kernel(MfmaRotArgs a) {
+// SW: the row is swiglu(gate, up) of two strided inputs (one workgroup per
+// CU: the up prefetch needs the registers two workgroups would share).
+template <int NT, int MODE, bool SW>
+__global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArgs a) {
     // The staged row: 128-element segment (chunk c, quarter i1) at
     // rowbuf + 256 (4c + i1) bytes, its 16-byte piece p at position
     // p ^ 2h(c, i1), h = i1 | ((c >> 2) & 1) << 2.  The swizzle makes both
@@ -237,17 +243,24 @@ __global__ __launch_bounds__(256, 2) void had512_mfma_kernel(MfmaRotArgs a) {
     const int rdbase = (cta * 4 + i1a) * 256 + 16 * g;
     // Row fetch: instruction j of wave w reads chunk c = 4j + w whole (1 KB,
     // lane l: piece l % 16 of quarter l / 16), K / 4 instructions per wave.
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, a.rows * n * 2);
+    const int64_t xbytes = a.rows > 0 ? ((a.rows - 1) * a.ld + n) * 2 : 0;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, xbytes);
+    const __amdgpu_buffer_rsrc_t ur = make_rsrc(SW ? a.up : a.x, xbytes);
     const int cpw = a.KC / 4;
     const int wi1 = lane >> 4, wp = lane & 15;
     v4i pre[NT * 2];
+    v4i preu[SW ? NT * 2 : 1];
     auto gload = [&](int64_t r) {
-        const uint32_t rb = (uint32_t)(r * n * 2) + (uint32_t)(wave * 1024 + lane * 16);
+        const uint32_t rb = (uint32_t)(r * a.ld * 2) + (uint32_t)(wave * 1024 + lane * 16);
 #pragma unroll
         for (int j = 0; j < NT * 2; ++j)
-            if (j < cpw)
+            if (j < cpw) {
                 pre[j] = __builtin_bit_cast(
                     v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, rb + j * 4096, 0, 0));
+                if constexpr (SW)
+                    preu[j] = __builtin_bit_cast(
+                        v4i, __builtin_amdgcn_raw_buffer_load_b128(ur, rb + j * 4096, 0, 0));
+            }
     };
     auto lstore = [&]() {
 #pragma unroll
@@ -255,7 +268,16 @@ __global__ __launch_bounds__(256, 2) void had512_mfma_kernel(MfmaRotArgs a) {
             if (j >= cpw) continue;
             const int c = 4 * j + wave;
             const int h = wi1 | (((c >> 2) & 1) << 2);
-            rowbuf[(c * 4 + wi1) * 16 + (wp ^ (2 * h))] = pre[j];
+            v4i val = pre[j];
+            if constexpr (SW) {
+                const v8h g8 = __builtin_bit_cast(v8h, pre[j]);
+                const v8h u8 = __builtin_bit_cast(v8h, preu[j]);
+                v8h o;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = swiglu1((float)g8[e], (float)u8[e]);
+                val = __builtin_bit_cast(v4i, o);
+            }
+            rowbuf[(c * 4 + wi1) * 16 + (wp ^ (2 * h))] = val;
         }
     };
     for (int i = threadIdx.x; i < (NT * 8 - a.KC) * 64; i += 256)
@@ -443,10 +465,11 @@ __global__ __launch_bounds__(256, 2) void had512_mfma_kernel(MfmaRotArgs a) {
 // Returns 1 if it launched, 0 if the shape is not covered.
 int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
-                    hipStream_t st) {
+                    hipStream_t st, const void *up, int64_t ld) {
     if (K < 9 || K > 32 || n != K * 512) return 0;
-    if (rows * n * 2 >= (int64_t)kOob) return 0;  // 32-bit buffer offsets
-    if (!srq_aligned(x, 16)) return 0;
+    if (ld < n) ld = n;
+    if (rows > 0 && ((rows - 1) * ld + n) * 2 >= (int64_t)kOob) return 0;  // 32-bit offsets
+    if (!srq_aligned(x, 16) || (up && !srq_aligned(up, 16)) || ld % 8) return 0;
     if (q && !srq_aligned(q, 16)) return 0;  // 16-byte code stores
     if (out && !srq_aligned(out, 8)) return 0;
     MfmaRotArgs a{};
@@ -460,20 +483,38 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     a.q = (uint8_t *)q;
     a.qscale = (f16 *)qscale;
     a.out = (f16 *)out;
-    // persistent blocks of 4 waves, up to 2 per CU (256 CUs), one row each
-    // at a time
-    int64_t blocks = rows;
-    if (blocks > 256 * 2) blocks = 256 * 2;
+    a.up = (const f16 *)up;
+    a.ld = ld;
+    // persistent blocks of 4 waves, up to 2 per CU (256 CUs; 1 with the
+    // SwiGLU input), one row each at a time
+    const int64_t cap = up ? 256 : 256 * 2;
+    const int64_t blocks = rows < cap ? rows : cap;
     const dim3 grid((unsigned)blocks), block(256);
     const int nt = (int)srq_cdiv(K, 8);
-    if (q) {
-        if (nt == 2) had512_mfma_kernel<2, 1><<<grid, block, 0, st>>>(a);
-        else if (nt == 3) had512_mfma_kernel<3, 1><<<grid, block, 0, st>>>(a);
-        else had512_mfma_kernel<4, 1><<<grid, block, 0, st>>>(a);
+    auto go = [&](auto ntc, auto modec, auto swc) {
+        had512_mfma_kernel<decltype(ntc)::value, decltype(modec)::value, decltype(swc)::value>
+            <<<grid, block, 0, st>>>(a);
+    };
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    using I4 = std::integral_constant<int, 4>;
+    using M0 = std::integral_constant<int, 0>;
+    using M1 = std::integral_constant<int, 1>;
+    using S0 = std::false_type;
+    using S1 = std::true_type;
+    if (up) {
+        if (!q) return 0;
+        if (nt == 2) go(I2{}, M1{}, S1{});
+        else if (nt == 3) go(I3{}, M1{}, S1{});
+        else go(I4{}, M1{}, S1{});
+    } else if (q) {
+        if (nt == 2) go(I2{}, M1{}, S0{});
+        else if (nt == 3) go(I3{}, M1{}, S0{});
+        else go(I4{}, M1{}, S0{});
     } else {
-        if (nt == 2) had512_mfma_kernel<2, 0><<<grid, block, 0, st>>>(a);
-        else if (nt == 3) had512_mfma_kernel<3, 0><<<grid, block, 0, st>>>(a);
-        else had512_mfma_kernel<4, 0><<<grid, block, 0, st>>>(a);
+        if (nt == 2) go(I2{}, M0{}, S0{});
+        else if (nt == 3) go(I3{}, M0{}, S0{});
+        else go(I4{}, M0{}, S0{});
     }
     return 1;
 }

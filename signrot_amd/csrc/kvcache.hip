@@ -96,6 +96,127 @@ __global__ __launch_bounds__(256) void append_kernel(Paged p, const uint8_t *__r
     }
 }
 
+// ------------------------------------------------ fused q/k/v post-GEMM
+// The decode-step work between the q/k/v projection and the attention
+// kernel, in one launch (modeling_llama.py:62-79 + kv_cache.py:295-415 +
+// kv_cache.py:157-158): for request b and the new token,
+//   q-head rows: RoPE -> (rotate) FWHT_D * had_scale -> fp16 -> q_out
+//   k-head rows: RoPE -> (rotate) FWHT_D * had_scale -> fp16 -> KV int4
+//                quantize -> cache slot of the new token
+//   v-head rows: KV int4 quantize -> cache slot
+// qkv f16 [B, (Hq + 2 Hk) D] is the projection output (q heads, k heads, v
+// heads).  Each D = 128 row is held by 16 lanes, 8 consecutive values per
+// lane: FWHT index bits 0-2 are butterflies in registers, bits 3-6 across
+// lanes (stages in ascending bit, as the FWHT kernel runs them), the RoPE
+// partner i +- 64 is lane l ^ 8.  Every per-element operation is the one the
+// separate ops apply (rope_lo/rope_hi, fp32 FWHT, f16_rn, kv_row_params,
+// kv_code), so the result equals rope_qk -> hadamard_transform ->
+// kv_quant_pack -> append_kv_i4 bit for bit.
+struct QkvArgs {
+    const f16 *qkv;
+    const f16 *cs, *sn;  // [cos_batch, D]
+    int cos_batch;
+    int64_t B;
+    int hq, hk;
+    float had_scale;
+    int rotate;
+    f16 *q_out;          // [B, hq, D]
+};
+
+SRQ_DEV float xor_lane(float v, int m) { return __shfl_xor(v, m, 64); }
+
+__global__ __launch_bounds__(256) void qkv_post_kernel(QkvArgs a, Paged p) {
+    constexpr int D = 128;
+    const int lane = threadIdx.x & 63;
+    const int l = lane & 15;                       // lane within the row group
+    const int hs = a.hq + 2 * a.hk;
+    const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+    const bool valid = row < a.B * hs;
+    const int64_t b = valid ? row / hs : 0;
+    const int slot = valid ? (int)(row - b * hs) : 0;
+    const int kind = slot < a.hq ? 0 : (slot < a.hq + a.hk ? 1 : 2);  // q, k, v
+    float v[8];
+    {
+        v8h x = valid ? *reinterpret_cast<const v8h *>(a.qkv + row * D + 8 * l) : (v8h){};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (float)x[e];
+    }
+    // RoPE (q and k rows); the shuffles run on every lane of the wave
+    {
+        const int64_t ct = a.cos_batch == 1 ? 0 : b;
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float o = xor_lane(v[e], 8);
+            const int i = 8 * l + e;
+            const float c = (float)a.cs[ct * D + i], sn = (float)a.sn[ct * D + i];
+            y[e] = (float)(l < 8 ? rope_lo(v[e], o, c, sn) : rope_hi(o, v[e], c, sn));
+        }
+        if (kind != 2) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = y[e];
+        }
+    }
+    if (a.rotate) {
+        float w[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = v[e];
+        fwht_regs<8>(w);
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float o = xor_lane(w[e], m);
+                w[e] = (l & m) ? o - w[e] : w[e] + o;
+            }
+        }
+        if (kind != 2) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (float)f16_rn(w[e] * a.had_scale);
+        }
+    }
+    if (kind == 0) {
+        if (valid) {
+            v8h o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (f16)v[e];
+            *reinterpret_cast<v8h *>(a.q_out + (b * a.hq + slot) * D + 8 * l) = o;
+        }
+    }
+    // KV quantizer: row max / min over the 16 lanes
+    float vmax = -INFINITY, vmin = INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        vmax = fmaxf(vmax, v[e]);
+        vmin = fminf(vmin, v[e]);
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+        vmax = fmaxf(vmax, xor_lane(vmax, m));
+        vmin = fminf(vmin, xor_lane(vmin, m));
+    }
+    if (!valid || kind == 0) return;
+    const int64_t len = seq_len_of(p, b);
+    const int64_t pos = len - 1;
+    if (pos < 0) return;
+    f16 scale, zero;
+    kv_row_params(vmax, vmin, scale, zero);
+    const float fs = (float)scale, fz = (float)zero;
+    u32 word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) word |= (u32)kv_code(v[e], fz, fs) << (4 * e);
+    const int kv = kind - 1;
+    const int64_t h = slot - a.hq - (kind == 2 ? a.hk : 0);
+    const int64_t page = p.indices[p.indptr[b] + pos / p.page];
+    const int64_t entry = pos % p.page;
+    const int64_t ri = row_index(p, page, kv, h, entry);
+    reinterpret_cast<u32 *>(p.data + ri * (D / 2))[l] = word;
+    if (l == 0) {
+        f16 pr[2] = {scale, zero};
+        reinterpret_cast<uint32_t *>(p.param)[ri] = *reinterpret_cast<const uint32_t *>(pr);
+    }
+}
+
 // --------------------------------------------------------------- decode
 constexpr int kTile = 32;
 constexpr int kD = 128;
@@ -751,5 +872,46 @@ extern "C" int srq_batch_decode_i4(void *o, const void *q, const void *kv_data,
                                                                           (int)num_chunks);
         SRQ_LAUNCH_CHECK("batch_decode_i4 (merge)");
     }
+    return SRQ_OK;
+}
+
+extern "C" int srq_qkv_rope_had_append(const void *qkv, const void *cos, const void *sin,
+                                       int64_t cos_batch, int64_t batch, int64_t n_q_heads,
+                                       int64_t n_kv_heads, int64_t head_dim, float had_scale,
+                                       int rotate, void *q_out, void *kv_data, void *kv_param,
+                                       const int32_t *kv_indptr, const int32_t *kv_indices,
+                                       const int32_t *last_page_offset, int64_t num_layers,
+                                       int64_t layer_idx, int64_t page_size, void *stream) {
+    const char *name = "qkv_rope_had_append";
+    int rc = check_paged(name, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset,
+                         num_layers, layer_idx, n_kv_heads, page_size, head_dim);
+    if (rc) return rc;
+    SRQ_CHECK_ARG(batch >= 0 && n_q_heads > 0 && n_kv_heads > 0 && n_q_heads <= 1024 &&
+                      n_kv_heads <= 1024,
+                  "%s: bad batch or head counts", name);
+    SRQ_CHECK_ARG(cos_batch == 1 || cos_batch == batch, "%s: cos/sin batch must be 1 or B",
+                  name);
+    if (batch == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(qkv && cos && sin && q_out, "%s: null pointer", name);
+    SRQ_CHECK_ARG(srq_aligned(qkv, 16) && srq_aligned(q_out, 16),
+                  "%s: qkv and q_out must be 16-byte aligned", name);
+    QkvArgs a;
+    a.qkv = (const f16 *)qkv;
+    a.cs = (const f16 *)cos;
+    a.sn = (const f16 *)sin;
+    a.cos_batch = (int)cos_batch;
+    a.B = batch;
+    a.hq = (int)n_q_heads;
+    a.hk = (int)n_kv_heads;
+    a.had_scale = had_scale;
+    a.rotate = rotate ? 1 : 0;
+    a.q_out = (f16 *)q_out;
+    Paged p = make_paged(kv_data, kv_param, kv_indptr, kv_indices, last_page_offset, num_layers,
+                         layer_idx, n_kv_heads, page_size, head_dim);
+    const int64_t rows = batch * (n_q_heads + 2 * n_kv_heads);
+    const int64_t blocks = srq_cdiv(rows, 16);
+    SRQ_CHECK_ARG(blocks <= 0x7fffffffLL, "%s: too many rows", name);
+    qkv_post_kernel<<<dim3((unsigned)blocks), 256, 0, (hipStream_t)stream>>>(a, p);
+    SRQ_LAUNCH_CHECK(name);
     return SRQ_OK;
 }

@@ -25,30 +25,6 @@ void srq_set_error(const char *fmt, ...) {
 extern "C" const char *srq_last_error(void) { return g_err; }
 extern "C" int srq_abi_version(void) { return 2; }
 
-// --------------------------------------------------------------------------
-// helpers
-
-SRQ_DEV u32 pack8_sym(const v8h &v, float s) {
-    u32 w = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) w |= (u32)(sym_code((float)v[i], s) & 0xF) << (4 * i);
-    return w;
-}
-
-SRQ_DEV float absmax8(const v8h &v, float m) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf((float)v[i]));
-    return m;
-}
-
-// Row scale from the exact fp32 max (fused.cu:93-95 order: divide, round to
-// fp16, then the clip multiply rounds again).
-SRQ_DEV f16 sym_row_scale(float amax, float clip) {
-    f16 s = f16_rn(amax / 7.f);
-    if (clip != 1.f) s = f16_rn((float)s * clip);
-    return s;
-}
-
 // Reduce `v` over the TPR threads that share a row.  TPR <= 64 stays inside
 // one wave; TPR > 64 adds one LDS hop.  Every thread of the block must call
 // this (it contains __syncthreads when TPR > 64).
@@ -306,12 +282,8 @@ __global__ __launch_bounds__(256) void kv_quant_pack_vec_kernel(
     vmax = group_max<TPR>(vmax);
     vmin = group_min<TPR>(vmin);
     if (row >= rows) return;
-    // fused.cu:246-252: diff rounds to fp16, the clamp(min=1e-5) rounds to
-    // fp16, the / 15 rounds again; zero = -min exactly.
-    f16 diff = f16_rn((float)(f16)vmax - (float)(f16)vmin);
-    diff = f16_rn(fmaxf((float)diff, 1e-5f));
-    const f16 scale = f16_rn((float)diff / 15.f);
-    const f16 zero = -(f16)vmin;
+    f16 scale, zero;
+    kv_row_params(vmax, vmin, scale, zero);
     if (lt == 0) {
         param[row * 2 + 0] = scale;
         param[row * 2 + 1] = zero;
@@ -336,10 +308,8 @@ __global__ __launch_bounds__(64) void kv_quant_pack_generic_kernel(
     }
     vmax = wave_max(vmax);
     vmin = wave_min(vmin);
-    f16 diff = f16_rn((float)(f16)vmax - (float)(f16)vmin);
-    diff = f16_rn(fmaxf((float)diff, 1e-5f));
-    const f16 scale = f16_rn((float)diff / 15.f);
-    const f16 zero = -(f16)vmin;
+    f16 scale, zero;
+    kv_row_params(vmax, vmin, scale, zero);
     if (threadIdx.x == 0) {
         param[row * 2 + 0] = scale;
         param[row * 2 + 1] = zero;

@@ -20,7 +20,7 @@ import torch
 
 from .. import _CUDA
 from ..functional import kernel
-from ..functional.hadamard import get_hadK, matmul_hadU_cuda
+from ..functional.hadamard import _inv_sqrt_f32, get_hadK, matmul_hadU_cuda
 from ..functional.quantization import rtn_weight_pack
 from ..nn.normalization import RMSNorm
 
@@ -87,11 +87,45 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         return _CUDA.w4a4_linear(q.view(-1, q.shape[-1]), s.view(-1), getattr(self, f"w_{name}"),
                                  getattr(self, f"s_{name}"))
 
-    def forward(self, hidden_states, cache, cos, sin, trace=None):
+    def forward(self, hidden_states, cache, cos, sin, trace=None, fused=True):
         """hidden_states fp16 [B, 1, hidden]; cos/sin fp16 [1 or B, 1, head_dim]
         for the new position; returns fp16 [B, 1, hidden].  The cache must
         already hold this layer's context (its first update was a prefill).
-        With a dict `trace`, the intermediates are stored in it (checkers)."""
+        With a dict `trace`, the intermediates are stored in it (checkers) and
+        the op-by-op path runs; otherwise (fused=True) the fused kernels run,
+        with bit-identical results."""
+        if fused and trace is None:
+            return self._forward_fused(hidden_states, cache, cos, sin)
+        return self._forward_ops(hidden_states, cache, cos, sin, trace)
+
+    def _forward_fused(self, hidden_states, cache, cos, sin):
+        """The decode step in 9 launches: rmsnorm_quant -> q/k/v GEMM ->
+        qkv_rope_had_append (RoPE, K/q Hadamard, KV quantize + append) ->
+        batch_decode_i4 -> head_had_quant -> o_proj GEMM + residual ->
+        rmsnorm_quant -> gate/up GEMM -> swiglu_had_sign_quant -> down GEMM
+        + residual."""
+        B = hidden_states.shape[0]
+        x2 = hidden_states.view(B, self.hidden)
+        n1, n2 = self.input_layernorm, self.post_attention_layernorm
+        q1, s1 = _CUDA.rmsnorm_quant(x2, n1.eps, n1.mean_dim)
+        qkv = _CUDA.w4a4_linear(q1, s1.view(-1), self.w_qkv, self.s_qkv)
+        attend, q_rot = cache.update_qkv_fused(qkv, cos, sin, self.layer_idx, self.n_heads)
+        attn = attend(q_rot)                                   # [B, Hq, D]
+        qa, sa = _CUDA.head_had_quant(attn, _inv_sqrt_f32(self.n_heads))
+        x2 = _CUDA.w4a4_linear_residual(qa, sa.view(-1), self.w_o, self.s_o, x2)
+        q2, s2 = _CUDA.rmsnorm_quant(x2, n2.eps, n2.mean_dim)
+        gu = _CUDA.w4a4_linear(q2, s2.view(-1), self.w_gu, self.s_gu)
+        if 9 <= self.down_k <= 32 and self.ffn == self.down_k * 512:
+            qd, sd = _CUDA.swiglu_had_sign_quant(gu, self.down_hadk, self.down_k,
+                                                 self.down_sign)
+        else:  # no fused SwiGLU form of this rotation size
+            a = kernel.swiglu(gu[:, : self.ffn], gu[:, self.ffn:])
+            qd, sd = _CUDA.had_sign_quant(a, self.down_hadk, self.down_k, self.down_sign)
+        out = _CUDA.w4a4_linear_residual(qd, sd.view(-1), self.w_down, self.s_down, x2, out=x2)
+        return out.view(B, 1, self.hidden)
+
+    def _forward_ops(self, hidden_states, cache, cos, sin, trace=None):
+        """Op-by-op decode step (the reference's sequence of ops)."""
         B = hidden_states.shape[0]
         D, Hq, Hk = self.head_dim, self.n_heads, self.n_kv
         x2 = hidden_states.view(B, self.hidden)

@@ -78,13 +78,17 @@ class _AttentionStub(object):
         q = q.view(batch_size, num_qo_heads, head_dim)
         if self.hadamard_dtype is not None:
             q = matmul_had_cuda(q, dtype=self.hadamard_dtype)
+        return self.attend_rotated(q, attention_kwargs, layer_idx).unsqueeze(1)
+
+    def attend_rotated(self, q, attention_kwargs, layer_idx):
+        """batch_decode_i4 of an already rotated q [B, Hq, D] -> [B, Hq, D]."""
         attn_output = torch.empty_like(q)
         tmp = self.tmp
-        if tmp is not None and tmp.shape[1] != num_qo_heads:
+        if tmp is not None and tmp.shape[1] != q.shape[1]:
             tmp = None
         batch_decode_i4(attn_output, q, **attention_kwargs, layer_idx=layer_idx, tmp=tmp,
                         num_chunks=self.num_chunks if tmp is not None else 1)
-        return attn_output.unsqueeze(1)
+        return attn_output
 
 
 class MultiLayerPagedKVCache4Bit(object):
@@ -236,6 +240,31 @@ class MultiLayerPagedKVCache4Bit(object):
                      layer_idx=layer_idx)
         return functools.partial(self._stub.forward, num_kv_heads=num_heads,
                                  attention_kwargs=specs, layer_idx=layer_idx)
+
+    def update_qkv_fused(self, qkv, cos, sin, layer_idx, num_q_heads):
+        """Decode-step form of update() + the stub's q rotation, one kernel:
+        qkv f16 [B, (Hq + 2 H) D] is the q/k/v projection output of the new
+        token; q and k get RoPE (cos/sin [1 or B, 1, D]) and the head-dim
+        Hadamard, k and v are quantized into the cache.  Returns the decode
+        function of a rotated q: attend(q_rot [B, Hq, D]) -> [B, Hq, D], and
+        q_rot.  Results equal rope_qk + update() + the stub bit for bit.  The
+        layer must already hold its prefill (one token per request here)."""
+        if self._needs_init[layer_idx]:
+            raise RuntimeError("update_qkv_fused: the layer has no prefill yet")
+        b_sz = qkv.shape[0]
+        assert b_sz == self.batch_size
+        if layer_idx == 0:
+            new_length = self.length + 1
+            self._ensure_page_cnt_per_batch(self.page_cnt_from_length(new_length))
+            self.length = new_length
+        specs = self.get_cache_specs_for_flash_infer(None)
+        rotate = self.hadamard_dtype is not None
+        q = _CUDA.qkv_rope_had_append(qkv, cos.contiguous(), sin.contiguous(), num_q_heads,
+                                      self.num_heads, **specs, layer_idx=layer_idx,
+                                      had_scale=1 / math.sqrt(self.head_dim), rotate=rotate)
+        attend = functools.partial(self._stub.attend_rotated, attention_kwargs=specs,
+                                   layer_idx=layer_idx)
+        return attend, q
 
     def _set_page_cnt(self, page_cnt: int):
         """indptr = b * page_cnt; indices[b, j] = j * B + b

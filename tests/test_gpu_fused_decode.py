@@ -1,0 +1,212 @@
+"""GPU parity of the fused decode-step kernels.
+
+Each fused entry point is checked bit for bit against the chain of
+separate ops it replaces (each of those is pinned against the oracle in the
+other GPU tests), and the fused decoder layer against the op-by-op layer,
+including the cache contents it leaves behind.  The chains are the
+reference's: RMSNorm -> Quantizer (modeling_llama.py), rope_qk -> K/q
+Hadamard -> kv_quant_pack -> append_kv_i4 (kv_cache.py:144-170, 295-415),
+transpose -> head-axis Hadamard -> Quantizer (modeling_llama.py:94, 117),
+swiglu -> OnlineHadamard -> Quantizer (modeling_llama.py:125-137), and the
+residual add after o_proj / down_proj.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import hadamard as oh
+from oracle import quant as oq
+from tests.gpu_util import assert_bitexact, outlier_input, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _ops():
+    from signrot_amd import _CUDA
+    return _CUDA
+
+
+@pytest.mark.parametrize("rows,cols,clip", [(1, 4096, 1.0), (32, 4096, 1.0), (33, 1024, 0.9),
+                                            (5, 8192, 1.0), (7, 8, 1.0), (64, 4104, 1.0)])
+def test_rmsnorm_quant_equals_rmsnorm_then_quant(rows, cols, clip):
+    C = _ops()
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = to_dev(outlier_input(rng, rows, cols, n_out=3, mag=30.0))
+    q, s, h = C.rmsnorm_quant(x, 1e-5, cols, clip, return_norm=True)
+    h_ref = C.rmsnorm(x, 1e-5, cols)
+    q_ref, s_ref = C.sym_quant_dynamic(h_ref, clip)
+    torch.cuda.synchronize()
+    assert_bitexact(to_np(h), to_np(h_ref), "normalized x")
+    assert_bitexact(to_np(q), to_np(q_ref), "codes")
+    assert_bitexact(to_np(s), to_np(s_ref), "scales")
+    q2, s2 = C.rmsnorm_quant(x, 1e-5, cols, clip)  # no normalized output
+    assert_bitexact(to_np(q2), to_np(q_ref), "codes (out=NULL)")
+    assert_bitexact(to_np(s2), to_np(s_ref), "scales (out=NULL)")
+
+
+def test_rmsnorm_quant_rejects_unsupported_width():
+    C = _ops()
+    x = torch.zeros(2, 8200, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="8192"):
+        C.rmsnorm_quant(x, 1e-5, 8200)
+
+
+@pytest.mark.parametrize("B,H,D", [(32, 32, 128), (1, 32, 128), (3, 8, 64), (4, 64, 128),
+                                   (2, 16, 256)])
+def test_head_had_quant_equals_unfused_chain(B, H, D):
+    from signrot_amd.functional.hadamard import _inv_sqrt_f32, matmul_hadU_cuda
+    C = _ops()
+    rng = np.random.default_rng(B * 100 + H + D)
+    x = to_dev((rng.standard_normal((B, H, D)) * 2.0).astype(np.float16))
+    q, s, rot = C.head_had_quant(x, _inv_sqrt_f32(H), return_rot=True)
+    # the decoder's op-by-op chain (modeling_llama.py:94, 117)
+    t = matmul_hadU_cuda(x.transpose(-1, -2).contiguous(), None, 1)
+    ref = t.transpose(-1, -2).reshape(B, H * D).contiguous()
+    q_ref, s_ref = C.sym_quant_dynamic(ref)
+    torch.cuda.synchronize()
+    assert_bitexact(to_np(rot), to_np(ref), "rotated rows")
+    assert_bitexact(to_np(q), to_np(q_ref), "codes vs sym_quant_dynamic")
+    assert_bitexact(to_np(s), to_np(s_ref), "scales vs sym_quant_dynamic")
+    qw, sw = oq.sym_quant_dynamic(to_np(rot))
+    assert_bitexact(to_np(q), qw, "codes vs the oracle quantizer of the rotated rows")
+    assert_bitexact(to_np(s).reshape(-1), sw.reshape(-1), "scales vs the oracle")
+    # rotation itself within the fp16 tolerance of the float64 closed form
+    want = oh.rotate(to_np(x).transpose(0, 2, 1).reshape(-1, H)).reshape(B, D, H)
+    np.testing.assert_allclose(to_np(rot).reshape(B, H, D).astype(np.float32),
+                               want.transpose(0, 2, 1).astype(np.float32), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("M", [1, 16, 32, 48, 200, 1024])
+def test_w4a4_linear_residual(M):
+    C = _ops()
+    rng = np.random.default_rng(M)
+    K, N = 512, 384
+    A = to_dev(oq.pack_i4(rng.integers(-8, 8, (M, K)).astype(np.int8)))
+    B = to_dev(oq.pack_i4(rng.integers(-8, 8, (N, K)).astype(np.int8)))
+    sa = to_dev((rng.random(M) * 0.02 + 1e-3).astype(np.float16))
+    sb = to_dev((rng.random(N) * 0.02 + 1e-3).astype(np.float16))
+    bias = to_dev((rng.standard_normal(N) * 0.1).astype(np.float16))
+    res = to_dev((rng.standard_normal((M, N)) * 3.0).astype(np.float16))
+    for b in (None, bias):
+        out = C.w4a4_linear_residual(A, sa, B, sb, res, bias=b)
+        ref = C.w4a4_linear(A, sa, B, sb, b) + res
+        torch.cuda.synchronize()
+        assert_bitexact(to_np(out), to_np(ref), f"linear + residual (bias={b is not None})")
+    inplace = res.clone()
+    C.w4a4_linear_residual(A, sa, B, sb, inplace, out=inplace)
+    ref = C.w4a4_linear(A, sa, B, sb) + res
+    torch.cuda.synchronize()
+    assert_bitexact(to_np(inplace), to_np(ref), "in-place residual")
+
+
+@pytest.mark.parametrize("rows,K", [(1, 28), (32, 28), (77, 28), (4, 12)])
+def test_swiglu_had_sign_quant_equals_chain(rows, K):
+    C = _ops()
+    rng = np.random.default_rng(rows + K)
+    n = K * 512
+    gu = to_dev((rng.standard_normal((rows, 2 * n)) * 2.0).astype(np.float16))
+    had, k = oh.get_hadK(n)
+    hk = to_dev(had.astype(np.float16))
+    sign = to_dev(rng.choice([-1, 1], n).astype(np.int8))
+    q, s = C.swiglu_had_sign_quant(gu, hk, k, sign)
+    a = C.swiglu(gu[:, :n].contiguous(), gu[:, n:].contiguous())
+    q_ref, s_ref = C.had_sign_quant(a, hk, k, sign)
+    torch.cuda.synchronize()
+    assert_bitexact(to_np(q), to_np(q_ref), "codes")
+    assert_bitexact(to_np(s), to_np(s_ref), "scales")
+
+
+def test_swiglu_had_sign_quant_rejects_generic_sizes():
+    C = _ops()
+    n = 28 * 64  # had_28 x H_64: no fused SwiGLU form
+    had, k = oh.get_hadK(n)
+    gu = torch.zeros(2, 2 * n, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="512"):
+        C.swiglu_had_sign_quant(gu, to_dev(had.astype(np.float16)), k)
+
+
+def _prefilled_cache(B, T, Hkv, Hq, page, layers, rng):
+    from signrot_amd.transformers import MultiLayerPagedKVCache4Bit
+    cache = MultiLayerPagedKVCache4Bit(B, page, T + 2, "cuda", layers, Hkv, 128,
+                                       group_size=Hq // Hkv)
+    for li in range(layers):
+        kv = rng.standard_normal((2, B, T, Hkv, 128)).astype(np.float16)
+        cache.update(to_dev(kv[0]), to_dev(kv[1]), li, {})
+    return cache
+
+
+def _clone_cache(cache):
+    import copy
+    c2 = copy.copy(cache)
+    c2.pages = cache.pages.clone()
+    c2.scales = cache.scales.clone()
+    c2._needs_init = list(cache._needs_init)
+    c2._kv_indices_full = cache._kv_indices_full.clone()
+    c2._last_page_offset = cache._last_page_offset.clone()
+    c2._kv_indptr_buf = cache._kv_indptr_buf.clone()
+    c2._spec_cache = dict(cache._spec_cache, kv_data=c2.pages, kv_param=c2.scales,
+                          kv_indices=c2._kv_indices_full, last_page_offset=c2._last_page_offset,
+                          kv_indptr=c2._kv_indptr_buf)
+    c2._stub = copy.copy(cache._stub)
+    return c2
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,page,cos_batch", [(3, 37, 8, 2, 16, 1), (32, 255, 32, 8, 256, 1),
+                                                       (2, 16, 4, 4, 16, 2)])
+def test_qkv_rope_had_append_equals_update_chain(B, T, Hq, Hkv, page, cos_batch):
+    from signrot_amd.functional import kernel
+    from signrot_amd.transformers.decode_layer import rope_cos_sin
+    rng = np.random.default_rng(B * 1000 + T)
+    cache_a = _prefilled_cache(B, T, Hkv, Hq, page, 2, rng)
+    cache_b = _clone_cache(cache_a)
+    D = 128
+    qkv = to_dev((rng.standard_normal((B, (Hq + 2 * Hkv) * D)) * 2.0).astype(np.float16))
+    if cos_batch == 1:
+        cos, sin = rope_cos_sin([T], D, 500000.0, "cuda")
+    else:
+        cos, sin = rope_cos_sin(list(range(T, T + B)), D, 10000.0, "cuda")
+        cos, sin = cos.view(B, 1, D), sin.view(B, 1, D)
+    for li in (0, 1):
+        # op-by-op: rope_qk, cache.update (K Hadamard, kv_quant_pack, append),
+        # the stub's q Hadamard
+        q = qkv[:, : Hq * D].contiguous().view(B, 1, Hq, D)
+        k = qkv[:, Hq * D: (Hq + Hkv) * D].contiguous().view(B, 1, Hkv, D)
+        v = qkv[:, (Hq + Hkv) * D:].contiguous().view(B, 1, Hkv, D)
+        kernel.rope_qk(q, k, cos, sin)
+        attend = cache_a.update(k, v, li, {"attention_mask": None})
+        out_a = attend(q).view(B, Hq, D)
+        attend_b, q_rot = cache_b.update_qkv_fused(qkv, cos, sin, li, Hq)
+        out_b = attend_b(q_rot)
+        from signrot_amd.transformers.kv_cache import matmul_had_cuda
+        q_ref = matmul_had_cuda(q.view(B, Hq, D), torch.float16)
+        torch.cuda.synchronize()
+        assert cache_a.length == cache_b.length
+        assert_bitexact(to_np(q_rot), to_np(q_ref), f"rotated q (layer {li})")
+        assert_bitexact(to_np(cache_b.pages), to_np(cache_a.pages), f"cache codes (layer {li})")
+        assert_bitexact(to_np(cache_b.scales), to_np(cache_a.scales), f"cache params (layer {li})")
+        assert_bitexact(to_np(out_b), to_np(out_a), f"attention output (layer {li})")
+
+
+@pytest.mark.parametrize("hidden,Hq,Hkv,ffn,T", [(1024, 8, 2, 14336, 40), (4096, 32, 8, 896, 300)])
+def test_fused_decode_layer_equals_op_by_op(hidden, Hq, Hkv, ffn, T):
+    from signrot_amd.transformers.decode_layer import W4A4LlamaDecodeLayer, rope_cos_sin
+    B, page = 4, 64
+    rng = np.random.default_rng(hidden + ffn)
+    layers = [W4A4LlamaDecodeLayer.random(hidden, Hq, Hkv, 128, ffn, layer_idx=i, seed=5 + i)
+              for i in range(2)]
+    cache_a = _prefilled_cache(B, T, Hkv, Hq, page, 2, rng)
+    cache_b = _clone_cache(cache_a)
+    h0_np = (rng.standard_normal((B, 1, hidden)) * 0.5).astype(np.float16)
+    h0 = to_dev(h0_np)
+    cos, sin = rope_cos_sin([T], 128, 500000.0, "cuda")
+    ha, hb = h0.clone(), h0
+    for layer in layers:
+        ha = layer(ha, cache_a, cos, sin, fused=False)
+        hb = layer(hb, cache_b, cos, sin, fused=True)
+    torch.cuda.synchronize()
+    assert_bitexact(to_np(hb), to_np(ha), "layer output")
+    assert_bitexact(to_np(cache_b.pages), to_np(cache_a.pages), "cache codes")
+    assert_bitexact(to_np(cache_b.scales), to_np(cache_a.scales), "cache params")
+    assert_bitexact(to_np(h0), h0_np, "input hidden state (must not be modified)")
