@@ -15,6 +15,7 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef unsigned int u32;
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 #define SRQ_DEV __device__ __forceinline__
 
@@ -145,33 +146,50 @@ SRQ_DEV float round16(float v) { return (float)f16_rn(v); }
 // ---------------------------------------------------------- int4 semantics
 // Symmetric code of one fp16 value given the fp16 scale, as the reference's
 // quantizers define it: q = clamp(round_half_even(fp16(x / s)), -8, 7), where
-// the fp16 quotient is the correctly rounded one (an IEEE fp32 division
-// rounded to fp16 is correctly rounded: 24 >= 2*11 + 2), NaN (0/0 on an
+// fp16(x / s) is the correctly rounded quotient (__hdiv), NaN (0/0 on an
 // all-zero row) gives 0 and ±inf saturates.
-SRQ_DEV int sym_code(float x, float s) {
-    float quot = round16(x / s);
-    float r = __builtin_rintf(quot);
-    if (r != r) return 0;
-    r = fminf(fmaxf(r, -8.f), 7.f);
-    return (int)r;
+//
+// No division per element: with r = fl32(1 / s), fp16(fl32(x * r)) equals
+// the correctly rounded fp16(x / s) whenever |x / s| >= 2^-14, and its code
+// equals the quotient's code for every fp16 pair (x, s > 0) -- checked
+// exhaustively over all fp16 pairs by tests/c/quot_exact.c; negative x
+// follow by symmetry of the rounding.  s == 0 gives r = inf: x * inf is
+// ±inf (saturates) and 0 * inf is NaN (code 0), as x / 0 and 0 / 0 are.
+SRQ_DEV float sym_recip(float s) { return 1.0f / s; }
+
+SRQ_DEV int sym_code_r(float x, float r) {
+    float quot = round16(x * r);
+    float c = __builtin_rintf(quot);
+    if (c != c) return 0;
+    c = fminf(fmaxf(c, -8.f), 7.f);
+    return (int)c;
 }
 
-// Unsigned asymmetric KV code: clamp(round_half_even(fp16(fp16(x + z) / s)), 0, 15).
-SRQ_DEV int kv_code(float x, float zero, float scale) {
+SRQ_DEV int sym_code(float x, float s) { return sym_code_r(x, sym_recip(s)); }
+
+// Unsigned asymmetric KV code: clamp(round_half_even(fp16(fp16(x + z) / s)),
+// 0, 15), the quotient by the same reciprocal identity (here the shifted
+// value is >= 0 and s > 0; quotients below 2^-14 give code 0 either way).
+SRQ_DEV int kv_code_r(float x, float zero, float rs) {
     float shifted = round16(x + zero);
-    float scaled = round16(shifted / scale);
-    float r = __builtin_rintf(scaled);
-    if (r != r) return 0;
-    r = fminf(fmaxf(r, 0.f), 15.f);
-    return (int)r;
+    float scaled = round16(shifted * rs);
+    float c = __builtin_rintf(scaled);
+    if (c != c) return 0;
+    c = fminf(fmaxf(c, 0.f), 15.f);
+    return (int)c;
+}
+
+SRQ_DEV int kv_code(float x, float zero, float scale) {
+    return kv_code_r(x, zero, sym_recip(scale));
 }
 
 // Eight symmetric codes packed into one 32-bit word, element i in bits
 // 4i .. 4i + 3 (the reference's nibble order).
 SRQ_DEV u32 pack8_sym(const v8h &v, float s) {
+    const float r = sym_recip(s);
     u32 w = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) w |= (u32)(sym_code((float)v[i], s) & 0xF) << (4 * i);
+    for (int i = 0; i < 8; ++i) w |= (u32)(sym_code_r((float)v[i], r) & 0xF) << (4 * i);
     return w;
 }
 
@@ -239,4 +257,76 @@ SRQ_DEV f16 rope_hi(float x0, float x1, float c, float s) {
     const f16 a = (f16)(x1 * c);
     const f16 b = (f16)(x0 * s);
     return (f16)((float)a + (float)b);
+}
+
+// ----------------------------------------------- packed-fp16 int4 quantizer
+// fp16(x * r) for both fp16 halves of w, each rounded once from the exact
+// product: with r = fl32(1 / s) this is the correctly rounded fp16 quotient
+// x / s whenever |x / s| >= 2^-14, and it gives the same int4 code for every
+// fp16 pair (tests/c/quot_exact.c checks all pairs).
+SRQ_DEV u32 quot2(u32 w, float r) {
+    u32 q;
+    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=&v"(q)
+        : "v"(w), "v"(r));
+    return q;
+}
+
+// packed fp16 quotients -> fp16 (round_half_even(q) + 1544): low nibble of
+// each half = code + 8
+template <bool CLAMP>
+SRQ_DEV u32 offset_codes(u32 q) {
+    v2h h = __builtin_bit_cast(v2h, q);
+    if (CLAMP)
+        h = __builtin_elementwise_min(__builtin_elementwise_max(h, (v2h){-8, -8}),
+                                      (v2h){7, 7});
+    h = h + (v2h){1544, 1544};
+    return __builtin_bit_cast(u32, h);
+}
+
+// eight offset codes (pairs a = (e0, e1), b = (e2, e3), c = (e4, e5),
+// d = (e6, e7), nibble in bits 0-3 and 16-19 of each) -> 32 bits of packed
+// two's-complement nibbles, e0 in bits 0-3 ... e7 in bits 28-31
+SRQ_DEV u32 pack8(u32 a, u32 b, u32 c, u32 d) {
+    const u32 x = __builtin_amdgcn_perm(b, a, 0x06020400u);  // e0 e2 e1 e3
+    const u32 y = __builtin_amdgcn_perm(d, c, 0x06020400u);  // e4 e6 e5 e7
+    const u32 lo = __builtin_amdgcn_perm(y, x, 0x05040100u); // e0 e2 e4 e6
+    const u32 hi = __builtin_amdgcn_perm(y, x, 0x07060302u); // e1 e3 e5 e7
+    return (lo | (hi << 4)) ^ 0x88888888u;
+}
+
+// Reciprocal for the packed quantizer: s == 0 (an all-zero row, or a
+// clipped scale that underflowed) becomes 2^-126, so x = 0 gives code 0 and
+// any other x saturates, which is what x / 0 gives after the reference's
+// round-and-clamp.
+SRQ_DEV float sym_rcp_safe(float s) { return 1.0f / fmaxf(s, 0x1p-126f); }
+
+// Can a quotient of this row round beyond ±7 (then the codes are clamped in
+// fp16 first)?  Never for clip = 1: s = fp16(amax / 7) >= amax / 7.002.
+SRQ_DEV bool sym_row_needs_clamp(float amax, float s) {
+    return !(amax <= 7.25f * fmaxf(s, 0x1p-126f));
+}
+
+// Eight symmetric int4 codes of finite fp16 values by the packed route
+// (2-3 VALU per value instead of a division), identical to pack8_sym.
+template <bool CLAMP>
+SRQ_DEV u32 pack8_sym_fast(const v8h &v, float rcp) {
+    const v4i w = __builtin_bit_cast(v4i, v);
+    return pack8(offset_codes<CLAMP>(quot2((u32)w[0], rcp)),
+                 offset_codes<CLAMP>(quot2((u32)w[1], rcp)),
+                 offset_codes<CLAMP>(quot2((u32)w[2], rcp)),
+                 offset_codes<CLAMP>(quot2((u32)w[3], rcp)));
+}
+
+// absmax8 that also flags a non-finite value (NaN or inf) in `bad`; rows
+// with one take the exact pack8_sym path (the reference maps a NaN to code 0).
+SRQ_DEV float absmax8_flag(const v8h &v, float m, bool &bad) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float a = fabsf((float)v[i]);
+        m = fmaxf(m, a);
+        bad |= !(a <= 65504.f);
+    }
+    return m;
 }

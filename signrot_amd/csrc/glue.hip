@@ -44,6 +44,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const f16 *__restrict__ x,
     acc = wave_sum(acc);
     const float inv = 1.0f / __builtin_sqrtf(acc / mean_dim + eps);
     float amax = 0.f;
+    bool bad = false;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = lane + 64 * i;
@@ -53,18 +54,28 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const f16 *__restrict__ x,
         v[i] = o;
         if (idx < nvec) {
             if (out) reinterpret_cast<v8h *>(out)[row * nvec + idx] = o;
-            if (QUANT) amax = absmax8(o, amax);
+            if (QUANT) amax = absmax8_flag(o, amax, bad);
         }
     }
     if (QUANT) {
         amax = wave_max(amax);
         const f16 s = sym_row_scale(amax, clip);
         if (lane == 0) qscale[row] = s;
-        const float sf = (float)s;
+        u32 *qr = q + row * nvec;
+        if (__builtin_amdgcn_ballot_w64(bad)) {
+            // a non-finite value: the exact per-element quantizer
+            const float sf = (float)s;
 #pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const int idx = lane + 64 * i;
-            if (idx < nvec) q[row * nvec + idx] = pack8_sym(v[i], sf);
+            for (int i = 0; i < VPT; ++i)
+                if (lane + 64 * i < nvec) qr[lane + 64 * i] = pack8_sym(v[i], sf);
+        } else {
+            const float rcp = sym_rcp_safe((float)s);
+            const bool clampit = sym_row_needs_clamp(amax, (float)s);
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
+                if (lane + 64 * i < nvec)
+                    qr[lane + 64 * i] = clampit ? pack8_sym_fast<true>(v[i], rcp)
+                                                : pack8_sym_fast<false>(v[i], rcp);
         }
     }
 }
@@ -121,54 +132,6 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const f16 *__restrict__ g,
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * 256) {
         out[i] = swiglu1((float)g[i], (float)u[i]);
-    }
-}
-
-// ------------------------------------------------- head Hadamard + quant
-// Input of the o_proj of a decode step (modeling_llama.py:94, 117): the
-// attention output x [B, H, D] is rotated over the head axis,
-//   y[b, h, d] = fp16(FWHT_H(x[b, :, d])[h] * scale),
-// and the row y[b] (element h * D + d) is quantized per token (symmetric
-// int4, sym_quant_dynamic arithmetic).  One block per b: thread d holds the
-// H values of column d in registers (stages in ascending bit, as the FWHT
-// kernel), the rotated row is staged in LDS as fp16, then packed eight
-// codes per 32-bit word.
-template <int H>
-__global__ __launch_bounds__(256) void head_had_quant_kernel(const f16 *__restrict__ x, int D,
-                                                             float scale, float clip,
-                                                             u32 *__restrict__ q,
-                                                             f16 *__restrict__ qscale,
-                                                             f16 *__restrict__ rot) {
-    __shared__ __attribute__((aligned(16))) f16 buf[H * 256];
-    __shared__ float red[4];
-    const int64_t b = blockIdx.x;
-    const f16 *xb = x + b * H * D;
-    float amax = 0.f;
-    const int d = threadIdx.x;
-    if (d < D) {
-        float v[H];
-#pragma unroll
-        for (int h = 0; h < H; ++h) v[h] = (float)xb[h * D + d];
-        fwht_regs<H>(v);
-#pragma unroll
-        for (int h = 0; h < H; ++h) {
-            const f16 y = f16_rn(v[h] * scale);
-            buf[h * D + d] = y;
-            amax = fmaxf(amax, fabsf((float)y));
-        }
-    }
-    amax = wave_max(amax);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    const f16 s = sym_row_scale(amax, clip);
-    if (threadIdx.x == 0) qscale[b] = s;
-    const float sf = (float)s;
-    const int nw = H * D / 8;
-    for (int w = threadIdx.x; w < nw; w += 256) {
-        const v8h v = *reinterpret_cast<const v8h *>(buf + 8 * w);
-        q[b * nw + w] = pack8_sym(v, sf);
-        if (rot) reinterpret_cast<v8h *>(rot)[b * nw + w] = v;
     }
 }
 
@@ -258,39 +221,3 @@ extern "C" int srq_swiglu(const void *gate, const void *up, int64_t n, void *out
     return SRQ_OK;
 }
 
-extern "C" int srq_head_had_quant(const void *x, int64_t batch, int64_t n_heads, int64_t head_dim,
-                                  float scale, float clip_ratio, void *q, void *qscale, void *rot,
-                                  void *stream) {
-    SRQ_CHECK_ARG(batch >= 0 && n_heads > 0 && head_dim > 0, "head_had_quant: bad shape");
-    SRQ_CHECK_ARG(n_heads <= 64 && (n_heads & (n_heads - 1)) == 0,
-                  "head_had_quant: n_heads=%lld must be a power of two <= 64",
-                  (long long)n_heads);
-    SRQ_CHECK_ARG(head_dim <= 256 && head_dim % 8 == 0,
-                  "head_had_quant: head_dim=%lld must be a multiple of 8 and <= 256",
-                  (long long)head_dim);
-    SRQ_CHECK_ARG(batch <= 0x7fffffffLL, "head_had_quant: batch > 2^31-1");
-    if (batch == 0) return SRQ_OK;
-    SRQ_CHECK_ARG(x && q && qscale, "head_had_quant: null pointer");
-    SRQ_CHECK_ARG(srq_aligned(q, 4) && (!rot || srq_aligned(rot, 16)),
-                  "head_had_quant: q must be 4-byte and rot 16-byte aligned");
-    const dim3 grid((unsigned)batch);
-    hipStream_t st = (hipStream_t)stream;
-    const int D = (int)head_dim;
-    switch (n_heads) {
-#define SRQ_HHQ(HH)                                                                         \
-    case HH:                                                                                \
-        head_had_quant_kernel<HH><<<grid, 256, 0, st>>>((const f16 *)x, D, scale, clip_ratio, \
-                                                        (u32 *)q, (f16 *)qscale, (f16 *)rot); \
-        break;
-        SRQ_HHQ(1)
-        SRQ_HHQ(2)
-        SRQ_HHQ(4)
-        SRQ_HHQ(8)
-        SRQ_HHQ(16)
-        SRQ_HHQ(32)
-        SRQ_HHQ(64)
-#undef SRQ_HHQ
-    }
-    SRQ_LAUNCH_CHECK("head_had_quant");
-    return SRQ_OK;
-}

@@ -42,7 +42,6 @@
 
 namespace {
 
-typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 
 SRQ_DEV v16f mfma32(v8h a, v8h b, v16f c) {
@@ -60,40 +59,6 @@ SRQ_DEV u32 pk16(float a, float b) {
 // turns into one v_max3_f32 with abs modifiers (an inline-asm v_max3 would
 // read MFMA results without the hazard wait states the compiler inserts)
 SRQ_DEV float absmax3(float m, float a, float b) { return fmaxf(fmaxf(m, fabsf(a)), fabsf(b)); }
-
-// fp16(x * r) for both fp16 halves of w, each rounded once from the exact
-// product (see the header for why this is the fp16 quotient x / s)
-SRQ_DEV u32 quot2(u32 w, float r) {
-    u32 q;
-    asm("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[1,0,0]\n\t"
-        "v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
-        : "=&v"(q)
-        : "v"(w), "v"(r));
-    return q;
-}
-
-// packed fp16 quotients -> fp16 (round_half_even(q) + 1544): low nibble of
-// each half = code + 8
-template <bool CLAMP>
-SRQ_DEV u32 offset_codes(u32 q) {
-    v2h h = __builtin_bit_cast(v2h, q);
-    if (CLAMP)
-        h = __builtin_elementwise_min(__builtin_elementwise_max(h, (v2h){-8, -8}),
-                                      (v2h){7, 7});
-    h = h + (v2h){1544, 1544};
-    return __builtin_bit_cast(u32, h);
-}
-
-// eight offset codes (pairs a = (e0, e1), b = (e2, e3), c = (e4, e5),
-// d = (e6, e7), nibble in bits 0-3 and 16-19 of each) -> 32 bits of packed
-// two's-complement nibbles, e0 in bits 0-3 ... e7 in bits 28-31
-SRQ_DEV u32 pack8(u32 a, u32 b, u32 c, u32 d) {
-    const u32 x = __builtin_amdgcn_perm(b, a, 0x06020400u);  // e0 e2 e1 e3
-    const u32 y = __builtin_amdgcn_perm(d, c, 0x06020400u);  // e4 e6 e5 e7
-    const u32 lo = __builtin_amdgcn_perm(y, x, 0x05040100u); // e0 e2 e4 e6
-    const u32 hi = __builtin_amdgcn_perm(y, x, 0x07060302u); // e1 e3 e5 e7
-    return (lo | (hi << 4)) ^ 0x88888888u;
-}
 
 constexpr uint32_t kOob = 0xFFFFFFF0u;
 

@@ -689,12 +689,10 @@ __global__ __launch_bounds__(NW * 64) void decode_kernel(DecodeArgs a) {
     }
 }
 
-// merge the per-chunk (o, m, d) records of one (request, query head)
-__global__ __launch_bounds__(128) void merge_kernel(const float *__restrict__ tmp, f16 *__restrict__ o,
-                                                    int64_t Hq, int chunks) {
-    const int64_t bh = blockIdx.x;
-    const int d = threadIdx.x;
-    const float *rec = tmp + bh * chunks * (kD + 4);
+// Merge of the per-chunk (o, m, d) records of one (request, query head) at
+// dim d: o = sum_c o_c 2^(m_c - m) / sum_c d_c 2^(m_c - m), m = max_c m_c
+// (decode.cuh:726-751), fp16.
+SRQ_DEV f16 merge_rec(const float *rec, int chunks, int d) {
     float mx = -INFINITY;
     for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, rec[c * (kD + 4) + kD]);
     float ov = 0.f, dv = 0.f;
@@ -704,7 +702,74 @@ __global__ __launch_bounds__(128) void merge_kernel(const float *__restrict__ tm
         ov += rec[c * (kD + 4) + d] * sc;
         dv += rec[c * (kD + 4) + kD + 1] * sc;
     }
-    o[bh * kD + d] = (f16)(dv > 0.f ? ov / dv : 0.f);
+    return (f16)(dv > 0.f ? ov / dv : 0.f);
+}
+
+__global__ __launch_bounds__(128) void merge_kernel(const float *__restrict__ tmp, f16 *__restrict__ o,
+                                                    int64_t Hq, int chunks) {
+    const int64_t bh = blockIdx.x;
+    const int d = threadIdx.x;
+    o[bh * kD + d] = merge_rec(tmp + bh * chunks * (kD + 4), chunks, d);
+}
+
+// ------------------------------------------------- head Hadamard + quant
+// Input of the o_proj of a decode step (modeling_llama.py:94, 117): the
+// attention output x [B, H, D] is rotated over the head axis,
+//   y[b, h, d] = fp16(FWHT_H(x[b, :, d])[h] * scale),
+// and the row y[b] (element h * D + d) is quantized per token (symmetric
+// int4, sym_quant_dynamic arithmetic).  One block per b: thread d holds the
+// H values of column d in registers (stages in ascending bit, as the FWHT
+// kernel), the rotated row is staged in LDS as fp16, then packed eight
+// codes per 32-bit word.
+template <int H>
+__global__ __launch_bounds__(256) void head_had_quant_kernel(const f16 *__restrict__ x, int D,
+                                                             float scale, float clip,
+                                                             u32 *__restrict__ q,
+                                                             f16 *__restrict__ qscale,
+                                                             f16 *__restrict__ rot) {
+    __shared__ __attribute__((aligned(16))) f16 buf[H * 256];
+    __shared__ float red[4];
+    __shared__ int redb[4];
+    const int64_t b = blockIdx.x;
+    const f16 *xb = x + b * H * D;
+    float amax = 0.f;
+    bool bad = false;
+    const int d = threadIdx.x;
+    if (d < D) {
+        float v[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) v[h] = (float)xb[h * D + d];
+        fwht_regs<H>(v);
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const f16 y = f16_rn(v[h] * scale);
+            buf[h * D + d] = y;
+            const float a = fabsf((float)y);
+            amax = fmaxf(amax, a);
+            bad |= !(a <= 65504.f);
+        }
+    }
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) {
+        red[threadIdx.x >> 6] = amax;
+        redb[threadIdx.x >> 6] = __builtin_amdgcn_ballot_w64(bad) != 0;
+    }
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const bool anybad = (redb[0] | redb[1] | redb[2] | redb[3]) != 0;
+    const f16 s = sym_row_scale(amax, clip);
+    if (threadIdx.x == 0) qscale[b] = s;
+    const float sf = (float)s;
+    const float rcp = sym_rcp_safe(sf);
+    const bool clampit = sym_row_needs_clamp(amax, sf);
+    const int nw = H * D / 8;
+    for (int w = threadIdx.x; w < nw; w += 256) {
+        const v8h v = *reinterpret_cast<const v8h *>(buf + 8 * w);
+        q[b * nw + w] = anybad    ? pack8_sym(v, sf)
+                        : clampit ? pack8_sym_fast<true>(v, rcp)
+                                  : pack8_sym_fast<false>(v, rcp);
+        if (rot) reinterpret_cast<v8h *>(rot)[b * nw + w] = v;
+    }
 }
 
 int check_paged(const char *name, const void *data, const void *param, const void *indptr,
@@ -875,6 +940,7 @@ extern "C" int srq_batch_decode_i4(void *o, const void *q, const void *kv_data,
     return SRQ_OK;
 }
 
+
 extern "C" int srq_qkv_rope_had_append(const void *qkv, const void *cos, const void *sin,
                                        int64_t cos_batch, int64_t batch, int64_t n_q_heads,
                                        int64_t n_kv_heads, int64_t head_dim, float had_scale,
@@ -915,3 +981,41 @@ extern "C" int srq_qkv_rope_had_append(const void *qkv, const void *cos, const v
     SRQ_LAUNCH_CHECK(name);
     return SRQ_OK;
 }
+
+extern "C" int srq_head_had_quant(const void *x, int64_t batch, int64_t n_heads, int64_t head_dim,
+                                  float scale, float clip_ratio, void *q, void *qscale, void *rot,
+                                  void *stream) {
+    SRQ_CHECK_ARG(batch >= 0 && n_heads > 0 && head_dim > 0, "head_had_quant: bad shape");
+    SRQ_CHECK_ARG(n_heads <= 64 && (n_heads & (n_heads - 1)) == 0,
+                  "head_had_quant: n_heads=%lld must be a power of two <= 64",
+                  (long long)n_heads);
+    SRQ_CHECK_ARG(head_dim <= 256 && head_dim % 8 == 0,
+                  "head_had_quant: head_dim=%lld must be a multiple of 8 and <= 256",
+                  (long long)head_dim);
+    SRQ_CHECK_ARG(batch <= 0x7fffffffLL, "head_had_quant: batch > 2^31-1");
+    if (batch == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(x && q && qscale, "head_had_quant: null pointer");
+    SRQ_CHECK_ARG(srq_aligned(q, 4) && (!rot || srq_aligned(rot, 16)),
+                  "head_had_quant: q must be 4-byte and rot 16-byte aligned");
+    const dim3 grid((unsigned)batch);
+    hipStream_t st = (hipStream_t)stream;
+    const int D = (int)head_dim;
+    switch (n_heads) {
+#define SRQ_HHQ(HH)                                                                       \
+    case HH:                                                                              \
+        head_had_quant_kernel<HH><<<grid, 256, 0, st>>>(                                  \
+            (const f16 *)x, D, scale, clip_ratio, (u32 *)q, (f16 *)qscale, (f16 *)rot);   \
+        break;
+        SRQ_HHQ(1)
+        SRQ_HHQ(2)
+        SRQ_HHQ(4)
+        SRQ_HHQ(8)
+        SRQ_HHQ(16)
+        SRQ_HHQ(32)
+        SRQ_HHQ(64)
+#undef SRQ_HHQ
+    }
+    SRQ_LAUNCH_CHECK("head_had_quant");
+    return SRQ_OK;
+}
+

@@ -66,6 +66,7 @@ __global__ __launch_bounds__(256) void sym_quant_dynamic_vec_kernel(
 
     v8h v[VPT];
     float amax = 0.f;
+    bool bad = false;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = lt + i * TPR;
@@ -74,18 +75,31 @@ __global__ __launch_bounds__(256) void sym_quant_dynamic_vec_kernel(
         } else {
             v[i] = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
         }
-        amax = absmax8(v[i], amax);
+        amax = absmax8_flag(v[i], amax, bad);
     }
     amax = row_reduce<TPR, 0>(amax, lds);
+    // non-finite values take the exact per-element path (row-uniform flag)
+    const float badf = row_reduce<TPR, 0>(bad ? 1.f : 0.f, lds);
     const f16 s = sym_row_scale(amax, clip);
     if (!valid) return;
     if (lt == 0) scale_out[row] = s;
     const float sf = (float)s;
     u32 *qr = q + row * nvec;
+    if (badf != 0.f) {
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-        const int idx = lt + i * TPR;
-        if (idx < nvec) qr[idx] = pack8_sym(v[i], sf);
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = lt + i * TPR;
+            if (idx < nvec) qr[idx] = pack8_sym(v[i], sf);
+        }
+    } else {
+        const float rcp = sym_rcp_safe(sf);
+        const bool clampit = sym_row_needs_clamp(amax, sf);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int idx = lt + i * TPR;
+            if (idx < nvec)
+                qr[idx] = clampit ? pack8_sym_fast<true>(v[i], rcp) : pack8_sym_fast<false>(v[i], rcp);
+        }
     }
 }
 

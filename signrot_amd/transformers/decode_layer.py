@@ -99,18 +99,18 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         return self._forward_ops(hidden_states, cache, cos, sin, trace)
 
     def _forward_fused(self, hidden_states, cache, cos, sin):
-        """The decode step in 9 launches: rmsnorm_quant -> q/k/v GEMM ->
+        """The decode step in 11 launches: rmsnorm_quant -> q/k/v GEMM ->
         qkv_rope_had_append (RoPE, K/q Hadamard, KV quantize + append) ->
-        batch_decode_i4 -> head_had_quant -> o_proj GEMM + residual ->
-        rmsnorm_quant -> gate/up GEMM -> swiglu_had_sign_quant -> down GEMM
-        + residual."""
+        batch_decode_i4 (+ split-KV merge) -> head_had_quant (head-axis
+        Hadamard + quantizer) -> o_proj GEMM + residual -> rmsnorm_quant ->
+        gate/up GEMM -> swiglu_had_sign_quant -> down GEMM + residual."""
         B = hidden_states.shape[0]
         x2 = hidden_states.view(B, self.hidden)
         n1, n2 = self.input_layernorm, self.post_attention_layernorm
         q1, s1 = _CUDA.rmsnorm_quant(x2, n1.eps, n1.mean_dim)
         qkv = _CUDA.w4a4_linear(q1, s1.view(-1), self.w_qkv, self.s_qkv)
-        attend, q_rot = cache.update_qkv_fused(qkv, cos, sin, self.layer_idx, self.n_heads)
-        attn = attend(q_rot)                                   # [B, Hq, D]
+        q_rot = cache.update_qkv_fused(qkv, cos, sin, self.layer_idx, self.n_heads)
+        attn = cache.decode_rotated(q_rot, self.layer_idx)     # [B, Hq, D]
         qa, sa = _CUDA.head_had_quant(attn, _inv_sqrt_f32(self.n_heads))
         x2 = _CUDA.w4a4_linear_residual(qa, sa.view(-1), self.w_o, self.s_o, x2)
         q2, s2 = _CUDA.rmsnorm_quant(x2, n2.eps, n2.mean_dim)

@@ -7,7 +7,7 @@ Differences from the reference, none of which change results:
     kernel needs as many KV heads as query heads; batch_decode_i4 here maps
     query head h to KV head h // group_size itself, so the cache is
     group_size times smaller and decode reads group_size times fewer bytes.
-  * The split-KV chunk count targets four 256-thread blocks per CU (the
+  * The split-KV chunk count targets two 256-thread blocks per CU (the
     reference targets two blocks of 128 threads, kv_cache.py:236-258).
   * Only the int4 path exists: disable_quant=True (fp16 cache) and lac=True
     (learned clipping, unused by the reference itself) raise
@@ -147,9 +147,11 @@ class MultiLayerPagedKVCache4Bit(object):
 
     @staticmethod
     def decode_chunks(batch_size, num_kv_heads, max_seq_len, cu_count):
-        """Split-KV chunk count: about four blocks per CU, at most one chunk
-        per 128 tokens of context, at most 1024."""
-        target_blocks = 4 * cu_count
+        """Split-KV chunk count: about two blocks per CU (the decode kernel's
+        register use leaves room for two four-wave blocks per CU, so further
+        chunks only queue), at most one chunk per 128 tokens of context, at
+        most 1024."""
+        target_blocks = 2 * cu_count
         chunks = max(1, -(-target_blocks // max(1, batch_size * num_kv_heads)))
         return max(1, min(chunks, max_seq_len // 128, 1024))
 
@@ -245,10 +247,10 @@ class MultiLayerPagedKVCache4Bit(object):
         """Decode-step form of update() + the stub's q rotation, one kernel:
         qkv f16 [B, (Hq + 2 H) D] is the q/k/v projection output of the new
         token; q and k get RoPE (cos/sin [1 or B, 1, D]) and the head-dim
-        Hadamard, k and v are quantized into the cache.  Returns the decode
-        function of a rotated q: attend(q_rot [B, Hq, D]) -> [B, Hq, D], and
-        q_rot.  Results equal rope_qk + update() + the stub bit for bit.  The
-        layer must already hold its prefill (one token per request here)."""
+        Hadamard, k and v are quantized into the cache.  Returns the rotated
+        q [B, Hq, D] for decode_rotated.  Results equal
+        rope_qk + update() + the stub's q rotation bit for bit.  The layer
+        must already hold its prefill (one new token per request here)."""
         if self._needs_init[layer_idx]:
             raise RuntimeError("update_qkv_fused: the layer has no prefill yet")
         b_sz = qkv.shape[0]
@@ -259,12 +261,14 @@ class MultiLayerPagedKVCache4Bit(object):
             self.length = new_length
         specs = self.get_cache_specs_for_flash_infer(None)
         rotate = self.hadamard_dtype is not None
-        q = _CUDA.qkv_rope_had_append(qkv, cos.contiguous(), sin.contiguous(), num_q_heads,
-                                      self.num_heads, **specs, layer_idx=layer_idx,
-                                      had_scale=1 / math.sqrt(self.head_dim), rotate=rotate)
-        attend = functools.partial(self._stub.attend_rotated, attention_kwargs=specs,
-                                   layer_idx=layer_idx)
-        return attend, q
+        return _CUDA.qkv_rope_had_append(qkv, cos.contiguous(), sin.contiguous(), num_q_heads,
+                                         self.num_heads, **specs, layer_idx=layer_idx,
+                                         had_scale=1 / math.sqrt(self.head_dim), rotate=rotate)
+
+    def decode_rotated(self, q_rot, layer_idx):
+        """Decode attention of an already rotated q [B, Hq, D] over this
+        layer's cache (after update_qkv_fused) -> [B, Hq, D]."""
+        return self._stub.attend_rotated(q_rot, self._spec_cache, layer_idx)
 
     def _set_page_cnt(self, page_cnt: int):
         """indptr = b * page_cnt; indices[b, j] = j * B + b

@@ -177,8 +177,8 @@ def test_qkv_rope_had_append_equals_update_chain(B, T, Hq, Hkv, page, cos_batch)
         kernel.rope_qk(q, k, cos, sin)
         attend = cache_a.update(k, v, li, {"attention_mask": None})
         out_a = attend(q).view(B, Hq, D)
-        attend_b, q_rot = cache_b.update_qkv_fused(qkv, cos, sin, li, Hq)
-        out_b = attend_b(q_rot)
+        q_rot = cache_b.update_qkv_fused(qkv, cos, sin, li, Hq)
+        out_b = cache_b.decode_rotated(q_rot, li)
         from signrot_amd.transformers.kv_cache import matmul_had_cuda
         q_ref = matmul_had_cuda(q.view(B, Hq, D), torch.float16)
         torch.cuda.synchronize()
