@@ -147,15 +147,23 @@ SRQ_DEV void kmix_regs(const RotArgs &a, float *buf, const float *hk, int nrows)
                 y[k] = a.fp32_had ? v : round16(v);
             }
         }
-        for (int k = 0; k < a.K; ++k) {
+        // all outputs of the column in registers first: the hadK reads then
+        // are not ordered behind stores to the row buffer
+        float o[KT];
+#pragma unroll
+        for (int k = 0; k < KT; ++k) {
+            if (k >= a.K) continue;
             const float *h = hk + k * a.K;
             float acc = 0.f;
 #pragma unroll
             for (int kk = 0; kk < KT; ++kk) {
                 if (kk < a.K) acc = __builtin_fmaf(h[kk], y[kk], acc);
             }
-            rb[k * a.m] = a.fp32_had ? acc : round16(acc);
+            o[k] = a.fp32_had ? acc : round16(acc);
         }
+#pragma unroll
+        for (int k = 0; k < KT; ++k)
+            if (k < a.K) rb[k * a.m] = o[k];
     }
     __syncthreads();
 }
@@ -193,6 +201,32 @@ SRQ_DEV float finish(const RotArgs &a, const float *rb, int i) {
     }
     if (a.sign) v *= (float)a.sign[i];
     return v;
+}
+
+// finish() of the 8 elements 8w .. 8w + 7, the signs read as one 8-byte
+// group (n % 8 == 0 on the quantizing paths)
+SRQ_DEV void finish8(const RotArgs &a, const float *rb, int w, float (&v)[8]) {
+    uint2 sg = make_uint2(0x01010101u, 0x01010101u);
+    if (a.sign) {
+        const int8_t *sp = a.sign + 8 * w;
+        if (reinterpret_cast<uintptr_t>(a.sign) % 8 == 0) {
+            sg = *reinterpret_cast<const uint2 *>(sp);
+        } else {
+            sg.x = (uint8_t)sp[0] | (uint8_t)sp[1] << 8 | (uint8_t)sp[2] << 16 | (u32)(uint8_t)sp[3] << 24;
+            sg.y = (uint8_t)sp[4] | (uint8_t)sp[5] << 8 | (uint8_t)sp[6] << 16 | (u32)(uint8_t)sp[7] << 24;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        float x = rb[8 * w + e];
+        if (a.K == 1) {
+            x *= a.scale;
+            if (!a.fp32_had && !a.io_f32) x = round16(x);
+        }
+        const int8_t sb = (int8_t)((e < 4 ? sg.x : sg.y) >> (8 * (e & 3)));
+        x *= (float)sb;
+        v[e] = x;
+    }
 }
 
 template <int MODE>
@@ -252,9 +286,12 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(RotArgs a) {
         const int nw = a.n / 8;
         if (a.rpb == 1) {
             float amax = 0.f;
-            for (int w = threadIdx.x; w < nw; w += kThreads)
+            for (int w = threadIdx.x; w < nw; w += kThreads) {
+                float v[8];
+                finish8(a, buf, w, v);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(round16(finish(a, buf, w * 8 + e))));
+                for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(round16(v[e])));
+            }
             amax = wave_max(amax);
             if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
             __syncthreads();
@@ -264,11 +301,14 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(RotArgs a) {
             if (threadIdx.x == 0) a.qscale[row0] = s;
             const float sf = (float)s;
             uint32_t *qr = a.q + row0 * nw;
+            const float rs = sym_recip(sf);
             for (int w = threadIdx.x; w < nw; w += kThreads) {
+                float v[8];
+                finish8(a, buf, w, v);
                 uint32_t word = 0;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    word |= (uint32_t)(sym_code(round16(finish(a, buf, w * 8 + e)), sf) & 0xF) << (4 * e);
+                    word |= (uint32_t)(sym_code_r(round16(v[e]), rs) & 0xF) << (4 * e);
                 qr[w] = word;
             }
         } else {
@@ -276,9 +316,12 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(RotArgs a) {
             if (wave < nrows) {
                 const float *rb = buf + wave * a.n;
                 float amax = 0.f;
-                for (int w = lane; w < nw; w += 64)
+                for (int w = lane; w < nw; w += 64) {
+                    float v[8];
+                    finish8(a, rb, w, v);
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(round16(finish(a, rb, w * 8 + e))));
+                    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(round16(v[e])));
+                }
                 amax = wave_max(amax);
                 f16 s = f16_rn(amax / 7.f);
                 if (a.clip != 1.f) s = f16_rn((float)s * a.clip);
@@ -286,11 +329,14 @@ __global__ __launch_bounds__(kThreads) void rotate_kernel(RotArgs a) {
                 if (lane == 0) a.qscale[row] = s;
                 const float sf = (float)s;
                 uint32_t *qr = a.q + row * nw;
+                const float rs = sym_recip(sf);
                 for (int w = lane; w < nw; w += 64) {
+                    float v[8];
+                    finish8(a, rb, w, v);
                     uint32_t word = 0;
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
-                        word |= (uint32_t)(sym_code(round16(finish(a, rb, w * 8 + e)), sf) & 0xF) << (4 * e);
+                        word |= (uint32_t)(sym_code_r(round16(v[e]), rs) & 0xF) << (4 * e);
                     qr[w] = word;
                 }
             }
