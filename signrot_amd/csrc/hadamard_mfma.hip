@@ -1,6 +1,7 @@
-// MFMA rotation kernel for n = K * 512 (9 <= K <= 32): the rotation of the
-// SignRot down_proj input (Llama-3 FFN 14336 = had_28 ⊗ H_512), optionally
-// fused with the SignRot sign and the per-token int4 quantizer.
+// MFMA rotation kernel for n = K * 512 and n = K * 1024 (9 <= K <= 32, K a
+// multiple of 4): the rotation of the SignRot down_proj input (Llama-3-8B
+// FFN 14336 = had_28 ⊗ H_512, Llama-3-70B FFN 28672 = had_28 ⊗ H_1024),
+// optionally fused with the SignRot sign and the per-token int4 quantizer.
 //
 // A block of 4 waves owns one token row at a time (persistent over rows).
 // The row sits in LDS in the lane order of the stage-A A operand; the next
@@ -23,6 +24,15 @@
 // registers (k-slot (g, e) <-> chunk 8(2s + e/4) + 4g + e%4), so lane
 // (c = l%32, g) receives runs of 4 consecutive i2 of chunk c.
 // out = fp16(fp32 sum)                        -- second rounding point
+//
+// H_1024 (P = 2): the row is 2K 512-chunks, chunk j = 2c + h for Hadamard
+// chunk c and bit 9 h.  Stages A and B run on the 512-chunks unchanged;
+// chunks 2c and 2c + 1 land in registers v and v + 4 (v / 4 even) of the
+// same lane, so the bit-9 butterfly is one more fp32 stage in registers
+// before the first rounding point (ascending bit order, as everywhere).
+// The K-mix then runs once per h, k-slot (g, e) of step s <-> chunk
+// c' = 16 s + 4 (e / 2) + 2 g + e % 2, i.e. tile 4 s + e / 2, register
+// group v / 4 = 2 (e % 2) + h: again the lane's own registers.
 // The K-mix result stays in registers as packed fp16 (with the sign applied
 // as an xor of the fp16 sign bit) while the block reduces the row max.
 //
@@ -65,7 +75,7 @@ constexpr uint32_t kOob = 0xFFFFFFF0u;
 struct MfmaRotArgs {
     const f16 *x;
     int64_t rows;
-    int KC;               // Kronecker factor K (number of 512-chunks)
+    int KC;               // Kronecker factor K
     const f16 *hadK;      // [KC, KC]
     const int8_t *sign;   // [n] or null
     float scale;          // fp32 1/sqrt(n)
@@ -100,8 +110,10 @@ SRQ_DEV void quant_store(const u32 (&w)[4][8], float rcp, uint8_t *qrow) {
 
 // SW: the row is swiglu(gate, up) of two strided inputs (one workgroup per
 // CU: the up prefetch needs the registers two workgroups would share).
-template <int NT, int MODE, bool SW>
-__global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArgs a) {
+// P: 512-chunks per Hadamard chunk (1: H_512, 2: H_1024; one workgroup per
+// CU, which holds twice the row in registers).
+template <int NT, int MODE, bool SW, int P>
+__global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kernel(MfmaRotArgs a) {
     // The staged row: 128-element segment (chunk c, quarter i1) at
     // rowbuf + 256 (4c + i1) bytes, its 16-byte piece p at position
     // p ^ 2h(c, i1), h = i1 | ((c >> 2) & 1) << 2.  The swizzle makes both
@@ -117,7 +129,8 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
     const int nt = wave;
     const int g = lane >> 5;
     const int ln = lane & 31;
-    const int n = a.KC * 512;
+    const int nc = a.KC * P;  // 512-chunks in the row
+    const int n = nc * 512;
 
     // ---- constants
     // H_128 B operand for this n-tile, k-steps 0..7: entry e of step ks is
@@ -149,37 +162,60 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
     v8h HB[2];
     {
         const __amdgpu_buffer_rsrc_t hr = make_rsrc(a.hadK, (int64_t)a.KC * a.KC * 2);
+        if constexpr (P == 1) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s)
+            for (int s = 0; s < 2; ++s)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int cp = 8 * (2 * s + h) + 4 * g;
-                const uint32_t off =
-                    (ln < a.KC && cp < a.KC) ? (uint32_t)((ln * a.KC + cp) * 2) : kOob;
-                const v4h v = __builtin_bit_cast(
-                    v4h, __builtin_amdgcn_raw_buffer_load_b64(hr, off, 0, 0));
+                for (int h = 0; h < 2; ++h) {
+                    const int cp = 8 * (2 * s + h) + 4 * g;
+                    const uint32_t off =
+                        (ln < a.KC && cp < a.KC) ? (uint32_t)((ln * a.KC + cp) * 2) : kOob;
+                    const v4h v = __builtin_bit_cast(
+                        v4h, __builtin_amdgcn_raw_buffer_load_b64(hr, off, 0, 0));
 #pragma unroll
-                for (int e = 0; e < 4; ++e) HB[s][4 * h + e] = v[e];
-            }
+                    for (int e = 0; e < 4; ++e) HB[s][4 * h + e] = v[e];
+                }
+        } else {
+            // k-slot pair (2 q, 2 q + 1) <-> chunks cp, cp + 1
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int cp = 16 * s + 4 * q + 2 * g;
+                    const uint32_t off =
+                        (ln < a.KC && cp < a.KC) ? (uint32_t)((ln * a.KC + cp) * 2) : kOob;
+                    const v2h v = __builtin_bit_cast(
+                        v2h, __builtin_amdgcn_raw_buffer_load_b32(hr, off, 0, 0));
+                    HB[s][2 * q] = v[0];
+                    HB[s][2 * q + 1] = v[1];
+                }
+        }
     }
-    u32 msk[4][8];
+    // msk[h][i1]: sign xor masks of the outputs of Hadamard chunk ln, half h
+    u32 msk[P][4][8];
 #pragma unroll
-    for (int i1 = 0; i1 < 4; ++i1)
-#pragma unroll
-        for (int p = 0; p < 8; ++p) msk[i1][p] = 0;
-    if (a.sign) {
-        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sign, n);
+    for (int h = 0; h < P; ++h)
 #pragma unroll
         for (int i1 = 0; i1 < 4; ++i1)
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                // int8 signs of i2 = 32 nt + 8u + 4g .. +3: bit 7 of each byte
-                const uint32_t off =
-                    ln < a.KC ? (uint32_t)(ln * 512 + i1 * 128 + 32 * nt + 8 * u + 4 * g) : kOob;
-                const u32 sw = __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
-                msk[i1][2 * u] = ((sw & 0x80u) << 8) | ((sw & 0x8000u) << 16);
-                msk[i1][2 * u + 1] = ((sw & 0x800000u) >> 8) | (sw & 0x80000000u);
-            }
+            for (int p = 0; p < 8; ++p) msk[h][i1][p] = 0;
+    if (a.sign) {
+        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sign, n);
+#pragma unroll
+        for (int h = 0; h < P; ++h)
+#pragma unroll
+            for (int i1 = 0; i1 < 4; ++i1)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    // int8 signs of i2 = 32 nt + 8u + 4g .. +3: bit 7 of each byte
+                    const uint32_t off =
+                        ln < a.KC ? (uint32_t)(ln * 512 * P + h * 512 + i1 * 128 + 32 * nt +
+                                               8 * u + 4 * g)
+                                  : kOob;
+                    const u32 sw = __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
+                    msk[h][i1][2 * u] = ((sw & 0x80u) << 8) | ((sw & 0x8000u) << 16);
+                    msk[h][i1][2 * u + 1] = ((sw & 0x800000u) >> 8) | (sw & 0x80000000u);
+                }
     }
 
     // Settle the prologue loads here: the empty asm consumes HB and msk,
@@ -195,9 +231,11 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
         HB[s2] = t.h;
     }
 #pragma unroll
-    for (int i1 = 0; i1 < 4; ++i1)
+    for (int h = 0; h < P; ++h)
 #pragma unroll
-        for (int p = 0; p < 8; ++p) asm volatile("" : "+v"(msk[i1][p]));
+        for (int i1 = 0; i1 < 4; ++i1)
+#pragma unroll
+            for (int p = 0; p < 8; ++p) asm volatile("" : "+v"(msk[h][i1][p]));
 
     // A-operand row of this lane in stage A: segment (chunk 8T + cta,
     // quarter i1a), piece 2 ks + g.
@@ -211,7 +249,7 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
     const int64_t xbytes = a.rows > 0 ? ((a.rows - 1) * a.ld + n) * 2 : 0;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, xbytes);
     const __amdgpu_buffer_rsrc_t ur = make_rsrc(SW ? a.up : a.x, xbytes);
-    const int cpw = a.KC / 4;
+    const int cpw = nc / 4;
     const int wi1 = lane >> 4, wp = lane & 15;
     v4i pre[NT * 2];
     v4i preu[SW ? NT * 2 : 1];
@@ -245,8 +283,8 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
             rowbuf[(c * 4 + wi1) * 16 + (wp ^ (2 * h))] = val;
         }
     };
-    for (int i = threadIdx.x; i < (NT * 8 - a.KC) * 64; i += 256)
-        rowbuf[a.KC * 64 + i] = (v4i){0, 0, 0, 0};
+    for (int i = threadIdx.x; i < (NT * 8 - nc) * 64; i += 256)
+        rowbuf[nc * 64 + i] = (v4i){0, 0, 0, 0};
 
     const int64_t step = gridDim.x;
     int64_t row = blockIdx.x;
@@ -264,15 +302,19 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
 
         // ---- stage A (H_128 over i2, this wave's 32 output columns) and
         // stage B (H_4 over i1), y = fp16(FWHT * 1/sqrt(n)) into the K-mix
-        // A operands ka[s][i1] (k-slot e <-> tile 2s + e/4, chunk 4g + e%4)
-        constexpr int NS = (NT + 1) / 2;
+        // A operands ka[s][h][i1] (P = 1: k-slot e <-> tile 2s + e/4, chunk
+        // 4g + e%4; P = 2: tile 4s + e/2, register group 2 (e%2) + h)
+        constexpr int TPS = 2 * P;  // tiles per K-mix step
+        constexpr int NS = (NT + TPS - 1) / TPS;
         union KA {
             v8h h;
             u32 w[4];
-        } ka[NS][4];
-        if (NT % 2) {
+        } ka[NS][P][4];
+        if (NT % TPS) {
 #pragma unroll
-            for (int i1 = 0; i1 < 4; ++i1) ka[NS - 1][i1].h = (v8h){};
+            for (int h = 0; h < P; ++h)
+#pragma unroll
+                for (int i1 = 0; i1 < 4; ++i1) ka[NS - 1][h][i1].h = (v8h){};
         }
         // (slots of chunks >= K hold zeros: their prefetch read zeros).
         // The 8 LDS reads of tile T + 1 are issued before the MFMAs of tile
@@ -282,9 +324,11 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
         auto rd = [&](int T, int ks) {
             return *reinterpret_cast<const v8h *>(rowb + T * 8192 + rdbase + 32 * (ks ^ ha));
         };
-        // Stage B + first rounding point for tile T's accumulators:
-        // register v -> ka[T/2][v%4] element 4 (T%2) + v/4; the pairs
-        // (v, v + 4) are adjacent elements.
+        // Stage B (+ the bit-9 stage for P = 2) and the first rounding
+        // point for tile T's accumulators.  P = 1: register v -> ka[T/2][0]
+        // [v%4] element 4 (T%2) + v/4, the pairs (v, v + 4) adjacent
+        // elements.  P = 2: registers (4h + i1, 4h + i1 + 8) -> ka[T/4][h]
+        // [i1] elements 2 (T%4), 2 (T%4) + 1.
         auto finish = [&](v16f d, int T) {
 #pragma unroll
             for (int v = 0; v < 16; v += 4) {
@@ -295,13 +339,32 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
                 d[v + 2] = b0 - b2;
                 d[v + 3] = b1 - b3;
             }
+            if constexpr (P == 1) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                if ((v / 4) % 2) continue;
-                float lo = d[v] * a.scale, hi = d[v + 4] * a.scale;
-                // pin the fp32 products: fp16(fp32(x * s)), two roundings
-                asm volatile("" : "+v"(lo), "+v"(hi));
-                ka[T / 2][v % 4].w[2 * (T % 2) + v / 8] = pk16(lo, hi);
+                for (int v = 0; v < 16; ++v) {
+                    if ((v / 4) % 2) continue;
+                    float lo = d[v] * a.scale, hi = d[v + 4] * a.scale;
+                    // pin the fp32 products: fp16(fp32(x * s)), two roundings
+                    asm volatile("" : "+v"(lo), "+v"(hi));
+                    ka[T / 2][0][v % 4].w[2 * (T % 2) + v / 8] = pk16(lo, hi);
+                }
+            } else {
+                // bit 9: chunk 2c (registers v) with chunk 2c + 1 (v + 4)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    if ((v / 4) % 2) continue;
+                    const float lo = d[v], hi = d[v + 4];
+                    d[v] = lo + hi;
+                    d[v + 4] = lo - hi;
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int i1 = 0; i1 < 4; ++i1) {
+                        float lo = d[4 * h + i1] * a.scale, hi = d[4 * h + i1 + 8] * a.scale;
+                        asm volatile("" : "+v"(lo), "+v"(hi));
+                        ka[T / 4][h][i1].w[T % 4] = pk16(lo, hi);
+                    }
             }
         };
         // Software pipeline over the tiles: the LDS reads of tile T + 1 and
@@ -332,33 +395,38 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
         finish(dprev, NT - 1);
 
         // ---- K-mix: round to fp16, apply the sign, keep; row max of |out|
-        u32 w[4][8];
+        u32 w[P][4][8];
         float amax = 0.f;
 #pragma unroll
-        for (int i1 = 0; i1 < 4; ++i1) {
-            v16f z = {};
-            z = mfma32(ka[0][i1].h, HB[0], z);
-            if (NS > 1) z = mfma32(ka[NS > 1 ? 1 : 0][i1].h, HB[1], z);
+        for (int h = 0; h < P; ++h)
 #pragma unroll
-            for (int p = 0; p < 8; ++p) {
-                amax = absmax3(amax, z[2 * p], z[2 * p + 1]);
-                w[i1][p] = pk16(z[2 * p], z[2 * p + 1]) ^ msk[i1][p];
+            for (int i1 = 0; i1 < 4; ++i1) {
+                v16f z = {};
+                z = mfma32(ka[0][h][i1].h, HB[0], z);
+                if (NS > 1) z = mfma32(ka[NS > 1 ? 1 : 0][h][i1].h, HB[1], z);
+#pragma unroll
+                for (int p = 0; p < 8; ++p) {
+                    amax = absmax3(amax, z[2 * p], z[2 * p + 1]);
+                    w[h][i1][p] = pk16(z[2 * p], z[2 * p + 1]) ^ msk[h][i1][p];
+                }
             }
-        }
         if (MODE == 0) {
             if (ln < a.KC) {
 #pragma unroll
-                for (int i1 = 0; i1 < 4; ++i1) {
-                    // runs of 4 fp16 (8 bytes) at i2 = 32 nt + 8u + 4g
-                    f16 *orow = a.out + row * n + ln * 512 + i1 * 128 + 32 * nt + 4 * g;
+                for (int h = 0; h < P; ++h)
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        uint2 pk;
-                        pk.x = w[i1][2 * u];
-                        pk.y = w[i1][2 * u + 1];
-                        *reinterpret_cast<uint2 *>(orow + 8 * u) = pk;
+                    for (int i1 = 0; i1 < 4; ++i1) {
+                        // runs of 4 fp16 (8 bytes) at i2 = 32 nt + 8u + 4g
+                        f16 *orow = a.out + row * n + ln * 512 * P + h * 512 + i1 * 128 +
+                                    32 * nt + 4 * g;
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            uint2 pk;
+                            pk.x = w[h][i1][2 * u];
+                            pk.y = w[h][i1][2 * u + 1];
+                            *reinterpret_cast<uint2 *>(orow + 8 * u) = pk;
+                        }
                     }
-                }
             }
             if (more) {
                 // every wave is done reading this row from LDS
@@ -393,9 +461,13 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
         const bool clampit = __builtin_amdgcn_readfirstlane(!(amax <= 7.25f * sq));
 
         if (ln < a.KC) {
-            uint8_t *qrow = reinterpret_cast<uint8_t *>(cbuf) + ln * 272 + 16 * nt + 2 * g;
-            if (clampit) quant_store<true>(w, rcp, qrow);
-            else quant_store<false>(w, rcp, qrow);
+#pragma unroll
+            for (int h = 0; h < P; ++h) {
+                uint8_t *qrow =
+                    reinterpret_cast<uint8_t *>(cbuf) + (P * ln + h) * 272 + 16 * nt + 2 * g;
+                if (clampit) quant_store<true>(w[h], rcp, qrow);
+                else quant_store<false>(w[h], rcp, qrow);
+            }
         }
         // the row's codes are staged; write them out 16 bytes per lane
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -406,7 +478,7 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
             // the global stores: the wait for the prefetch (vmcnt counts in
             // order) then does not also wait for this row's code stores
             constexpr int R = (NT * 8 * 16 + 255) / 256;
-            const int pieces = a.KC * 16;
+            const int pieces = nc * 16;
             v4i cv[R];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -431,7 +503,15 @@ __global__ __launch_bounds__(256, SW ? 1 : 2) void had512_mfma_kernel(MfmaRotArg
 int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
                     hipStream_t st, const void *up, int64_t ld) {
-    if (K < 9 || K > 32 || n != K * 512) return 0;
+    // K % 4 == 0: the row fetch moves 4 chunks per instruction and the hadK
+    // loads take runs of 2 or 4 table entries (every Hadamard order above 2
+    // is a multiple of 4)
+    if (K < 9 || K > 32 || K % 4) return 0;
+    int P;
+    if (n == K * 512) P = 1;
+    else if (n == K * 1024) P = 2;
+    else return 0;
+    if (up && P != 1) return 0;  // SwiGLU form: H_512 chunks only
     if (ld < n) ld = n;
     if (rows > 0 && ((rows - 1) * ld + n) * 2 >= (int64_t)kOob) return 0;  // 32-bit offsets
     if (!srq_aligned(x, 16) || (up && !srq_aligned(up, 16)) || ld % 8) return 0;
@@ -451,35 +531,49 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     a.up = (const f16 *)up;
     a.ld = ld;
     // persistent blocks of 4 waves, up to 2 per CU (256 CUs; 1 with the
-    // SwiGLU input), one row each at a time
-    const int64_t cap = up ? 256 : 256 * 2;
+    // SwiGLU input or H_1024 chunks), one row each at a time
+    const int64_t cap = (up || P == 2) ? 256 : 256 * 2;
     const int64_t blocks = rows < cap ? rows : cap;
     const dim3 grid((unsigned)blocks), block(256);
-    const int nt = (int)srq_cdiv(K, 8);
-    auto go = [&](auto ntc, auto modec, auto swc) {
-        had512_mfma_kernel<decltype(ntc)::value, decltype(modec)::value, decltype(swc)::value>
-            <<<grid, block, 0, st>>>(a);
+    auto go = [&](auto ntc, auto modec, auto swc, auto pc) {
+        had512_mfma_kernel<decltype(ntc)::value, decltype(modec)::value, decltype(swc)::value,
+                           decltype(pc)::value><<<grid, block, 0, st>>>(a);
     };
     using I2 = std::integral_constant<int, 2>;
     using I3 = std::integral_constant<int, 3>;
     using I4 = std::integral_constant<int, 4>;
+    using I7 = std::integral_constant<int, 7>;
+    using I8 = std::integral_constant<int, 8>;
     using M0 = std::integral_constant<int, 0>;
     using M1 = std::integral_constant<int, 1>;
     using S0 = std::false_type;
     using S1 = std::true_type;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    auto mode = [&](auto modec) {
+        if (P == 1) {
+            // tiles of 8 chunks: K = 12, 16 | 20, 24 | 28, 32
+            const int nt = (int)srq_cdiv(K, 8);
+            if (nt == 2) go(I2{}, modec, S0{}, P1{});
+            else if (nt == 3) go(I3{}, modec, S0{}, P1{});
+            else go(I4{}, modec, S0{}, P1{});
+        } else {
+            // 2K chunks; tiles past the row's chunks hold zeros
+            if (K <= 16) go(I4{}, modec, S0{}, P2{});
+            else if (K <= 28) go(I7{}, modec, S0{}, P2{});
+            else go(I8{}, modec, S0{}, P2{});
+        }
+    };
     if (up) {
         if (!q) return 0;
-        if (nt == 2) go(I2{}, M1{}, S1{});
-        else if (nt == 3) go(I3{}, M1{}, S1{});
-        else go(I4{}, M1{}, S1{});
+        const int nt = (int)srq_cdiv(K, 8);
+        if (nt == 2) go(I2{}, M1{}, S1{}, P1{});
+        else if (nt == 3) go(I3{}, M1{}, S1{}, P1{});
+        else go(I4{}, M1{}, S1{}, P1{});
     } else if (q) {
-        if (nt == 2) go(I2{}, M1{}, S0{});
-        else if (nt == 3) go(I3{}, M1{}, S0{});
-        else go(I4{}, M1{}, S0{});
+        mode(M1{});
     } else {
-        if (nt == 2) go(I2{}, M0{}, S0{});
-        else if (nt == 3) go(I3{}, M0{}, S0{});
-        else go(I4{}, M0{}, S0{});
+        mode(M0{});
     }
     return 1;
 }

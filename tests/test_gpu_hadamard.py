@@ -49,7 +49,8 @@ def test_hadamard_transform_closed_form(C, n, dtype):
         assert np.all(np.abs(out.astype(np.float64) - want) <= acc + 1e-30)
 
 
-@pytest.mark.parametrize("n", [4096, 14336, 28672, 12 * 64, 11008, 128, 32, 6144, 10240])
+@pytest.mark.parametrize("n", [4096, 14336, 28672, 12 * 64, 11008, 128, 32, 6144, 10240,
+                               12288, 20480])
 def test_online_hadamard_vs_oracle(C, n):
     rng = np.random.default_rng(n + 1)
     x = outlier_input(rng, 9, n, n_out=min(8, n // 4), mag=50.0)
@@ -85,14 +86,16 @@ def test_online_hadamard_fp32_mode(C):
 @pytest.mark.parametrize("n,rows", [(4096, 16), (14336, 64), (28672, 5), (128, 33),
                                     (11008, 3), (32, 10), (14336, 7), (14336, 3001),
                                     (14336, 1), (14336, 513), (14336, 1024),
-                                    (6144, 9), (10240, 13)])
+                                    (6144, 9), (10240, 13), (28672, 700), (12288, 3),
+                                    (20480, 2)])
 @pytest.mark.parametrize("use_sign", [False, True])
 def test_had_sign_quant_bitexact(C, n, rows, use_sign):
     rng = np.random.default_rng(n + rows)
     x = outlier_input(rng, rows, n, n_out=min(8, n // 4), mag=100.0)
     _, k = oh.get_hadK(n)
     hk = _hadk(k) if k > 1 else None
-    sign = to_dev(rng.choice([-1, 1], n).astype(np.int8)) if use_sign else None
+    sign_np = rng.choice([-1, 1], n).astype(np.int8) if use_sign else np.ones(n, np.int8)
+    sign = to_dev(sign_np) if use_sign else None
     xd = to_dev(x)
     rot = C.online_hadamard(xd, hk, k, sign)
     q, s = C.had_sign_quant(xd, hk, k, sign)
@@ -102,6 +105,14 @@ def test_had_sign_quant_bitexact(C, n, rows, use_sign):
     # same as the unfused GPU composition
     q2, s2 = C.sym_quant_dynamic(rot.view(rows, n))
     assert torch.equal(q, q2) and torch.equal(s, s2)
+    # the rotation itself on the first and last rows and on rows next to the
+    # persistent kernels' grid strides (256 and 512 blocks)
+    idx = sorted({i for i in (0, 255, 256, 511, 512, rows - 1) if i < rows})
+    want = oh.online_hadamard(x[idx], sign_np)
+    got = to_np(rot)[idx]
+    np.testing.assert_allclose(got.astype(np.float32), want.astype(np.float32),
+                               rtol=1e-2, atol=1e-2)
+    assert np.mean(got.view(np.uint16) != want.view(np.uint16)) < 5e-3
 
 
 def test_zero_sign_raises_in_module():
@@ -112,13 +123,14 @@ def test_zero_sign_raises_in_module():
         m(torch.zeros(2, 4096, dtype=torch.float16, device="cuda"))
 
 
+@pytest.mark.parametrize("n", [14336, 28672])
 @pytest.mark.parametrize("case", ["zeros", "tiny", "subnormal_scale", "clip", "huge"])
-def test_had_sign_quant_edge_cases(C, case):
-    """Rows the MFMA fast path (n = 28 x 512) must treat like the reference:
-    an all-zero row (scale 0, codes 0), tiny values (subnormal fp16 scale),
-    a row whose scale underflows to 0, clip < 1 (codes clamp at -8), and
-    large magnitudes."""
-    n, rows = 14336, 8
+def test_had_sign_quant_edge_cases(C, case, n):
+    """Rows the MFMA fast paths (n = 28 x 512, 28 x 1024) must treat like the
+    reference: an all-zero row (scale 0, codes 0), tiny values (subnormal
+    fp16 scale), a row whose scale underflows to 0, clip < 1 (codes clamp
+    at -8), and large magnitudes."""
+    rows = 8
     rng = np.random.default_rng(42)
     x = rng.standard_normal((rows, n)).astype(np.float16)
     clip = 1.0
@@ -145,13 +157,14 @@ def test_had_sign_quant_edge_cases(C, case):
     assert_bitexact(to_np(q), qw, "codes")
 
 
+@pytest.mark.parametrize("n", [14336, 28672])
 @pytest.mark.parametrize("clip", [1.0, 0.8])
-def test_had_sign_quant_mixed_rows(C, clip):
+def test_had_sign_quant_mixed_rows(C, clip, n):
     """One launch whose persistent blocks meet rows of every kind in turn:
     ordinary rows, all-zero rows, rows whose fp16 scale is subnormal or
     underflows (the clamped path) and large rows -- each row's codes and
     scale must not depend on its neighbours."""
-    n, rows = 14336, 1100
+    rows = 1100
     rng = np.random.default_rng(7)
     x = outlier_input(rng, rows, n, n_out=8, mag=50.0).astype(np.float32)
     kind = rng.integers(0, 5, rows)
