@@ -380,14 +380,16 @@ def measured_traffic(kernel, M, K, N):
     return entry.get("hbm_bytes")
 
 
-def gemm_kernel_name(M):
-    """Kernel srq_w4a4_linear launches for M rows (gemm.hip dispatch)."""
+def gemm_kernel_name(M, N):
+    """Kernel srq_w4a4_linear launches for M x N outputs (gemm.hip dispatch)."""
     if M <= 32:
         return "gemm_stream_kernel (srq_w4a4_linear)"
     if M <= 64:
         return "gemm_skinny_kernel (srq_w4a4_linear)"
     if M >= 1024:
-        return "gemm_big_kernel (srq_w4a4_linear)"
+        if -(-M // 256) * -(-N // 256) >= 256:
+            return "gemm_sq_kernel (srq_w4a4_linear, 256 x 256 tiles)"
+        return "gemm_big_kernel (srq_w4a4_linear, 256 x 128 tiles)"
     return "gemm_tile_kernel (srq_w4a4_linear)"
 
 
@@ -525,8 +527,8 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 1),
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
-                     "traffic": measured_traffic(gemm_kernel_name(M).split()[0], M, K, N),
-                     "kernel": gemm_kernel_name(M),
+                     "traffic": measured_traffic(gemm_kernel_name(M, N).split()[0], M, K, N),
+                     "kernel": gemm_kernel_name(M, N),
                      "algorithmic_ops": ops, "avg_launch_us": round(gemm_ms * 1e3, 2)},
         "kernels": {
             "had_sign_quant": {"avg_us": round(had_ms * 1e3, 2), "bound": "hbm",

@@ -267,6 +267,43 @@ SRQ_DEV int swz(int r) {
     return (r / (256 / KBB)) % (KBB / 16);
 }
 
+// Store a wave's FM x FN block of 32x32 accumulators (lane holds column
+// lane & 31, rows 8 (v / 4) + 4 (lane / 32) + v % 4), each row and column
+// scale loaded once.
+template <int FM, int FN>
+SRQ_DEV void store_block32(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t nb,
+                           const v16i (&acc)[FM][FN], int lane) {
+    float sbv[FN];
+    int64_t gnv[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        gnv[j] = nb + j * 32 + (lane & 31);
+        sbv[j] = (!e.C && gnv[j] < N) ? (float)e.sb[gnv[j]] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t gm = mb + i * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+            if (gm >= M) continue;
+            const float sa = e.C ? 0.f : (float)e.sa[gm];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                if (gnv[j] >= N) continue;
+                const int val = acc[i][j][v] >> 8;
+                if (e.C) {
+                    e.C[gm * N + gnv[j]] = val;
+                } else {
+                    const float a = (float)val * sa;
+                    f16 o = f16_rn(a * sbv[j]);
+                    if (e.bias) o = f16_rn((float)o + (float)e.bias[gnv[j]]);
+                    if (e.res) o = f16_rn((float)o + (float)e.res[gm * N + gnv[j]]);
+                    e.out[gm * N + gnv[j]] = o;
+                }
+            }
+        }
+}
+
 // One K step of a compute wave: the stage holds BM A rows then the B rows.
 template <int FM, int FN, int KBB, int BM = kBigBM>
 SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {
@@ -444,37 +481,120 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
         sl = sl == 2 ? 0 : sl + 1;
     }
 
-    // 32x32 accumulator layout: lane holds column lane & 31, rows
-    // 8 (v / 4) + 4 (lane / 32) + v % 4
-    float sbv[FN];
-    int64_t gnv[FN];
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        gnv[j] = n0 + wn * (FN * 32) + j * 32 + (lane & 31);
-        sbv[j] = (!e.C && gnv[j] < N) ? (float)e.sb[gnv[j]] : 0.f;
+    store_block32<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Square-tile kernel for large M x N: 256 x 256 block per workgroup of 8
+// waves (2 x 4), each a 128 x 64 compute tile of 32x32x32 int8 MFMAs.  The
+// accumulators of a 256 x 256 tile fill half the CU's register file, which
+// leaves no room for producer waves (VGPRs are allocated per wave at the
+// kernel's count), so every wave issues an eighth of the DMA itself: 8
+// buffer -> LDS instructions per 128-byte K step, into a 2-stage ring
+// (2 x 64 KiB; the next step's DMA lands while this one is multiplied).
+// Against the 256 x 128 tile this moves a third fewer operand bytes from L2
+// into LDS per MFMA op, the data movement that sets the large-M GEMM's
+// power draw (measured 369 vs 459 us at M = 8192, K = 14336, N = 4096; 64-
+// byte steps in 2-4 stages: 397-410 us).  Stage layout, swizzle and
+// fragment reads are gemm_big_kernel's (big_compute).  (Split-K over two
+// workgroups per tile for grids below 256 tiles was measured and dropped:
+// at M = 2048, N = 4096 it took 120 us without any partial exchange -- the
+// 256 x 128 kernel takes 108-113 -- and 200 us with the device-scope
+// fences the exchange needs, which write back and invalidate the XCD's L2
+// under the other workgroups' operand panels.)
+
+constexpr int kSqBM = 256, kSqBN = 256;
+constexpr int kSqRows = kSqBM + kSqBN;
+
+template <int KBB, int NSTG>
+__global__ __launch_bounds__(512, 1) void gemm_sq_kernel(const uint8_t *__restrict__ A,
+                                                        const uint8_t *__restrict__ B,
+                                                        int64_t M, int64_t N, int64_t K, Epi e) {
+    constexpr int FM = 4, FN = 2, WGN = 4, kWaves = 8;
+    constexpr int kStage = kSqRows * KBB;
+    constexpr int kRowsPerDma = 1024 / KBB;               // rows per 1 KiB DMA block
+    constexpr int kDma = kSqRows / kRowsPerDma;           // DMA blocks per stage
+    constexpr int kDmaPerWave = kDma / kWaves;
+    static_assert(kDmaPerWave * kWaves == kDma, "DMA split");
+    static_assert(NSTG >= 2 && NSTG <= 4, "vmcnt waits below cover 0 .. 2 steps ahead");
+    static_assert(NSTG * kStage <= 160 * 1024, "LDS");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTG * kStage];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t tile = blockIdx.x;
+    // XCD-aware tile order, as in gemm_big_kernel
+    const int64_t tiles_m = (M + kSqBM - 1) / kSqBM;
+    const int64_t tiles_n = (N + kSqBN - 1) / kSqBN;
+    int64_t m0, n0;
+    if (tiles_m % 4 == 0 && tiles_n % 2 == 0) {
+        const int64_t x = tile % 8, i = tile / 8;
+        const int64_t bm = tiles_m / 4, bn = tiles_n / 2;
+        m0 = ((x % 4) * bm + i / bn) * kSqBM;
+        n0 = ((x / 4) * bn + i % bn) * kSqBN;
+    } else {
+        m0 = (tile / tiles_n) * kSqBM;
+        n0 = (tile % tiles_n) * kSqBN;
     }
+    const int64_t KB = K / 2;
+    const int steps = (int)((KB + KBB - 1) / KBB);
+
+    // DMA block i = kDmaPerWave * wave + q covers stage rows R i .. R i + R - 1
+    // (R = kRowsPerDma): lane l fetches chunk (l % C) ^ f(r) of row
+    // r = R i + l / C; rows outside the matrix and chunks past the K tail
+    // read as zeros (offset kOob)
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)smem;
+    constexpr int C = KBB / 16;
+    uint32_t roff[kDmaPerWave];
+    int jc[kDmaPerWave];
+#pragma unroll
+    for (int q = 0; q < kDmaPerWave; ++q) {
+        const int i = wave * kDmaPerWave + q;
+        const int r = kRowsPerDma * i + lane / C;
+        jc[q] = ((lane % C) ^ swz<KBB>(r)) * 16;
+        const bool isa = kRowsPerDma * i < kSqBM;
+        const int64_t row = isa ? m0 + r : n0 + r - kSqBM;
+        roff[q] = row < (isa ? M : N) ? (uint32_t)(row * KB) : kOob;
+    }
+    auto issue = [&](int st) {
+        const int64_t kb0 = (int64_t)st * KBB;
+        const bool tail = kb0 + KBB > KB;
+        const int sl = st % NSTG;
+#pragma unroll
+        for (int q = 0; q < kDmaPerWave; ++q) {
+            const int i = wave * kDmaPerWave + q;
+            const uint32_t dst = lds0 + sl * kStage + i * 1024;
+            uint32_t off = roff[q] == kOob ? kOob : roff[q] + (uint32_t)kb0 + jc[q];
+            if (tail && kb0 + jc[q] >= KB) off = kOob;
+            dma16(kRowsPerDma * i < kSqBM ? ar : br, off, dst);
+        }
+    };
+#pragma unroll
+    for (int p = 0; p < NSTG - 1; ++p)
+        if (p < steps) issue(p);
+
+    const int wm = wave / WGN, wn = wave % WGN;
+    v16i acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t gm = m0 + wm * (FM * 32) + i * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-            if (gm >= M) continue;
-            const float sa = e.C ? 0.f : (float)e.sa[gm];
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                if (gnv[j] >= N) continue;
-                const int val = acc[i][j][v] >> 8;
-                if (e.C) {
-                    e.C[gm * N + gnv[j]] = val;
-                } else {
-                    const float a = (float)val * sa;
-                    f16 o = f16_rn(a * sbv[j]);
-                    if (e.bias) o = f16_rn((float)o + (float)e.bias[gnv[j]]);
-                    if (e.res) o = f16_rn((float)o + (float)e.res[gm * N + gnv[j]]);
-                    e.out[gm * N + gnv[j]] = o;
-                }
-            }
-        }
+        for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){};
+    for (int s = 0; s < steps; ++s) {
+        // this wave's DMA of step s is done; the steps after it that were
+        // issued may stay in flight (vmcnt counts the wave's DMA in order)
+        const int ahead = min(NSTG - 2, steps - 1 - s);
+        if (ahead >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * kDmaPerWave) : "memory");
+        else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // every wave's DMA of step s has landed, and every wave is done with
+        // step s - 1, whose stage step s + NSTG - 1 now overwrites
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (s + NSTG - 1 < steps) issue(s + NSTG - 1);
+        big_compute<FM, FN, KBB, kSqBM>(smem + (s % NSTG) * kStage, wm, wn, lane, acc);
+    }
+    store_block32<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1046,6 +1166,10 @@ int run_gemm(const char *name, const void *A, const void *B, int64_t M, int64_t 
     } else if (M <= 64) {
         gemm_skinny_kernel<4, 8, 2><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
+    } else if (M >= 1024 && srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN) >= 256) {
+        // enough 256 x 256 tiles to cover the 256 CUs
+        const int64_t tiles = srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN);
+        gemm_sq_kernel<128, 2><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(a, b, M, N, K, e);
     } else if (M >= 1024) {
         const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
         // 4 compute waves (128 x 64 each) + 4 producer waves

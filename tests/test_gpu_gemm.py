@@ -27,6 +27,9 @@ GEMM_SHAPES = [
     (32, 6144, 4096), (32, 28672, 4096), (32, 4096, 14336), (24, 4112, 16384),
     (16, 1000, 8192), (1, 57344, 8192), (3, 17, 4128), (20, 50, 96), (32, 16, 32),
     (9, 4096, 2048), (32, 300, 8320), (2, 70000, 256), (32, 64, 28672),
+    # 256 x 256 tile kernel (>= 256 such tiles): XCD-aware tile order, ragged
+    # M and N with a K tail (row-major order), a grid of two waves of tiles
+    (4096, 4096, 1024), (4352, 4160, 4128), (8192, 4096, 640),
 ]
 
 
@@ -51,6 +54,11 @@ def test_matmul_extreme_values(C):
     b2 = np.full((17, K // 2), 0x77, np.uint8)
     c2 = to_np(C.matmul(to_dev(a), to_dev(b2)))
     assert np.all(c2 == -56 * K)
+    # the 256 x 256 tile kernel at the cfg4 down-proj depth
+    a = np.full((4096, K // 2), 0x88, np.uint8)
+    b = np.full((4096, K // 2), 0x77, np.uint8)
+    c3 = to_np(C.matmul(to_dev(a), to_dev(b)))
+    assert np.all(c3 == -56 * K)
     # the streaming kernel's deepest configuration (M = 32, K = 16384)
     K = 16384
     a = np.full((32, K // 2), 0x88, np.uint8)
@@ -61,7 +69,7 @@ def test_matmul_extreme_values(C):
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 4096, 4096), (33, 300, 768),
                                    (128, 4096, 14336), (2048, 4096, 14336), (7, 5, 64),
                                    (32, 6144, 4096), (32, 28672, 4096), (32, 4096, 14336),
-                                   (13, 4100, 8192)])
+                                   (13, 4100, 8192), (4096, 4096, 2048)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_w4a4_linear_bitexact(C, M, N, K, bias):
     rng = np.random.default_rng(M + N + K + bias)
@@ -93,3 +101,4 @@ def test_matmul_empty(C):
     a = torch.zeros(0, 16, dtype=torch.uint8, device="cuda")
     b = torch.zeros(5, 16, dtype=torch.uint8, device="cuda")
     assert C.matmul(a, b).shape == (0, 5)
+
