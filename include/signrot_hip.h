@@ -140,6 +140,20 @@ int srq_swiglu_had_sign_quant(const void *gate, const void *up, int64_t ld, int6
                               int64_t n, int64_t K, const void *hadK, const int8_t *sign,
                               float clip_ratio, void *q, void *scale, void *stream);
 
+/* srq_swiglu_had_sign_quant for the expert-sorted rows of the MoE down
+ * projection: row r's sign is row expert_ids[r] of sign int8 [num_experts, n]
+ * (an id outside [0, num_experts) takes sign +1, as srq_sym_quant_dynamic_moe
+ * does); sign NULL: no sign.  Bit-identical to srq_swiglu, then the rotation
+ * (srq_online_hadamard, no sign), then srq_sym_quant_dynamic_moe.  gate, up
+ * f16 with row stride ld >= n; needs n = K * 512 with 9 <= K <= 32, K % 4 ==
+ * 0, else SRQ_EUNSUPPORTED.  Replaces swiglu -> matmul_hadU_cuda ->
+ * sym_quant_dynamic_moe of SignRotMoEBlock.forward (signrot/nn/moe.py:186-
+ * 236, kernels/moe.cu:60-101); the reference has no fused form. */
+int srq_swiglu_had_sign_quant_moe(const void *gate, const void *up, int64_t ld, int64_t rows,
+                                  int64_t n, int64_t K, const void *hadK, const int8_t *sign,
+                                  const int32_t *expert_ids, int64_t num_experts,
+                                  float clip_ratio, void *q, void *scale, void *stream);
+
 /* ----------------------------------------------------- paged int4 KV cache */
 /* Cache layout (signrot/kernels/include/flashinfer/page.cuh:18-112):
  *   kv_data  u8  [pages, num_layers, 2, num_heads, page_size, head_dim/2]

@@ -514,6 +514,33 @@ def sym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio=1.0):
     return q, scale
 
 
+def swiglu_had_sign_quant_moe(gate, up, hadK, K, sign, expert_ids, clip_ratio=1.0):
+    """swiglu(gate, up) -> online Hadamard (had_K x H_{n/K}) -> per-expert
+    sign -> per-token int4 quantizer, one launch, for the expert-sorted rows
+    of the MoE down projection: gate, up f16 [rows, n], sign int8
+    [num_experts, n] or None, expert_ids int32 [rows].  Bit-identical to
+    swiglu, matmul_hadU_cuda, sym_quant_dynamic_moe.  Returns (q u8
+    [rows, n/2], scale f16 [rows, 1])."""
+    name = "swiglu_had_sign_quant_moe"
+    _check(name, [(gate, "gate"), (up, "up"), (hadK, "hadK"), (expert_ids, "expert_ids")],
+           [torch.float16, torch.float16, torch.float16, torch.int32])
+    if gate.dim() != 2 or up.shape != gate.shape:
+        raise RuntimeError(f"{name}: gate and up must be 2D and of one shape")
+    rows, n = gate.shape
+    if expert_ids.numel() != rows:
+        raise RuntimeError(f"{name}: expert_ids must have one entry per row")
+    _check_had(name, n, hadK, K, None, False)
+    sign = _moe_sign(name, sign, n)
+    E = sign.shape[0] if sign is not None else 0
+    q = torch.empty((rows, n // 2), dtype=torch.uint8, device=gate.device)
+    scale = torch.empty((rows, 1), dtype=torch.float16, device=gate.device)
+    if rows:
+        _call("srq_swiglu_had_sign_quant_moe", _ptr(gate), _ptr(up), n, rows, n, int(K),
+              _ptr(hadK), _ptr(sign), _ptr(expert_ids), E, float(clip_ratio), _ptr(q),
+              _ptr(scale), _stream(gate))
+    return q, scale
+
+
 def asym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio=1.0):
     """The asymmetric activation path (bindings.cpp:134-159) is not part of
     this build's W4A4 path."""

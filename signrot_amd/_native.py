@@ -23,6 +23,8 @@ SIGNATURES = {
     "srq_matmul_s4s4": [_p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_residual": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
+    "srq_swiglu_had_sign_quant_moe": [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _f32,
+                                      _p, _p, _p],
     "srq_hadamard_transform": [_p, _p, _i64, _i64, _f32, _i32, _p],
     "srq_online_hadamard": [_p, _p, _i64, _i64, _i64, _p, _p, _i32, _p],
     "srq_had_sign_quant": [_p, _i64, _i64, _i64, _p, _p, _i32, _f32, _p, _p, _p],

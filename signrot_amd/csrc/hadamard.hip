@@ -402,7 +402,8 @@ int check_rotation(const char *name, const void *x, int64_t rows, int64_t n, int
 
 int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
-                    hipStream_t st, const void *up = nullptr, int64_t ld = 0);
+                    hipStream_t st, const void *up = nullptr, int64_t ld = 0,
+                    const int32_t *sign_row = nullptr, int64_t n_sign_rows = 0);
 
 extern "C" int srq_hadamard_transform(const void *x, void *out, int64_t rows, int64_t n,
                                       float scale, int dtype, void *stream) {
@@ -505,7 +506,34 @@ extern "C" int srq_swiglu_had_sign_quant(const void *gate, const void *up, int64
         SRQ_LAUNCH_CHECK("swiglu_had_sign_quant");
         return SRQ_OK;
     }
-    srq_set_error("swiglu_had_sign_quant: needs n = K * 512 with 9 <= K <= 32 (n=%lld, K=%lld)",
-                  (long long)n, (long long)K);
+    srq_set_error("swiglu_had_sign_quant: needs n = K * 512 with 9 <= K <= 32, K %% 4 == 0 "
+                  "(n=%lld, K=%lld)", (long long)n, (long long)K);
+    return SRQ_EUNSUPPORTED;
+}
+
+extern "C" int srq_swiglu_had_sign_quant_moe(const void *gate, const void *up, int64_t ld,
+                                             int64_t rows, int64_t n, int64_t K,
+                                             const void *hadK, const int8_t *sign,
+                                             const int32_t *expert_ids, int64_t num_experts,
+                                             float clip_ratio, void *q, void *scale,
+                                             void *stream) {
+    int rc = check_rotation("swiglu_had_sign_quant_moe", gate, rows, n, K, hadK);
+    if (rc) return rc;
+    if (rows == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(up && q && scale, "swiglu_had_sign_quant_moe: null pointer");
+    SRQ_CHECK_ARG(!sign || (expert_ids && num_experts > 0),
+                  "swiglu_had_sign_quant_moe: sign needs expert_ids and num_experts > 0");
+    SRQ_CHECK_ARG(ld >= n && ld % 8 == 0, "swiglu_had_sign_quant_moe: ld=%lld must be >= n and "
+                  "a multiple of 8", (long long)ld);
+    SRQ_CHECK_ARG(srq_aligned(gate, 16) && srq_aligned(up, 16) && srq_aligned(q, 16),
+                  "swiglu_had_sign_quant_moe: gate, up and q must be 16-byte aligned");
+    if (srq_had512_mfma(gate, rows, n, K, hadK, sign, clip_ratio, q, scale, nullptr,
+                        (hipStream_t)stream, up, ld, sign ? expert_ids : nullptr,
+                        num_experts)) {
+        SRQ_LAUNCH_CHECK("swiglu_had_sign_quant_moe");
+        return SRQ_OK;
+    }
+    srq_set_error("swiglu_had_sign_quant_moe: needs n = K * 512 with 9 <= K <= 32, K %% 4 == 0 "
+                  "(n=%lld, K=%lld)", (long long)n, (long long)K);
     return SRQ_EUNSUPPORTED;
 }

@@ -85,6 +85,10 @@ struct MfmaRotArgs {
     f16 *out;             // rotation mode: fp16 rows of n
     const f16 *up;        // SwiGLU input: x is the gate, this the up projection
     int64_t ld;           // row stride of x (and up), elements
+    // per-row sign (MoE down-proj input): row r takes row sign_row[r] of the
+    // [n_sign_rows, n] sign table (ids outside the table: sign +1)
+    const int32_t *sign_row;
+    int64_t n_sign_rows;
 };
 
 // Quantize one row's packed K-mix results w (this lane: chunk ln, i2 runs
@@ -199,8 +203,28 @@ __global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kerne
         for (int i1 = 0; i1 < 4; ++i1)
 #pragma unroll
             for (int p = 0; p < 8; ++p) msk[h][i1][p] = 0;
-    if (a.sign) {
-        const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sign, n);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sign, a.sign_row ? a.n_sign_rows * n : n);
+    // the sign masks of row r's sign row (called before the next row's
+    // prefetch is issued, so waiting for them leaves the prefetch in flight)
+    auto load_row_msk = [&](int64_t r) {
+        const int64_t e = a.sign_row[r];
+        const bool ok = e >= 0 && e < a.n_sign_rows && ln < a.KC;
+#pragma unroll
+        for (int h = 0; h < P; ++h)
+#pragma unroll
+            for (int i1 = 0; i1 < 4; ++i1)
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t off =
+                        ok ? (uint32_t)(e * n + ln * 512 * P + h * 512 + i1 * 128 + 32 * nt +
+                                        8 * u + 4 * g)
+                           : kOob;
+                    const u32 sw = __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
+                    msk[h][i1][2 * u] = ((sw & 0x80u) << 8) | ((sw & 0x8000u) << 16);
+                    msk[h][i1][2 * u + 1] = ((sw & 0x800000u) >> 8) | (sw & 0x80000000u);
+                }
+    };
+    if (a.sign && !a.sign_row) {
 #pragma unroll
         for (int h = 0; h < P; ++h)
 #pragma unroll
@@ -298,6 +322,7 @@ __global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kerne
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         const bool more = row + step < a.rows;
+        if (a.sign && a.sign_row) load_row_msk(row);
         if (more) gload(row + step);
 
         // ---- stage A (H_128 over i2, this wave's 32 output columns) and
@@ -502,7 +527,8 @@ __global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kerne
 // Returns 1 if it launched, 0 if the shape is not covered.
 int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
-                    hipStream_t st, const void *up, int64_t ld) {
+                    hipStream_t st, const void *up, int64_t ld, const int32_t *sign_row,
+                    int64_t n_sign_rows) {
     // K % 4 == 0: the row fetch moves 4 chunks per instruction and the hadK
     // loads take runs of 2 or 4 table entries (every Hadamard order above 2
     // is a multiple of 4)
@@ -530,6 +556,8 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     a.out = (f16 *)out;
     a.up = (const f16 *)up;
     a.ld = ld;
+    a.sign_row = sign_row;
+    a.n_sign_rows = n_sign_rows;
     // persistent blocks of 4 waves, up to 2 per CU (256 CUs; 1 with the
     // SwiGLU input or H_1024 chunks), one row each at a time
     const int64_t cap = (up || P == 2) ? 256 : 256 * 2;

@@ -20,6 +20,7 @@ this build.
 """
 import torch
 
+from .. import _CUDA
 from ..functional import kernel
 from ..functional.hadamard import get_hadK, matmul_hadU_cuda
 
@@ -35,6 +36,9 @@ class SignRotMoEBlock(torch.nn.Module):
                 "SignRotMoEBlock(asym=True): asymmetric activations are not part of this "
                 "build's W4A4 path")
         self.gate = gate  # router linear (16-bit activations), left untouched
+        # grouped path: one launch for swiglu + rotation + sign + quantizer
+        # of the down-proj input where the rotation has an MFMA form
+        self.fuse_down = True
         self.top_k = top_k
         self.norm_topk_prob = norm_topk_prob
         self.asym = asym
@@ -132,6 +136,17 @@ class SignRotMoEBlock(torch.nn.Module):
         else:
             gate_h = self._gemm_dequant_loop(q_a, s_a, counts, self.w_gate, self.s_gate)
             up_h = self._gemm_dequant_loop(q_a, s_a, counts, self.w_up, self.s_up)
+        if self.fuse_down and self.use_grouped and not self.fp32_had and self.K % 4 == 0 and \
+                9 <= self.K <= 32 and gate_h.shape[1] == self.K * 512:
+            # swiglu, rotation, per-expert sign and quantizer in one launch
+            # (bit-identical to the three steps below)
+            q_d, s_d = _CUDA.swiglu_had_sign_quant_moe(gate_h, up_h, self.had_K.half(), self.K,
+                                                       self.sign_down, eid, self.clip_ratio)
+            y = self._gemm_dequant_grouped(q_d, s_d, offsets, self.w_down, self.s_down)
+            inv = torch.argsort(perm)
+            y = y.to(x_dtype)[inv].view(-1, self.top_k, hidden_dim)
+            out = (y * routing_weights.unsqueeze(-1)).sum(dim=1)
+            return out.view(batch_size, seq_len, hidden_dim), router_logits
         inter = kernel.swiglu(gate_h, up_h)
 
         # the Hadamard is identical for every expert; the had_adj sign is per

@@ -289,3 +289,40 @@ def test_block_graph_replay_on_new_inputs():
         want, _ = blk(x_new)
         torch.cuda.synchronize()
         assert torch.equal(out_static, want), f"replay {i} differs from eager"
+
+
+@pytest.mark.parametrize("rows,n,K,experts,clip,with_sign", [
+    (600, 14336, 28, 8, 1.0, True), (37, 6144, 12, 16, 0.8, True), (5, 10240, 20, 4, 1.0, True),
+    (300, 14336, 28, 8, 1.0, False)])
+def test_swiglu_had_sign_quant_moe(C, rows, n, K, experts, clip, with_sign):
+    """The fused MoE down-proj input op equals swiglu -> rotation (no sign) ->
+    sym_quant_dynamic_moe bit for bit, with expert ids in random order, ids
+    outside the sign table (sign +1), and more rows than persistent blocks
+    (each row's sign masks are loaded for that row)."""
+    from oracle import hadamard as oh
+    rng = np.random.default_rng(rows + n)
+    gate = to_dev((rng.standard_normal((rows, n)) * 2).astype(np.float16))
+    up = to_dev((rng.standard_normal((rows, n)) * 2).astype(np.float16))
+    eid_np = rng.integers(0, experts, rows).astype(np.int32)
+    eid_np[: min(rows, 3)] = [-1, experts, 1 << 20][: min(rows, 3)]
+    eid = to_dev(eid_np)
+    sign = to_dev(rng.choice([-1, 1], (experts, n)).astype(np.int8)) if with_sign else None
+    hk = to_dev(oh.had_table(K).astype(np.float32)).half()
+    q, s = C.swiglu_had_sign_quant_moe(gate, up, hk, K, sign, eid, clip)
+    inter = C.swiglu(gate, up)
+    rot = C.online_hadamard(inter, hk, K, None)
+    q2, s2 = C.sym_quant_dynamic_moe(rot, sign, eid, clip)
+    assert torch.equal(s, s2), "scales"
+    assert torch.equal(q, q2), "codes"
+
+
+@torch.no_grad()
+def test_block_fused_down_equals_unfused():
+    blk = _block(4096, 14336, 8, 2, True, seed=5)
+    x = torch.randn(1, 96, 4096, device=DEV, dtype=torch.float16)
+    blk.fuse_down = True
+    out, _ = blk(x)
+    blk.fuse_down = False
+    out2, _ = blk(x)
+    assert torch.equal(out, out2)
+    assert torch.isfinite(out).all()
