@@ -133,7 +133,8 @@ int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_t K,
  * arithmetic), then the rotation, sign and quantizer of srq_had_sign_quant.
  * Bit-identical to srq_swiglu followed by srq_had_sign_quant.  gate, up f16
  * with row stride ld >= n (e.g. the two halves of one [rows, 2n] gate/up
- * projection); needs n = K * 512 with 9 <= K <= 32, else SRQ_EUNSUPPORTED.
+ * projection); needs K % 4 == 0 and n = K * 512 (9 <= K <= 32) or n = K *
+ * 1024 (9 <= K <= 28), else SRQ_EUNSUPPORTED.
  * Replaces swiglu -> OnlineHadamard -> Quantizer of the decoder MLP
  * (e2e/quantized_llama/modeling_llama.py:125-137; fused.cu:367-390). */
 int srq_swiglu_had_sign_quant(const void *gate, const void *up, int64_t ld, int64_t rows,

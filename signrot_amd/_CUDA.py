@@ -441,6 +441,15 @@ def swiglu(gate, up):
 
 # -------------------------------------------------------------------- MoE
 
+def swiglu_had_fusable(n, K):
+    """Whether swiglu_had_sign_quant has a kernel for rotation size n = K x
+    2^k (the MFMA rotation's shapes: H_512 chunks with 9 <= K <= 32, H_1024
+    chunks with 9 <= K <= 28; K a multiple of 4)."""
+    if K % 4:
+        return False
+    return (9 <= K <= 32 and n == K * 512) or (9 <= K <= 28 and n == K * 1024)
+
+
 def swiglu_had_sign_quant(gu, hadK, K, sign=None, clip_ratio=1.0):
     """swiglu(gu[..., :n], gu[..., n:]) followed by had_sign_quant, one launch,
     for a gate/up projection output gu f16 [..., 2n]: (q u8 [..., n/2], scale

@@ -506,8 +506,8 @@ extern "C" int srq_swiglu_had_sign_quant(const void *gate, const void *up, int64
         SRQ_LAUNCH_CHECK("swiglu_had_sign_quant");
         return SRQ_OK;
     }
-    srq_set_error("swiglu_had_sign_quant: needs n = K * 512 with 9 <= K <= 32, K %% 4 == 0 "
-                  "(n=%lld, K=%lld)", (long long)n, (long long)K);
+    srq_set_error("swiglu_had_sign_quant: needs K %% 4 == 0 and n = K * 512 (9 <= K <= 32) or "
+                  "n = K * 1024 (9 <= K <= 28) (n=%lld, K=%lld)", (long long)n, (long long)K);
     return SRQ_EUNSUPPORTED;
 }
 

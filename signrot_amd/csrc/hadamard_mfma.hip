@@ -113,7 +113,8 @@ SRQ_DEV void quant_store(const u32 (&w)[4][8], float rcp, uint8_t *qrow) {
 }
 
 // SW: the row is swiglu(gate, up) of two strided inputs (one workgroup per
-// CU: the up prefetch needs the registers two workgroups would share).
+// CU: the up prefetch needs the registers two workgroups would share; with
+// H_1024 chunks up to K = 28).
 // P: 512-chunks per Hadamard chunk (1: H_512, 2: H_1024; one workgroup per
 // CU, which holds twice the row in registers).
 template <int NT, int MODE, bool SW, int P>
@@ -537,7 +538,9 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     if (n == K * 512) P = 1;
     else if (n == K * 1024) P = 2;
     else return 0;
-    if (up && P != 1) return 0;  // SwiGLU form: H_512 chunks only
+    // the SwiGLU form of H_1024 holds gate and up prefetches of a 2K-chunk
+    // row: it fits the register file up to K = 28 (K = 32 would spill)
+    if (up && P == 2 && K > 28) return 0;
     if (ld < n) ld = n;
     if (rows > 0 && ((rows - 1) * ld + n) * 2 >= (int64_t)kOob) return 0;  // 32-bit offsets
     if (!srq_aligned(x, 16) || (up && !srq_aligned(up, 16)) || ld % 8) return 0;
@@ -594,10 +597,15 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     };
     if (up) {
         if (!q) return 0;
-        const int nt = (int)srq_cdiv(K, 8);
-        if (nt == 2) go(I2{}, M1{}, S1{}, P1{});
-        else if (nt == 3) go(I3{}, M1{}, S1{}, P1{});
-        else go(I4{}, M1{}, S1{}, P1{});
+        if (P == 1) {
+            const int nt = (int)srq_cdiv(K, 8);
+            if (nt == 2) go(I2{}, M1{}, S1{}, P1{});
+            else if (nt == 3) go(I3{}, M1{}, S1{}, P1{});
+            else go(I4{}, M1{}, S1{}, P1{});
+        } else {
+            if (K <= 16) go(I4{}, M1{}, S1{}, P2{});
+            else go(I7{}, M1{}, S1{}, P2{});
+        }
     } else if (q) {
         mode(M1{});
     } else {

@@ -115,7 +115,7 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         x2 = _CUDA.w4a4_linear_residual(qa, sa.view(-1), self.w_o, self.s_o, x2)
         q2, s2 = _CUDA.rmsnorm_quant(x2, n2.eps, n2.mean_dim)
         gu = _CUDA.w4a4_linear(q2, s2.view(-1), self.w_gu, self.s_gu)
-        if 9 <= self.down_k <= 32 and self.ffn == self.down_k * 512:
+        if _CUDA.swiglu_had_fusable(self.ffn, self.down_k):
             qd, sd = _CUDA.swiglu_had_sign_quant(gu, self.down_hadk, self.down_k,
                                                  self.down_sign)
         else:  # no fused SwiGLU form of this rotation size

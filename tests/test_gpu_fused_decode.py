@@ -13,6 +13,7 @@ residual add after o_proj / down_proj.
 import math
 
 import numpy as np
+import scipy.linalg
 import pytest
 import torch
 
@@ -101,14 +102,17 @@ def test_w4a4_linear_residual(M):
     assert_bitexact(to_np(inplace), to_np(ref), "in-place residual")
 
 
-@pytest.mark.parametrize("rows,K", [(1, 28), (32, 28), (77, 28), (4, 12)])
-def test_swiglu_had_sign_quant_equals_chain(rows, K):
+@pytest.mark.parametrize("rows,K,chunk", [(1, 28, 512), (32, 28, 512), (77, 28, 512),
+                                         (4, 12, 512), (1, 28, 1024), (32, 28, 1024),
+                                         (300, 28, 1024), (4, 12, 1024), (6, 20, 1024)])
+def test_swiglu_had_sign_quant_equals_chain(rows, K, chunk):
     C = _ops()
-    rng = np.random.default_rng(rows + K)
-    n = K * 512
+    rng = np.random.default_rng(rows + K + chunk)
+    n = K * chunk
     gu = to_dev((rng.standard_normal((rows, 2 * n)) * 2.0).astype(np.float16))
-    had, k = oh.get_hadK(n)
-    hk = to_dev(had.astype(np.float16))
+    # the K table named by the case (get_hadK(20480) would pick 40 x 512)
+    k = K
+    hk = to_dev(oh.had_table(K).astype(np.float16))
     sign = to_dev(rng.choice([-1, 1], n).astype(np.int8))
     q, s = C.swiglu_had_sign_quant(gu, hk, k, sign)
     a = C.swiglu(gu[:, :n].contiguous(), gu[:, n:].contiguous())
@@ -125,6 +129,12 @@ def test_swiglu_had_sign_quant_rejects_generic_sizes():
     gu = torch.zeros(2, 2 * n, dtype=torch.float16, device="cuda")
     with pytest.raises(RuntimeError, match="512"):
         C.swiglu_had_sign_quant(gu, to_dev(had.astype(np.float16)), k)
+    # K = 32 with H_1024 chunks: the SwiGLU form stops at K = 28
+    assert not C.swiglu_had_fusable(32 * 1024, 32) and C.swiglu_had_fusable(28 * 1024, 28)
+    h32 = to_dev(scipy.linalg.hadamard(32).astype(np.float16))
+    gu = torch.zeros(2, 2 * 32 * 1024, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="1024"):
+        C.swiglu_had_sign_quant(gu, h32, 32)
 
 
 def _prefilled_cache(B, T, Hkv, Hq, page, layers, rng):
