@@ -533,7 +533,7 @@ def main():
                                "algorithmic_bytes": had_bytes,
                                "achieved_GBs": round(had_gbs, 1),
                                "frac_hbm": round(had_gbs / PEAK_HBM_GBS, 4),
-                               "traffic": measured_traffic("had512_mfma_kernel<4, 1, false>", M, K, N)},
+                               "traffic": measured_traffic("had512_mfma_kernel<4, 1, false, 1>", M, K, N)},
             "w4a4_linear": {"avg_us": round(gemm_ms * 1e3, 2), "bound": "mfma",
                             "algorithmic_bytes": gemm_bytes,
                             "achieved_TOPS": round(gemm_tops, 1),
