@@ -85,6 +85,27 @@ int srq_w4a4_linear(const void *A, const void *a_scale, const void *B,
                     const void *b_scale, const void *bias, int64_t M, int64_t N,
                     int64_t K, void *out, void *stream);
 
+/* int4 GEMM with unsigned A: C i32 [M, N] = A · Bᵀ, A u8 [M, K/2] of uint4
+ * codes (0..15, the asymmetric activation quantizer's), B u8 [N, K/2] of
+ * two's-complement int4; same shape rules as srq_matmul_s4s4.
+ * Replaces _CUDA.matmul_ui4_si4 (signrot/kernels/bindings.cpp:31-47,
+ * gemm.cu:47-85). */
+int srq_matmul_u4s4(const void *A, const void *B, int64_t M, int64_t N, int64_t K,
+                    int32_t *C, void *stream);
+
+/* Fused W4A4 linear for asymmetric activations: v = A · Bᵀ (A uint4 codes)
+ * - a_zero[m] * b_sum[n] in int32 (wrapping), then out f16 [M, N] =
+ * fp16((float(v) * float(a_scale[m])) * float(b_scale[n])), then (bias !=
+ * NULL) fp16(out + bias[n]).  a_zero int8 [M] (the quantizer's zero point
+ * cast to int8), b_sum int32 [N] (srq_sum_i4 of B's rows).  Bit-identical to
+ * srq_matmul_u4s4, srq_matmul_colrow_i8_i32, the int32 subtraction and
+ * srq_sym_dequant (+ bias).  Replaces the zeros_x branch of
+ * Linear4bit.forward (signrot/nn/linear.py:35-50). */
+int srq_w4a4_linear_asym(const void *A, const void *a_scale, const int8_t *a_zero,
+                         const void *B, const void *b_scale, const int32_t *b_sum,
+                         const void *bias, int64_t M, int64_t N, int64_t K, void *out,
+                         void *stream);
+
 /* srq_w4a4_linear with the decoder's residual add fused into the epilogue:
  * out = fp16(lin + residual[m, n]) after the dequant (and bias), as torch's
  * fp16 `residual + linear(x)` rounds it.  residual f16 [M, N]; out may be the
@@ -266,6 +287,50 @@ int srq_rope_qk(void *q, void *k, const void *cos, const void *sin, int64_t n_se
  * Replaces _CUDA.swiglu (bindings.cpp:411-421, fused.cu:367-390). */
 int srq_swiglu(const void *gate, const void *up, int64_t n, void *out, void *stream);
 
+/* ------------------------------------------------ asymmetric activations */
+
+/* Per-token asymmetric uint4 quantizer: per row of x f16 [rows, cols],
+ * hmin/hmax = fp16(min/max) (times clip_ratio, rounded, when clip != 1),
+ * scale = fp16(fp16(hmax - hmin) / 15), zero = fp16(rne(fp16(-hmin /
+ * scale))), q = clamp(__half2int_rn(fp16(x / scale)) + __half2int_rn(zero),
+ * 0, 15); outputs q u8 [rows, ceil(cols/2)] (column 2j in the low nibble),
+ * scale f16 [rows], zero f16 [rows].
+ * Replaces _CUDA.asym_quant_dynamic (signrot/kernels/bindings.cpp:337-358,
+ * fused.cu:143-195). */
+int srq_asym_quant_dynamic(const void *x, int64_t rows, int64_t cols, float clip_ratio,
+                           void *q, void *scale, void *zero, void *stream);
+
+/* srq_asym_quant_dynamic of expert-sorted rows, row r first multiplied by
+ * sign[expert_ids[r]] (int8 [num_experts, cols], exact; NULL: no sign; an id
+ * outside [0, num_experts) takes +1).  Replaces _CUDA.asym_quant_dynamic_moe
+ * (signrot/kernels/bindings.cpp:134-159, moe.cu:104-152). */
+int srq_asym_quant_dynamic_moe(const void *x, const int8_t *sign, const int32_t *expert_ids,
+                               int64_t num_experts, int64_t rows, int64_t cols,
+                               float clip_ratio, void *q, void *scale, void *zero,
+                               void *stream);
+
+/* Asymmetric quantizer with a given per-row scale and zero (f16 [rows]):
+ * q = clamp(__half2int_rn(fp16(x / scale)) + __half2int_rn(zero), lo, hi)
+ * with [lo, hi] = [0, 15] (is_signed == 0, uint4) or [-8, 7] (two's-
+ * complement int4), packed as srq_asym_quant_dynamic.  Replaces
+ * _CUDA.asym_quant_f16_ui4 / asym_quant_f16_si4 (signrot/kernels/
+ * bindings.cpp:270-312, quant.cu:133-207). */
+int srq_asym_quant(const void *x, const void *scale, const void *zero, int64_t rows,
+                   int64_t cols, int is_signed, void *q, void *stream);
+
+/* out int32 [rows] = sum over both nibbles of each byte of row r of x u8
+ * [rows, packed_cols], sign-extended when is_signed (int32, wrapping).
+ * Replaces _CUDA.sum_i4 (signrot/kernels/bindings.cpp:437-451,
+ * quant.cu:233-321). */
+int srq_sum_i4(const void *x, int64_t rows, int64_t packed_cols, int is_signed, int32_t *out,
+               void *stream);
+
+/* out int32 [rows, cols] = int32(a_col[r]) * b_row[c] (wrapping).  Replaces
+ * _CUDA.matmul_colrow_i8_i32 (signrot/kernels/bindings.cpp:453-477,
+ * quant.cu:341-383). */
+int srq_matmul_colrow_i8_i32(const int8_t *a_col, const int32_t *b_row, int64_t rows,
+                             int64_t cols, int32_t *out, void *stream);
+
 /* --------------------------------------------------------------- MoE */
 
 /* Grouped int4 x int4 -> int32 GEMM over `problem_count` problems whose
@@ -275,9 +340,9 @@ int srq_swiglu(const void *gate, const void *up, int64_t n, void *out, void *str
  * row stride lda[p] codes), B at ptr_B[p] (packed int4 [n, k/2], row stride
  * ldb[p] codes), and writes C_p[i * ldc[p] + j] = sum_k A_p[i,k] B_p[j,k]
  * (int32) at ptr_C[p].  Each k must be a multiple of 32 and <= 131072 (not
- * checkable on the host).  signed_a == 0 (unsigned asymmetric activations)
- * returns SRQ_EUNSUPPORTED.  Per element identical to srq_matmul_s4s4 on
- * each problem.
+ * checkable on the host).  signed_a == 0: A holds unsigned asymmetric codes
+ * (0..15), as matmul_ui4_si4.  Per element identical to srq_matmul_s4s4
+ * (srq_matmul_u4s4) on each problem.
  * Replaces _CUDA.matmul_grouped (signrot/kernels/bindings.cpp:49-91,
  * gemm_grouped.cu:54-107). */
 int srq_matmul_grouped(const int32_t *problem_sizes, const int64_t *ptr_A,
@@ -296,6 +361,18 @@ int srq_matmul_grouped(const int32_t *problem_sizes, const int64_t *ptr_A,
 int srq_w4a4_linear_moe(const void *A, const void *a_scale, const void *B, const void *b_scale,
                         const int32_t *expert_offsets, int64_t num_experts, int64_t rows,
                         int64_t N, int64_t K, void *out, void *stream);
+
+/* srq_w4a4_linear_moe for asymmetric activations: A holds uint4 codes, and
+ * before the dequant each int32 product becomes v - a_zero[row] *
+ * b_sum[e, col] (wrapping), a_zero int8 [rows], b_sum int32 [num_experts, N]
+ * (srq_sum_i4 of each expert's weight rows).  Bit-identical to
+ * srq_matmul_grouped (signed_a = 0) followed by srq_sym_dequant_moe with
+ * zero_row and w_sum.  Replaces that pair in SignRotMoEBlock's asym path
+ * (signrot/nn/moe.py:126-134). */
+int srq_w4a4_linear_moe_asym(const void *A, const void *a_scale, const int8_t *a_zero,
+                             const void *B, const void *b_scale, const int32_t *b_sum,
+                             const int32_t *expert_offsets, int64_t num_experts, int64_t rows,
+                             int64_t N, int64_t K, void *out, void *stream);
 
 /* Per-row symmetric int4 quantization of expert-sorted rows with the
  * per-expert SignRot sign fused in: row r is multiplied by

@@ -32,6 +32,13 @@ def sym_quant_dynamic_moe(x_f16, sign_i8, expert_ids, clip_ratio=1.0):
     return oq.sym_quant_dynamic(apply_sign(x_f16, sign_i8, expert_ids), clip_ratio)
 
 
+def asym_quant_dynamic_moe(x_f16, sign_i8, expert_ids, clip_ratio=1.0):
+    """asym_quant_dynamic_moe_kernel (moe.cu:104-152): asym_quant_dynamic of
+    the sign-flipped rows.  Returns (packed uint4 u8, scale f16 [rows, 1],
+    zero f16 [rows, 1])."""
+    return oq.asym_quant_dynamic(apply_sign(x_f16, sign_i8, expert_ids), clip_ratio)
+
+
 def sym_dequant_moe(c_i32, scale_row_f16, w_scales_f16, expert_ids, zero_row=None,
                     w_sum=None):
     """sym_dequant_moe_kernel (moe.cu:202-226): qval = q - zero_row[r] *

@@ -184,3 +184,120 @@ def rtn_weight(w_f16, bits=4, symmetric_grid=False):
     codes = np.rint((w_fq.astype(F32) / s16.astype(F32)).astype(F16).astype(F32))
     codes = np.clip(codes, -8, 7).astype(np.int8)
     return codes, s16, w_fq
+
+
+# ------------------------------------------------- asymmetric activations
+
+def wrap_i32(v):
+    """Two's-complement int32 wrap of an integer array (the reference's int
+    additions overflow this way on the GPU)."""
+    v = np.asarray(v, np.int64)
+    return ((v + 2 ** 31) % 2 ** 32) - 2 ** 31
+
+
+def asym_params(x_f16, clip_ratio=1.0):
+    """Per-row scale and zero of asym_quant_dynamic_kernel
+    (signrot/kernels/fused.cu:155-179): vmin, vmax exact; hmin = fp16(vmin),
+    hmax = fp16(vmax); if clip != 1 each is fp16(float(h) * clip);
+    diff = fp16(hmax - hmin); scale = fp16(diff / 15.f);
+    ratio = fp16(-hmin / scale) (fp32 division); zero = fp16(nearbyint(ratio))
+    (round half to even).  Returns (scale f16 [rows], zero f16 [rows])."""
+    x = np.asarray(x_f16, dtype=F16).astype(F32)
+    hmin = x.min(axis=-1).astype(F16)
+    hmax = x.max(axis=-1).astype(F16)
+    if clip_ratio != 1.0:
+        hmin = (hmin.astype(F32) * F32(clip_ratio)).astype(F16)
+        hmax = (hmax.astype(F32) * F32(clip_ratio)).astype(F16)
+    diff = (hmax.astype(F32) - hmin.astype(F32)).astype(F16)
+    scale = (diff.astype(F32) / F32(15.0)).astype(F16)
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        ratio = (-hmin.astype(F32) / scale.astype(F32)).astype(F16)
+    zero = np.rint(ratio.astype(F32)).astype(F16)
+    return scale, zero
+
+
+def asym_codes(x_f16, scale_f16, zero_f16, qmin=0, qmax=15):
+    """q = clamp(__half2int_rn(__hdiv(x, scale)) + __half2int_rn(zero), qmin,
+    qmax) (fused.cu:183-193; quant.cu:156-158, 201-203), the int addition
+    in int32 (wrapping: ±inf quotients saturate to INT_MAX / INT_MIN)."""
+    x = np.asarray(x_f16, dtype=F16).astype(F32)
+    s = np.asarray(scale_f16, dtype=F16).reshape(-1).astype(F32)[:, None]
+    z = half2int_rn(np.asarray(zero_f16, dtype=F16).reshape(-1))[:, None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        quot = (x / s).astype(F16)
+    return np.clip(wrap_i32(half2int_rn(quot) + z), qmin, qmax).astype(np.int64)
+
+
+def pack_u4(q):
+    """UInt4Subbyte packing: unsigned nibbles, column 2j low, 2j+1 high (an
+    odd last column leaves the high nibble 0)."""
+    return pack_i4(np.asarray(q, np.int64) & 0xF)
+
+
+def unpack_u4(p):
+    """The unsigned nibbles of a packed u8 tensor, low then high."""
+    p = np.asarray(p, dtype=np.uint8)
+    out = np.empty(p.shape[:-1] + (p.shape[-1] * 2,), np.int64)
+    out[..., 0::2] = p & 0xF
+    out[..., 1::2] = p >> 4
+    return out
+
+
+def asym_quant_dynamic(x_f16, clip_ratio=1.0):
+    """_CUDA.asym_quant_dynamic (bindings.cpp:337-358, fused.cu:143-195):
+    returns (packed u8 [rows, ceil(cols/2)] of uint4 codes, scale f16
+    [rows, 1], zero f16 [rows, 1])."""
+    scale, zero = asym_params(x_f16, clip_ratio)
+    q = asym_codes(x_f16, scale, zero)
+    return pack_u4(q), scale[:, None], zero[:, None]
+
+
+def asym_quant_f16_ui4(x_f16, scale_f16, zero_f16):
+    """_CUDA.asym_quant_f16_ui4 (quant.cu:182-207): uint4 codes for a given
+    per-row scale and zero."""
+    return pack_u4(asym_codes(x_f16, scale_f16, zero_f16, 0, 15))
+
+
+def asym_quant_f16_si4(x_f16, scale_f16, zero_f16):
+    """_CUDA.asym_quant_f16_si4 (quant.cu:133-162): the same arithmetic
+    clamped to [-8, 7], two's-complement nibbles."""
+    return pack_i4(asym_codes(x_f16, scale_f16, zero_f16, -8, 7))
+
+
+def sum_i4(x_u8, is_signed=True):
+    """_CUDA.sum_i4 (bindings.cpp:437-451, quant.cu:233-321): per row, the
+    sum of both nibbles of every byte, sign-extended when is_signed.
+    int32 [rows, 1]."""
+    v = unpack_i4(x_u8) if is_signed else unpack_u4(x_u8)
+    return wrap_i32(v.sum(axis=-1))[:, None].astype(np.int32)
+
+
+def matmul_colrow_i8_i32(a_col_i8, b_row_i32):
+    """_CUDA.matmul_colrow_i8_i32 (bindings.cpp:453-477, quant.cu:341-383):
+    out[r, c] = int32(a[r]) * b[c] (int32, wrapping)."""
+    a = np.asarray(a_col_i8, np.int64).reshape(-1, 1)
+    b = np.asarray(b_row_i32, np.int64).reshape(1, -1)
+    return wrap_i32(a * b).astype(np.int32)
+
+
+def matmul_u4s4(a_u8, b_u8):
+    """_CUDA.matmul_ui4_si4 (bindings.cpp:31-47 -> gemm.cu:47-85): C = A · Bᵀ
+    with A's nibbles unsigned (0..15) and B's two's complement, int32 (a
+    float64 matmul, exact: every partial sum is an integer below 2^53)."""
+    a = unpack_u4(a_u8).astype(np.float64)
+    b = unpack_i4(b_u8).astype(np.float64)
+    return wrap_i32((a @ b.T).astype(np.int64)).astype(np.int32)
+
+
+def w4a4_linear_asym(a_u8, a_scale_f16, a_zero_i8, b_u8, b_scale_f16, bias_f16=None):
+    """Linear4bit.forward on an asymmetric PackedQuantizedTensor
+    (nn/linear.py:35-50): x = matmul_ui4_si4(A, W); x -= matmul_colrow_i8_i32(
+    zeros_x, sum_i4(W)ᵀ) (int32); sym_dequant(x, scales_x, weight_scales)
+    (+ bias)."""
+    c = matmul_u4s4(a_u8, b_u8).astype(np.int64)
+    ws = sum_i4(b_u8).reshape(-1)
+    c = wrap_i32(c - matmul_colrow_i8_i32(a_zero_i8, ws).astype(np.int64))
+    out = sym_dequant(c, a_scale_f16, b_scale_f16)
+    if bias_f16 is not None:
+        out = add_bias(out, bias_f16)
+    return out

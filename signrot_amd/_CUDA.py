@@ -75,6 +75,44 @@ def matmul(A, B):
     return C
 
 
+def matmul_ui4_si4(A, B):
+    """C i32 [M, N] = A · Bᵀ with A's codes unsigned (uint4) and B's int4
+    (bindings.cpp:31-47)."""
+    _check("matmul_ui4_si4", [(A, "A"), (B, "B")], [torch.uint8, torch.uint8])
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[1]:
+        raise RuntimeError(f"matmul_ui4_si4: expected A [M, K/2] and B [N, K/2], got "
+                           f"{tuple(A.shape)} and {tuple(B.shape)}")
+    M, N, K = A.shape[0], B.shape[0], A.shape[1] * 2
+    C = torch.empty((M, N), dtype=torch.int32, device=A.device)
+    _call("srq_matmul_u4s4", _ptr(A), _ptr(B), M, N, K, _ptr(C), _stream(A))
+    return C
+
+
+def w4a4_linear_asym(A, a_scale, a_zero, B, b_scale, b_sum, bias=None):
+    """Fused W4A4 linear for asymmetric activations: (A·Bᵀ - a_zero ⊗ b_sum)
+    (int32) -> sym_dequant (+ bias); A uint4 codes [M, K/2], a_zero int8
+    [M], b_sum int32 [N] (sum_i4 of B).  The zeros_x branch of
+    Linear4bit.forward (linear.py:35-50) in one launch."""
+    _check("w4a4_linear_asym", [(A, "A"), (a_scale, "a_scale"), (a_zero, "a_zero"), (B, "B"),
+                                (b_scale, "b_scale"), (b_sum, "b_sum"), (bias, "bias")],
+           [torch.uint8, torch.float16, torch.int8, torch.uint8, torch.float16, torch.int32,
+            torch.float16])
+    if A.dim() != 2 or B.dim() != 2 or A.shape[1] != B.shape[1]:
+        raise RuntimeError(f"w4a4_linear_asym: expected A [M, K/2] and B [N, K/2], got "
+                           f"{tuple(A.shape)} and {tuple(B.shape)}")
+    M, N, K = A.shape[0], B.shape[0], A.shape[1] * 2
+    if a_scale.numel() != M or a_zero.numel() != M:
+        raise RuntimeError("w4a4_linear_asym: a_scale and a_zero must have M elements")
+    if b_scale.numel() != N or b_sum.numel() != N:
+        raise RuntimeError("w4a4_linear_asym: b_scale and b_sum must have N elements")
+    if bias is not None and bias.numel() != N:
+        raise RuntimeError("w4a4_linear_asym: bias must have N elements")
+    out = torch.empty((M, N), dtype=torch.float16, device=A.device)
+    _call("srq_w4a4_linear_asym", _ptr(A), _ptr(a_scale), _ptr(a_zero), _ptr(B), _ptr(b_scale),
+          _ptr(b_sum), _ptr(bias), M, N, K, _ptr(out), _stream(A))
+    return out
+
+
 def w4a4_linear(A, a_scale, B, b_scale, bias=None):
     """Fused matmul + sym_dequant (+ fp16 bias): out f16 [M, N]."""
     _check("w4a4_linear", [(A, "A"), (a_scale, "a_scale"), (B, "B"), (b_scale, "b_scale"),
@@ -173,6 +211,76 @@ def sym_quant_dynamic(x, clip_ratio=1.0):
     _call("srq_sym_quant_dynamic", _ptr(x), rows, cols, float(clip_ratio), _ptr(q), _ptr(scale),
           _stream(x))
     return q, scale
+
+
+# ------------------------------------------------- asymmetric activations
+
+def asym_quant_dynamic(x, clip_ratio=1.0):
+    """(q u8 [rows, ceil(cols/2)] of uint4 codes, scale f16 [rows, 1], zero
+    f16 [rows, 1]) (bindings.cpp:337-358)."""
+    _check("asym_quant_dynamic", [(x, "x")])
+    if x.dim() != 2:
+        raise RuntimeError("asym_quant_dynamic expects a 2D [rows, cols] tensor")
+    if x.dtype != torch.float16:
+        raise RuntimeError("asym_quant_dynamic expects fp16 input")
+    rows, cols = x.shape
+    q = torch.empty((rows, (cols + 1) // 2), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((rows, 1), dtype=torch.float16, device=x.device)
+    zero = torch.empty((rows, 1), dtype=torch.float16, device=x.device)
+    _call("srq_asym_quant_dynamic", _ptr(x), rows, cols, float(clip_ratio), _ptr(q),
+          _ptr(scale), _ptr(zero), _stream(x))
+    return q, scale, zero
+
+
+def _asym_given(name, x, scale, zero, is_signed):
+    _check(name, [(x, "x"), (scale, "scale"), (zero, "zeros")],
+           [torch.float16, torch.float16, torch.float16])
+    if x.dim() != 2:
+        raise RuntimeError(f"{name} expects a 2D [rows, cols] tensor")
+    rows, cols = x.shape
+    if scale.numel() != rows or zero.numel() != rows:
+        raise RuntimeError(f"{name}: scale and zeros need one entry per row")
+    q = torch.empty((rows, (cols + 1) // 2), dtype=torch.uint8, device=x.device)
+    _call("srq_asym_quant", _ptr(x), _ptr(scale), _ptr(zero), rows, cols, int(is_signed),
+          _ptr(q), _stream(x))
+    return q
+
+
+def asym_quant_f16_ui4(x, scale, zero):
+    """uint4 codes for a given per-row scale and zero (bindings.cpp:292-312)."""
+    return _asym_given("asym_quant_f16_ui4", x, scale, zero, False)
+
+
+def asym_quant_f16_si4(x, scale, zero):
+    """The same arithmetic clamped to [-8, 7], int4 codes (bindings.cpp:270-290)."""
+    return _asym_given("asym_quant_f16_si4", x, scale, zero, True)
+
+
+def sum_i4(x, is_signed=True):
+    """int32 [rows, 1] sum of each packed row's nibbles (bindings.cpp:437-451)."""
+    _check("sum_i4", [(x, "x")], [torch.uint8])
+    if x.dim() != 2:
+        raise RuntimeError("sum_i4 expects a 2D tensor of shape [rows, packed_cols]")
+    rows, pc = x.shape
+    out = torch.empty((rows, 1), dtype=torch.int32, device=x.device)
+    _call("srq_sum_i4", _ptr(x), rows, pc, 1 if is_signed else 0, _ptr(out), _stream(x))
+    return out
+
+
+def matmul_colrow_i8_i32(a_col, b_row):
+    """out int32 [N, C] = a_col int8 [N, 1] x b_row int32 [1, C]
+    (bindings.cpp:453-477)."""
+    _check("matmul_colrow_i8_i32", [(a_col, "a_col"), (b_row, "b_row")],
+           [torch.int8, torch.int32])
+    if a_col.dim() != 2 or a_col.shape[1] != 1:
+        raise RuntimeError("a_col must be 2D with shape [N, 1]")
+    if b_row.dim() != 2 or b_row.shape[0] != 1:
+        raise RuntimeError("b_row must be 2D with shape [1, C]")
+    rows, cols = a_col.shape[0], b_row.shape[1]
+    out = torch.empty((rows, cols), dtype=torch.int32, device=a_col.device)
+    _call("srq_matmul_colrow_i8_i32", _ptr(a_col), _ptr(b_row), rows, cols, _ptr(out),
+          _stream(a_col))
+    return out
 
 
 def kv_quant_pack(x):
@@ -476,8 +584,8 @@ def matmul_grouped(problem_sizes, ptr_A, ptr_B, ptr_C, lda, ldb, ldc, signed_a=T
     descriptors in device memory (bindings.cpp:49-91): problem_sizes int32
     [P, 3] rows (m, n, k); ptr_* int64 [P] device addresses; ld* int64 [P]
     row strides (codes for A/B, int32 elements for C).  Writes through ptr_C;
-    returns None.  signed_a=False (unsigned asymmetric A) is not part of this
-    build's W4A4 path."""
+    returns None.  signed_a=False: A holds unsigned (asymmetric) codes, as
+    matmul_ui4_si4."""
     name = "matmul_grouped"
     _check(name, [(problem_sizes, "problem_sizes"), (ptr_A, "ptr_A"), (ptr_B, "ptr_B"),
                   (ptr_C, "ptr_C"), (lda, "lda"), (ldb, "ldb"), (ldc, "ldc")])
@@ -551,10 +659,24 @@ def swiglu_had_sign_quant_moe(gate, up, hadK, K, sign, expert_ids, clip_ratio=1.
 
 
 def asym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio=1.0):
-    """The asymmetric activation path (bindings.cpp:134-159) is not part of
-    this build's W4A4 path."""
-    raise RuntimeError("asym_quant_dynamic_moe: asymmetric activations are not part of this "
-                       "build's W4A4 path")
+    """asym_quant_dynamic of expert-sorted rows with the per-expert sign fused
+    (bindings.cpp:134-159).  Returns (q u8 [rows, ceil(cols/2)] uint4 codes,
+    scale f16 [rows, 1], zero f16 [rows, 1])."""
+    name = "asym_quant_dynamic_moe"
+    _check(name, [(x, "x"), (expert_ids, "expert_ids")])
+    if x.dim() != 2 or x.dtype != torch.float16:
+        raise RuntimeError("asym_quant_dynamic_moe expects a 2D fp16 [rows, cols] tensor")
+    if expert_ids.dtype != torch.int32 or expert_ids.numel() != x.shape[0]:
+        raise RuntimeError("expert_ids must be int32 with one entry per row")
+    rows, cols = x.shape
+    sign = _moe_sign(name, sign, cols)
+    E = sign.shape[0] if sign is not None else 0
+    q = torch.empty((rows, (cols + 1) // 2), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((rows, 1), dtype=torch.float16, device=x.device)
+    zero = torch.empty((rows, 1), dtype=torch.float16, device=x.device)
+    _call("srq_asym_quant_dynamic_moe", _ptr(x), _ptr(sign), _ptr(expert_ids), E, rows, cols,
+          float(clip_ratio), _ptr(q), _ptr(scale), _ptr(zero), _stream(x))
+    return q, scale, zero
 
 
 def sym_dequant_moe(q, scale_row, w_scales, expert_ids, zero_row=None, w_sum=None):
@@ -607,4 +729,30 @@ def w4a4_linear_moe(A, a_scale, B, b_scale, expert_offsets):
     out = torch.empty((R, N), dtype=torch.float16, device=A.device)
     _call("srq_w4a4_linear_moe", _ptr(A), _ptr(a_scale), _ptr(B), _ptr(b_scale),
           _ptr(expert_offsets), E, R, N, K, _ptr(out), _stream(A))
+    return out
+
+
+def w4a4_linear_moe_asym(A, a_scale, a_zero, B, b_scale, b_sum, expert_offsets):
+    """w4a4_linear_moe for asymmetric (uint4) activation codes: the int32
+    product minus a_zero[row] * b_sum[e, col] before the dequant; a_zero int8
+    [R], b_sum int32 [E, N].  Bit-identical to matmul_grouped(signed_a=False)
+    + sym_dequant_moe(zero_row, w_sum)."""
+    name = "w4a4_linear_moe_asym"
+    _check(name, [(A, "A"), (a_scale, "a_scale"), (a_zero, "a_zero"), (B, "B"),
+                  (b_scale, "b_scale"), (b_sum, "b_sum"), (expert_offsets, "expert_offsets")],
+           [torch.uint8, torch.float16, torch.int8, torch.uint8, torch.float16, torch.int32,
+            torch.int32])
+    if A.dim() != 2 or B.dim() != 3 or B.shape[2] != A.shape[1]:
+        raise RuntimeError(f"{name}: expected A [R, K/2] and B [E, N, K/2], got "
+                           f"{tuple(A.shape)} and {tuple(B.shape)}")
+    R, E, N, K = A.shape[0], B.shape[0], B.shape[1], A.shape[1] * 2
+    if a_scale.numel() != R or a_zero.numel() != R or tuple(b_scale.shape) != (E, N):
+        raise RuntimeError(f"{name}: a_scale / a_zero must have R entries, b_scale be [E, N]")
+    if tuple(b_sum.shape) != (E, N):
+        raise RuntimeError(f"{name}: b_sum must be [E, N]")
+    if expert_offsets.numel() != E + 1:
+        raise RuntimeError(f"{name}: expert_offsets must have num_experts + 1 entries")
+    out = torch.empty((R, N), dtype=torch.float16, device=A.device)
+    _call("srq_w4a4_linear_moe_asym", _ptr(A), _ptr(a_scale), _ptr(a_zero), _ptr(B),
+          _ptr(b_scale), _ptr(b_sum), _ptr(expert_offsets), E, R, N, K, _ptr(out), _stream(A))
     return out

@@ -23,6 +23,14 @@ SIGNATURES = {
     "srq_matmul_s4s4": [_p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_residual": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
+    "srq_matmul_u4s4": [_p, _p, _i64, _i64, _i64, _p, _p],
+    "srq_w4a4_linear_asym": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
+    "srq_w4a4_linear_moe_asym": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
+    "srq_asym_quant_dynamic": [_p, _i64, _i64, _f32, _p, _p, _p, _p],
+    "srq_asym_quant_dynamic_moe": [_p, _p, _p, _i64, _i64, _i64, _f32, _p, _p, _p, _p],
+    "srq_asym_quant": [_p, _p, _p, _i64, _i64, _i32, _p, _p],
+    "srq_sum_i4": [_p, _i64, _i64, _i32, _p, _p],
+    "srq_matmul_colrow_i8_i32": [_p, _p, _i64, _i64, _p, _p],
     "srq_swiglu_had_sign_quant_moe": [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _f32,
                                       _p, _p, _p],
     "srq_hadamard_transform": [_p, _p, _i64, _i64, _f32, _i32, _p],

@@ -183,6 +183,41 @@ SRQ_DEV int kv_code(float x, float zero, float scale) {
     return kv_code_r(x, zero, sym_recip(scale));
 }
 
+// __half2int_rn of an fp16 value held in fp32: round half to even, NaN -> 0,
+// values beyond the int32 range (±inf) saturate.
+SRQ_DEV int h2i_rn(float v) {
+    if (v != v) return 0;
+    if (v >= 2147483648.f) return 0x7fffffff;
+    if (v <= -2147483648.f) return (int)0x80000000;
+    return (int)__builtin_rintf(v);
+}
+
+// Per-row parameters of the asymmetric activation quantizer
+// (signrot/kernels/fused.cu:166-179) from the row's exact fp32 min and max:
+// hmin, hmax in fp16 (each times clip, rounded, when clip != 1);
+// diff = fp16(hmax - hmin); scale = fp16(diff / 15);
+// ratio = fp16(-hmin / scale); zero = fp16(round_half_even(ratio)).
+SRQ_DEV void asym_row_params(float vmin, float vmax, float clip, f16 &scale, f16 &zero) {
+    f16 hmin = f16_rn(vmin), hmax = f16_rn(vmax);
+    if (clip != 1.f) {
+        hmin = f16_rn((float)hmin * clip);
+        hmax = f16_rn((float)hmax * clip);
+    }
+    const f16 diff = f16_rn((float)hmax - (float)hmin);
+    scale = f16_rn((float)diff / 15.f);
+    const f16 ratio = f16_rn(-(float)hmin / (float)scale);
+    zero = f16_rn(__builtin_rintf((float)ratio));
+}
+
+// Asymmetric code: clamp(__half2int_rn(fp16(x / s)) + zero_i, lo, hi), the
+// quotient correctly rounded (fp32 division, then one fp16 rounding) and the
+// int addition wrapping in int32 as the reference's does.
+SRQ_DEV int asym_code(float x, float s, int zero_i, int lo, int hi) {
+    const float quot = round16(x / s);
+    const int c = (int)((u32)h2i_rn(quot) + (u32)zero_i);
+    return c < lo ? lo : (c > hi ? hi : c);
+}
+
 // Eight symmetric codes packed into one 32-bit word, element i in bits
 // 4i .. 4i + 3 (the reference's nibble order).
 SRQ_DEV u32 pack8_sym(const v8h &v, float s) {

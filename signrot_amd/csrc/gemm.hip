@@ -40,6 +40,26 @@ SRQ_DEV v4i unpack8(u32 w0, u32 w1) {
     return r;
 }
 
+// Unsigned A (matmul_ui4_si4): the nibbles u (0..15) stay in the low half of
+// each byte, a non-negative int8, in the same element order as unpack8; with
+// B unpacked as 16 w the MFMA accumulates 16 * sum(u * w) exactly
+// (|.| <= 1920 K < 2^31) and the epilogue shifts right by 4.
+SRQ_DEV v4i unpack8u(u32 w0, u32 w1) {
+    v4i r;
+    r[0] = (int)(w0 & 0x0F0F0F0Fu);
+    r[1] = (int)((w0 >> 4) & 0x0F0F0F0Fu);
+    r[2] = (int)(w1 & 0x0F0F0F0Fu);
+    r[3] = (int)((w1 >> 4) & 0x0F0F0F0Fu);
+    return r;
+}
+
+// A-operand unpack: signed (UA = false) or unsigned (UA = true) nibbles
+template <bool UA>
+SRQ_DEV v4i unpack8a(u32 w0, u32 w1) {
+    if constexpr (UA) return unpack8u(w0, w1);
+    else return unpack8(w0, w1);
+}
+
 SRQ_DEV v4i mfma16(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
@@ -63,10 +83,22 @@ struct Epi {
     const f16 *sb;     // [N]
     const f16 *bias;   // [N] or null
     const f16 *res;    // [M, N] residual added last (may alias out) or null
+    int ua;            // A holds unsigned nibbles (accumulator = 16 sum, not 256 sum)
+    const int8_t *zr;  // asymmetric activations: zero point per row [M] (with ws) or null
+    const int32_t *ws; // sum of each weight row's codes [N]
 };
 
+// The int32 product of output (m, n) from the MFMA accumulator: sum(a * w),
+// minus zr[m] * ws[n] (int32 arithmetic, wrapping, as the reference's
+// matmul_colrow_i8_i32 and `x -= zeros` do) when zero points are given.
+SRQ_DEV int epi_val(const Epi &e, int acc, int64_t m, int64_t n) {
+    int v = acc >> (e.ua ? 4 : 8);
+    if (e.zr) v = (int)((u32)v - (u32)(int)e.zr[m] * (u32)e.ws[n]);
+    return v;
+}
+
 SRQ_DEV void store_one(const Epi &e, int64_t N, int64_t m, int64_t n, int acc256) {
-    const int v = acc256 >> 8;
+    const int v = epi_val(e, acc256, m, n);
     if (e.C) {
         e.C[m * N + n] = v;
     } else {
@@ -101,7 +133,7 @@ SRQ_DEV void store_block(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 if (gnv[j] >= N) continue;
-                const int v = acc[i][j][r] >> 8;
+                const int v = epi_val(e, acc[i][j][r], gm, gnv[j]);
                 if (e.C) {
                     e.C[gm * N + gnv[j]] = v;
                 } else {
@@ -126,7 +158,7 @@ constexpr int kBK = 256;             // int4 elements per step
 constexpr int kBKB = kBK / 2;        // bytes per row per step
 constexpr int kLdsRow = kBKB + 16;   // padded LDS row stride (bytes)
 
-template <int BM, int BN>
+template <int BM, int BN, bool UA>
 __global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t *__restrict__ A,
                                                         const uint8_t *__restrict__ B,
                                                         int64_t M, int64_t N, int64_t K,
@@ -219,7 +251,7 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t *__restric
             if (kk + 1 < kBKB / 32) fetch(kk + 1, (kk + 1) & 1);
             v4i fa[FM], fb[FN];
 #pragma unroll
-            for (int i = 0; i < FM; ++i) fa[i] = unpack8(wa[kk & 1][i].x, wa[kk & 1][i].y);
+            for (int i = 0; i < FM; ++i) fa[i] = unpack8a<UA>(wa[kk & 1][i].x, wa[kk & 1][i].y);
 #pragma unroll
             for (int j = 0; j < FN; ++j) fb[j] = unpack8(wb[kk & 1][j].x, wb[kk & 1][j].y);
 #pragma unroll
@@ -290,7 +322,7 @@ SRQ_DEV void store_block32(const Epi &e, int64_t M, int64_t N, int64_t mb, int64
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
                 if (gnv[j] >= N) continue;
-                const int val = acc[i][j][v] >> 8;
+                const int val = epi_val(e, acc[i][j][v], gm, gnv[j]);
                 if (e.C) {
                     e.C[gm * N + gnv[j]] = val;
                 } else {
@@ -305,7 +337,7 @@ SRQ_DEV void store_block32(const Epi &e, int64_t M, int64_t N, int64_t mb, int64
 }
 
 // One K step of a compute wave: the stage holds BM A rows then the B rows.
-template <int FM, int FN, int KBB, int BM = kBigBM>
+template <int FM, int FN, int KBB, int BM = kBigBM, bool UA = false>
 SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {
     constexpr int NPP = KBB / 32;  // 16-byte fragment fetches per step
     const int rr = lane & 31;
@@ -333,7 +365,7 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
         const int pp = sl >> 1, h = sl & 1;
 #pragma unroll
         for (int i = 0; i < FM; ++i)
-            ua[buf][i] = unpack8((u32)fa[pp & 1][i][2 * h], (u32)fa[pp & 1][i][2 * h + 1]);
+            ua[buf][i] = unpack8a<UA>((u32)fa[pp & 1][i][2 * h], (u32)fa[pp & 1][i][2 * h + 1]);
 #pragma unroll
         for (int jn = 0; jn < FN; ++jn)
             ub[buf][jn] = unpack8((u32)fb[pp & 1][jn][2 * h], (u32)fb[pp & 1][jn][2 * h + 1]);
@@ -367,7 +399,7 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
 // WGM x WGN compute waves, each FM x FN blocks of 32 x 32 (a (32 FM) x
 // (32 FN) wave tile), plus NPROD producer waves; the block tile is always
 // kBigBM x kBigBN.
-template <int NPROD, int WGM, int WGN, int FM, int FN, int KBB, int NSTG>
+template <int NPROD, int WGM, int WGN, int FM, int FN, int KBB, int NSTG, bool UA>
 __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
     const uint8_t *__restrict__ A, const uint8_t *__restrict__ B, int64_t M, int64_t N,
     int64_t K, Epi e) {
@@ -477,7 +509,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
         // step s has landed; every wave is done with step s - 1
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        big_compute<FM, FN, KBB>(smem + sl * kStage, wm, wn, lane, acc);
+        big_compute<FM, FN, KBB, kBigBM, UA>(smem + sl * kStage, wm, wn, lane, acc);
         sl = sl == 2 ? 0 : sl + 1;
     }
 
@@ -506,7 +538,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
 constexpr int kSqBM = 256, kSqBN = 256;
 constexpr int kSqRows = kSqBM + kSqBN;
 
-template <int KBB, int NSTG>
+template <int KBB, int NSTG, bool UA>
 __global__ __launch_bounds__(512, 1) void gemm_sq_kernel(const uint8_t *__restrict__ A,
                                                         const uint8_t *__restrict__ B,
                                                         int64_t M, int64_t N, int64_t K, Epi e) {
@@ -592,7 +624,7 @@ __global__ __launch_bounds__(512, 1) void gemm_sq_kernel(const uint8_t *__restri
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         if (s + NSTG - 1 < steps) issue(s + NSTG - 1);
-        big_compute<FM, FN, KBB, kSqBM>(smem + (s % NSTG) * kStage, wm, wn, lane, acc);
+        big_compute<FM, FN, KBB, kSqBM, UA>(smem + (s % NSTG) * kStage, wm, wn, lane, acc);
     }
     store_block32<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane);
 }
@@ -605,7 +637,7 @@ __global__ __launch_bounds__(512, 1) void gemm_sq_kernel(const uint8_t *__restri
 // exactly one wave), U steps in flight; the slices' int32 partials are
 // summed through LDS (exact).
 
-template <int MB, int KW, int U>
+template <int MB, int KW, int U, bool UA>
 __global__ __launch_bounds__(KW * 64) void gemm_skinny_kernel(const uint8_t *__restrict__ A,
                                                              const uint8_t *__restrict__ B,
                                                              int64_t M, int64_t N, int64_t K,
@@ -645,8 +677,8 @@ __global__ __launch_bounds__(KW * 64) void gemm_skinny_kernel(const uint8_t *__r
             const v4i b1 = unpack8((u32)wb[u][2], (u32)wb[u][3]);
 #pragma unroll
             for (int i = 0; i < MB; ++i) {
-                const v4i a0 = unpack8((u32)wa[u][i][0], (u32)wa[u][i][1]);
-                const v4i a1 = unpack8((u32)wa[u][i][2], (u32)wa[u][i][3]);
+                const v4i a0 = unpack8a<UA>((u32)wa[u][i][0], (u32)wa[u][i][1]);
+                const v4i a1 = unpack8a<UA>((u32)wa[u][i][2], (u32)wa[u][i][3]);
                 acc[i] = mfma16(a0, b0, acc[i]);
                 acc[i] = mfma16(a1, b1, acc[i]);
             }
@@ -698,7 +730,7 @@ constexpr int kStreamKW = 8;
 constexpr int kStreamS = 4;
 constexpr int kStreamMaxCb = 16;   // column blocks per workgroup
 
-template <int MB, int NSUB, bool AUNP>
+template <int MB, int NSUB, bool AUNP, bool UA>
 __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
     const uint8_t *__restrict__ A, const uint8_t *__restrict__ B, int64_t M, int64_t N,
     int64_t K, Epi e) {
@@ -776,8 +808,8 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
             for (int i = 0; i < MB; ++i)
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    aun[s][i][t][0] = unpack8((u32)areg[s][i][t][0], (u32)areg[s][i][t][1]);
-                    aun[s][i][t][1] = unpack8((u32)areg[s][i][t][2], (u32)areg[s][i][t][3]);
+                    aun[s][i][t][0] = unpack8a<UA>((u32)areg[s][i][t][0], (u32)areg[s][i][t][1]);
+                    aun[s][i][t][1] = unpack8a<UA>((u32)areg[s][i][t][2], (u32)areg[s][i][t][3]);
                 }
     }
     __syncthreads();
@@ -836,8 +868,8 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
                     } else {
                         v4i w = areg[s][i][t];
                         asm volatile("" : "+v"(w));  // unpack per use, not hoisted out of j
-                        a0 = unpack8((u32)w[0], (u32)w[1]);
-                        a1 = unpack8((u32)w[2], (u32)w[3]);
+                        a0 = unpack8a<UA>((u32)w[0], (u32)w[1]);
+                        a1 = unpack8a<UA>((u32)w[2], (u32)w[3]);
                     }
                     acc[i] = mfma16(a0, b0, acc[i]);
                     acc[i] = mfma16(a1, b1, acc[i]);
@@ -865,9 +897,10 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
                 for (int r = 0; r < 4; ++r) {
                     const int m = i * 16 + 4 * (lane >> 4) + r;
                     const int idx = i * 256 + (4 * (lane >> 4) + r) * 16 + rr;
-                    const int v = sm[idx] >> 8;
+                    const int raw = sm[idx];
                     sm[idx] = 0;
                     if (m < M && gn < N) {
+                        const int v = epi_val(e, raw, m, gn);
                         if (e.C) {
                             e.C[m * N + gn] = v;
                         } else {
@@ -884,6 +917,7 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
 
 // Launch the stream kernel if the shape fits its register and LDS budget;
 // returns false otherwise.
+template <bool UA>
 bool launch_stream(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64_t K,
                    const Epi &e, hipStream_t st) {
     if (M > 32) return false;
@@ -894,7 +928,7 @@ bool launch_stream(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int
     if (cb_per > kStreamMaxCb) return false;
     const dim3 grid((unsigned)((ncb + cb_per - 1) / cb_per)), block(kStreamKW * 64);
 #define SRQ_STREAM(MB, NSUB, AUNP) \
-    gemm_stream_kernel<MB, NSUB, AUNP><<<grid, block, 0, st>>>(a, b, M, N, K, e)
+    gemm_stream_kernel<MB, NSUB, AUNP, UA><<<grid, block, 0, st>>>(a, b, M, N, K, e)
     if (M <= 16) {
         if (per <= 2) SRQ_STREAM(1, 2, true);
         else if (per <= 4) SRQ_STREAM(1, 4, true);
@@ -942,6 +976,10 @@ struct GroupedArgs {
     int64_t N, K;
     const f16 *sa, *sb;
     f16 *out;
+    // asymmetric activations (expert-offset form, unsigned A): zero point per
+    // row [R] and per-expert weight row sums [P, N]
+    const int8_t *zr;
+    const int32_t *ws;
 };
 
 struct GroupedProb {
@@ -987,7 +1025,7 @@ SRQ_DEV int64_t grouped_tiles(const GroupedProb &r) {
     return ((r.m + kGrpBM - 1) / kGrpBM) * ((r.n + kGrpBN - 1) / kGrpBN);
 }
 
-template <int NPROD>
+template <int NPROD, bool UA>
 __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(GroupedArgs g) {
     constexpr int WGN = 2, FM = 2, FN = 2, KBB = 128, NSTG = 3;
     constexpr int kCompute = 4;
@@ -1080,7 +1118,7 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
         for (int s = 0; s < steps; ++s) {
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            big_compute<FM, FN, KBB, kGrpBM>(smem + sl * kStage, wm, wn, lane, acc);
+            big_compute<FM, FN, KBB, kGrpBM, UA>(smem + sl * kStage, wm, wn, lane, acc);
             sl = sl == 2 ? 0 : sl + 1;
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1107,7 +1145,10 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
 #pragma unroll
                 for (int j = 0; j < FN; ++j) {
                     if (gnv[j] >= pr.n) continue;
-                    const int val = acc[i][j][v] >> 8;
+                    int val = acc[i][j][v] >> (UA ? 4 : 8);
+                    if (g.zr)  // the sym_dequant_moe zero correction, int32 wrapping
+                        val = (int)((u32)val - (u32)(int)g.zr[pr.row0 + gm] *
+                                                   (u32)g.ws[(int64_t)p * g.N + gnv[j]]);
                     if (g.out) {
                         const float a = (float)val * sa;
                         g.out[(pr.row0 + gm) * g.N + gnv[j]] = f16_rn(a * sbv[j]);
@@ -1147,33 +1188,32 @@ __global__ void fill_zero_epilogue(int64_t M, int64_t N, Epi e) {
         store_one(e, N, i / N, i % N, 0);
 }
 
-int run_gemm(const char *name, const void *A, const void *B, int64_t M, int64_t N, int64_t K,
-             const Epi &e, hipStream_t st) {
-    if (M == 0 || N == 0) return SRQ_OK;
-    const uint8_t *a = (const uint8_t *)A;
-    const uint8_t *b = (const uint8_t *)B;
+// Kernel choice by shape; UA: A holds unsigned nibbles (Epi::ua).
+template <bool UA>
+void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64_t K,
+                 const Epi &e, hipStream_t st) {
     if (K == 0) {
         const int64_t blocks = std::min<int64_t>(srq_cdiv(M * N, 256), 4096);
         fill_zero_epilogue<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(M, N, e);
-    } else if (launch_stream(a, b, M, N, K, e, st)) {
+    } else if (launch_stream<UA>(a, b, M, N, K, e, st)) {
         // M <= 32: persistent weight-streaming kernel
     } else if (M <= 16) {
-        gemm_skinny_kernel<1, 8, 4><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
+        gemm_skinny_kernel<1, 8, 4, UA><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
     } else if (M <= 32) {
-        gemm_skinny_kernel<2, 8, 4><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
+        gemm_skinny_kernel<2, 8, 4, UA><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
     } else if (M <= 64) {
-        gemm_skinny_kernel<4, 8, 2><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
+        gemm_skinny_kernel<4, 8, 2, UA><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
     } else if (M >= 1024 && srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN) >= 256) {
         // enough 256 x 256 tiles to cover the 256 CUs
         const int64_t tiles = srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN);
-        gemm_sq_kernel<128, 2><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(a, b, M, N, K, e);
+        gemm_sq_kernel<128, 2, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(a, b, M, N, K, e);
     } else if (M >= 1024) {
         const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
         // 4 compute waves (128 x 64 each) + 4 producer waves
-        gemm_big_kernel<4, 2, 2, 4, 2, 128, 3><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(
+        gemm_big_kernel<4, 2, 2, 4, 2, 128, 3, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
     } else {
         // mid-size M: the tile shrinks with M so the grid still covers the
@@ -1181,13 +1221,22 @@ int run_gemm(const char *name, const void *A, const void *B, int64_t M, int64_t 
         auto tile = [&](auto bm, auto bn) {
             constexpr int BM = decltype(bm)::value, BN = decltype(bn)::value;
             const int64_t tiles = srq_cdiv(M, BM) * srq_cdiv(N, BN);
-            gemm_tile_kernel<BM, BN><<<dim3((unsigned)tiles), dim3(256), 0, st>>>(a, b, M, N, K, e);
+            gemm_tile_kernel<BM, BN, UA><<<dim3((unsigned)tiles), dim3(256), 0, st>>>(a, b, M, N, K, e);
         };
         if (M <= 128) tile(std::integral_constant<int, 64>{}, std::integral_constant<int, 32>{});
         else if (M <= 256) tile(std::integral_constant<int, 64>{}, std::integral_constant<int, 64>{});
         else if (M <= 512) tile(std::integral_constant<int, 128>{}, std::integral_constant<int, 64>{});
         else tile(std::integral_constant<int, 128>{}, std::integral_constant<int, 128>{});
     }
+}
+
+int run_gemm(const char *name, const void *A, const void *B, int64_t M, int64_t N, int64_t K,
+             const Epi &e, hipStream_t st) {
+    if (M == 0 || N == 0) return SRQ_OK;
+    const uint8_t *a = (const uint8_t *)A;
+    const uint8_t *b = (const uint8_t *)B;
+    if (e.ua) launch_gemm<true>(a, b, M, N, K, e, st);
+    else launch_gemm<false>(a, b, M, N, K, e, st);
     SRQ_LAUNCH_CHECK(name);
     return SRQ_OK;
 }
@@ -1202,6 +1251,37 @@ extern "C" int srq_matmul_s4s4(const void *A, const void *B, int64_t M, int64_t 
     Epi e{};
     e.C = C;
     return run_gemm("matmul", A, B, M, N, K, e, (hipStream_t)stream);
+}
+
+extern "C" int srq_matmul_u4s4(const void *A, const void *B, int64_t M, int64_t N, int64_t K,
+                               int32_t *C, void *stream) {
+    int rc = check_gemm("matmul_ui4_si4", A, B, M, N, K);
+    if (rc) return rc;
+    SRQ_CHECK_ARG(C || M == 0 || N == 0, "matmul_ui4_si4: null output");
+    Epi e{};
+    e.C = C;
+    e.ua = 1;
+    return run_gemm("matmul_ui4_si4", A, B, M, N, K, e, (hipStream_t)stream);
+}
+
+extern "C" int srq_w4a4_linear_asym(const void *A, const void *a_scale, const int8_t *a_zero,
+                                    const void *B, const void *b_scale, const int32_t *b_sum,
+                                    const void *bias, int64_t M, int64_t N, int64_t K,
+                                    void *out, void *stream) {
+    int rc = check_gemm("w4a4_linear_asym", A, B, M, N, K);
+    if (rc) return rc;
+    if (M && N)
+        SRQ_CHECK_ARG(out && a_scale && a_zero && b_scale && b_sum,
+                      "w4a4_linear_asym: null pointer");
+    Epi e{};
+    e.out = (f16 *)out;
+    e.sa = (const f16 *)a_scale;
+    e.sb = (const f16 *)b_scale;
+    e.bias = (const f16 *)bias;
+    e.ua = 1;
+    e.zr = a_zero;
+    e.ws = b_sum;
+    return run_gemm("w4a4_linear_asym", A, B, M, N, K, e, (hipStream_t)stream);
 }
 
 extern "C" int srq_w4a4_linear(const void *A, const void *a_scale, const void *B,
@@ -1246,11 +1326,6 @@ extern "C" int srq_matmul_grouped(const int32_t *problem_sizes, const int64_t *p
     SRQ_CHECK_ARG(problem_count >= 0 && problem_count <= 0x7fffffffLL,
                   "matmul_grouped: bad problem_count");
     if (problem_count == 0) return SRQ_OK;
-    if (!signed_a) {
-        srq_set_error("matmul_grouped: unsigned (asymmetric) A operands are not part of this "
-                      "build's W4A4 path");
-        return SRQ_EUNSUPPORTED;
-    }
     SRQ_CHECK_ARG(problem_sizes && ptr_A && ptr_B && ptr_C && lda && ldb && ldc,
                   "matmul_grouped: null pointer");
     GroupedArgs g{};
@@ -1262,7 +1337,10 @@ extern "C" int srq_matmul_grouped(const int32_t *problem_sizes, const int64_t *p
     g.lda = lda;
     g.ldb = ldb;
     g.ldc = ldc;
-    gemm_grouped_kernel<4><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
+    if (signed_a)
+        gemm_grouped_kernel<4, false><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
+    else
+        gemm_grouped_kernel<4, true><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
     SRQ_LAUNCH_CHECK("matmul_grouped");
     return SRQ_OK;
 }
@@ -1294,7 +1372,42 @@ extern "C" int srq_w4a4_linear_moe(const void *A, const void *a_scale, const voi
     g.sa = (const f16 *)a_scale;
     g.sb = (const f16 *)b_scale;
     g.out = (f16 *)out;
-    gemm_grouped_kernel<4><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
+    gemm_grouped_kernel<4, false><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
     SRQ_LAUNCH_CHECK("w4a4_linear_moe");
+    return SRQ_OK;
+}
+
+extern "C" int srq_w4a4_linear_moe_asym(const void *A, const void *a_scale, const int8_t *a_zero,
+                                        const void *B, const void *b_scale, const int32_t *b_sum,
+                                        const int32_t *expert_offsets, int64_t num_experts,
+                                        int64_t rows, int64_t N, int64_t K, void *out,
+                                        void *stream) {
+    SRQ_CHECK_ARG(num_experts >= 0 && num_experts <= 0x7fffffffLL && rows >= 0 && N >= 0 &&
+                      K >= 0, "w4a4_linear_moe_asym: bad shape");
+    SRQ_CHECK_ARG(K % 32 == 0 && K <= 131072, "w4a4_linear_moe_asym: K=%lld must be a multiple of "
+                  "32 and <= 131072", (long long)K);
+    if (num_experts == 0 || rows == 0 || N == 0) return SRQ_OK;
+    if (rows * (K / 2) >= 0xFFFFFFF0LL || N * (K / 2) >= 0xFFFFFFF0LL) {
+        srq_set_error("w4a4_linear_moe_asym: operand larger than 4 GiB");
+        return SRQ_EUNSUPPORTED;
+    }
+    SRQ_CHECK_ARG(A && a_scale && a_zero && B && b_scale && b_sum && expert_offsets && out,
+                  "w4a4_linear_moe_asym: null pointer");
+    SRQ_CHECK_ARG(srq_aligned(A, 16) && srq_aligned(B, 16),
+                  "w4a4_linear_moe_asym: A and B must be 16-byte aligned");
+    GroupedArgs g{};
+    g.P = (int)num_experts;
+    g.offsets = expert_offsets;
+    g.A = (const uint8_t *)A;
+    g.B = (const uint8_t *)B;
+    g.N = N;
+    g.K = K;
+    g.sa = (const f16 *)a_scale;
+    g.sb = (const f16 *)b_scale;
+    g.out = (f16 *)out;
+    g.zr = a_zero;
+    g.ws = b_sum;
+    gemm_grouped_kernel<4, true><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
+    SRQ_LAUNCH_CHECK("w4a4_linear_moe_asym");
     return SRQ_OK;
 }

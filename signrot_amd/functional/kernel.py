@@ -21,6 +21,14 @@ __all__ = [
     "asym_quant_dynamic_moe",
     "sym_dequant_moe",
     "w4a4_linear_moe",
+    "matmul_ui4_si4",
+    "asym_quant_dynamic",
+    "asym_quant_f16_si4",
+    "asym_quant_f16_ui4",
+    "sum_i4",
+    "matmul_colrow_i8_i32",
+    "w4a4_linear_asym",
+    "w4a4_linear_moe_asym",
     "PackedQuantizedTensor",
 ]
 
@@ -89,6 +97,77 @@ def w4a4_linear(A, a_scale, B, b_scale, bias=None):
     out = _CUDA.w4a4_linear(A, a_scale.reshape(-1), B, b_scale.reshape(-1),
                             None if bias is None else bias.reshape(-1))
     return out.view(*A_shape_excl_last, B.shape[0])
+
+
+def matmul_ui4_si4(A, B):
+    """uint4 x int4 -> int32 over the last dim (kernel.py:75-81)."""
+    assert A.shape[-1] % 32 == 0, "A.shape[-1]: {} must be multiplication of 32".format(
+        A.shape[-1])
+    A, A_shape_excl_last = flatten_last_dim_and_return_shape(A)
+    B, B_shape_excl_last = flatten_last_dim_and_return_shape(B)
+    return _CUDA.matmul_ui4_si4(A, B).view(*A_shape_excl_last, *B_shape_excl_last)
+
+
+def w4a4_linear_asym(A, a_scale, a_zero, B, b_scale, b_sum, bias=None):
+    """Fused matmul_ui4_si4 - zeros ⊗ weight_sum + sym_dequant (+ bias):
+    fp16 [..., N] (the zeros_x branch of Linear4bit.forward in one launch)."""
+    A, A_shape_excl_last = flatten_last_dim_and_return_shape(A)
+    out = _CUDA.w4a4_linear_asym(A, a_scale.reshape(-1), a_zero.reshape(-1), B,
+                                 b_scale.reshape(-1), b_sum.reshape(-1),
+                                 None if bias is None else bias.reshape(-1))
+    return out.view(*A_shape_excl_last, B.shape[0])
+
+
+def asym_quant_dynamic(x, clip_ratio=1.0):
+    """Fused per-row amin/amax + scale/zero + asymmetric uint4 quantize/pack
+    (kernel.py:113-120): (q, scale, zero), scale and zero shaped
+    (*x.shape[:-1], 1)."""
+    assert x.dtype == torch.float16
+    x, shape_excl_last = flatten_last_dim_and_return_shape(x.contiguous())
+    q, scale, zero = _CUDA.asym_quant_dynamic(x, clip_ratio)
+    return (q.view(*shape_excl_last, -1), scale.view(*shape_excl_last, 1),
+            zero.view(*shape_excl_last, 1))
+
+
+def asym_quant_f16_si4(q, scale, zero):
+    """(kernel.py:188-194)"""
+    assert q.dtype == torch.float16
+    assert scale.dtype == zero.dtype == torch.float16
+    q, q_shape_excl_last = flatten_last_dim_and_return_shape(q)
+    return _CUDA.asym_quant_f16_si4(q, scale.reshape(-1), zero.reshape(-1)).view(
+        *q_shape_excl_last, -1)
+
+
+def asym_quant_f16_ui4(q, scale, zero):
+    """(kernel.py:197-203)"""
+    assert q.dtype == torch.float16
+    assert scale.dtype == zero.dtype == torch.float16
+    q, q_shape_excl_last = flatten_last_dim_and_return_shape(q)
+    return _CUDA.asym_quant_f16_ui4(q, scale.reshape(-1), zero.reshape(-1)).view(
+        *q_shape_excl_last, -1)
+
+
+def sum_i4(x, is_signed=True, dtype=torch.int32):
+    """(kernel.py:206-212)"""
+    assert x.dtype == torch.uint8, "packed int4 tensor must be torch.uint8"
+    x, x_shape_excl_last = flatten_last_dim_and_return_shape(x)
+    out = _CUDA.sum_i4(x, is_signed).view(*x_shape_excl_last, 1)
+    if dtype is not None and out.dtype != dtype:
+        out = out.to(dtype=dtype)
+    return out
+
+
+def matmul_colrow_i8_i32(a_col, b_row):
+    """(kernel.py:215-227)"""
+    assert a_col.dtype == torch.int8, "a_col must be torch.int8"
+    assert b_row.dtype == torch.int32, "b_row must be torch.int32"
+    a_col, a_shape_excl_last = flatten_last_dim_and_return_shape(a_col)
+    assert a_col.shape[1] == 1, "a_col must have last dimension == 1"
+    if b_row.dim() == 1:
+        b_row = b_row.view(1, -1)
+    assert b_row.dim() == 2 and b_row.shape[0] == 1, "b_row must have shape [1, C]"
+    out = _CUDA.matmul_colrow_i8_i32(a_col.contiguous(), b_row.contiguous())
+    return out.view(*a_shape_excl_last, b_row.shape[1])
 
 
 def sym_quant(x, scale):
@@ -169,9 +248,10 @@ def sym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio=1.0):
 
 
 def asym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio=1.0):
-    """(kernel.py:131-134) -- the asymmetric activation path is not part of
-    this build; raises RuntimeError."""
-    return _CUDA.asym_quant_dynamic_moe(x, sign, expert_ids, clip_ratio)
+    """asym_quant_dynamic variant of sym_quant_dynamic_moe -> (q, scale,
+    zero) (kernel.py:131-134)."""
+    assert x.dtype == torch.float16
+    return _CUDA.asym_quant_dynamic_moe(x.contiguous(), sign, expert_ids, clip_ratio)
 
 
 def sym_dequant_moe(q, scale_row, w_scales, expert_ids, zero_row=None, w_sum=None):
@@ -187,3 +267,11 @@ def w4a4_linear_moe(A, a_scale, B, b_scale, expert_offsets):
     """Fused grouped int4 GEMM + expert-indexed dequant over expert-sorted
     rows (one launch; bit-identical to matmul_grouped + sym_dequant_moe)."""
     return _CUDA.w4a4_linear_moe(A, a_scale.reshape(-1), B, b_scale, expert_offsets)
+
+
+def w4a4_linear_moe_asym(A, a_scale, a_zero, B, b_scale, b_sum, expert_offsets):
+    """w4a4_linear_moe for asymmetric activation codes (one launch;
+    bit-identical to matmul_grouped(signed_a=False) + sym_dequant_moe with
+    zero_row and w_sum)."""
+    return _CUDA.w4a4_linear_moe_asym(A, a_scale.reshape(-1), a_zero.reshape(-1), B, b_scale,
+                                      b_sum, expert_offsets)

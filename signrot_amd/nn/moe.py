@@ -15,8 +15,10 @@ the fused grouped GEMM + expert-indexed dequant (srq_w4a4_linear_moe); the
 reference runs matmul_grouped then sym_dequant_moe, which is the same
 arithmetic.  `use_grouped=False` is the reference's per-expert loop over the
 dense kernels (host-synced; the equivalence oracle), bit-identical to the
-grouped path.  The asymmetric activation path (asym=True) is not part of
-this build.
+grouped path.  asym=True quantizes activations to uint4 with per-token zero
+points (asym_quant_dynamic / asym_quant_dynamic_moe) and the grouped GEMM
+subtracts zero_row * w_sum before the dequant (srq_w4a4_linear_moe_asym),
+the reference's matmul_grouped(signed_a=False) + sym_dequant_moe arithmetic.
 """
 import torch
 
@@ -31,10 +33,6 @@ class SignRotMoEBlock(torch.nn.Module):
                  sign_down=None, wsum_gate=None, wsum_up=None, wsum_down=None,
                  asym=False, clip_ratio=1.0, fp32_had=False, use_grouped=True):
         super().__init__()
-        if asym:
-            raise NotImplementedError(
-                "SignRotMoEBlock(asym=True): asymmetric activations are not part of this "
-                "build's W4A4 path")
         self.gate = gate  # router linear (16-bit activations), left untouched
         # grouped path: one launch for swiglu + rotation + sign + quantizer
         # of the down-proj input where the rotation has an MFMA form
@@ -69,22 +67,44 @@ class SignRotMoEBlock(torch.nn.Module):
 
     @staticmethod
     def stack_experts(linears, need_wsum=False):
-        """Stack per-expert Linear4bit weights [E, out, in/2] and fp16 scales
-        [E, out] (moe.py:71-78)."""
-        if need_wsum:
-            raise NotImplementedError("int4 row sums belong to the asymmetric path")
+        """Stack per-expert Linear4bit weights [E, out, in/2], fp16 scales
+        [E, out] and, for the asymmetric path, the int4 row sums [E, out]
+        (moe.py:71-78)."""
         w = torch.stack([m.weight for m in linears])
         s = torch.stack([m.weight_scales.view(-1).to(torch.float16) for m in linears])
-        return w.contiguous(), s.contiguous(), None
+        wsum = None
+        if need_wsum:
+            wsum = torch.stack([kernel.sum_i4(m.weight).view(-1) for m in linears])
+        return w.contiguous(), s.contiguous(), wsum
+
+    def _ensure_wsum(self):
+        """Row sums of every expert's weight codes for the zero correction
+        (moe.py:80-86), computed once when the block was built without them."""
+        if not self.asym or self.wsum_gate is not None:
+            return
+        e = self.num_experts
+        self.wsum_gate = kernel.sum_i4(self.w_gate).view(e, -1)
+        self.wsum_up = kernel.sum_i4(self.w_up).view(e, -1)
+        self.wsum_down = kernel.sum_i4(self.w_down).view(e, -1)
+
+    def _quantize(self, x):
+        """(codes, scales, zeros int8 or None) (moe.py:88-93)."""
+        if self.asym:
+            q, s, z = kernel.asym_quant_dynamic(x, self.clip_ratio)
+            return q, s, z.to(torch.int8)
+        q, s = kernel.sym_quant_dynamic(x, self.clip_ratio)
+        return q, s, None
 
     # ------------------------------------------------------------ projections
 
     @staticmethod
-    def _gemm_dequant_grouped(q, s, offsets, w, s_w):
-        return kernel.w4a4_linear_moe(q, s, w, s_w, offsets)
+    def _gemm_dequant_grouped(q, s, z, offsets, w, s_w, wsum):
+        if z is None:
+            return kernel.w4a4_linear_moe(q, s, w, s_w, offsets)
+        return kernel.w4a4_linear_moe_asym(q, s, z, w, s_w, wsum, offsets)
 
     @staticmethod
-    def _gemm_dequant_loop(q, s, counts, w, s_w):
+    def _gemm_dequant_loop(q, s, z, counts, w, s_w, wsum):
         """Per-expert loop over the dense kernels (moe.py:138-159); host-syncs
         on counts."""
         out = torch.empty(q.shape[0], w.shape[1], dtype=torch.float16, device=q.device)
@@ -94,7 +114,11 @@ class SignRotMoEBlock(torch.nn.Module):
                 continue
             rows = slice(row, row + m)
             row += m
-            i32 = kernel.matmul_si4_si4(q[rows], w[e])
+            if z is not None:
+                i32 = kernel.matmul_ui4_si4(q[rows], w[e])
+                i32 -= kernel.matmul_colrow_i8_i32(z[rows], wsum[e].view(1, -1))
+            else:
+                i32 = kernel.matmul_si4_si4(q[rows], w[e])
             out[rows] = kernel.sym_dequant(i32, s[rows], s_w[e].view(-1, 1))
         return out
 
@@ -119,49 +143,62 @@ class SignRotMoEBlock(torch.nn.Module):
         batch_size, seq_len, hidden_dim = hidden_states.shape
         x = hidden_states.view(-1, hidden_dim)
         x_dtype = x.dtype
+        self._ensure_wsum()
         router_logits, routing_weights, perm, counts, flat_e = self.route(x)
         tok = perm // self.top_k
         eid = flat_e[perm].to(torch.int32)
 
         # each token's top-k experts and gate/up projections read the same
         # codes: quantize once per token, then gather rows
-        q_tok, s_tok = kernel.sym_quant_dynamic(x.to(torch.float16), self.clip_ratio)
+        q_tok, s_tok, z_tok = self._quantize(x.to(torch.float16))
         q_a, s_a = q_tok[tok], s_tok[tok]
+        z_a = z_tok[tok] if z_tok is not None else None
 
         if self.use_grouped:
             offsets = torch.zeros(self.num_experts + 1, dtype=torch.int32, device=x.device)
             offsets[1:] = torch.cumsum(counts, 0)
-            gate_h = self._gemm_dequant_grouped(q_a, s_a, offsets, self.w_gate, self.s_gate)
-            up_h = self._gemm_dequant_grouped(q_a, s_a, offsets, self.w_up, self.s_up)
+            gate_h = self._gemm_dequant_grouped(q_a, s_a, z_a, offsets, self.w_gate, self.s_gate,
+                                                self.wsum_gate)
+            up_h = self._gemm_dequant_grouped(q_a, s_a, z_a, offsets, self.w_up, self.s_up,
+                                              self.wsum_up)
         else:
-            gate_h = self._gemm_dequant_loop(q_a, s_a, counts, self.w_gate, self.s_gate)
-            up_h = self._gemm_dequant_loop(q_a, s_a, counts, self.w_up, self.s_up)
-        if self.fuse_down and self.use_grouped and not self.fp32_had and self.K % 4 == 0 and \
-                9 <= self.K <= 32 and gate_h.shape[1] == self.K * 512:
+            gate_h = self._gemm_dequant_loop(q_a, s_a, z_a, counts, self.w_gate, self.s_gate,
+                                             self.wsum_gate)
+            up_h = self._gemm_dequant_loop(q_a, s_a, z_a, counts, self.w_up, self.s_up,
+                                           self.wsum_up)
+
+        if self.fuse_down and self.use_grouped and not self.asym and not self.fp32_had and \
+                _CUDA.swiglu_had_fusable(gate_h.shape[1], self.K) and gate_h.shape[1] == \
+                self.K * 512:
             # swiglu, rotation, per-expert sign and quantizer in one launch
             # (bit-identical to the three steps below)
             q_d, s_d = _CUDA.swiglu_had_sign_quant_moe(gate_h, up_h, self.had_K.half(), self.K,
                                                        self.sign_down, eid, self.clip_ratio)
-            y = self._gemm_dequant_grouped(q_d, s_d, offsets, self.w_down, self.s_down)
-            inv = torch.argsort(perm)
-            y = y.to(x_dtype)[inv].view(-1, self.top_k, hidden_dim)
-            out = (y * routing_weights.unsqueeze(-1)).sum(dim=1)
-            return out.view(batch_size, seq_len, hidden_dim), router_logits
-        inter = kernel.swiglu(gate_h, up_h)
-
-        # the Hadamard is identical for every expert; the had_adj sign is per
-        # row, from the [E, inter] table
-        h = inter.float() if self.fp32_had else inter
-        h = matmul_hadU_cuda(h, self.had_K, self.K).to(torch.float16)
-
-        if self.use_grouped:
-            q_d, s_d = kernel.sym_quant_dynamic_moe(h, self.sign_down, eid, self.clip_ratio)
-            y = self._gemm_dequant_grouped(q_d, s_d, offsets, self.w_down, self.s_down)
+            y = self._gemm_dequant_grouped(q_d, s_d, None, offsets, self.w_down, self.s_down,
+                                           None)
         else:
-            if self.sign_down is not None:
-                h = h * self.sign_down[eid.long()]
-            q_d, s_d = kernel.sym_quant_dynamic(h, self.clip_ratio)
-            y = self._gemm_dequant_loop(q_d, s_d, counts, self.w_down, self.s_down)
+            inter = kernel.swiglu(gate_h, up_h)
+            # the Hadamard is identical for every expert; the had_adj sign is
+            # per row, from the [E, inter] table
+            h = inter.float() if self.fp32_had else inter
+            h = matmul_hadU_cuda(h, self.had_K, self.K).to(torch.float16)
+            if self.use_grouped:
+                if self.asym:
+                    q_d, s_d, z_d = kernel.asym_quant_dynamic_moe(h, self.sign_down, eid,
+                                                                  self.clip_ratio)
+                    z_d = z_d.to(torch.int8)
+                else:
+                    q_d, s_d = kernel.sym_quant_dynamic_moe(h, self.sign_down, eid,
+                                                            self.clip_ratio)
+                    z_d = None
+                y = self._gemm_dequant_grouped(q_d, s_d, z_d, offsets, self.w_down, self.s_down,
+                                               self.wsum_down)
+            else:
+                if self.sign_down is not None:
+                    h = h * self.sign_down[eid.long()]
+                q_d, s_d, z_d = self._quantize(h)
+                y = self._gemm_dequant_loop(q_d, s_d, z_d, counts, self.w_down, self.s_down,
+                                            self.wsum_down)
 
         # deterministic un-permute + weighted sum (no atomics: a captured
         # graph replays bit-identically)

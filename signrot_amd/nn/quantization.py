@@ -56,3 +56,30 @@ class SymQuantizer(QuantizerBase):
 
     def extra_repr(self) -> str:
         return f"maxq={self.maxq}, clip_ratio={self.clip_ratio}"
+
+
+class AsymQuantizer(QuantizerBase):
+    """Per-token asymmetric uint4 quantizer (quantization.py:59-83): one fused
+    launch (row min/max, scale, zero, quantize, pack) -> PackedQuantizedTensor
+    whose zeros_x is the zero point cast to int8."""
+
+    def __init__(self, *, bits: int = 4, clip_ratio: float = 1.0):
+        super().__init__(clip_ratio=clip_ratio)
+        self.maxq = get_minq_maxq(bits, sym=False)[1]
+
+    def forward(self, x: torch.Tensor) -> kernel.PackedQuantizedTensor:
+        quantized_x, scales_x, zeros_x = kernel.asym_quant_dynamic(x, self.clip_ratio)
+        return kernel.PackedQuantizedTensor(quantized_x, scales_x, zeros_x.to(torch.int8))
+
+    def forward_reference(self, x: torch.Tensor) -> kernel.PackedQuantizedTensor:
+        """Unfused composition (quantization.py:69-79): torch min/max/div/round
+        in x's dtype, then the given-parameter kernel."""
+        min_val = x.amin(dim=-1, keepdim=True) * self.clip_ratio
+        max_val = x.amax(dim=-1, keepdim=True) * self.clip_ratio
+        scales_x = (max_val - min_val) / self.maxq
+        zeros_x = (-min_val / scales_x).round()
+        quantized_x = kernel.asym_quant_f16_ui4(x, scales_x, zeros_x)
+        return kernel.PackedQuantizedTensor(quantized_x, scales_x, zeros_x.to(torch.int8))
+
+    def extra_repr(self) -> str:
+        return f"maxq={self.maxq}, clip_ratio={self.clip_ratio}"

@@ -73,7 +73,17 @@ def test_empty_inputs_are_noops(lib):
     assert lib.srq_sym_dequant_moe(None, None, None, None, None, None, 8, 0, 16, None, None) == 0
 
 
-def test_grouped_unsigned_is_unsupported(lib):
+def test_asym_argument_errors(lib):
     z = ctypes.c_void_p(16)
-    assert lib.srq_matmul_grouped(z, z, z, z, z, z, z, 2, 0, None) == -2
-    assert "asymmetric" in lib.srq_last_error().decode()
+    assert lib.srq_asym_quant_dynamic(z, 4, 0, 1.0, z, z, z, None) == -1
+    assert "empty rows" in lib.srq_last_error().decode()
+    assert lib.srq_asym_quant_dynamic_moe(z, z, None, 4, 4, 8, 1.0, z, z, z, None) == -1
+    assert "expert_ids" in lib.srq_last_error().decode()
+    assert lib.srq_matmul_u4s4(None, None, 4, 4, 48, None, None) == -1
+    assert "multiple of 32" in lib.srq_last_error().decode()
+    assert lib.srq_w4a4_linear_asym(z, z, None, z, z, z, None, 4, 4, 64, z, None) == -1
+    assert "null" in lib.srq_last_error().decode()
+    # empty inputs are no-ops
+    assert lib.srq_sum_i4(None, 0, 16, 1, None, None) == 0
+    assert lib.srq_matmul_colrow_i8_i32(None, None, 0, 8, None, None) == 0
+    assert lib.srq_asym_quant(None, None, None, 0, 8, 0, None, None) == 0

@@ -151,13 +151,6 @@ def test_matmul_grouped_vs_oracle(C):
         assert_bitexact(c[off[e]:off[e + 1]], want[e], f"problem {e}")
 
 
-def test_matmul_grouped_unsigned_is_unsupported(C):
-    ps = torch.zeros((1, 3), dtype=torch.int32, device=DEV)
-    z = torch.zeros(1, dtype=torch.int64, device=DEV)
-    with pytest.raises(RuntimeError):
-        C.matmul_grouped(ps, z, z, z, z, z, z, False)
-
-
 @pytest.mark.parametrize("counts,n,k", [([3, 0, 5, 1], 300, 768),
                                         ([130, 125, 140, 111, 128, 119, 135, 136], 14336, 4096),
                                         ([0, 0], 128, 128), ([1], 4096, 14336)])
