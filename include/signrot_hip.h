@@ -149,6 +149,18 @@ int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_t K,
                        const void *hadK, const int8_t *sign, int fp32_had,
                        float clip_ratio, void *q, void *scale, void *stream);
 
+/* Rotation + sign of srq_had_sign_quant followed by the per-token asymmetric
+ * uint4 quantizer of srq_asym_quant_dynamic (row min/max of the rotated,
+ * signed fp16 values, scale, zero point, codes): q u8 [rows, n/2], scale
+ * and zero f16 [rows].  Bit-identical to srq_online_hadamard followed by
+ * srq_asym_quant_dynamic.  Needs K % 4 == 0 and n = K * 512 or K * 1024
+ * (9 <= K <= 32), else SRQ_EUNSUPPORTED.  Replaces OnlineHadamard followed
+ * by AsymQuantizer (signrot/nn/hadamard.py:26-42, nn/quantization.py:59-67,
+ * kernels/fused.cu:143-195); the reference has no fused form. */
+int srq_had_sign_asym_quant(const void *x, int64_t rows, int64_t n, int64_t K,
+                            const void *hadK, const int8_t *sign, float clip_ratio, void *q,
+                            void *scale, void *zero, void *stream);
+
 /* srq_had_sign_quant whose input row is SwiGLU of two strided rows:
  * x[r, i] = fp16(fp16(silu(gate[r*ld + i])) * up[r*ld + i]) (the srq_swiglu
  * arithmetic), then the rotation, sign and quantizer of srq_had_sign_quant.

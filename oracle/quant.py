@@ -201,10 +201,14 @@ def asym_params(x_f16, clip_ratio=1.0):
     hmax = fp16(vmax); if clip != 1 each is fp16(float(h) * clip);
     diff = fp16(hmax - hmin); scale = fp16(diff / 15.f);
     ratio = fp16(-hmin / scale) (fp32 division); zero = fp16(nearbyint(ratio))
-    (round half to even).  Returns (scale f16 [rows], zero f16 [rows])."""
+    (round half to even).  The reductions are fminf / fmaxf from ±FLT_MAX
+    (fused.cu:155-163): NaN values are skipped, an all-NaN row gives
+    hmin = +inf, hmax = -inf.  Returns (scale f16 [rows], zero f16 [rows])."""
     x = np.asarray(x_f16, dtype=F16).astype(F32)
-    hmin = x.min(axis=-1).astype(F16)
-    hmax = x.max(axis=-1).astype(F16)
+    fmax32 = np.finfo(F32).max
+    with np.errstate(over="ignore"):  # ±FLT_MAX -> ±inf in fp16, as __float2half
+        hmin = np.fmin.reduce(x, axis=-1, initial=fmax32).astype(F16)
+        hmax = np.fmax.reduce(x, axis=-1, initial=-fmax32).astype(F16)
     if clip_ratio != 1.0:
         hmin = (hmin.astype(F32) * F32(clip_ratio)).astype(F16)
         hmax = (hmax.astype(F32) * F32(clip_ratio)).astype(F16)

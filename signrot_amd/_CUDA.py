@@ -342,6 +342,35 @@ def had_sign_quant(x, hadK, K, sign=None, clip_ratio=1.0, fp32_had=False):
     return q, scale
 
 
+def had_asym_fusable(n, K):
+    """Whether had_sign_asym_quant has a one-launch kernel for n = K x 2^k."""
+    return K % 4 == 0 and 9 <= K <= 32 and n in (K * 512, K * 1024)
+
+
+def had_sign_asym_quant(x, hadK, K, sign=None, clip_ratio=1.0):
+    """online_hadamard followed by asym_quant_dynamic: (q u8 [..., n/2] uint4
+    codes, scale f16 [..., 1], zero f16 [..., 1]).  One launch where the
+    rotation has an MFMA form (had_asym_fusable), else the two ops in turn
+    (the same results)."""
+    _check("had_sign_asym_quant", [(x, "x"), (hadK, "hadK"), (sign, "sign")],
+           [torch.float16, torch.float16, torch.int8])
+    n = x.shape[-1]
+    _check_had("had_sign_asym_quant", n, hadK, K, sign, False)
+    rows = x.numel() // n if n else 0
+    if not had_asym_fusable(n, K):
+        rot = online_hadamard(x.reshape(rows, n), hadK, K, sign)
+        q, s, z = asym_quant_dynamic(rot, clip_ratio)
+        return (q.view(*x.shape[:-1], -1), s.view(*x.shape[:-1], 1),
+                z.view(*x.shape[:-1], 1))
+    q = torch.empty((*x.shape[:-1], n // 2), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((*x.shape[:-1], 1), dtype=torch.float16, device=x.device)
+    zero = torch.empty((*x.shape[:-1], 1), dtype=torch.float16, device=x.device)
+    if rows:
+        _call("srq_had_sign_asym_quant", _ptr(x), rows, n, int(K), _ptr(hadK), _ptr(sign),
+              float(clip_ratio), _ptr(q), _ptr(scale), _ptr(zero), _stream(x))
+    return q, scale, zero
+
+
 def _check_had(name, n, hadK, K, sign, fp32_had):
     if K > 1:
         if hadK is None or tuple(hadK.shape[-2:]) != (K, K) or hadK.numel() != K * K:

@@ -26,6 +26,7 @@ SIGNATURES = {
     "srq_matmul_u4s4": [_p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_asym": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_moe_asym": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
+    "srq_had_sign_asym_quant": [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _p, _p, _p],
     "srq_asym_quant_dynamic": [_p, _i64, _i64, _f32, _p, _p, _p, _p],
     "srq_asym_quant_dynamic_moe": [_p, _p, _p, _i64, _i64, _i64, _f32, _p, _p, _p, _p],
     "srq_asym_quant": [_p, _p, _p, _i64, _i64, _i32, _p, _p],

@@ -323,12 +323,29 @@ SRQ_DEV u32 offset_codes(u32 q) {
 // eight offset codes (pairs a = (e0, e1), b = (e2, e3), c = (e4, e5),
 // d = (e6, e7), nibble in bits 0-3 and 16-19 of each) -> 32 bits of packed
 // two's-complement nibbles, e0 in bits 0-3 ... e7 in bits 28-31
-SRQ_DEV u32 pack8(u32 a, u32 b, u32 c, u32 d) {
+SRQ_DEV u32 pack8_raw(u32 a, u32 b, u32 c, u32 d) {
     const u32 x = __builtin_amdgcn_perm(b, a, 0x06020400u);  // e0 e2 e1 e3
     const u32 y = __builtin_amdgcn_perm(d, c, 0x06020400u);  // e4 e6 e5 e7
     const u32 lo = __builtin_amdgcn_perm(y, x, 0x05040100u); // e0 e2 e4 e6
     const u32 hi = __builtin_amdgcn_perm(y, x, 0x07060302u); // e1 e3 e5 e7
-    return (lo | (hi << 4)) ^ 0x88888888u;
+    // each selected byte is the low byte of an fp16 in [1536, 1551]: the
+    // code itself, high nibble clear
+    return lo | (hi << 4);
+}
+
+SRQ_DEV u32 pack8(u32 a, u32 b, u32 c, u32 d) { return pack8_raw(a, b, c, d) ^ 0x88888888u; }
+
+// Packed fp16 quotients -> asymmetric uint4 codes in the low nibble of each
+// half: clamp to [-zi, 15 - zi] (exact in fp16 for |zi| <= 511), round half
+// to even by + 1536 (ulp 1 in [1024, 2048); 1536 is even, so the sum rounds
+// as the quotient does), then + zi (exact): clamp(rne(q) + zi, 0, 15),
+// which is the reference's clamp(__half2int_rn(q) + zi, 0, 15) for finite q.
+SRQ_DEV u32 asym_offset_codes(u32 q, v2h lo, v2h hi, v2h zo) {
+    v2h h = __builtin_bit_cast(v2h, q);
+    h = __builtin_elementwise_min(__builtin_elementwise_max(h, lo), hi);
+    h = h + (v2h){1536, 1536};
+    h = h + zo;
+    return __builtin_bit_cast(u32, h);
 }
 
 // Reciprocal for the packed quantizer: s == 0 (an all-zero row, or a

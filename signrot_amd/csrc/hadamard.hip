@@ -403,7 +403,8 @@ int check_rotation(const char *name, const void *x, int64_t rows, int64_t n, int
 int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
                     hipStream_t st, const void *up = nullptr, int64_t ld = 0,
-                    const int32_t *sign_row = nullptr, int64_t n_sign_rows = 0);
+                    const int32_t *sign_row = nullptr, int64_t n_sign_rows = 0,
+                    void *qzero = nullptr);
 
 extern "C" int srq_hadamard_transform(const void *x, void *out, int64_t rows, int64_t n,
                                       float scale, int dtype, void *stream) {
@@ -535,5 +536,24 @@ extern "C" int srq_swiglu_had_sign_quant_moe(const void *gate, const void *up, i
     }
     srq_set_error("swiglu_had_sign_quant_moe: needs n = K * 512 with 9 <= K <= 32, K %% 4 == 0 "
                   "(n=%lld, K=%lld)", (long long)n, (long long)K);
+    return SRQ_EUNSUPPORTED;
+}
+
+extern "C" int srq_had_sign_asym_quant(const void *x, int64_t rows, int64_t n, int64_t K,
+                                       const void *hadK, const int8_t *sign, float clip_ratio,
+                                       void *q, void *scale, void *zero, void *stream) {
+    int rc = check_rotation("had_sign_asym_quant", x, rows, n, K, hadK);
+    if (rc) return rc;
+    if (rows == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(q && scale && zero, "had_sign_asym_quant: null output");
+    SRQ_CHECK_ARG(srq_aligned(x, 16) && srq_aligned(q, 16),
+                  "had_sign_asym_quant: x and q must be 16-byte aligned");
+    if (srq_had512_mfma(x, rows, n, K, hadK, sign, clip_ratio, q, scale, nullptr,
+                        (hipStream_t)stream, nullptr, 0, nullptr, 0, zero)) {
+        SRQ_LAUNCH_CHECK("had_sign_asym_quant");
+        return SRQ_OK;
+    }
+    srq_set_error("had_sign_asym_quant: needs K %% 4 == 0 and n = K * 512 or K * 1024 with "
+                  "9 <= K <= 32 (n=%lld, K=%lld)", (long long)n, (long long)K);
     return SRQ_EUNSUPPORTED;
 }

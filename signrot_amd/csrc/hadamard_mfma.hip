@@ -82,6 +82,7 @@ struct MfmaRotArgs {
     float clip;
     uint8_t *q;           // quant mode: packed codes, rows of n/2 bytes
     f16 *qscale;          // quant mode: [rows]
+    f16 *qzero;           // asymmetric quant mode: zero points [rows]
     f16 *out;             // rotation mode: fp16 rows of n
     const f16 *up;        // SwiGLU input: x is the gate, this the up projection
     int64_t ld;           // row stride of x (and up), elements
@@ -112,13 +113,46 @@ SRQ_DEV void quant_store(const u32 (&w)[4][8], float rcp, uint8_t *qrow) {
         }
 }
 
+// Asymmetric uint4 codes of the same values (MODE 2), same staging layout:
+// FAST, the packed route (finite row, s > 0, |zi| <= 511); otherwise each
+// code by the exact per-element arithmetic (asym_code).
+template <bool FAST>
+SRQ_DEV void quant_store_asym(const u32 (&w)[4][8], float rcp, v2h lo, v2h hi, v2h zo,
+                              float s, int zi, uint8_t *qrow) {
+#pragma unroll
+    for (int i1 = 0; i1 < 4; ++i1)
+#pragma unroll
+        for (int u = 0; u < 4; u += 2) {
+            u32 r;
+            if constexpr (FAST) {
+                r = pack8_raw(asym_offset_codes(quot2(w[i1][2 * u], rcp), lo, hi, zo),
+                              asym_offset_codes(quot2(w[i1][2 * u + 1], rcp), lo, hi, zo),
+                              asym_offset_codes(quot2(w[i1][2 * u + 2], rcp), lo, hi, zo),
+                              asym_offset_codes(quot2(w[i1][2 * u + 3], rcp), lo, hi, zo));
+            } else {
+                r = 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const v2h pr = __builtin_bit_cast(v2h, w[i1][2 * u + e / 2]);
+                    r |= (u32)(asym_code((float)pr[e & 1], s, zi, 0, 15) & 0xF) << (4 * e);
+                }
+            }
+            uint8_t *p = qrow + i1 * 64 + 4 * u;
+            *reinterpret_cast<uint16_t *>(p) = (uint16_t)r;
+            *reinterpret_cast<uint16_t *>(p + 4) = (uint16_t)(r >> 16);
+        }
+}
+
+// MODE: 0 rotation (fp16 out), 1 + symmetric int4 quantizer, 2 + asymmetric
+// uint4 quantizer (row min/max, scale and zero point).
 // SW: the row is swiglu(gate, up) of two strided inputs (one workgroup per
 // CU: the up prefetch needs the registers two workgroups would share; with
 // H_1024 chunks up to K = 28).
 // P: 512-chunks per Hadamard chunk (1: H_512, 2: H_1024; one workgroup per
 // CU, which holds twice the row in registers).
 template <int NT, int MODE, bool SW, int P>
-__global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kernel(MfmaRotArgs a) {
+__global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had512_mfma_kernel(
+    MfmaRotArgs a) {
     // The staged row: 128-element segment (chunk c, quarter i1) at
     // rowbuf + 256 (4c + i1) bytes, its 16-byte piece p at position
     // p ^ 2h(c, i1), h = i1 | ((c >> 2) & 1) << 2.  The swizzle makes both
@@ -127,8 +161,10 @@ __global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kerne
     // LDS banks.  Chunks K .. 8 NT - 1 stay zero.
     __shared__ v4i rowbuf[NT * 8 * 64];
     // codes of one row for coalesced stores: chunk c's 256 bytes at 272 c
-    __shared__ v4i cbuf[MODE == 1 ? NT * 8 * 17 : 1];
-    __shared__ float red[2][4];
+    __shared__ v4i cbuf[MODE >= 1 ? NT * 8 * 17 : 1];
+    // row reduction, double-buffered by row parity: MODE 1 max |x| per wave;
+    // MODE 2 min, max and the non-finite flag per wave
+    __shared__ float red[2][MODE == 2 ? 12 : 4];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nt = wave;
@@ -421,8 +457,14 @@ __global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kerne
         finish(dprev, NT - 1);
 
         // ---- K-mix: round to fp16, apply the sign, keep; row max of |out|
+        // (MODE 2: packed min and max of the signed fp16 values -- NaN-
+        // ignoring, as the reference's fminf / fmaxf -- and a NaN-propagating
+        // max of |x| that flags non-finite rows; lanes past the K chunks
+        // hold no outputs and stay out)
         u32 w[P][4][8];
         float amax = 0.f;
+        v2h mn2 = (v2h){(f16)__builtin_inff(), (f16)__builtin_inff()};
+        v2h mx2 = -mn2, ab2 = (v2h){0, 0};
 #pragma unroll
         for (int h = 0; h < P; ++h)
 #pragma unroll
@@ -432,8 +474,14 @@ __global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kerne
                 if (NS > 1) z = mfma32(ka[NS > 1 ? 1 : 0][h][i1].h, HB[1], z);
 #pragma unroll
                 for (int p = 0; p < 8; ++p) {
-                    amax = absmax3(amax, z[2 * p], z[2 * p + 1]);
+                    if (MODE != 2) amax = absmax3(amax, z[2 * p], z[2 * p + 1]);
                     w[h][i1][p] = pk16(z[2 * p], z[2 * p + 1]) ^ msk[h][i1][p];
+                    if (MODE == 2 && ln < a.KC) {
+                        const v2h v = __builtin_bit_cast(v2h, w[h][i1][p]);
+                        mn2 = __builtin_elementwise_min(mn2, v);
+                        mx2 = __builtin_elementwise_max(mx2, v);
+                        ab2 = __builtin_elementwise_maximum(ab2, __builtin_elementwise_abs(v));
+                    }
                 }
             }
         if (MODE == 0) {
@@ -464,35 +512,81 @@ __global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kerne
             continue;
         }
 
-        // ---- block row max (this barrier also ends every wave's LDS reads
-        // of the row, so the prefetched row may be written afterwards)
-        amax = wave_max_dpp(amax);
-        if (lane == 0) red[it & 1][wave] = amax;
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        amax = round16(fmaxf(fmaxf(red[it & 1][0], red[it & 1][1]),
-                             fmaxf(red[it & 1][2], red[it & 1][3])));
+        if constexpr (MODE == 1) {
+            // ---- block row max (this barrier also ends every wave's LDS
+            // reads of the row, so the prefetched row may be written after)
+            amax = wave_max_dpp(amax);
+            if (lane == 0) red[it & 1][wave] = amax;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            amax = round16(fmaxf(fmaxf(red[it & 1][0], red[it & 1][1]),
+                                 fmaxf(red[it & 1][2], red[it & 1][3])));
 
-        f16 s16 = f16_rn(amax / 7.f);
-        if (a.clip != 1.f) s16 = f16_rn((float)s16 * a.clip);
-        // quotient divisor: s itself, or 2^-126 when s == 0 -- then every
-        // nonzero x overflows to ±inf and clamps to 7 / -8, and x == 0 gives
-        // 0, which is what x / 0 yields after the reference's __half2int_rn
-        // (saturation, NaN -> 0)
-        const float sq = fmaxf((float)s16, 0x1p-126f);
-        const float rcp = 1.0f / sq;
-        if (threadIdx.x == 0) a.qscale[row] = s16;
-        // row-uniform: can any |x / s| round beyond ±7?
-        const bool clampit = __builtin_amdgcn_readfirstlane(!(amax <= 7.25f * sq));
+            f16 s16 = f16_rn(amax / 7.f);
+            if (a.clip != 1.f) s16 = f16_rn((float)s16 * a.clip);
+            // quotient divisor: s itself, or 2^-126 when s == 0 -- then every
+            // nonzero x overflows to ±inf and clamps to 7 / -8, and x == 0
+            // gives 0, which is what x / 0 yields after the reference's
+            // __half2int_rn (saturation, NaN -> 0)
+            const float sq = fmaxf((float)s16, 0x1p-126f);
+            const float rcp = 1.0f / sq;
+            if (threadIdx.x == 0) a.qscale[row] = s16;
+            // row-uniform: can any |x / s| round beyond ±7?
+            const bool clampit = __builtin_amdgcn_readfirstlane(!(amax <= 7.25f * sq));
 
-        if (ln < a.KC) {
+            if (ln < a.KC) {
 #pragma unroll
-            for (int h = 0; h < P; ++h) {
-                uint8_t *qrow =
-                    reinterpret_cast<uint8_t *>(cbuf) + (P * ln + h) * 272 + 16 * nt + 2 * g;
-                if (clampit) quant_store<true>(w[h], rcp, qrow);
-                else quant_store<false>(w[h], rcp, qrow);
+                for (int h = 0; h < P; ++h) {
+                    uint8_t *qrow =
+                        reinterpret_cast<uint8_t *>(cbuf) + (P * ln + h) * 272 + 16 * nt + 2 * g;
+                    if (clampit) quant_store<true>(w[h], rcp, qrow);
+                    else quant_store<false>(w[h], rcp, qrow);
+                }
+            }
+        } else {
+            // ---- block row min / max and non-finite flag (the barrier also
+            // ends every wave's LDS reads of the row)
+            float fmn = fminf((float)mn2[0], (float)mn2[1]);
+            float fmx = fmaxf((float)mx2[0], (float)mx2[1]);
+            const bool badl = !((float)ab2[0] <= 65504.f) || !((float)ab2[1] <= 65504.f);
+            fmn = -wave_max_dpp(-fmn);
+            fmx = wave_max_dpp(fmx);
+            const bool wbad = __builtin_amdgcn_ballot_w64(badl) != 0;
+            if (lane == 0) {
+                red[it & 1][wave] = fmn;
+                red[it & 1][4 + wave] = fmx;
+                red[it & 1][8 + wave] = wbad ? 1.f : 0.f;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            const float* rr = red[it & 1];
+            const float vmin = fminf(fminf(rr[0], rr[1]), fminf(rr[2], rr[3]));
+            const float vmax = fmaxf(fmaxf(rr[4], rr[5]), fmaxf(rr[6], rr[7]));
+            const bool bad = (rr[8] + rr[9] + rr[10] + rr[11]) != 0.f;
+            f16 sh, zh;
+            asym_row_params(vmin, vmax, a.clip, sh, zh);
+            if (threadIdx.x == 0) {
+                a.qscale[row] = sh;
+                a.qzero[row] = zh;
+            }
+            const float sf = (float)sh;
+            const int zi = h2i_rn((float)zh);
+            const bool fast = __builtin_amdgcn_readfirstlane(!bad && sf > 0.f && zi >= -511 &&
+                                                             zi <= 511);
+            const float rcp = 1.0f / fmaxf(sf, 0x1p-126f);
+            const v2h lo2 = (v2h){(f16)(float)(-zi), (f16)(float)(-zi)};
+            const v2h hi2 = (v2h){(f16)(float)(15 - zi), (f16)(float)(15 - zi)};
+            const v2h zo2 = (v2h){(f16)(float)zi, (f16)(float)zi};
+            if (ln < a.KC) {
+#pragma unroll
+                for (int h = 0; h < P; ++h) {
+                    uint8_t *qrow =
+                        reinterpret_cast<uint8_t *>(cbuf) + (P * ln + h) * 272 + 16 * nt + 2 * g;
+                    if (fast) quant_store_asym<true>(w[h], rcp, lo2, hi2, zo2, sf, zi, qrow);
+                    else quant_store_asym<false>(w[h], rcp, lo2, hi2, zo2, sf, zi, qrow);
+                }
             }
         }
         // the row's codes are staged; write them out 16 bytes per lane
@@ -529,7 +623,7 @@ __global__ __launch_bounds__(256, (SW || P == 2) ? 1 : 2) void had512_mfma_kerne
 int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
                     hipStream_t st, const void *up, int64_t ld, const int32_t *sign_row,
-                    int64_t n_sign_rows) {
+                    int64_t n_sign_rows, void *qzero) {
     // K % 4 == 0: the row fetch moves 4 chunks per instruction and the hadK
     // loads take runs of 2 or 4 table entries (every Hadamard order above 2
     // is a multiple of 4)
@@ -541,6 +635,7 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     // the SwiGLU form of H_1024 holds gate and up prefetches of a 2K-chunk
     // row: it fits the register file up to K = 28 (K = 32 would spill)
     if (up && P == 2 && K > 28) return 0;
+    if (qzero && (up || !q)) return 0;  // asymmetric codes: plain rows only
     if (ld < n) ld = n;
     if (rows > 0 && ((rows - 1) * ld + n) * 2 >= (int64_t)kOob) return 0;  // 32-bit offsets
     if (!srq_aligned(x, 16) || (up && !srq_aligned(up, 16)) || ld % 8) return 0;
@@ -561,9 +656,11 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     a.ld = ld;
     a.sign_row = sign_row;
     a.n_sign_rows = n_sign_rows;
+    a.qzero = (f16 *)qzero;
     // persistent blocks of 4 waves, up to 2 per CU (256 CUs; 1 with the
-    // SwiGLU input or H_1024 chunks), one row each at a time
-    const int64_t cap = (up || P == 2) ? 256 : 256 * 2;
+    // SwiGLU input, H_1024 chunks or the asymmetric quantizer), one row each
+    // at a time
+    const int64_t cap = (up || P == 2 || qzero) ? 256 : 256 * 2;
     const int64_t blocks = rows < cap ? rows : cap;
     const dim3 grid((unsigned)blocks), block(256);
     auto go = [&](auto ntc, auto modec, auto swc, auto pc) {
@@ -577,6 +674,7 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     using I8 = std::integral_constant<int, 8>;
     using M0 = std::integral_constant<int, 0>;
     using M1 = std::integral_constant<int, 1>;
+    using M2 = std::integral_constant<int, 2>;
     using S0 = std::false_type;
     using S1 = std::true_type;
     using P1 = std::integral_constant<int, 1>;
@@ -606,6 +704,8 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
             if (K <= 16) go(I4{}, M1{}, S1{}, P2{});
             else go(I7{}, M1{}, S1{}, P2{});
         }
+    } else if (q && qzero) {
+        mode(M2{});
     } else if (q) {
         mode(M1{});
     } else {

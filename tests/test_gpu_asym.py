@@ -274,3 +274,39 @@ def test_moe_block_asym_grouped_equals_loop(hidden, inter, tokens):
     assert torch.equal(logits, logits2)
     assert torch.equal(out, out2)
     assert torch.isfinite(out).all()
+
+
+def _hadk(k):
+    from oracle import hadamard as oh
+    return to_dev(oh.had_table(k).astype(np.float16))
+
+
+@pytest.mark.parametrize("n,K,rows,clip,use_sign", [
+    (14336, 28, 2048, 1.0, True), (14336, 28, 7, 0.8, True), (28672, 28, 300, 1.0, True),
+    (12288, 12, 5, 1.0, False), (6144, 12, 513, 1.0, True), (4096, 1, 9, 1.0, True)])
+def test_had_sign_asym_quant(C, n, K, rows, clip, use_sign):
+    """Fused rotation + sign + asymmetric quantizer == online_hadamard then
+    asym_quant_dynamic (GPU chain) == the oracle's quantizer on the GPU's
+    rotated values, bit for bit (the K = 1 shape takes the two-launch form)."""
+    rng = np.random.default_rng(n + rows)
+    x = outlier_input(rng, rows, n, n_out=8, mag=40.0)
+    if rows >= 7:
+        x[1] = 0                          # all-zero row
+        x[2] = np.float16(1.5)            # constant row (rotates to one spike)
+        x[3] *= 300                       # large
+        x[4, 5] = np.float16(np.inf)      # non-finite rows take the exact route
+        x[5, 9] = np.float16(np.nan)
+        x[6] = np.abs(x[6]) + np.float16(20)
+    hk = _hadk(K) if K > 1 else None
+    sign = to_dev(rng.choice([-1, 1], n).astype(np.int8)) if use_sign else None
+    xd = to_dev(x)
+    q, s, z = C.had_sign_asym_quant(xd, hk, K, sign, clip)
+    rot = C.online_hadamard(xd, hk, K, sign)
+    q2, s2, z2 = C.asym_quant_dynamic(rot, clip)
+    assert torch.equal(s, s2), "scale vs chain"
+    assert np.array_equal(_zero_bits(to_np(z)), _zero_bits(to_np(z2))), "zero vs chain"
+    assert torch.equal(q, q2), "codes vs chain"
+    qw, sw, zw = oq.asym_quant_dynamic(to_np(rot), clip)
+    assert_bitexact(to_np(s), sw, "scale")
+    assert np.array_equal(_zero_bits(to_np(z)), _zero_bits(zw)), "zero"
+    assert_bitexact(to_np(q), qw, "codes")

@@ -61,6 +61,17 @@ def test_degenerate_rows():
     assert np.all(oq.unpack_u4(q) == 0)
 
 
+def test_nan_values_are_skipped_by_the_row_reductions():
+    # fminf / fmaxf skip NaN: [NaN, -1, 14] has the parameters of [-1, 14]
+    # (scale 1, zero 1); the NaN's own code is clamp(0 + zero) = 1
+    codes, s, z = _q([np.nan, -1.0, 14.0])
+    assert (s, z) == (1.0, 1.0)
+    assert codes.tolist() == [1, 0, 15]
+    # an all-NaN row: hmin = +inf, hmax = -inf, diff = -inf, scale = -inf
+    q, s2, z2 = oq.asym_quant_dynamic(np.full((1, 4), np.nan, F16))
+    assert np.isneginf(s2[0, 0]) and np.isnan(z2[0, 0])
+
+
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_round_trip_within_half_scale(seed):
     rng = np.random.default_rng(seed)
