@@ -273,6 +273,69 @@ def bench_qlinear(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9, reps=2
     return res
 
 
+def bench_qlinear_asym(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9):
+    """The cfg2 QLinear with asymmetric activations (the signrot preset's
+    --a_asym): had_sign_asym_quant (rotation + sign + uint4 quantizer with
+    per-token zero points) + w4a4_linear_asym (unsigned-A GEMM, zero
+    correction, dequant), per-kernel and whole-QLinear averages."""
+    from signrot_amd import _native
+    from signrot_amd.functional.hadamard import get_hadK
+    st = torch.cuda.current_stream()
+    g = torch.Generator(device=dev).manual_seed(seed)
+    had, k = get_hadK(K)
+    hadk = had.half().to(dev).contiguous()
+    sign = (torch.randint(0, 2, (K,), device=dev, generator=g).to(torch.int8) * 2 - 1)
+    set_bytes = M * K * 2 + N * K // 2 + M * K // 2 + M * N * 2
+    nsets = max(1, min(256, math.ceil(min_bytes / set_bytes)))
+    x0 = torch.randn(M, K, device=dev, generator=g)
+    ch = torch.randperm(K, device=dev, generator=g)[:n_out]
+    x0[:, ch] *= mag
+    x0 = (x0 + 0.5).half()
+    xs = [x0] + [x0.clone() for _ in range(min(nsets, 8) - 1)]
+    wts = [_rand_w(N, K, dev, g) for _ in range(nsets)]
+    wsum = [torch.empty(N, dtype=torch.int32, device=dev) for _ in range(nsets)]
+    for w, ws in zip(wts, wsum):
+        _native.call("srq_sum_i4", w.data_ptr(), N, K // 2, 1, ws.data_ptr(), st.cuda_stream)
+    wsc = (torch.rand(N, device=dev, generator=g) * 1e-3 + 1e-4).half()
+    qb = [torch.empty(M, K // 2, dtype=torch.uint8, device=dev) for _ in range(len(xs))]
+    sb = [torch.empty(M, dtype=torch.float16, device=dev) for _ in range(len(xs))]
+    zb = [torch.empty(M, dtype=torch.float16, device=dev) for _ in range(len(xs))]
+    zi = [torch.empty(M, dtype=torch.int8, device=dev) for _ in range(len(xs))]
+    ob = [torch.empty(M, N, dtype=torch.float16, device=dev) for _ in range(len(xs))]
+
+    def had(i):
+        j = i % len(xs)
+        _native.call("srq_had_sign_asym_quant", xs[j].data_ptr(), M, K, k, hadk.data_ptr(),
+                     sign.data_ptr(), 1.0, qb[j].data_ptr(), sb[j].data_ptr(), zb[j].data_ptr(),
+                     st.cuda_stream)
+        zi[j].copy_(zb[j])  # AsymQuantizer's zeros_x.to(torch.int8)
+
+    def gemm(i):
+        j = i % len(xs)
+        _native.call("srq_w4a4_linear_asym", qb[j].data_ptr(), sb[j].data_ptr(),
+                     zi[j].data_ptr(), wts[i % nsets].data_ptr(), wsc.data_ptr(),
+                     wsum[i % nsets].data_ptr(), None, M, N, K, ob[j].data_ptr(),
+                     st.cuda_stream)
+
+    def both(i):
+        had(i)
+        gemm(i)
+
+    n = max(20, min(nsets, 64))
+    t_all = _time_launches(both, n, st) * 1e3
+    t_had = _time_launches(had, n, st) * 1e3
+    t_gemm = _time_launches(gemm, n, st) * 1e3
+    ops = 2.0 * M * N * K
+    res = {"M": M, "K": K, "N": N, "hadamard": f"had_{k} x H_{K // k}", "weight_sets": nsets,
+           "qlinear": _roof(t_all, ops, M * K * 2 + N * K // 2 + M * N * 2 + M * 4 + N * 6),
+           "had_sign_asym_quant": _roof(t_had, 0.0, M * K * 2 + M * K // 2 + M * 4),
+           "w4a4_linear_asym": _roof(t_gemm, ops, M * K // 2 + N * K // 2 + M * N * 2 + M * 3
+                                     + N * 6)}
+    del xs, wts, qb, sb, zb, zi, ob
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_mlp70b(dev, M, seed, hidden=8192, ffn=28672, reps=10, min_bytes=2.2e9):
     """Config 4: Llama-3-70B-shape W4A4 MLP block: per-token int4 quant of x,
     the gate and up W4A4 linears as one GEMM over the concatenated weights
@@ -351,11 +414,13 @@ def bench_moe(dev, seed, tokens=512, hidden=4096, ffn=14336, experts=8, top_k=2,
 
 def bench_configs(args, dev):
     """The BASELINE.json configs other than the headline one, each at its
-    own shape (configs[0], the cfg2 M sweep, configs[3], configs[4])."""
+    own shape (configs[0], the cfg2 M sweep, configs[3], configs[4]), and the
+    cfg2 QLinear with asymmetric activations."""
     out = {"cfg1_qproj_M16": bench_qlinear(dev, 16, 4096, 4096, args.seed + 10, n_out=4,
                                            mag=100.0),
            "cfg2_sweep": [bench_qlinear(dev, m, 14336, 4096, args.seed + 20 + m)
                           for m in (1, 16, 128, 2048, 8192)],
+           "cfg2_asym_M2048": bench_qlinear_asym(dev, 2048, 14336, 4096, args.seed + 25),
            "cfg4_mlp70b": [bench_mlp70b(dev, m, args.seed + 30 + m) for m in (1, 32, 512, 4096)],
            "cfg5_moe": bench_moe(dev, args.seed + 40)}
     return out

@@ -5,7 +5,7 @@ import torch
 from .. import _CUDA
 from ..functional import kernel
 from ..functional.hadamard import get_hadK, matmul_hadU_cuda
-from .quantization import Quantizer
+from .quantization import AsymQuantizer, Quantizer
 
 
 class OnlineHadamard(torch.nn.Module):
@@ -81,12 +81,12 @@ class OnlineHadamard(torch.nn.Module):
 
 
 class HadamardQuantizer(torch.nn.Module):
-    """Fused Sequential(OnlineHadamard, Quantizer): rotation, sign and
-    per-token int4 quantization in one launch, bit-identical to running the
-    two modules in sequence.  Holds the original modules (state_dict keys
-    unchanged under `had.` / `quantizer.`)."""
+    """Fused Sequential(OnlineHadamard, Quantizer or AsymQuantizer): rotation,
+    sign and per-token int4 (or asymmetric uint4) quantization in one launch,
+    bit-identical to running the two modules in sequence.  Holds the original
+    modules (state_dict keys unchanged under `had.` / `quantizer.`)."""
 
-    def __init__(self, had: OnlineHadamard, quantizer: Quantizer):
+    def __init__(self, had: OnlineHadamard, quantizer):
         super().__init__()
         self.had = had
         self.quantizer = quantizer
@@ -95,9 +95,16 @@ class HadamardQuantizer(torch.nn.Module):
         h = self.had
         if x.dtype != torch.float16 or not x.is_cuda:
             return self.quantizer(h(x))
+        if isinstance(self.quantizer, AsymQuantizer):
+            if h.fp32_had:
+                return self.quantizer(h(x))
+            q, s, z = _CUDA.had_sign_asym_quant(x.contiguous(), h._hadk(x.device), h.rem_dim,
+                                                h._sign(), self.quantizer.clip_ratio)
+            return kernel.PackedQuantizedTensor(q, s, z.to(torch.int8))
         q, s = kernel.had_sign_quant(x, h._hadk(x.device), h.rem_dim, h._sign(),
                                      self.quantizer.clip_ratio, h.fp32_had)
         return kernel.PackedQuantizedTensor(q, s)
+
 
 
 def fuse_online_hadamard(module: torch.nn.Module) -> torch.nn.Module:
@@ -109,7 +116,7 @@ def fuse_online_hadamard(module: torch.nn.Module) -> torch.nn.Module:
             out, i = [], 0
             while i < len(mods):
                 if (i + 1 < len(mods) and isinstance(mods[i], OnlineHadamard)
-                        and type(mods[i + 1]) is Quantizer):
+                        and type(mods[i + 1]) in (Quantizer, AsymQuantizer)):
                     out.append(HadamardQuantizer(mods[i], mods[i + 1]))
                     i += 2
                 else:

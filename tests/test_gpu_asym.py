@@ -310,3 +310,27 @@ def test_had_sign_asym_quant(C, n, K, rows, clip, use_sign):
     assert_bitexact(to_np(s), sw, "scale")
     assert np.array_equal(_zero_bits(to_np(z)), _zero_bits(zw)), "zero"
     assert_bitexact(to_np(q), qw, "codes")
+
+
+@torch.no_grad()
+def test_hadamard_asym_quantizer_module_and_linear():
+    """Sequential(OnlineHadamard, AsymQuantizer, Linear4bit) fused by
+    fuse_online_hadamard gives the unfused sequence's output bit for bit."""
+    from signrot_amd.nn import (AsymQuantizer, HadamardQuantizer, Linear4bit, OnlineHadamard,
+                                fuse_online_hadamard)
+    rng = np.random.default_rng(21)
+    n, out_f = 14336, 512
+    lin = Linear4bit(n, out_f).to(DEV)
+    lin.weight.copy_(to_dev(rng.integers(0, 256, (out_f, n // 2)).astype(np.uint8)))
+    lin.weight_scales.copy_(to_dev(np.full((out_f, 1), 1e-3, np.float32)))
+    had = OnlineHadamard(n, lin, had_adj=True).to(DEV)
+    had.had_adj_sign.copy_(to_dev(rng.choice([-1, 1], n).astype(np.int8)))
+    seq = torch.nn.Sequential(had, AsymQuantizer(), lin)
+    x = to_dev(outlier_input(rng, 33, n, mag=50.0))
+    want = seq(x)
+    holder = torch.nn.Module()
+    holder.mlp = seq
+    fuse_online_hadamard(holder)
+    assert isinstance(holder.mlp[0], HadamardQuantizer)
+    got = holder.mlp(x)
+    assert torch.equal(got, want)

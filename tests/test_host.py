@@ -68,3 +68,16 @@ def test_fuse_online_hadamard_rewrites_pairs():
     assert block.down_proj[1] is lin
     # state-dict keys move under the fused module, values unchanged
     assert len(block.state_dict()) == len(keys)
+
+
+def test_fuse_online_hadamard_rewrites_asym_pairs():
+    from signrot_amd.nn import (AsymQuantizer, HadamardQuantizer, Linear4bit, OnlineHadamard,
+                                fuse_online_hadamard)
+    lin = Linear4bit(14336, 64)
+    block = torch.nn.Module()
+    block.down_proj = torch.nn.Sequential(OnlineHadamard(14336, lin, had_adj=True),
+                                          AsymQuantizer(clip_ratio=0.9), lin)
+    fuse_online_hadamard(block)
+    assert isinstance(block.down_proj[0], HadamardQuantizer)
+    assert isinstance(block.down_proj[0].quantizer, AsymQuantizer)
+    assert block.down_proj[1] is lin
