@@ -412,17 +412,40 @@ def bench_moe(dev, seed, tokens=512, hidden=4096, ffn=14336, experts=8, top_k=2,
     return res
 
 
+def bench_prefill_attention(dev, B, T, Hq, Hkv, seed, reps=20):
+    """Prefill attention of the layer's first update (the flash-attn 2 call
+    it replaces): causal GQA over fp16 q/k/v [B, T, H, 128].  Work is the
+    causal half of QK^T and PV: 4 * B * Hq * 128 * T (T + 1) / 2 flops."""
+    from signrot_amd import _CUDA
+    st = torch.cuda.current_stream()
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(B, T, Hq, 128, device=dev, generator=g).half()
+    k = torch.randn(B, T, Hkv, 128, device=dev, generator=g).half()
+    v = torch.randn(B, T, Hkv, 128, device=dev, generator=g).half()
+    t = _time_launches(lambda i: _CUDA.prefill_attention(q, k, v), reps, st) * 1e3
+    flops = 4.0 * B * Hq * 128 * T * (T + 1) / 2
+    res = {"B": B, "T": T, "Hq": Hq, "Hkv": Hkv, "us": round(t, 2),
+           "TFLOP/s": round(flops / t * 1e-6, 1),
+           "mfma_frac_f16": round(flops / t * 1e-6 / 2500.0, 4)}
+    del q, k, v
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_configs(args, dev):
     """The BASELINE.json configs other than the headline one, each at its
-    own shape (configs[0], the cfg2 M sweep, configs[3], configs[4]), and the
-    cfg2 QLinear with asymmetric activations."""
+    own shape (configs[0], the cfg2 M sweep, configs[3], configs[4]), the cfg2
+    QLinear with asymmetric activations, and the prefill attention (Llama-70B
+    heads)."""
     out = {"cfg1_qproj_M16": bench_qlinear(dev, 16, 4096, 4096, args.seed + 10, n_out=4,
                                            mag=100.0),
            "cfg2_sweep": [bench_qlinear(dev, m, 14336, 4096, args.seed + 20 + m)
                           for m in (1, 16, 128, 2048, 8192)],
            "cfg2_asym_M2048": bench_qlinear_asym(dev, 2048, 14336, 4096, args.seed + 25),
            "cfg4_mlp70b": [bench_mlp70b(dev, m, args.seed + 30 + m) for m in (1, 32, 512, 4096)],
-           "cfg5_moe": bench_moe(dev, args.seed + 40)}
+           "cfg5_moe": bench_moe(dev, args.seed + 40),
+           "prefill_attention": [bench_prefill_attention(dev, 1, t, 64, 8, args.seed + 50 + t)
+                                 for t in (512, 2048, 8192)]}
     return out
 
 

@@ -286,6 +286,24 @@ int srq_head_had_quant(const void *x, int64_t batch, int64_t n_heads, int64_t he
                        float scale, float clip_ratio, void *q, void *qscale, void *rot,
                        void *stream);
 
+/* Causal (or full) grouped-query softmax attention over fp16 q
+ * [batch, seq_len, n_q_heads, 128] and k, v [batch, seq_len, n_kv_heads, 128]
+ * given by element strides per token and per sequence (last two dims dense,
+ * so q/k/v may be column slices of a fused projection output); q head h reads
+ * kv head h / (n_q_heads / n_kv_heads).  out f16 [batch, seq_len, n_q_heads,
+ * 128] dense.  attention_mask int32 [batch, seq_len] or NULL: keys at 0
+ * entries are dropped and the output rows at 0 entries are zero (the
+ * unpad / varlen / pad round trip of flash-attn).  Logits are
+ * q.k * sm_scale; fp32 softmax, P rounded to fp16 for the PV product.
+ * Replaces the prefill call of transformers' _flash_attention_forward
+ * (flash-attn 2) in e2e/quantized_llama/modeling_llama.py:81-90. */
+int srq_prefill_attention(const void *q, const void *k, const void *v,
+                          const int32_t *attention_mask, int64_t batch, int64_t seq_len,
+                          int64_t n_q_heads, int64_t n_kv_heads, int64_t head_dim,
+                          int64_t q_tok_stride, int64_t q_seq_stride, int64_t kv_tok_stride,
+                          int64_t kv_seq_stride, float sm_scale, int causal, void *out,
+                          void *stream);
+
 /* In-place rotary embedding of q f16 [n_seqs, seq_len, n_q_heads, head_dim]
  * and k f16 [n_seqs, seq_len, n_k_heads, head_dim] with cos, sin f16
  * [cos_batch, seq_len, head_dim] (cos_batch 1 or n_seqs); each of the three

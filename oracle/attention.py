@@ -107,3 +107,41 @@ def decode(q_f16, data, param, indptr, indices, last, layer):
             p = np.exp(logits - logits.max())
             out[b, h] = (p[:, None] * v[:, h // g, :]).sum(0) / p.sum()
     return out
+
+
+def prefill(q, k, v, mask=None, causal=True, sm_scale=None):
+    """Prefill attention (the flash-attn 2 call of e2e/quantized_llama/
+    modeling_llama.py:81-90 through transformers==4.57.6
+    _flash_attention_forward, a dependency absent from the reference tree).
+
+    q [B, T, Hq, D], k/v [B, T, Hkv, D] (any float dtype, promoted to
+    float64); q head h reads kv head h // (Hq // Hkv).  With mask [B, T]
+    (the HF attention_mask), the call unpads the valid tokens of each
+    sequence, runs varlen attention over them (causal = key position <=
+    query position among the valid tokens, since q and k lengths agree), and
+    pads the result back with zero rows; for one sequence that is: query i
+    (mask 1) attends keys j with mask[j] = 1 and j <= i; query rows with
+    mask 0 are zero.  Logits q.k * sm_scale (default 1/sqrt(D)).  Returns
+    float64 [B, T, Hq, D]."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    B, T, Hq, D = q.shape
+    Hkv = k.shape[2]
+    group = Hq // Hkv
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
+    out = np.zeros((B, T, Hq, D))
+    allowed = np.ones((T, T), bool)
+    if causal:
+        allowed = np.tril(allowed)
+    for b in range(B):
+        keep = np.ones(T, bool) if mask is None else np.asarray(mask[b]) != 0
+        ok = allowed & keep[None, :]
+        for h in range(Hq):
+            s = q[b, :, h] @ k[b, :, h // group].T * scale
+            s = np.where(ok, s, -np.inf)
+            rows = keep & ok.any(axis=1)
+            s = s[rows]
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            out[b, rows, h] = (p / p.sum(axis=1, keepdims=True)) @ v[b, :, h // group]
+    return out

@@ -34,7 +34,7 @@ def _stream(t):
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-def _check(name, tensors, dtypes=None):
+def _check(name, tensors, dtypes=None, contiguous=True):
     dev = None
     for i, (t, tname) in enumerate(tensors):
         if t is None:
@@ -44,7 +44,7 @@ def _check(name, tensors, dtypes=None):
         if t.device.type != "cuda":
             raise RuntimeError(
                 f"{name}: expected '{tname}' on a GPU device, got {t.device}")
-        if not t.is_contiguous():
+        if contiguous and not t.is_contiguous():
             raise RuntimeError(f"{name}: expected contiguous tensor for argument '{tname}'")
         if dev is None:
             dev = t.device
@@ -537,6 +537,47 @@ def head_had_quant(x, scale, clip_ratio=1.0, return_rot=False):
     _call("srq_head_had_quant", _ptr(x), B, H, D, float(scale), float(clip_ratio), _ptr(q),
           _ptr(qs), _ptr(rot), _stream(x))
     return (q, qs, rot) if return_rot else (q, qs)
+
+
+def prefill_attention(q, k, v, attention_mask=None, causal=True, softmax_scale=None):
+    """Prefill attention over fp16 q [B, T, Hq, 128], k/v [B, T, Hkv, 128]
+    -> out fp16 [B, T, Hq, 128]: the flash-attn 2 call of the layer's first
+    update (e2e/quantized_llama/modeling_llama.py:81-90).  q/k/v may be
+    strided views (dense last two dims, e.g. slices of a fused q/k/v
+    projection).  attention_mask [B, T] (HF layout, any integer or bool
+    dtype) drops the keys at 0 entries and zeroes those output rows."""
+    _check("prefill_attention", [(q, "q"), (k, "k"), (v, "v")],
+           [torch.float16, torch.float16, torch.float16], contiguous=False)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise RuntimeError("prefill_attention expects [B, T, H, D] q/k/v")
+    B, T, Hq, D = q.shape
+    if tuple(k.shape) != tuple(v.shape) or k.shape[0] != B or k.shape[1] != T or k.shape[3] != D:
+        raise RuntimeError("prefill_attention: k and v must be [B, T, Hkv, D] matching q")
+    if k.stride() != v.stride():
+        raise RuntimeError("prefill_attention: k and v must have the same strides")
+    for t, name in ((q, "q"), (k, "k")):
+        if t.stride(3) != 1 or t.stride(2) != D:
+            raise RuntimeError(f"prefill_attention: {name} must be dense in its last two dims")
+    mask = None
+    if attention_mask is not None:
+        if tuple(attention_mask.shape) != (B, T):
+            raise RuntimeError("prefill_attention: attention_mask must be [B, T]")
+        if attention_mask.device != q.device:
+            raise RuntimeError("prefill_attention: attention_mask is on another device")
+        mask = attention_mask.to(torch.int32).contiguous()
+    out = torch.empty(B, T, Hq, D, dtype=torch.float16, device=q.device)
+
+    def strides(t):
+        # a size-1 dim's stride is never used to address; give it the dense value
+        tok = t.stride(1) if T > 1 else t.shape[2] * D
+        return tok, (t.stride(0) if B > 1 else T * tok)
+
+    (q_tok, q_seq), (kv_tok, kv_seq) = strides(q), strides(k)
+    scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    _call("srq_prefill_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(mask), B, T, Hq, k.shape[2],
+          D, q_tok, q_seq, kv_tok, kv_seq, scale, 1 if causal else 0,
+          _ptr(out), _stream(q))
+    return out
 
 
 def rope_qk(q, k, cos, sin):

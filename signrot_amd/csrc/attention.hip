@@ -1,0 +1,256 @@
+// Prefill attention over fp16 q/k/v: the causal, grouped-query softmax
+// attention that the quantized Llama layer runs on the first (prefill) call
+// of a layer, where the reference calls flash-attn 2 through transformers'
+// _flash_attention_forward (e2e/quantized_llama/modeling_llama.py:81-90).
+// Key positions whose attention_mask entry is 0 are dropped and the output
+// rows of masked query positions are zero, which is what the unpad ->
+// varlen attention -> pad round trip of that call produces.
+//
+// One block = 4 waves = 128 query rows of one (sequence, q head); wave w
+// owns rows [32 w, 32 w + 32).  Everything is computed transposed so that
+// one lane owns one query row (column l % 32 of the MFMA output):
+//   S^T[key][q] = K_tile (64 x 128) . Q^T            fp16 MFMA 32x32x16
+//   O^T[d][q]  += V^T (128 x 64)  . P^T               fp16 MFMA 32x32x16
+// The MFMA output layout (lane l, register v -> row 8(v/4) + 4(l/32) + v%4,
+// column l%32) leaves each lane 16 keys of its own row per 32-key block, so
+// the running max / sum of the online softmax are in-lane values plus one
+// exchange with lane l ^ 32; P^T becomes the B operand of the PV product
+// straight from the lane's registers if the 16 k-slots of each PV step are
+// assigned to keys in that same order (k-slot j of lane half g <-> key
+// 8(j/4) + 4g + j%4 of the 16-key step), and V^T is read from LDS in the
+// matching order (two 8-byte reads per operand).  V is transposed once,
+// when the tile is stored to LDS.
+// Logits are q.k * sm_scale * log2(e); probabilities use exp2, P is rounded
+// to fp16 for the PV product (as flash-attn does), O and the row sum stay
+// fp32, and out = fp16(O / sum).
+#include "common.h"
+
+namespace {
+
+constexpr int HD = 128;          // head dim
+constexpr int QT = 128;          // query rows per block (4 waves x 32)
+constexpr int KT = 64;           // keys per tile
+constexpr int KS = HD + 8;       // Ks row stride (halves)
+constexpr int VS = KT + 8;       // Vt row stride (halves)
+
+struct AttnArgs {
+    const f16 *q, *k, *v;
+    const int32_t *mask;         // [B, T] or null
+    f16 *out;                    // [B, T, Hq, HD]
+    int64_t q_tok, q_seq;        // strides (elements) of q: token, sequence
+    int64_t kv_tok, kv_seq;      // strides of k and v
+    int T, Hq, group;            // group = Hq / Hkv
+    float c;                     // sm_scale * log2(e)
+    int causal;
+};
+
+SRQ_DEV v16f mfma32(v8h a, v8h b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
+    __shared__ __align__(16) f16 Ks[KT * KS];
+    __shared__ __align__(16) f16 Vt[HD * VS];
+    __shared__ float kbias[KT];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 5, ln = lane & 31;
+    // heaviest causal tiles first
+    const int qtile = a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int hq = blockIdx.y, b = blockIdx.z;
+    const int hk = hq / a.group;
+    const int q0 = qtile * QT;
+    const int qrow = q0 + wave * 32 + ln;          // this lane's query row
+    const int wave_last = q0 + wave * 32 + 31;     // last row of this wave
+
+    const f16 *qb = a.q + (int64_t)b * a.q_seq + (int64_t)hq * HD;
+    const f16 *kb = a.k + (int64_t)b * a.kv_seq + (int64_t)hk * HD;
+    const f16 *vb = a.v + (int64_t)b * a.kv_seq + (int64_t)hk * HD;
+    const int32_t *mb = a.mask ? a.mask + (int64_t)b * a.T : nullptr;
+
+    // Q^T as B operand: k-slot j of step kk <-> d = 16 kk + 8 g + j
+    v8h qf[HD / 16];
+    {
+        const bool ok = qrow < a.T;
+        const f16 *qr = qb + (int64_t)(ok ? qrow : 0) * a.q_tok + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < HD / 16; ++kk) {
+            v8h t = *reinterpret_cast<const v8h *>(qr + 16 * kk);
+            qf[kk] = ok ? t : (v8h)(f16)0;
+        }
+    }
+
+    v16f o[HD / 32];
+#pragma unroll
+    for (int i = 0; i < HD / 32; ++i) o[i] = (v16f)0.f;
+    float m = -INFINITY, l = 0.f;
+
+    const int kv_end = a.causal ? min(a.T, q0 + QT) : a.T;
+    const int ntiles = (kv_end + KT - 1) / KT;
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int k0 = t * KT;
+        __syncthreads();
+        // K tile, row-major: thread -> row tid / 4, 32 halves from (tid % 4) * 32
+        {
+            const int r = tid >> 2, d0 = (tid & 3) * 32;
+            const int key = k0 + r;
+            const bool ok = key < a.T;
+            const f16 *src = kb + (int64_t)(ok ? key : 0) * a.kv_tok + d0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v8h x = *reinterpret_cast<const v8h *>(src + 8 * i);
+                *reinterpret_cast<v8h *>(&Ks[r * KS + d0 + 8 * i]) = ok ? x : (v8h)(f16)0;
+            }
+        }
+        // V tile, transposed: thread -> keys 2 (tid % 32) + {0, 1}, d from 16 (tid / 32)
+        {
+            const int kp = tid & 31, d0 = (tid >> 5) * 16;
+            const int key = k0 + 2 * kp;
+            const bool ok0 = key < a.T, ok1 = key + 1 < a.T;
+            const f16 *s0 = vb + (int64_t)(ok0 ? key : 0) * a.kv_tok + d0;
+            const f16 *s1 = vb + (int64_t)(ok1 ? key + 1 : 0) * a.kv_tok + d0;
+            v8h x0[2], x1[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                v8h u0 = *reinterpret_cast<const v8h *>(s0 + 8 * i);
+                v8h u1 = *reinterpret_cast<const v8h *>(s1 + 8 * i);
+                x0[i] = ok0 ? u0 : (v8h)(f16)0;
+                x1[i] = ok1 ? u1 : (v8h)(f16)0;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                v2h pr;
+                pr[0] = x0[j / 8][j % 8];
+                pr[1] = x1[j / 8][j % 8];
+                *reinterpret_cast<v2h *>(&Vt[(d0 + j) * VS + 2 * kp]) = pr;
+            }
+        }
+        if (tid < KT) {
+            const int key = k0 + tid;
+            const bool ok = key < a.T && (!mb || mb[key] != 0);
+            kbias[tid] = ok ? 0.f : -INFINITY;
+        }
+        __syncthreads();
+        if (a.causal && k0 > wave_last) continue;   // no key of this tile is visible
+
+        // S^T, two 32-key blocks
+        v16f s[2];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb) {
+            s[sb] = (v16f)0.f;
+            const f16 *kr = &Ks[(32 * sb + ln) * KS + 8 * g];
+#pragma unroll
+            for (int kk = 0; kk < HD / 16; ++kk)
+                s[sb] = mfma32(*reinterpret_cast<const v8h *>(kr + 16 * kk), qf[kk], s[sb]);
+        }
+        // scale, mask, tile max
+        float mt = -INFINITY;
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int kr = 32 * sb + 8 * (v / 4) + 4 * g + (v % 4);
+                float x = s[sb][v] * a.c + kbias[kr];
+                if (a.causal && k0 + kr > qrow) x = -INFINITY;
+                s[sb][v] = x;
+                mt = fmaxf(mt, x);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m, mt);
+        const float mu = mn == -INFINITY ? 0.f : mn;
+        const float alpha = __builtin_amdgcn_exp2f(m - mu);
+        m = mn;
+        float ps = 0.f;
+        v8h pb[4];
+#pragma unroll
+        for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const float p = __builtin_amdgcn_exp2f(s[sb][v] - mu);
+                ps += p;
+                pb[2 * sb + v / 8][v % 8] = (f16)p;
+            }
+        l = l * alpha + ps;
+#pragma unroll
+        for (int i = 0; i < HD / 32; ++i) o[i] *= alpha;
+        // O^T += V^T P^T; PV step st covers keys 16 st .. 16 st + 15 of the tile
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+            for (int db = 0; db < HD / 32; ++db) {
+                const f16 *vr = &Vt[(32 * db + ln) * VS + 16 * st + 4 * g];
+                v4h lo = *reinterpret_cast<const v4h *>(vr);
+                v4h hi = *reinterpret_cast<const v4h *>(vr + 8);
+                v8h av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o[db] = mfma32(av, pb[st], o[db]);
+            }
+    }
+
+    if (qrow >= a.T) return;
+    l += __shfl_xor(l, 32);
+    const bool live = (!mb || mb[qrow] != 0) && l > 0.f;
+    const float inv = live ? 1.f / l : 0.f;
+    f16 *orow = a.out + ((int64_t)b * a.T + qrow) * ((int64_t)a.Hq * HD) + (int64_t)hq * HD;
+#pragma unroll
+    for (int db = 0; db < HD / 32; ++db)
+#pragma unroll
+        for (int grp = 0; grp < 4; ++grp) {
+            v4h r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = (f16)(o[db][4 * grp + i] * inv);
+            *reinterpret_cast<v4h *>(orow + 32 * db + 8 * grp + 4 * g) = r;
+        }
+}
+
+}  // namespace
+
+extern "C" int srq_prefill_attention(const void *q, const void *k, const void *v,
+                                     const int32_t *attention_mask, int64_t batch,
+                                     int64_t seq_len, int64_t n_q_heads, int64_t n_kv_heads,
+                                     int64_t head_dim, int64_t q_tok_stride,
+                                     int64_t q_seq_stride, int64_t kv_tok_stride,
+                                     int64_t kv_seq_stride, float sm_scale, int causal,
+                                     void *out, void *stream) {
+    SRQ_CHECK_ARG(batch >= 0 && seq_len >= 0 && n_q_heads >= 0 && n_kv_heads > 0,
+                  "prefill_attention: bad shape");
+    SRQ_CHECK_ARG(head_dim == HD, "prefill_attention: head_dim=%lld, only 128 is supported",
+                  (long long)head_dim);
+    SRQ_CHECK_ARG(n_q_heads % n_kv_heads == 0,
+                  "prefill_attention: n_q_heads=%lld is not a multiple of n_kv_heads=%lld",
+                  (long long)n_q_heads, (long long)n_kv_heads);
+    if (batch == 0 || seq_len == 0 || n_q_heads == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(q && k && v && out, "prefill_attention: null pointer");
+    SRQ_CHECK_ARG(seq_len <= (1 << 30) && n_q_heads <= 65535 && batch <= 65535,
+                  "prefill_attention: shape out of range");
+    SRQ_CHECK_ARG(q_tok_stride >= n_q_heads * HD && kv_tok_stride >= n_kv_heads * HD &&
+                      q_seq_stride >= seq_len * q_tok_stride &&
+                      kv_seq_stride >= seq_len * kv_tok_stride,
+                  "prefill_attention: strides smaller than the [B, T, H, 128] extent");
+    SRQ_CHECK_ARG(q_tok_stride % 8 == 0 && kv_tok_stride % 8 == 0 && q_seq_stride % 8 == 0 &&
+                      kv_seq_stride % 8 == 0,
+                  "prefill_attention: strides must be multiples of 8 elements");
+    SRQ_CHECK_ARG(srq_aligned(q, 16) && srq_aligned(k, 16) && srq_aligned(v, 16) &&
+                      srq_aligned(out, 16),
+                  "prefill_attention: q, k, v and out must be 16-byte aligned");
+    AttnArgs a;
+    a.q = (const f16 *)q;
+    a.k = (const f16 *)k;
+    a.v = (const f16 *)v;
+    a.mask = attention_mask;
+    a.out = (f16 *)out;
+    a.q_tok = q_tok_stride;
+    a.q_seq = q_seq_stride;
+    a.kv_tok = kv_tok_stride;
+    a.kv_seq = kv_seq_stride;
+    a.T = (int)seq_len;
+    a.Hq = (int)n_q_heads;
+    a.group = (int)(n_q_heads / n_kv_heads);
+    a.c = sm_scale * 1.4426950408889634f;
+    a.causal = causal ? 1 : 0;
+    dim3 grid((unsigned)srq_cdiv(seq_len, QT), (unsigned)n_q_heads, (unsigned)batch);
+    prefill_attn_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a);
+    SRQ_LAUNCH_CHECK("prefill_attention");
+    return SRQ_OK;
+}

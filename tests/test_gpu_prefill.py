@@ -1,0 +1,110 @@
+"""GPU parity of the prefill attention (the flash-attn 2 call of
+e2e/quantized_llama/modeling_llama.py:81-90) against the float64 oracle,
+tolerance 1e-2 abs + rel (fp16 inputs and output, P rounded to fp16 as in
+flash-attn); masked query rows are exactly zero."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from tests.gpu_util import to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def C():
+    from signrot_amd import _CUDA
+    return _CUDA
+
+
+def _inputs(B, T, Hq, Hkv, seed, mag=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = (torch.randn(B, T, Hq, 128, generator=g) * mag).half()
+    k = (torch.randn(B, T, Hkv, 128, generator=g) * mag).half()
+    v = torch.randn(B, T, Hkv, 128, generator=g).half()
+    return q, k, v
+
+
+def _check(got, q, k, v, mask, causal, what):
+    want = oa.prefill(q.numpy(), k.numpy(), v.numpy(), None if mask is None else mask.numpy(),
+                      causal)
+    got = to_np(got).astype(np.float64)
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2, err_msg=what)
+    if mask is not None:
+        dead = mask.numpy() == 0
+        assert np.all(got[dead] == 0), what
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,causal,masked", [
+    (1, 1, 4, 4, True, False), (2, 77, 8, 2, True, True), (1, 128, 4, 1, True, False),
+    (1, 129, 2, 2, True, False), (1, 300, 32, 8, True, False), (2, 200, 4, 4, False, True),
+    (1, 1031, 8, 8, True, False), (3, 65, 6, 3, False, False)])
+def test_prefill_matches_oracle(C, B, T, Hq, Hkv, causal, masked):
+    q, k, v = _inputs(B, T, Hq, Hkv, seed=T * 7 + B)
+    mask = None
+    if masked:
+        mask = torch.ones(B, T, dtype=torch.int64)
+        mask[0, : T // 3] = 0                   # left padding
+        if B > 1:
+            mask[1, 1::5] = 0                   # holes
+    dev = "cuda:0"
+    out = C.prefill_attention(q.to(dev), k.to(dev), v.to(dev),
+                              None if mask is None else mask.to(dev), causal)
+    torch.cuda.synchronize()
+    _check(out, q, k, v, mask, causal, f"B={B} T={T} Hq={Hq} Hkv={Hkv} causal={causal}")
+
+
+def test_prefill_large_logits(C):
+    """Logits far above 1 (|q.k| * scale in the hundreds): the running max
+    keeps exp2 in range."""
+    q, k, v = _inputs(1, 333, 4, 2, seed=5, mag=6.0)
+    out = C.prefill_attention(q.cuda(), k.cuda(), v.cuda())
+    torch.cuda.synchronize()
+    _check(out, q, k, v, None, True, "large logits")
+
+
+def test_prefill_strided_qkv_slices(C):
+    """q/k/v as column slices of one fused projection output."""
+    B, T, Hq, Hkv = 2, 150, 8, 2
+    g = torch.Generator().manual_seed(9)
+    qkv = torch.randn(B, T, (Hq + 2 * Hkv) * 128, generator=g).half().cuda()
+    q = qkv[..., : Hq * 128].view(B, T, Hq, 128)
+    k = qkv[..., Hq * 128:(Hq + Hkv) * 128].view(B, T, Hkv, 128)
+    v = qkv[..., (Hq + Hkv) * 128:].view(B, T, Hkv, 128)
+    got = C.prefill_attention(q, k, v)
+    want = C.prefill_attention(q.contiguous(), k.contiguous(), v.contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    _check(got, q.cpu(), k.cpu(), v.cpu(), None, True, "strided")
+
+
+def test_prefill_full_size_vs_fp32(C):
+    """Llama-70B heads at T = 2048 against a float32 torch reference on the
+    GPU (per kv-head group, explicit matmuls), tolerance 1e-2."""
+    B, T, Hq, Hkv = 1, 2048, 64, 8
+    g = torch.Generator(device="cuda:0").manual_seed(1)
+    q = torch.randn(B, T, Hq, 128, device="cuda:0", generator=g).half()
+    k = torch.randn(B, T, Hkv, 128, device="cuda:0", generator=g).half()
+    v = torch.randn(B, T, Hkv, 128, device="cuda:0", generator=g).half()
+    out = C.prefill_attention(q, k, v).float()
+    causal = torch.ones(T, T, dtype=torch.bool, device="cuda:0").tril()
+    G = Hq // Hkv
+    for h in range(0, Hq, 9):
+        qh = q[0, :, h].float()
+        kh = k[0, :, h // G].float()
+        vh = v[0, :, h // G].float()
+        s = (qh @ kh.t().contiguous()) * 128 ** -0.5
+        s = s.masked_fill(~causal, float("-inf"))
+        ref = torch.softmax(s, dim=-1) @ vh
+        torch.testing.assert_close(out[0, :, h], ref, rtol=1e-2, atol=1e-2)
+
+
+def test_prefill_rejects_bad_shapes(C):
+    q = torch.zeros(1, 4, 4, 64, dtype=torch.float16, device="cuda:0")
+    with pytest.raises(RuntimeError, match="head_dim"):
+        C.prefill_attention(q, q, q)
+    q = torch.zeros(1, 4, 6, 128, dtype=torch.float16, device="cuda:0")
+    k = torch.zeros(1, 4, 4, 128, dtype=torch.float16, device="cuda:0")
+    with pytest.raises(RuntimeError, match="multiple"):
+        C.prefill_attention(q, k, k)

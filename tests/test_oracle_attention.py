@@ -112,3 +112,64 @@ def test_decode_page_permutation_invariance():
     param2[perm] = param
     got = oa.decode(q, data2, param2, indptr, perm[indices].astype(np.int32), last, 1)
     np.testing.assert_array_equal(got, ref)
+
+
+# ---------------------------------------------------------------- prefill
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,causal", [(2, 33, 4, 2, True), (1, 70, 2, 2, False),
+                                               (2, 17, 8, 1, True)])
+def test_prefill_matches_torch_sdpa(B, T, Hq, Hkv, causal):
+    rng = np.random.default_rng(B * 100 + T)
+    q = rng.standard_normal((B, T, Hq, 128))
+    k = rng.standard_normal((B, T, Hkv, 128))
+    v = rng.standard_normal((B, T, Hkv, 128))
+    mask = (rng.random((B, T)) > 0.25).astype(np.int32)
+    mask[:, 0] = 1
+    got = oa.prefill(q, k, v, mask, causal)
+    G = Hq // Hkv
+    for b in range(B):
+        qq = torch.from_numpy(q[b]).permute(1, 0, 2)
+        kk = torch.from_numpy(k[b]).permute(1, 0, 2).repeat_interleave(G, dim=0)
+        vv = torch.from_numpy(v[b]).permute(1, 0, 2).repeat_interleave(G, dim=0)
+        allow = torch.from_numpy(mask[b] != 0)[None, :].expand(T, T)
+        if causal:
+            allow = allow & torch.ones(T, T, dtype=torch.bool).tril()
+        ref = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, attn_mask=allow)
+        ref = ref.permute(1, 0, 2).numpy()
+        live = mask[b] != 0
+        np.testing.assert_allclose(got[b][live], ref[live], rtol=1e-10, atol=1e-10)
+        assert np.all(got[b][~live] == 0)
+
+
+def test_prefill_closed_forms():
+    T, D = 9, 128
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal((1, T, 1, D))
+    q = rng.standard_normal((1, T, 1, D))
+    k = np.zeros((1, T, 1, D))           # equal logits: causal cumulative mean
+    got = oa.prefill(q, k, v)
+    want = np.cumsum(v[0, :, 0], axis=0) / np.arange(1, T + 1)[:, None]
+    np.testing.assert_allclose(got[0, :, 0], want, rtol=1e-12)
+    # a key far above the rest takes all the weight once it is visible
+    k2 = np.zeros((1, T, 1, D))
+    k2[0, 4, 0] = 50.0
+    q2 = np.ones((1, T, 1, D))
+    got2 = oa.prefill(q2, k2, v)
+    np.testing.assert_allclose(got2[0, 4:, 0], np.broadcast_to(v[0, 4, 0], (T - 4, D)),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_prefill_left_padding_is_unpadding():
+    """A left-padded sequence gives, on its valid rows, the attention of the
+    unpadded sequence alone (the unpad / varlen / pad round trip)."""
+    rng = np.random.default_rng(11)
+    T, pad = 20, 6
+    q = rng.standard_normal((1, T, 2, 128))
+    k = rng.standard_normal((1, T, 1, 128))
+    v = rng.standard_normal((1, T, 1, 128))
+    mask = np.ones((1, T), np.int32)
+    mask[0, :pad] = 0
+    got = oa.prefill(q, k, v, mask)
+    alone = oa.prefill(q[:, pad:], k[:, pad:], v[:, pad:])
+    np.testing.assert_allclose(got[0, pad:], alone[0], rtol=1e-12, atol=1e-12)
+    assert np.all(got[0, :pad] == 0)
