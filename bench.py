@@ -52,6 +52,9 @@ def parse():
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run plain device copies of a known size (the reference "
                         "kernel for scaling the FETCH_SIZE / WRITE_SIZE counters)")
+    p.add_argument("--prefill-attention-only", action="store_true",
+                   help="only measure the prefill attention (Llama-70B heads, T = 512, "
+                        "2048, 8192) and print its results")
     p.add_argument("--cpu-rows", type=int, default=256,
                    help="rows of the CPU baseline sample")
     p.add_argument("--min-bytes", type=float, default=640e6,
@@ -502,6 +505,11 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.prefill_attention_only:
+        for t in (512, 2048, 8192):
+            print(json.dumps(bench_prefill_attention(dev, 1, t, 64, 8, args.seed + 50 + t)),
+                  flush=True)
+        return
     if args.calibrate_copy:
         calibrate_copy(dev)
         return
