@@ -67,7 +67,7 @@ def make_inputs(args, dev):
     sign from the calibration rule on the rotated X; W N(0, 0.02) fp16 with
     the sign folded by column, RTN per-channel symmetric int4."""
     from signrot_amd import _CUDA
-    from signrot_amd.functional.hadamard import get_hadK
+    from signrot_amd.functional.hadamard import adj_sign_from_rotated, get_hadK
     from signrot_amd.functional.quantization import rtn_weight_pack
 
     M, K, N = args.M, args.K, args.N
@@ -80,9 +80,7 @@ def make_inputs(args, dev):
     had, k = get_hadK(K)
     hadk = had.half().to(dev).contiguous() if k > 1 else None
     # sign-adjust vector (fake_quant/quant_utils.py:362-367) on the rotated X
-    rot = _CUDA.online_hadamard(x, hadk, k, None)
-    t = rot.abs().amax(dim=-1).argmax()
-    sign = ((rot[t] >= 0).to(torch.int8) * 2 - 1).contiguous()
+    sign = adj_sign_from_rotated(_CUDA.online_hadamard(x, hadk, k, None)).contiguous()
     # weights: N(0, 0.02), fold sign, RTN on the symmetric grid (A18 rule)
     w = (torch.randn(N, K, generator=g) * 0.02).half().to(dev)
     wq, s16, wfq = rtn_weight_pack(w * sign, symmetric_grid=True)
@@ -140,8 +138,7 @@ def bench_decode_layer(args, dev):
                                     generator=gen))
     cache.scales[..., 0].uniform_(0.02, 0.3, generator=gen)
     cache.scales[..., 1].uniform_(-2.0, 2.0, generator=gen)
-    cache.length = T
-    cache._needs_init = [False] * NL
+    cache.mark_prefilled(T)
     h0 = (torch.randn(B, 1, hidden, device=dev, generator=gen) * 0.5).half()
     cos, sin = rope_cos_sin([T], D, layers[0].rope_theta, dev)
     # the reference's graph protocol (kv_cache.py:435-460): index buffers are
@@ -404,7 +401,7 @@ def bench_moe(dev, seed, tokens=512, hidden=4096, ffn=14336, experts=8, top_k=2,
     st = torch.cuda.current_stream()
     with torch.no_grad():
         t = _time_launches(lambda i: blk(xs[i % len(xs)]), reps, st) * 1e3
-        _, _, perm, counts, _ = blk.route(xs[0].view(-1, hidden))
+        counts = blk.route(xs[0].view(-1, hidden)).counts
     rows = tokens * top_k
     ops = 2.0 * rows * 3 * hidden * ffn
     nbytes = 3 * experts * ffn * hidden // 2

@@ -70,7 +70,7 @@ int srq_kv_quant_pack(const void *x, int64_t rows, int64_t cols,
 /* ------------------------------------------------------------------- GEMM */
 
 /* C i32 [M, N] = A · Bᵀ over packed int4 A u8 [M, K/2], B u8 [N, K/2].
- * K % 32 == 0, K <= 131072; A, B 16-byte aligned.
+ * K % 32 == 0, K < 131072 (int32 accumulator bound); A, B 16-byte aligned.
  * Replaces _CUDA.matmul (bindings.cpp:13-29, gemm.cu:7-45). */
 int srq_matmul_s4s4(const void *A, const void *B, int64_t M, int64_t N, int64_t K,
                     int32_t *C, void *stream);
@@ -369,7 +369,7 @@ int srq_matmul_colrow_i8_i32(const int8_t *a_col, const int32_t *b_row, int64_t 
  * (m, n, k) = problem_sizes[3p .. 3p+2] (int32), A at ptr_A[p] (packed int4,
  * row stride lda[p] codes), B at ptr_B[p] (packed int4 [n, k/2], row stride
  * ldb[p] codes), and writes C_p[i * ldc[p] + j] = sum_k A_p[i,k] B_p[j,k]
- * (int32) at ptr_C[p].  Each k must be a multiple of 32 and <= 131072 (not
+ * (int32) at ptr_C[p].  Each k must be a multiple of 32 and < 131072 (not
  * checkable on the host).  signed_a == 0: A holds unsigned asymmetric codes
  * (0..15), as matmul_ui4_si4.  Per element identical to srq_matmul_s4s4
  * (srq_matmul_u4s4) on each problem.

@@ -24,10 +24,13 @@ def half2int_rn(h):
 def sym_scale(x_f16, clip_ratio=1.0):
     """Per-row scale of sym_quant_dynamic_kernel (signrot/kernels/fused.cu:
     80-95): amax = max|x| (exact), scale = fp16(amax / 7.f); if clip != 1,
-    scale = fp16(float(scale) * clip)."""
+    scale = fp16(float(scale) * clip).  The reduction is fmaxf from 0.f
+    (fused.cu:83-88, 17-21): NaN values are skipped, so an all-NaN row has
+    amax 0 and scale 0, and an inf makes the scale inf."""
     x = np.asarray(x_f16, dtype=F16)
-    amax = np.abs(x.astype(F32)).max(axis=-1) if x.shape[-1] else np.zeros(x.shape[:-1], F32)
-    scale = (amax.astype(F32) / F32(7.0)).astype(F16)
+    amax = np.fmax.reduce(np.abs(x.astype(F32)), axis=-1, initial=F32(0.0))
+    with np.errstate(over="ignore"):
+        scale = (amax.astype(F32) / F32(7.0)).astype(F16)
     if clip_ratio != 1.0:
         scale = (scale.astype(F32) * F32(clip_ratio)).astype(F16)
     return scale
@@ -125,17 +128,23 @@ def kv_quant_pack(x_f16):
       hmin, hmax exact; diff = fp16(hmax - hmin); diff = fp16(max(diff, 1e-5));
       scale = fp16(diff / 15); zero = -hmin;
       q = clamp(rne(fp16(fp16(x + zero) / scale)), 0, 15), packed low-first.
+    The row max / min are fmaxf / fminf from -FLT_MAX / FLT_MAX
+    (fused.cu:236-245, 17-28): NaN values are skipped (an all-NaN row gives
+    hmax = fp16(-FLT_MAX) = -inf, hmin = +inf), the 1e-5 clamp is fmaxf too
+    (a NaN difference becomes 1e-5), and a NaN quotient gives code 0.
     Returns (u8 [..., D/2], f16 param [..., 2] = [scale, zero])."""
     x = np.asarray(x_f16, dtype=F16)
     xf = x.astype(F32)
-    hmax = xf.max(axis=-1, keepdims=True)
-    hmin = xf.min(axis=-1, keepdims=True)
-    diff = (hmax - hmin).astype(F16).astype(F32)
-    diff = np.maximum(diff, F32(1e-5)).astype(F16).astype(F32)
-    scale = (diff / F32(15.0)).astype(F16)
-    zero = (-hmin).astype(F16)
-    shifted = (xf + zero.astype(F32)).astype(F16).astype(F32)
+    fmax32 = np.finfo(F32).max
+    with np.errstate(over="ignore", invalid="ignore"):
+        hmax = np.fmax.reduce(xf, axis=-1, keepdims=True, initial=-fmax32).astype(F16)
+        hmin = np.fmin.reduce(xf, axis=-1, keepdims=True, initial=fmax32).astype(F16)
+        diff = (hmax.astype(F32) - hmin.astype(F32)).astype(F16).astype(F32)
+        diff = np.fmax(diff, F32(1e-5)).astype(F16).astype(F32)
+        scale = (diff / F32(15.0)).astype(F16)
+    zero = -hmin
     with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        shifted = (xf + zero.astype(F32)).astype(F16).astype(F32)
         scaled = (shifted / scale.astype(F32)).astype(F16)
     q = np.clip(half2int_rn(scaled), 0, 15).astype(np.uint8)
     packed = (q[..., 0::2] | (q[..., 1::2] << 4)).astype(np.uint8)

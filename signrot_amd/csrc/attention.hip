@@ -4,7 +4,10 @@
 // _flash_attention_forward (e2e/quantized_llama/modeling_llama.py:81-90).
 // Key positions whose attention_mask entry is 0 are dropped and the output
 // rows of masked query positions are zero, which is what the unpad ->
-// varlen attention -> pad round trip of that call produces.
+// varlen attention -> pad round trip of that call produces.  Masked keys and
+// masked query rows are never read (their K, V and q stage as zeros), so
+// whatever a padded position holds, NaN or inf included, cannot reach a
+// live row -- the unpad step of the reference never reads them either.
 //
 // One block = 4 waves = 128 query rows of one (sequence, q head); wave w
 // owns rows [32 w, 32 w + 32).  Everything is computed transposed so that
@@ -72,7 +75,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
     // Q^T as B operand: k-slot j of step kk <-> d = 16 kk + 8 g + j
     v8h qf[HD / 16];
     {
-        const bool ok = qrow < a.T;
+        const bool ok = qrow < a.T && (!mb || mb[qrow] != 0);
         const f16 *qr = qb + (int64_t)(ok ? qrow : 0) * a.q_tok + 8 * g;
 #pragma unroll
         for (int kk = 0; kk < HD / 16; ++kk) {
@@ -96,7 +99,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
         {
             const int r = tid >> 2, d0 = (tid & 3) * 32;
             const int key = k0 + r;
-            const bool ok = key < a.T;
+            const bool ok = key < a.T && (!mb || mb[key] != 0);
             const f16 *src = kb + (int64_t)(ok ? key : 0) * a.kv_tok + d0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -108,7 +111,8 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
         {
             const int kp = tid & 31, d0 = (tid >> 5) * 16;
             const int key = k0 + 2 * kp;
-            const bool ok0 = key < a.T, ok1 = key + 1 < a.T;
+            const bool ok0 = key < a.T && (!mb || mb[key] != 0);
+            const bool ok1 = key + 1 < a.T && (!mb || mb[key + 1] != 0);
             const f16 *s0 = vb + (int64_t)(ok0 ? key : 0) * a.kv_tok + d0;
             const f16 *s1 = vb + (int64_t)(ok1 ? key + 1 : 0) * a.kv_tok + d0;
             v8h x0[2], x1[2];
@@ -152,7 +156,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int kr = 32 * sb + 8 * (v / 4) + 4 * g + (v % 4);
-                float x = s[sb][v] * a.c + kbias[kr];
+                float x = kbias[kr] == 0.f ? s[sb][v] * a.c : -INFINITY;
                 if (a.causal && k0 + kr > qrow) x = -INFINITY;
                 s[sb][v] = x;
                 mt = fmaxf(mt, x);

@@ -119,14 +119,16 @@ SRQ_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t bytes) {
 // lane l's 16 (dma16) or 4 (dma4) bytes from buffer offset voff land at LDS
 // byte address lds + 16 l (resp. + 4 l).  They count in vmcnt like any vector
 // load; the caller waits with an explicit s_waitcnt before reading the LDS.
+// The LDS base goes in M0 as a "{m0}" operand, so the compiler sets M0 itself
+// and knows the register is taken (nothing it keeps in M0 is overwritten).
 SRQ_DEV void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :: "s"(lds), "v"(voff), "s"(r) : "memory");
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :: "v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 
 SRQ_DEV void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-                 :: "s"(lds), "v"(voff), "s"(r) : "memory");
+    asm volatile("buffer_load_dword %0, %1, 0 offen lds"
+                 :: "v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 
 // ------------------------------------------------------- fp16 rounding

@@ -11,7 +11,8 @@
 //   hi(w) =  w       & 0xF0F0F0F0   -> bytes 16 * (high nibbles)
 // are int8 values equal to 16x the signed codes, with no sign-extension
 // work.  The MFMA then accumulates 256 * sum(a*b) exactly (|.| <= 2^14 * K <
-// 2^31 for K <= 131072) and the epilogue shifts right by 8.  The lo/hi split
+// 2^31 for K < 131072; K = 131072 with every code -8 reaches 2^31 and would
+// wrap, so K <= 131040) and the epilogue shifts right by 8.  The lo/hi split
 // permutes K inside each 16-element group; A and B go through the same
 // permutation, so the integer dot product is unchanged -- bit-exact.
 //
@@ -1164,7 +1165,7 @@ int check_gemm(const char *name, const void *A, const void *B, int64_t M, int64_
                int64_t K) {
     SRQ_CHECK_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative shape", name);
     SRQ_CHECK_ARG(K % 32 == 0, "%s: K=%lld must be a multiple of 32", name, (long long)K);
-    SRQ_CHECK_ARG(K <= 131072, "%s: K=%lld > 131072 (int32 accumulator bound)", name,
+    SRQ_CHECK_ARG(K < 131072, "%s: K=%lld >= 131072 (int32 accumulator bound)", name,
                   (long long)K);
     SRQ_CHECK_ARG(M <= 0x7fffffffLL && N <= 0x7fffffffLL, "%s: M or N > 2^31-1", name);
     // operands are read through 32-bit-offset buffer resources
@@ -1351,8 +1352,8 @@ extern "C" int srq_w4a4_linear_moe(const void *A, const void *a_scale, const voi
                                    void *out, void *stream) {
     SRQ_CHECK_ARG(num_experts >= 0 && num_experts <= 0x7fffffffLL && rows >= 0 && N >= 0 &&
                       K >= 0, "w4a4_linear_moe: bad shape");
-    SRQ_CHECK_ARG(K % 32 == 0 && K <= 131072, "w4a4_linear_moe: K=%lld must be a multiple of "
-                  "32 and <= 131072", (long long)K);
+    SRQ_CHECK_ARG(K % 32 == 0 && K < 131072, "w4a4_linear_moe: K=%lld must be a multiple of "
+                  "32 and < 131072", (long long)K);
     if (num_experts == 0 || rows == 0 || N == 0) return SRQ_OK;
     if (rows * (K / 2) >= 0xFFFFFFF0LL || N * (K / 2) >= 0xFFFFFFF0LL) {
         srq_set_error("w4a4_linear_moe: operand larger than 4 GiB");
@@ -1384,8 +1385,8 @@ extern "C" int srq_w4a4_linear_moe_asym(const void *A, const void *a_scale, cons
                                         void *stream) {
     SRQ_CHECK_ARG(num_experts >= 0 && num_experts <= 0x7fffffffLL && rows >= 0 && N >= 0 &&
                       K >= 0, "w4a4_linear_moe_asym: bad shape");
-    SRQ_CHECK_ARG(K % 32 == 0 && K <= 131072, "w4a4_linear_moe_asym: K=%lld must be a multiple of "
-                  "32 and <= 131072", (long long)K);
+    SRQ_CHECK_ARG(K % 32 == 0 && K < 131072, "w4a4_linear_moe_asym: K=%lld must be a multiple of "
+                  "32 and < 131072", (long long)K);
     if (num_experts == 0 || rows == 0 || N == 0) return SRQ_OK;
     if (rows * (K / 2) >= 0xFFFFFFF0LL || N * (K / 2) >= 0xFFFFFFF0LL) {
         srq_set_error("w4a4_linear_moe_asym: operand larger than 4 GiB");

@@ -113,6 +113,28 @@ SRQ_DEV void quant_store(const u32 (&w)[4][8], float rcp, uint8_t *qrow) {
         }
 }
 
+// The same codes for a row holding a NaN or inf (after the rotation), by the
+// exact per-element arithmetic: the quotient of the packed route is NaN there
+// and would not give the reference's code 0.  r = 1 / s is inf for s == 0
+// and 0 for s == inf, so x * r behaves as the reference's x / s.
+SRQ_DEV void quant_store_exact(const u32 (&w)[4][8], float s, uint8_t *qrow) {
+    const float r = sym_recip(s);
+#pragma unroll
+    for (int i1 = 0; i1 < 4; ++i1)
+#pragma unroll
+        for (int u = 0; u < 4; u += 2) {
+            u32 c = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const v2h pr = __builtin_bit_cast(v2h, w[i1][2 * u + e / 2]);
+                c |= (u32)(sym_code_r((float)pr[e & 1], r) & 0xF) << (4 * e);
+            }
+            uint8_t *p = qrow + i1 * 64 + 4 * u;
+            *reinterpret_cast<uint16_t *>(p) = (uint16_t)c;
+            *reinterpret_cast<uint16_t *>(p + 4) = (uint16_t)(c >> 16);
+        }
+}
+
 // Asymmetric uint4 codes of the same values (MODE 2), same staging layout:
 // FAST, the packed route (finite row, s > 0, |zi| <= 511); otherwise each
 // code by the exact per-element arithmetic (asym_code).
@@ -162,9 +184,9 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
     __shared__ v4i rowbuf[NT * 8 * 64];
     // codes of one row for coalesced stores: chunk c's 256 bytes at 272 c
     __shared__ v4i cbuf[MODE >= 1 ? NT * 8 * 17 : 1];
-    // row reduction, double-buffered by row parity: MODE 1 max |x| per wave;
-    // MODE 2 min, max and the non-finite flag per wave
-    __shared__ float red[2][MODE == 2 ? 12 : 4];
+    // row reduction, double-buffered by row parity: MODE 1 max |x| and the
+    // non-finite flag per wave; MODE 2 min, max and the non-finite flag
+    __shared__ float red[2][MODE == 2 ? 12 : 8];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nt = wave;
@@ -457,10 +479,10 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
         finish(dprev, NT - 1);
 
         // ---- K-mix: round to fp16, apply the sign, keep; row max of |out|
-        // (MODE 2: packed min and max of the signed fp16 values -- NaN-
-        // ignoring, as the reference's fminf / fmaxf -- and a NaN-propagating
-        // max of |x| that flags non-finite rows; lanes past the K chunks
-        // hold no outputs and stay out)
+        // (NaN-ignoring, as the reference's fmaxf).  MODE 2: packed min and
+        // max of the signed fp16 values (NaN-ignoring, as fminf / fmaxf).
+        // MODE 1 and 2: a NaN-propagating max of |x| that flags rows with a
+        // NaN or inf; lanes past the K chunks hold no outputs and stay out.
         u32 w[P][4][8];
         float amax = 0.f;
         v2h mn2 = (v2h){(f16)__builtin_inff(), (f16)__builtin_inff()};
@@ -476,10 +498,12 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
                 for (int p = 0; p < 8; ++p) {
                     if (MODE != 2) amax = absmax3(amax, z[2 * p], z[2 * p + 1]);
                     w[h][i1][p] = pk16(z[2 * p], z[2 * p + 1]) ^ msk[h][i1][p];
-                    if (MODE == 2 && ln < a.KC) {
+                    if (MODE >= 1 && ln < a.KC) {
                         const v2h v = __builtin_bit_cast(v2h, w[h][i1][p]);
-                        mn2 = __builtin_elementwise_min(mn2, v);
-                        mx2 = __builtin_elementwise_max(mx2, v);
+                        if (MODE == 2) {
+                            mn2 = __builtin_elementwise_min(mn2, v);
+                            mx2 = __builtin_elementwise_max(mx2, v);
+                        }
                         ab2 = __builtin_elementwise_maximum(ab2, __builtin_elementwise_abs(v));
                     }
                 }
@@ -516,12 +540,19 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
             // ---- block row max (this barrier also ends every wave's LDS
             // reads of the row, so the prefetched row may be written after)
             amax = wave_max_dpp(amax);
-            if (lane == 0) red[it & 1][wave] = amax;
+            const bool badl = !((float)ab2[0] <= 65504.f) || !((float)ab2[1] <= 65504.f);
+            const bool wbad = __builtin_amdgcn_ballot_w64(badl) != 0;
+            if (lane == 0) {
+                red[it & 1][wave] = amax;
+                red[it & 1][4 + wave] = wbad ? 1.f : 0.f;
+            }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            amax = round16(fmaxf(fmaxf(red[it & 1][0], red[it & 1][1]),
-                                 fmaxf(red[it & 1][2], red[it & 1][3])));
+            const float *rr = red[it & 1];
+            amax = round16(fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3])));
+            const bool bad =
+                __builtin_amdgcn_readfirstlane((rr[4] + rr[5] + rr[6] + rr[7]) != 0.f);
 
             f16 s16 = f16_rn(amax / 7.f);
             if (a.clip != 1.f) s16 = f16_rn((float)s16 * a.clip);
@@ -540,7 +571,8 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
                 for (int h = 0; h < P; ++h) {
                     uint8_t *qrow =
                         reinterpret_cast<uint8_t *>(cbuf) + (P * ln + h) * 272 + 16 * nt + 2 * g;
-                    if (clampit) quant_store<true>(w[h], rcp, qrow);
+                    if (bad) quant_store_exact(w[h], (float)s16, qrow);
+                    else if (clampit) quant_store<true>(w[h], rcp, qrow);
                     else quant_store<false>(w[h], rcp, qrow);
                 }
             }

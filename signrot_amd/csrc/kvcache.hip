@@ -753,9 +753,12 @@ __global__ __launch_bounds__(256) void head_had_quant_kernel(const f16 *__restri
         }
     }
     amax = wave_max(amax);
+    // the ballot runs with the whole wave active (inside the lane-0 branch it
+    // would see lane 0's flag only)
+    const bool wbad = __builtin_amdgcn_ballot_w64(bad) != 0;
     if ((threadIdx.x & 63) == 0) {
         red[threadIdx.x >> 6] = amax;
-        redb[threadIdx.x >> 6] = __builtin_amdgcn_ballot_w64(bad) != 0;
+        redb[threadIdx.x >> 6] = wbad;
     }
     __syncthreads();
     amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));

@@ -118,6 +118,29 @@ def _had_on(hadK, device, dtype):
     return h
 
 
+def adj_sign_from_rotated(x_rot: torch.Tensor) -> torch.Tensor:
+    """The SignRot sign-adjust vector from one rotated calibration batch
+    (fake_quant/quant_utils.py:362-367): the token whose largest |value| is
+    the largest of the batch (the massive-outlier token; the first such token
+    on ties), and the sign pattern of that token, with 0 counted as +1.
+
+    x_rot [T, n] or [B, T, n] (only batch 0 is used, as the reference does);
+    returns int8 [n] of ±1 on x_rot's device."""
+    tokens = x_rot[0] if x_rot.dim() == 3 else x_rot
+    if tokens.dim() != 2 or tokens.shape[0] == 0:
+        raise ValueError("adj_sign_from_rotated expects [T, n] or [B, T, n] with T > 0")
+    peak = tokens.abs().amax(dim=-1).argmax()
+    return torch.where(tokens[peak] >= 0, 1, -1).to(torch.int8)
+
+
+def fold_adj_sign_into_linear(linear: torch.nn.Linear, sign: torch.Tensor) -> None:
+    """W <- W * sign by input column (quant_utils.py:367), in the weight's own
+    dtype: a ±1 factor is exact.  Done before weight quantization, so the
+    rotated-and-flipped activation meets the matching flipped weight."""
+    w = linear.weight.data
+    linear.weight.data = w * sign.to(device=w.device, dtype=w.dtype)
+
+
 def apply_exact_had_to_linear(module, had_dim=-1, output=False):
     """Fold a Hadamard into a Linear's weight (hadamard.py:94-130); offline."""
     assert isinstance(module, torch.nn.Linear)

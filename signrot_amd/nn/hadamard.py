@@ -4,7 +4,8 @@ import torch
 
 from .. import _CUDA
 from ..functional import kernel
-from ..functional.hadamard import get_hadK, matmul_hadU_cuda
+from ..functional.hadamard import (adj_sign_from_rotated, fold_adj_sign_into_linear, get_hadK,
+                                   matmul_hadU_cuda)
 from .quantization import AsymQuantizer, Quantizer
 
 
@@ -67,6 +68,30 @@ class OnlineHadamard(torch.nn.Module):
         if sign is not None:
             x = x * sign
         return x.to(x_dtype)
+
+    @torch.no_grad()
+    def calibrate_adj_sign(self, x: torch.Tensor, fold_into=None) -> torch.Tensor:
+        """Set had_adj_sign from one calibration batch x (un-rotated, as it
+        reaches this module) by the SignRot rule (fake_quant/quant_utils.py:
+        362-367): rotate without a sign, take the sign pattern of the token
+        with the largest |value|, and fold it into `fold_into` (a float
+        torch.nn.Linear, before its weights are quantized), or into the tied
+        module when that is a float Linear.  Returns the int8 sign."""
+        if self.had_adj_sign is None:
+            raise RuntimeError("calibrate_adj_sign needs a module built with had_adj=True")
+        x_dtype = x.dtype
+        h = x.float() if self.fp32_had else x
+        rot = matmul_hadU_cuda(h, self.had_rem_dim, self.rem_dim).to(x_dtype)
+        sign = adj_sign_from_rotated(rot)
+        self.had_adj_sign.copy_(sign.to(self.had_adj_sign.device))
+        self._had_adj_ready_flag = None
+        target = fold_into if fold_into is not None else self.module
+        if isinstance(target, torch.nn.Linear):
+            fold_adj_sign_into_linear(target, sign)
+        elif fold_into is not None:
+            raise TypeError("the sign folds into a float torch.nn.Linear only (fold before "
+                            "quantizing: a flipped int4 code -8 has no +8)")
+        return sign
 
     @property
     def _had_adj_ready_cached(self):

@@ -1,25 +1,33 @@
-"""MoE block over stacked int4 expert weights (signrot/nn/moe.py:28-236).
+"""MoE feed-forward block over stacked int4 expert weights, with the
+constructor, buffers and outputs of the reference's SignRotMoEBlock
+(signrot/nn/moe.py:28-236).
 
-Same constructor, buffers and forward as the reference's SignRotMoEBlock:
+A forward is four steps over the (token, choice) rows of the batch:
 
-  router -> permute the (token, choice) rows by expert -> quantize each
-  token once (its top-k experts and gate/up read the same codes) -> grouped
-  gate/up W4A4 linears -> swiglu -> one online Hadamard over all rows (the
-  transform is expert-independent) -> per-expert SignRot sign fused into the
-  down-proj quantizer -> grouped down W4A4 linear -> weighted un-permute.
+  1. routing: softmax router probabilities (fp32), top-k, optional
+     renormalisation, weights cast to the input dtype; the rows are ordered
+     by expert (a stable sort), giving per-expert row ranges;
+  2. gate/up: every token is quantized once -- its k rows and both
+     projections read the same codes -- then one grouped W4A4 GEMM with the
+     expert-indexed dequant per projection (srq_w4a4_linear_moe);
+  3. down: SwiGLU, the had_K ⊗ H rotation (one transform for all rows: it
+     does not depend on the expert), the expert's SignRot sign and the
+     quantizer -- one fused launch where the rotation has an MFMA form --
+     then the grouped down GEMM;
+  4. combine: each row goes back to its (token, choice) slot and the k rows
+     of a token are summed with their routing weights.
 
-Every routing step is a fixed-shape device op (argsort / index_add_ /
-cumsum), nothing is read back to the host on the grouped path, so a forward
-is graph-capturable.  The grouped path runs each projection as one launch of
-the fused grouped GEMM + expert-indexed dequant (srq_w4a4_linear_moe); the
-reference runs matmul_grouped then sym_dequant_moe, which is the same
-arithmetic.  `use_grouped=False` is the reference's per-expert loop over the
-dense kernels (host-synced; the equivalence oracle), bit-identical to the
-grouped path.  asym=True quantizes activations to uint4 with per-token zero
-points (asym_quant_dynamic / asym_quant_dynamic_moe) and the grouped GEMM
-subtracts zero_row * w_sum before the dequant (srq_w4a4_linear_moe_asym),
-the reference's matmul_grouped(signed_a=False) + sym_dequant_moe arithmetic.
+Nothing is read back to the host on the grouped path, so a forward can be
+captured in a HIP graph.  `use_grouped=False` runs the gate/up/down GEMMs as
+one dense launch per expert over the same rows (the row counts are read on
+the host): the reference's per-expert loop, kept as the equivalence check,
+bit-identical to the grouped path.  `asym=True` quantizes activations to
+uint4 with per-row zero points and the GEMMs subtract zero_row * w_sum before
+the dequant, as the reference's matmul_grouped(signed_a=False) +
+sym_dequant_moe do.
 """
+from typing import NamedTuple, Optional
+
 import torch
 
 from .. import _CUDA
@@ -27,182 +35,190 @@ from ..functional import kernel
 from ..functional.hadamard import get_hadK, matmul_hadU_cuda
 
 
+class MoERouting(NamedTuple):
+    """Routing of one batch: `logits` [T, E]; `weights` [T, k] in the input
+    dtype; row r of the expert-ordered batch is (token, choice) row
+    `order[r]` (= token * k + choice), expert `expert[r]` (int32); the rows of
+    expert e are `offsets[e] : offsets[e + 1]` (int32 [E + 1]); `counts` [E]."""
+    logits: torch.Tensor
+    weights: torch.Tensor
+    order: torch.Tensor
+    expert: torch.Tensor
+    counts: torch.Tensor
+    offsets: torch.Tensor
+
+
+class _Codes(NamedTuple):
+    q: torch.Tensor                 # packed u8 [rows, K / 2]
+    scale: torch.Tensor             # f16 [rows, 1]
+    zero: Optional[torch.Tensor]    # int8 [rows, 1] (asymmetric) or None
+
+    def rows(self, index):
+        return _Codes(self.q[index], self.scale[index],
+                      None if self.zero is None else self.zero[index])
+
+
 class SignRotMoEBlock(torch.nn.Module):
+    """Buffers (non-persistent, as in the reference): w_gate / w_up u8
+    [E, inter, hidden/2], w_down u8 [E, hidden, inter/2], s_* f16 [E, out],
+    sign_down int8 [E, inter] or None, wsum_* int32 [E, out] (asym; computed
+    on first use when not given), had_K [K, K] on the weights' device."""
+
     def __init__(self, gate, *, top_k, norm_topk_prob,
                  w_gate, s_gate, w_up, s_up, w_down, s_down,
                  sign_down=None, wsum_gate=None, wsum_up=None, wsum_down=None,
                  asym=False, clip_ratio=1.0, fp32_had=False, use_grouped=True):
         super().__init__()
-        self.gate = gate  # router linear (16-bit activations), left untouched
-        # grouped path: one launch for swiglu + rotation + sign + quantizer
-        # of the down-proj input where the rotation has an MFMA form
-        self.fuse_down = True
+        experts, inter, half_hidden = w_gate.shape
+        if tuple(w_up.shape) != (experts, inter, half_hidden) or \
+                tuple(w_down.shape) != (experts, 2 * half_hidden, inter // 2):
+            raise ValueError("w_gate / w_up must be [E, inter, hidden/2] and w_down "
+                             "[E, hidden, inter/2]")
+        self.gate = gate
         self.top_k = top_k
         self.norm_topk_prob = norm_topk_prob
         self.asym = asym
         self.clip_ratio = clip_ratio
         self.fp32_had = fp32_had
         self.use_grouped = use_grouped
-
-        self.num_experts, self.intermediate_size = w_gate.shape[0], w_gate.shape[1]
-        self.hidden_size = w_gate.shape[2] * 2
-        assert w_down.shape == (self.num_experts, self.hidden_size, self.intermediate_size // 2)
-
-        self.register_buffer("w_gate", w_gate, persistent=False)
-        self.register_buffer("w_up", w_up, persistent=False)
-        self.register_buffer("w_down", w_down, persistent=False)
-        self.register_buffer("s_gate", s_gate, persistent=False)
-        self.register_buffer("s_up", s_up, persistent=False)
-        self.register_buffer("s_down", s_down, persistent=False)
-        self.register_buffer("sign_down", sign_down, persistent=False)
-        self.register_buffer("wsum_gate", wsum_gate, persistent=False)
-        self.register_buffer("wsum_up", wsum_up, persistent=False)
-        self.register_buffer("wsum_down", wsum_down, persistent=False)
-
-        had_K, self.K = get_hadK(self.intermediate_size)
-        if had_K is not None:
-            # on the weights' device, so a forward never uploads it again
-            had_K = had_K.to(w_gate.device, torch.float32 if fp32_had else torch.float16)
-        self.register_buffer("had_K", had_K, persistent=False)
+        # grouped path: swiglu + rotation + sign + quantizer of the down-proj
+        # input in one launch where the rotation has an MFMA form
+        self.fuse_down = True
+        self.num_experts, self.intermediate_size, self.hidden_size = experts, inter, 2 * half_hidden
+        for name, t in (("w_gate", w_gate), ("w_up", w_up), ("w_down", w_down),
+                        ("s_gate", s_gate), ("s_up", s_up), ("s_down", s_down),
+                        ("sign_down", sign_down), ("wsum_gate", wsum_gate),
+                        ("wsum_up", wsum_up), ("wsum_down", wsum_down)):
+            self.register_buffer(name, t, persistent=False)
+        table, self.K = get_hadK(inter)
+        if table is not None:
+            table = table.to(w_gate.device, torch.float32 if fp32_had else torch.float16)
+        self.register_buffer("had_K", table, persistent=False)
 
     @staticmethod
     def stack_experts(linears, need_wsum=False):
-        """Stack per-expert Linear4bit weights [E, out, in/2], fp16 scales
-        [E, out] and, for the asymmetric path, the int4 row sums [E, out]
-        (moe.py:71-78)."""
-        w = torch.stack([m.weight for m in linears])
-        s = torch.stack([m.weight_scales.view(-1).to(torch.float16) for m in linears])
+        """(w u8 [E, out, in/2], s f16 [E, out], wsum int32 [E, out] or None)
+        from per-expert Linear4bit modules (moe.py:71-78)."""
+        first = linears[0].weight
+        w = first.new_empty((len(linears), *first.shape))
+        s = torch.empty((len(linears), first.shape[0]), dtype=torch.float16, device=first.device)
+        for e, lin in enumerate(linears):
+            w[e].copy_(lin.weight)
+            s[e].copy_(lin.weight_scales.reshape(-1))
         wsum = None
         if need_wsum:
-            wsum = torch.stack([kernel.sum_i4(m.weight).view(-1) for m in linears])
-        return w.contiguous(), s.contiguous(), wsum
+            wsum = kernel.sum_i4(w.view(-1, w.shape[-1])).view(len(linears), -1)
+        return w, s, wsum
 
-    def _ensure_wsum(self):
-        """Row sums of every expert's weight codes for the zero correction
-        (moe.py:80-86), computed once when the block was built without them."""
-        if not self.asym or self.wsum_gate is not None:
-            return
-        e = self.num_experts
-        self.wsum_gate = kernel.sum_i4(self.w_gate).view(e, -1)
-        self.wsum_up = kernel.sum_i4(self.w_up).view(e, -1)
-        self.wsum_down = kernel.sum_i4(self.w_down).view(e, -1)
+    # --------------------------------------------------------------- pieces
 
-    def _quantize(self, x):
-        """(codes, scales, zeros int8 or None) (moe.py:88-93)."""
+    def _weights(self, proj):
+        """(codes, scales, row sums or None) of one projection; the row sums
+        of the asymmetric path are computed once, for all experts in one
+        launch."""
+        w = getattr(self, "w_" + proj)
+        wsum = None
+        if self.asym:
+            wsum = getattr(self, "wsum_" + proj)
+            if wsum is None:
+                wsum = kernel.sum_i4(w.view(-1, w.shape[-1])).view(self.num_experts, -1)
+                setattr(self, "wsum_" + proj, wsum)
+        return w, getattr(self, "s_" + proj), wsum
+
+    def _quant(self, x) -> _Codes:
         if self.asym:
             q, s, z = kernel.asym_quant_dynamic(x, self.clip_ratio)
-            return q, s, z.to(torch.int8)
+            return _Codes(q, s, z.to(torch.int8))
         q, s = kernel.sym_quant_dynamic(x, self.clip_ratio)
-        return q, s, None
+        return _Codes(q, s, None)
 
-    # ------------------------------------------------------------ projections
+    def _quant_per_expert(self, h, expert) -> _Codes:
+        """Quantizer of the down-proj input with row r flipped by
+        sign_down[expert[r]] (fused into the quantizer)."""
+        if self.asym:
+            q, s, z = kernel.asym_quant_dynamic_moe(h, self.sign_down, expert, self.clip_ratio)
+            return _Codes(q, s, z.to(torch.int8))
+        q, s = kernel.sym_quant_dynamic_moe(h, self.sign_down, expert, self.clip_ratio)
+        return _Codes(q, s, None)
 
-    @staticmethod
-    def _gemm_dequant_grouped(q, s, z, offsets, w, s_w, wsum):
-        if z is None:
-            return kernel.w4a4_linear_moe(q, s, w, s_w, offsets)
-        return kernel.w4a4_linear_moe_asym(q, s, z, w, s_w, wsum, offsets)
-
-    @staticmethod
-    def _gemm_dequant_loop(q, s, z, counts, w, s_w, wsum):
-        """Per-expert loop over the dense kernels (moe.py:138-159); host-syncs
-        on counts."""
-        out = torch.empty(q.shape[0], w.shape[1], dtype=torch.float16, device=q.device)
-        row = 0
-        for e, m in enumerate(counts.tolist()):
-            if m == 0:
+    def _project(self, codes: _Codes, route: MoERouting, proj):
+        """Expert-ordered rows times their expert's weights, dequantized to
+        fp16 [rows, out]."""
+        w, s_w, wsum = self._weights(proj)
+        if self.use_grouped:
+            if codes.zero is None:
+                return kernel.w4a4_linear_moe(codes.q, codes.scale, w, s_w, route.offsets)
+            return kernel.w4a4_linear_moe_asym(codes.q, codes.scale, codes.zero, w, s_w, wsum,
+                                               route.offsets)
+        # one dense launch per expert with rows (host-synced on the counts)
+        out = torch.empty((codes.q.shape[0], w.shape[1]), dtype=torch.float16,
+                          device=codes.q.device)
+        bounds = route.offsets.tolist()
+        for e in range(self.num_experts):
+            lo, hi = bounds[e], bounds[e + 1]
+            if lo == hi:
                 continue
-            rows = slice(row, row + m)
-            row += m
-            if z is not None:
-                i32 = kernel.matmul_ui4_si4(q[rows], w[e])
-                i32 -= kernel.matmul_colrow_i8_i32(z[rows], wsum[e].view(1, -1))
+            part = codes.rows(slice(lo, hi))
+            if part.zero is None:
+                acc = kernel.matmul_si4_si4(part.q, w[e])
             else:
-                i32 = kernel.matmul_si4_si4(q[rows], w[e])
-            out[rows] = kernel.sym_dequant(i32, s[rows], s_w[e].view(-1, 1))
+                acc = kernel.matmul_ui4_si4(part.q, w[e]) - \
+                    kernel.matmul_colrow_i8_i32(part.zero, wsum[e].view(1, -1))
+            out[lo:hi] = kernel.sym_dequant(acc, part.scale, s_w[e].view(-1, 1))
         return out
 
-    # ---------------------------------------------------------------- forward
+    def _down_input(self, gate_h, up_h, route: MoERouting) -> _Codes:
+        """SwiGLU -> rotation -> per-expert sign -> quantizer."""
+        inter = gate_h.shape[1]
+        if (self.fuse_down and self.use_grouped and not self.asym and not self.fp32_had
+                and inter == self.K * 512 and _CUDA.swiglu_had_fusable(inter, self.K)):
+            q, s = _CUDA.swiglu_had_sign_quant_moe(gate_h, up_h, self.had_K.half(), self.K,
+                                                   self.sign_down, route.expert, self.clip_ratio)
+            return _Codes(q, s, None)
+        h = kernel.swiglu(gate_h, up_h)
+        if self.fp32_had:
+            h = h.float()
+        h = matmul_hadU_cuda(h, self.had_K, self.K).to(torch.float16)
+        if self.use_grouped:
+            return self._quant_per_expert(h, route.expert)
+        if self.sign_down is not None:
+            h = h * self.sign_down[route.expert.long()]
+        return self._quant(h)
 
-    def route(self, x):
-        """Router logits, top-k weights (in x's dtype) and the expert-sorted
-        row order (moe.py:168-185)."""
-        router_logits = self.gate(x)
-        routing_weights = torch.softmax(router_logits, dim=1, dtype=torch.float)
-        routing_weights, selected = torch.topk(routing_weights, self.top_k, dim=-1)
+    # -------------------------------------------------------------- forward
+
+    def route(self, x) -> MoERouting:
+        """Router probabilities in fp32, top-k (renormalised when
+        norm_topk_prob), weights in x's dtype (moe.py:168-185); rows ordered
+        by expert with fixed-shape device ops only (a stable sort and a
+        scatter-add for the counts: no host reads)."""
+        logits = self.gate(x)
+        probs = torch.softmax(logits, dim=1, dtype=torch.float)
+        top_p, top_e = torch.topk(probs, self.top_k, dim=-1)
         if self.norm_topk_prob:
-            routing_weights /= routing_weights.sum(dim=-1, keepdim=True)
-        routing_weights = routing_weights.to(x.dtype)
-        flat_e = selected.reshape(-1)
-        perm = torch.argsort(flat_e, stable=True)
+            top_p /= top_p.sum(dim=-1, keepdim=True)
+        choice = top_e.reshape(-1)
+        order = torch.argsort(choice, stable=True)
         counts = torch.zeros(self.num_experts, dtype=torch.int32, device=x.device)
-        counts.index_add_(0, flat_e, torch.ones_like(flat_e, dtype=torch.int32))
-        return router_logits, routing_weights, perm, counts, flat_e
+        counts.scatter_add_(0, choice, torch.ones_like(choice, dtype=torch.int32))
+        offsets = torch.zeros(self.num_experts + 1, dtype=torch.int32, device=x.device)
+        torch.cumsum(counts, 0, out=offsets[1:])
+        return MoERouting(logits, top_p.to(x.dtype), order, choice[order].to(torch.int32),
+                          counts, offsets)
 
     def forward(self, hidden_states: torch.Tensor):
-        batch_size, seq_len, hidden_dim = hidden_states.shape
-        x = hidden_states.view(-1, hidden_dim)
-        x_dtype = x.dtype
-        self._ensure_wsum()
-        router_logits, routing_weights, perm, counts, flat_e = self.route(x)
-        tok = perm // self.top_k
-        eid = flat_e[perm].to(torch.int32)
-
-        # each token's top-k experts and gate/up projections read the same
-        # codes: quantize once per token, then gather rows
-        q_tok, s_tok, z_tok = self._quantize(x.to(torch.float16))
-        q_a, s_a = q_tok[tok], s_tok[tok]
-        z_a = z_tok[tok] if z_tok is not None else None
-
-        if self.use_grouped:
-            offsets = torch.zeros(self.num_experts + 1, dtype=torch.int32, device=x.device)
-            offsets[1:] = torch.cumsum(counts, 0)
-            gate_h = self._gemm_dequant_grouped(q_a, s_a, z_a, offsets, self.w_gate, self.s_gate,
-                                                self.wsum_gate)
-            up_h = self._gemm_dequant_grouped(q_a, s_a, z_a, offsets, self.w_up, self.s_up,
-                                              self.wsum_up)
-        else:
-            gate_h = self._gemm_dequant_loop(q_a, s_a, z_a, counts, self.w_gate, self.s_gate,
-                                             self.wsum_gate)
-            up_h = self._gemm_dequant_loop(q_a, s_a, z_a, counts, self.w_up, self.s_up,
-                                           self.wsum_up)
-
-        if self.fuse_down and self.use_grouped and not self.asym and not self.fp32_had and \
-                _CUDA.swiglu_had_fusable(gate_h.shape[1], self.K) and gate_h.shape[1] == \
-                self.K * 512:
-            # swiglu, rotation, per-expert sign and quantizer in one launch
-            # (bit-identical to the three steps below)
-            q_d, s_d = _CUDA.swiglu_had_sign_quant_moe(gate_h, up_h, self.had_K.half(), self.K,
-                                                       self.sign_down, eid, self.clip_ratio)
-            y = self._gemm_dequant_grouped(q_d, s_d, None, offsets, self.w_down, self.s_down,
-                                           None)
-        else:
-            inter = kernel.swiglu(gate_h, up_h)
-            # the Hadamard is identical for every expert; the had_adj sign is
-            # per row, from the [E, inter] table
-            h = inter.float() if self.fp32_had else inter
-            h = matmul_hadU_cuda(h, self.had_K, self.K).to(torch.float16)
-            if self.use_grouped:
-                if self.asym:
-                    q_d, s_d, z_d = kernel.asym_quant_dynamic_moe(h, self.sign_down, eid,
-                                                                  self.clip_ratio)
-                    z_d = z_d.to(torch.int8)
-                else:
-                    q_d, s_d = kernel.sym_quant_dynamic_moe(h, self.sign_down, eid,
-                                                            self.clip_ratio)
-                    z_d = None
-                y = self._gemm_dequant_grouped(q_d, s_d, z_d, offsets, self.w_down, self.s_down,
-                                               self.wsum_down)
-            else:
-                if self.sign_down is not None:
-                    h = h * self.sign_down[eid.long()]
-                q_d, s_d, z_d = self._quantize(h)
-                y = self._gemm_dequant_loop(q_d, s_d, z_d, counts, self.w_down, self.s_down,
-                                            self.wsum_down)
-
-        # deterministic un-permute + weighted sum (no atomics: a captured
-        # graph replays bit-identically)
-        inv = torch.argsort(perm)
-        y = y.to(x_dtype)[inv].view(-1, self.top_k, hidden_dim)
-        out = (y * routing_weights.unsqueeze(-1)).sum(dim=1)
-        return out.view(batch_size, seq_len, hidden_dim), router_logits
+        shape = hidden_states.shape
+        x = hidden_states.reshape(-1, shape[-1])
+        route = self.route(x)
+        codes = self._quant(x.to(torch.float16)).rows(route.order // self.top_k)
+        gate_h = self._project(codes, route, "gate")
+        up_h = self._project(codes, route, "up")
+        y = self._project(self._down_input(gate_h, up_h, route), route, "down")
+        # back to (token, choice) order by a scatter through the permutation
+        # (no atomics: a replayed graph gives the same bits), then the
+        # weighted sum over each token's k choices
+        slots = torch.empty_like(y, dtype=x.dtype)
+        slots[route.order] = y.to(x.dtype)
+        slots = slots.view(x.shape[0], self.top_k, shape[-1])
+        out = (slots * route.weights.unsqueeze(-1)).sum(dim=1)
+        return out.view(shape), route.logits

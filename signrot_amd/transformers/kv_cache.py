@@ -1,19 +1,28 @@
-"""Paged int4 KV cache and decode-attention stub, mirroring
-signrot/transformers/kv_cache.py:60-498 on the HIP op table.
+"""Paged int4 KV cache and decode attention, with the interface of the
+reference's signrot/transformers/kv_cache.py (MultiLayerPagedKVCache4Bit,
+update() returning the decode attention of the layer, the spec dict of the
+flashinfer-style ops, refresh/freeze of the specs for graph capture).
 
-Differences from the reference, none of which change results:
+Design:
+  * `pages` u8 [P, L, 2, H, page, D/2] and `scales` f16 [P, L, 2, H, page, 2]
+    are the reference's tensors (same names, shapes and content), so code
+    that reads or writes them directly keeps working.
+  * `_PageTable` owns the three index tensors the HIP ops read (indptr,
+    indices, last-page length).  They are allocated once and rewritten in
+    place, so a captured HIP graph keeps valid addresses; the physical page
+    of (request b, page j) is j * B + b, the reference's assignment
+    (kv_cache.py:417-433), which lets the pool grow by appending.
+  * `_SplitDecoder` holds the split-KV workspace and the chunk count, and
+    `update()` returns a `_LayerAttention` callable bound to one layer.
   * KV heads are stored once.  The reference repeats each KV head
-    `group_size` times in the cache (kv_cache.py:346-353) because its decode
-    kernel needs as many KV heads as query heads; batch_decode_i4 here maps
-    query head h to KV head h // group_size itself, so the cache is
-    group_size times smaller and decode reads group_size times fewer bytes.
-  * The split-KV chunk count targets two 256-thread blocks per CU (the
-    reference targets two blocks of 128 threads, kv_cache.py:236-258).
-  * Only the int4 path exists: disable_quant=True (fp16 cache) and lac=True
+    `group_size` times (kv_cache.py:346-353) because its decode kernel needs
+    as many KV heads as query heads; batch_decode_i4 here maps query head h
+    to KV head h // group_size itself, so the cache and the decode traffic
+    are group_size times smaller.  Results are the same.
+  * Only the int4 cache exists: disable_quant=True (fp16 cache) and lac=True
     (learned clipping, unused by the reference itself) raise
     NotImplementedError.
 """
-import functools
 import math
 from typing import Any, Dict, Optional
 
@@ -24,18 +33,16 @@ from ..functional import kernel as signrot_kernel
 
 
 def unpack_i4_and_asym_dequantize(q, scale, zero, lac: bool = False):
-    """uint4 unpack (low nibble first) and q * scale - zero
-    (kv_cache.py:60-68)."""
+    """uint4 codes (low nibble first) -> q * scale - zero, or
+    scale * (q - zero) with lac (kv_cache.py:60-68)."""
     assert q.dtype == torch.uint8
-    q = torch.stack((q & 0x0F, (q >> 4) & 0x0F), dim=-1).view(*q.shape[:-1], q.shape[-1] * 2)
-    if lac:
-        return scale * (q - zero)
-    return q * scale - zero
+    codes = torch.stack((q & 0x0F, q >> 4), dim=-1).flatten(-2)
+    return scale * (codes - zero) if lac else codes * scale - zero
 
 
 def matmul_had_cuda(X, dtype):
-    """Sylvester WHT over the last dim scaled by 1/sqrt(n) in `dtype`
-    (kv_cache.py:70-73)."""
+    """Head-dim Walsh-Hadamard transform, scaled by 1/sqrt(n), computed in
+    `dtype` and returned in X's dtype (kv_cache.py:70-73)."""
     n = X.shape[-1]
     out = _CUDA.hadamard_transform(X.to(dtype).contiguous(), scale=1 / math.sqrt(n))
     return out.to(X.dtype).view(X.shape)
@@ -59,46 +66,121 @@ def batch_decode_i4(o, q, kv_data, kv_param, kv_indptr, kv_indices, last_page_of
                                  last_page_offset, layer_idx, tmp, num_chunks)
 
 
-class _AttentionStub(object):
-    """Decode attention over the cache (kv_cache.py:144-170): q [B, 1, Hq, D]
-    is rotated by the head-dim Hadamard (matching the rotated keys), then
-    batch_decode_i4; returns [B, 1, Hq, D]."""
+def _pages_for(length, page_size):
+    return -(-length // page_size)
 
-    def __init__(self, cache_page_size, device, n_layers, disable_quant, hadamard_dtype):
-        self.cache_page_size = cache_page_size
-        self.n_layers = n_layers
-        self.disable_quant = disable_quant
+
+def _last_page_len(length: int, page_size: int) -> int:
+    """Tokens held by the last page of a request of `length` tokens (0 for
+    an empty request, a full page when length is a multiple of it)."""
+    if length == 0:
+        return 0
+    return (length - 1) % page_size + 1
+
+
+class _PageTable:
+    """Request -> physical page map of a batch whose requests all hold the
+    same number of pages, in three persistent int32 tensors:
+      indptr [B + 1]   request b's pages are indices[indptr[b] : indptr[b+1]]
+      indices [capacity] physical page of (b, j) = j * B + b
+      last [B]         tokens in each request's last page."""
+
+    def __init__(self, batch, capacity, device):
+        self.batch = batch
+        self.device = device
+        self._row = torch.arange(batch + 1, device=device, dtype=torch.int32)
+        self.indptr = torch.empty(batch + 1, device=device, dtype=torch.int32)
+        self.last = torch.empty(batch, device=device, dtype=torch.int32)
+        self.indices = torch.empty(capacity, device=device, dtype=torch.int32)
+        self._written_for = -1
+
+    def grow(self, capacity):
+        """A larger indices tensor (the pool grew); the caller re-points the
+        spec dict at it."""
+        self.indices = torch.empty(capacity, device=self.device, dtype=torch.int32)
+        self._written_for = -1
+
+    def set_pages(self, per_request: int):
+        torch.mul(self._row, per_request, out=self.indptr)
+        if per_request != self._written_for:
+            j = torch.arange(per_request, device=self.device, dtype=torch.int32)
+            b = torch.arange(self.batch, device=self.device, dtype=torch.int32)
+            self.indices[: per_request * self.batch].copy_((j * self.batch + b[:, None]).flatten())
+            self._written_for = per_request
+
+    def set_uniform(self, length: int, page_size: int):
+        self.last.fill_(_last_page_len(length, page_size))
+        self.set_pages(_pages_for(length, page_size))
+
+    def set_from_mask(self, attention_mask, page_size: int):
+        """Per-request lengths from an HF attention_mask [B, T]; every request
+        must need the same number of pages (the shared page count is read on
+        the host)."""
+        lens = attention_mask.sum(dim=-1, dtype=torch.int32)
+        pages = (lens + page_size - 1) // page_size
+        lo, hi = int(pages.min()), int(pages.max())
+        if lo != hi:
+            raise NotImplementedError("Current implementation does not support the case where "
+                                      "batches have different number of pages")
+        self.last.copy_(torch.where(lens > 0, (lens - 1) % page_size + 1, 0))
+        self.set_pages(lo)
+
+    def clone(self):
+        t = _PageTable.__new__(_PageTable)
+        t.batch, t.device, t._row = self.batch, self.device, self._row
+        t.indptr, t.last, t.indices = self.indptr.clone(), self.last.clone(), self.indices.clone()
+        t._written_for = self._written_for
+        return t
+
+
+class _SplitDecoder:
+    """batch_decode_i4 with a fixed split-KV configuration: `num_chunks`
+    chunks per (request, KV head) and their fp32 workspace `tmp`
+    [B, Hq, chunks, D + 4] (no workspace for one chunk)."""
+
+    def __init__(self, batch, num_qo_heads, head_dim, chunks, device, hadamard_dtype):
+        self.num_chunks = chunks
         self.hadamard_dtype = hadamard_dtype
-        self.num_chunks = 1
-        self.tmp = None
+        self.tmp = (torch.empty((batch, num_qo_heads, chunks, head_dim + 4), dtype=torch.float32,
+                                device=device) if chunks > 1 else None)
 
-    def forward(self, q, num_kv_heads, attention_kwargs, layer_idx):
-        batch_size, q_len, num_qo_heads, head_dim = q.shape
-        assert q_len == 1
-        q = q.view(batch_size, num_qo_heads, head_dim)
-        if self.hadamard_dtype is not None:
-            q = matmul_had_cuda(q, dtype=self.hadamard_dtype)
-        return self.attend_rotated(q, attention_kwargs, layer_idx).unsqueeze(1)
+    def attend(self, q_rot, spec, layer_idx):
+        """o [B, Hq, D] for an already rotated q [B, Hq, D]."""
+        o = torch.empty_like(q_rot)
+        split = self.tmp is not None and self.tmp.shape[1] == q_rot.shape[1]
+        batch_decode_i4(o, q_rot, **spec, layer_idx=layer_idx,
+                        tmp=self.tmp if split else None,
+                        num_chunks=self.num_chunks if split else 1)
+        return o
 
-    def attend_rotated(self, q, attention_kwargs, layer_idx):
-        """batch_decode_i4 of an already rotated q [B, Hq, D] -> [B, Hq, D]."""
-        attn_output = torch.empty_like(q)
-        tmp = self.tmp
-        if tmp is not None and tmp.shape[1] != q.shape[1]:
-            tmp = None
-        batch_decode_i4(attn_output, q, **attention_kwargs, layer_idx=layer_idx, tmp=tmp,
-                        num_chunks=self.num_chunks if tmp is not None else 1)
-        return attn_output
+
+class _LayerAttention:
+    """What update() returns after an append: q [B, 1, Hq, D] -> attention
+    over this layer's cache, [B, 1, Hq, D] (the reference's
+    _AttentionStub.forward bound to one layer, kv_cache.py:144-170).  q is
+    rotated by the head-dim Hadamard first, matching the rotated keys."""
+
+    def __init__(self, decoder: _SplitDecoder, spec, layer_idx):
+        self.decoder, self.spec, self.layer_idx = decoder, spec, layer_idx
+
+    def __call__(self, q):
+        B, T, Hq, D = q.shape
+        if T != 1:
+            raise ValueError("decode attention takes one query token per request")
+        q = q.view(B, Hq, D)
+        if self.decoder.hadamard_dtype is not None:
+            q = matmul_had_cuda(q, dtype=self.decoder.hadamard_dtype)
+        return self.decoder.attend(q, self.spec, self.layer_idx).unsqueeze(1)
 
 
 class MultiLayerPagedKVCache4Bit(object):
-    """Paged int4 KV cache for all layers (kv_cache.py:173-498).
+    """Paged int4 KV cache for all layers of a model (the reference's
+    MultiLayerPagedKVCache4Bit, kv_cache.py:173-498).
 
     pages  u8  [pages, n_layers, 2, num_heads, page_size, head_dim / 2]
-    scales f16 [pages, n_layers, 2, num_heads, page_size, 2]
-    Physical page of (request b, page j) is j * batch_size + b.
-    `num_heads` is the number of KV heads; `group_size` is the number of
-    query heads per KV head."""
+    scales f16 [pages, n_layers, 2, num_heads, page_size, 2]  ([scale, zero])
+    `num_heads` is the number of KV heads; `group_size` the number of query
+    heads per KV head."""
 
     def __init__(self, batch_size, page_size, max_seq_len, device, n_layers, num_heads,
                  head_dim, disable_quant=False, hadamard_dtype=torch.float16, group_size=1,
@@ -109,212 +191,200 @@ class MultiLayerPagedKVCache4Bit(object):
             raise NotImplementedError("learned activation clipping (lac=True) is not built")
         if head_dim != 128:
             raise ValueError("head_dim must be 128")
-        self.lac = lac
-        self.page_size = page_size
         self.batch_size = batch_size
-        self.disable_quant = disable_quant
+        self.page_size = page_size
+        self.max_seq_len = max_seq_len
         self.num_heads = num_heads
         self.head_dim = head_dim
-        max_page_cnt = self.page_cnt_from_length(max_seq_len)
-        self.pages = torch.empty((max_page_cnt * batch_size, n_layers, 2, num_heads, page_size,
-                                  head_dim // 2), dtype=torch.uint8, device=device)
-        self.scales = torch.empty((max_page_cnt * batch_size, n_layers, 2, num_heads, page_size,
-                                   2), dtype=torch.float16, device=device)
-        self.max_seq_len = max_seq_len
-        self._needs_init = [True] * n_layers
-        self.length = 0
-        self.device = device
-        self.hadamard_dtype = hadamard_dtype
         self.group_size = group_size
-        self._stub = _AttentionStub(self.page_size, device, n_layers, disable_quant,
-                                    hadamard_dtype)
-        # persistent index buffers, refreshed in place (graph-safe addresses)
-        self._kv_indices_full = torch.empty(self.pages.shape[0], device=device, dtype=torch.int32)
-        self._spec_page_cnt = None
-        self._last_page_offset = torch.empty(batch_size, device=device, dtype=torch.int32)
-        self._indptr_base = torch.arange(batch_size + 1, device=device, dtype=torch.int32)
-        self._kv_indptr_buf = torch.empty(batch_size + 1, device=device, dtype=torch.int32)
-        self._specs_frozen = False
-        self._spec_cache = {
-            "kv_data": self.pages,
-            "kv_param": self.scales,
-            "kv_indptr": self._kv_indptr_buf,
-            "kv_indices": self._kv_indices_full,
-            "last_page_offset": self._last_page_offset,
-        }
-        self._configure_decode_split(batch_size, num_heads * group_size, head_dim,
-                                     max_seq_len, device)
+        self.hadamard_dtype = hadamard_dtype
+        self.disable_quant = disable_quant
+        self.lac = lac
+        self.device = device
+        self.length = 0
+        pool = _pages_for(max_seq_len, page_size) * batch_size
+        self.pages = torch.empty((pool, n_layers, 2, num_heads, page_size, head_dim // 2),
+                                 dtype=torch.uint8, device=device)
+        self.scales = torch.empty((pool, n_layers, 2, num_heads, page_size, 2),
+                                  dtype=torch.float16, device=device)
+        self._filled = [False] * n_layers          # layer holds its prefill
+        self._table = _PageTable(batch_size, pool, device)
+        self._frozen = False
+        self._spec = {}
+        self._point_spec()
+        cus = torch.cuda.get_device_properties(device).multi_processor_count
+        chunks = self.decode_chunks(batch_size, num_heads, max_seq_len, cus)
+        self._decoder = _SplitDecoder(batch_size, num_heads * group_size, head_dim, chunks,
+                                      device, hadamard_dtype)
+
+    def _point_spec(self):
+        """The keyword arguments of the paged ops, rebuilt whenever a tensor
+        is reallocated (the dict object itself stays the same)."""
+        self._spec.update(kv_data=self.pages, kv_param=self.scales,
+                          kv_indptr=self._table.indptr, kv_indices=self._table.indices,
+                          last_page_offset=self._table.last)
 
     @staticmethod
     def decode_chunks(batch_size, num_kv_heads, max_seq_len, cu_count):
-        """Split-KV chunk count: about two blocks per CU (the decode kernel's
-        register use leaves room for two four-wave blocks per CU, so further
-        chunks only queue), at most one chunk per 128 tokens of context, at
-        most 1024."""
-        target_blocks = 2 * cu_count
-        chunks = max(1, -(-target_blocks // max(1, batch_size * num_kv_heads)))
-        return max(1, min(chunks, max_seq_len // 128, 1024))
-
-    def _configure_decode_split(self, batch_size, num_qo_heads, head_dim, max_seq_len, device):
-        cus = torch.cuda.get_device_properties(device).multi_processor_count
-        chunks = self.decode_chunks(batch_size, self.num_heads, max_seq_len, cus)
-        self._stub.num_chunks = chunks
-        if chunks > 1:
-            self._stub.tmp = torch.empty((batch_size, num_qo_heads, chunks, head_dim + 4),
-                                         dtype=torch.float32, device=device)
+        """Split-KV chunks per (request, KV head): enough blocks for about two
+        per CU (the decode kernel's registers leave room for two four-wave
+        blocks per CU, so more chunks only queue), at least 128 tokens per
+        chunk, at most 1024 chunks."""
+        blocks = max(1, batch_size * num_kv_heads)
+        want = -(-2 * cu_count // blocks)
+        return max(1, min(want, max_seq_len // 128, 1024))
 
     def page_cnt_from_length(self, length):
         return (length + self.page_size - 1) // self.page_size
-
-    def _ensure_page_cnt_per_batch(self, expected_page_cnt_per_batch):
-        """Grow the page pool by doubling (kv_cache.py:260-289)."""
-        expected_total = expected_page_cnt_per_batch * self.batch_size
-        current_total = self.pages.shape[0]
-        if expected_total <= current_total:
-            return
-        grow_to_total = max(expected_total, current_total * 2)
-        add_total = grow_to_total - current_total
-        self.pages = torch.cat([self.pages, self.pages.new_empty((add_total,
-                                                                  *self.pages.shape[1:]))])
-        self.scales = torch.cat([self.scales, self.scales.new_empty((add_total,
-                                                                     *self.scales.shape[1:]))])
-        self._kv_indices_full = torch.empty(self.pages.shape[0], device=self.device,
-                                            dtype=torch.int32)
-        self._spec_page_cnt = None
-        self._spec_cache.update(kv_data=self.pages, kv_param=self.scales,
-                                kv_indices=self._kv_indices_full)
 
     @property
     def seen_tokens(self):
         return self.length
 
-    def update(self, key_states, value_states, layer_idx, cache_kwargs: Optional[Dict[str, Any]]
-               = None):
-        """Quantize and store K/V [B, T, H, D] of one layer (kv_cache.py:291-415).
-        The first call per layer fills (init_kv_i4) and returns the inputs;
-        later calls (T == 1) append and return the decode stub bound to this
-        layer."""
-        cache_kwargs = cache_kwargs or {}
-        b_sz, added_length, num_heads, head_dim = key_states.shape
-        assert num_heads == self.num_heads, "update() takes the KV heads"
-        orig_key_states, orig_value_states = key_states, value_states
+    def _reserve(self, tokens):
+        """Make room for `tokens` per request, doubling the pool when it runs
+        out (appended pages keep the j * B + b assignment of the old ones)."""
+        need = self.page_cnt_from_length(tokens) * self.batch_size
+        have = self.pages.shape[0]
+        if need <= have:
+            return
+        total = max(need, 2 * have)
+        extra = total - have
+        self.pages = torch.cat([self.pages, self.pages.new_empty((extra, *self.pages.shape[1:]))])
+        self.scales = torch.cat([self.scales,
+                                 self.scales.new_empty((extra, *self.scales.shape[1:]))])
+        self._table.grow(total)
+        self._point_spec()
+
+    def _quantize(self, key_states, value_states):
+        """Head-dim Hadamard of K (as the decode query gets), then the int4
+        quantizer of K and V: codes [B, T, H, D/2] and params [B, T, H, 2]."""
+        k = key_states
         if self.hadamard_dtype is not None:
-            key_states = matmul_had_cuda(key_states, dtype=self.hadamard_dtype)
-        key_states, k_param = signrot_kernel.kv_quant_pack(key_states)
-        value_states, v_param = signrot_kernel.kv_quant_pack(value_states)
-        k_param = k_param.view(self.batch_size * added_length, num_heads, 2)
-        v_param = v_param.view(self.batch_size * added_length, num_heads, 2)
-        qhd = self.pages.shape[-1]
-        assert b_sz == self.batch_size
+            k = matmul_had_cuda(k, dtype=self.hadamard_dtype)
+        kq, kp = signrot_kernel.kv_quant_pack(k)
+        vq, vp = signrot_kernel.kv_quant_pack(value_states)
+        return kq, kp, vq, vp
+
+    def update(self, key_states, value_states, layer_idx,
+               cache_kwargs: Optional[Dict[str, Any]] = None):
+        """Quantize and store K/V [B, T, H, D] of one layer (the reference's
+        update, kv_cache.py:291-415).  The first call for a layer is the
+        prefill: the tokens are written in bulk (init_kv_i4; with an
+        attention_mask only its 1-positions) and the fp16 inputs are returned
+        for the prefill attention.  Later calls append one token per request
+        (append_kv_i4) and return the layer's decode attention."""
+        B, T, H, D = key_states.shape
+        if H != self.num_heads:
+            raise ValueError(f"update() takes the {self.num_heads} KV heads, got {H}")
+        if B != self.batch_size:
+            raise ValueError(f"batch {B} != the cache's {self.batch_size}")
+        mask = (cache_kwargs or {}).get("attention_mask")
+        kq, kp, vq, vp = self._quantize(key_states, value_states)
         if layer_idx == 0:
-            new_length = self.length + added_length
-            self._ensure_page_cnt_per_batch(self.page_cnt_from_length(new_length))
-            self.length = new_length
-        attention_mask = cache_kwargs.get("attention_mask")
-        specs = self.get_cache_specs_for_flash_infer(attention_mask)
-        if self._needs_init[layer_idx]:
-            self._needs_init[layer_idx] = False
-            if attention_mask is not None:
-                keep = torch.nonzero(attention_mask.flatten(), as_tuple=False).flatten()
-                key_states = key_states.reshape(-1, num_heads * qhd)[keep]
-                value_states = value_states.reshape(-1, num_heads * qhd)[keep]
-                k_param = k_param.reshape(-1, num_heads * 2)[keep]
-                v_param = v_param.reshape(-1, num_heads * 2)[keep]
-                seqlens = torch.nn.functional.pad(
-                    torch.cumsum(attention_mask.sum(dim=-1, dtype=torch.int32), dim=0,
-                                 dtype=torch.int32), (1, 0))
+            self._reserve(self.length + T)
+            self.length += T
+        spec = self.get_cache_specs_for_flash_infer(mask)
+        if not self._filled[layer_idx]:
+            self._filled[layer_idx] = True
+            kq, kp = kq.reshape(B * T, H, D // 2), kp.reshape(B * T, H, 2)
+            vq, vp = vq.reshape(B * T, H, D // 2), vp.reshape(B * T, H, 2)
+            if mask is None:
+                starts = torch.arange(B + 1, device=self.device, dtype=torch.int32) * T
             else:
-                seqlens = torch.arange(self.batch_size + 1, device=self.device,
-                                       dtype=torch.int32) * added_length
-            init_kv_i4(**specs,
-                       k=key_states.reshape(-1, num_heads, qhd).contiguous(),
-                       v=value_states.reshape(-1, num_heads, qhd).contiguous(),
-                       k_param=k_param.reshape(-1, num_heads, 2).contiguous(),
-                       v_param=v_param.reshape(-1, num_heads, 2).contiguous(),
-                       seqlen_indptr=seqlens, layer_idx=layer_idx)
-            return orig_key_states, orig_value_states
-        assert added_length == 1
-        append_kv_i4(**specs,
-                     k=key_states.view(self.batch_size, num_heads, qhd),
-                     v=value_states.view(self.batch_size, num_heads, qhd),
-                     k_param=k_param.view(-1, num_heads, 2),
-                     v_param=v_param.view(-1, num_heads, 2),
-                     layer_idx=layer_idx)
-        return functools.partial(self._stub.forward, num_kv_heads=num_heads,
-                                 attention_kwargs=specs, layer_idx=layer_idx)
+                live = mask.flatten().nonzero().flatten()
+                kq, kp, vq, vp = kq[live], kp[live], vq[live], vp[live]
+                counts = mask.sum(dim=-1, dtype=torch.int32)
+                starts = torch.zeros(B + 1, device=self.device, dtype=torch.int32)
+                torch.cumsum(counts, dim=0, out=starts[1:])
+            init_kv_i4(**spec, k=kq.contiguous(), v=vq.contiguous(), k_param=kp.contiguous(),
+                       v_param=vp.contiguous(), seqlen_indptr=starts, layer_idx=layer_idx)
+            return key_states, value_states
+        if T != 1:
+            raise ValueError("after the prefill, update() appends one token per request")
+        append_kv_i4(**spec, k=kq.view(B, H, D // 2), v=vq.view(B, H, D // 2),
+                     k_param=kp.view(B, H, 2), v_param=vp.view(B, H, 2), layer_idx=layer_idx)
+        return _LayerAttention(self._decoder, spec, layer_idx)
 
     def update_qkv_fused(self, qkv, cos, sin, layer_idx, num_q_heads):
-        """Decode-step form of update() + the stub's q rotation, one kernel:
-        qkv f16 [B, (Hq + 2 H) D] is the q/k/v projection output of the new
-        token; q and k get RoPE (cos/sin [1 or B, 1, D]) and the head-dim
-        Hadamard, k and v are quantized into the cache.  Returns the rotated
-        q [B, Hq, D] for decode_rotated.  Results equal
-        rope_qk + update() + the stub's q rotation bit for bit.  The layer
-        must already hold its prefill (one new token per request here)."""
-        if self._needs_init[layer_idx]:
+        """Decode-step form of update() plus the decode query's rotation, one
+        kernel: qkv f16 [B, (Hq + 2 H) D] is the q/k/v projection output of
+        the new token; q and k get RoPE (cos/sin [1 or B, 1, D]) and the
+        head-dim Hadamard, k and v are quantized into the cache.  Returns the
+        rotated q [B, Hq, D] for decode_rotated.  Bit for bit the same as
+        rope_qk + update() + the query rotation.  The layer must hold its
+        prefill already."""
+        if not self._filled[layer_idx]:
             raise RuntimeError("update_qkv_fused: the layer has no prefill yet")
-        b_sz = qkv.shape[0]
-        assert b_sz == self.batch_size
+        if qkv.shape[0] != self.batch_size:
+            raise ValueError(f"batch {qkv.shape[0]} != the cache's {self.batch_size}")
         if layer_idx == 0:
-            new_length = self.length + 1
-            self._ensure_page_cnt_per_batch(self.page_cnt_from_length(new_length))
-            self.length = new_length
-        specs = self.get_cache_specs_for_flash_infer(None)
-        rotate = self.hadamard_dtype is not None
+            self._reserve(self.length + 1)
+            self.length += 1
+        spec = self.get_cache_specs_for_flash_infer(None)
         return _CUDA.qkv_rope_had_append(qkv, cos.contiguous(), sin.contiguous(), num_q_heads,
-                                         self.num_heads, **specs, layer_idx=layer_idx,
-                                         had_scale=1 / math.sqrt(self.head_dim), rotate=rotate)
+                                         self.num_heads, **spec, layer_idx=layer_idx,
+                                         had_scale=1 / math.sqrt(self.head_dim),
+                                         rotate=self.hadamard_dtype is not None)
 
     def decode_rotated(self, q_rot, layer_idx):
         """Decode attention of an already rotated q [B, Hq, D] over this
         layer's cache (after update_qkv_fused) -> [B, Hq, D]."""
-        return self._stub.attend_rotated(q_rot, self._spec_cache, layer_idx)
+        return self._decoder.attend(q_rot, self._spec, layer_idx)
 
-    def _set_page_cnt(self, page_cnt: int):
-        """indptr = b * page_cnt; indices[b, j] = j * B + b
-        (kv_cache.py:417-433)."""
-        torch.mul(self._indptr_base, page_cnt, out=self._kv_indptr_buf)
-        if self._spec_page_cnt == page_cnt:
-            return
-        self._spec_page_cnt = page_cnt
-        idx = (torch.arange(page_cnt, device=self.device, dtype=torch.int32) *
-               self.batch_size).unsqueeze(0) + torch.arange(
-                   self.batch_size, device=self.device, dtype=torch.int32).unsqueeze(1)
-        self._kv_indices_full[:page_cnt * self.batch_size].copy_(idx.reshape(-1))
+    # ---------------------------------------------------------- index specs
+    def specs(self):
+        """The op keyword arguments (kv_data, kv_param, kv_indptr, kv_indices,
+        last_page_offset) as they stand."""
+        return self._spec
 
     def refresh_specs(self, length: Optional[int] = None):
-        """Index buffers for a uniform-length batch (kv_cache.py:435-456)."""
-        if length is None:
-            length = self.length
-        page_cnt = self.page_cnt_from_length(length)
-        page_ptr = length % self.page_size
-        if length != 0 and page_ptr == 0:
-            page_ptr = self.page_size
-        self._last_page_offset.fill_(page_ptr)
-        self._set_page_cnt(page_cnt)
-        return self._spec_cache
+        """Rewrite the index tensors in place for a batch of `length` tokens
+        per request (default: the current length) and return the specs.  A
+        graph-captured decode step calls this before each replay, with the
+        specs frozen inside the capture (kv_cache.py:435-464)."""
+        self._table.set_uniform(self.length if length is None else length, self.page_size)
+        return self._spec
 
     def freeze_specs(self, frozen=True):
-        self._specs_frozen = frozen
+        """While frozen, update() uses the index tensors as they are (no
+        refresh), so it can be captured in a graph."""
+        self._frozen = frozen
 
     def get_cache_specs_for_flash_infer(self, attention_mask):
-        if attention_mask is None:
-            return self._spec_cache if self._specs_frozen else self.refresh_specs()
-        seqlens = attention_mask.sum(dim=-1, dtype=torch.int32)
-        page_cnt = self.page_cnt_from_length(seqlens)
-        if (page_cnt[0] != page_cnt).any():
-            raise NotImplementedError("Current implementation does not support the case where "
-                                      "batches have different number of pages")
-        page_cnt = int(page_cnt[0])
-        page_ptr = seqlens % self.page_size
-        page_ptr = torch.where((seqlens != 0) & (page_ptr == 0), self.page_size, page_ptr)
-        self._last_page_offset.copy_(page_ptr)
-        self._set_page_cnt(page_cnt)
-        return self._spec_cache
+        if attention_mask is not None:
+            self._table.set_from_mask(attention_mask, self.page_size)
+        elif not self._frozen:
+            self._table.set_uniform(self.length, self.page_size)
+        return self._spec
+
+    def mark_prefilled(self, length: int):
+        """Declare that every layer holds `length` tokens per request, written
+        into `pages` / `scales` directly (benchmarks and tests with synthetic
+        contexts); the next update() of each layer appends."""
+        self._reserve(length)
+        self.length = length
+        self._filled = [True] * len(self._filled)
+
+    def clone(self):
+        """An independent copy: own pages, scales and index tensors, same
+        state (length, prefilled layers, split-KV configuration)."""
+        c = object.__new__(MultiLayerPagedKVCache4Bit)
+        c.__dict__.update(self.__dict__)
+        c.pages, c.scales = self.pages.clone(), self.scales.clone()
+        c._filled = list(self._filled)
+        c._table = self._table.clone()
+        c._spec = {}
+        c._point_spec()
+        dec = _SplitDecoder.__new__(_SplitDecoder)
+        dec.__dict__.update(self._decoder.__dict__)
+        dec.tmp = None if self._decoder.tmp is None else torch.empty_like(self._decoder.tmp)
+        c._decoder = dec
+        return c
 
     def reset(self):
         self.length = 0
-        self._needs_init = [True] * len(self._needs_init)
+        self._filled = [False] * len(self._filled)
 
     def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
         return self.length

@@ -44,6 +44,10 @@ def test_abi_version(lib):
     (lambda L: L.srq_kv_quant_pack(None, 4, 7, None, None, None), "even"),
     (lambda L: L.srq_matmul_s4s4(None, None, 4, 4, 48, None, None), "multiple of 32"),
     (lambda L: L.srq_matmul_s4s4(None, None, 4, 4, 262144, None, None), "131072"),
+    # 2^14 * 131072 = 2^31 wraps the int32 accumulator: the bound is strict
+    (lambda L: L.srq_matmul_s4s4(None, None, 4, 4, 131072, None, None), "131072"),
+    (lambda L: L.srq_w4a4_linear_moe(None, None, None, None, None, 8, 16, 64, 131072, None,
+                                     None), "131072"),
     (lambda L: L.srq_hadamard_transform(None, None, 4, 24, 1.0, 0, None), "power of two"),
     (lambda L: L.srq_online_hadamard(None, None, 4, 14336, 28, None, None, 0, None), "hadK"),
     (lambda L: L.srq_had_sign_quant(None, 4, 21 * 64, 3, None, None, 0, 1.0, None, None,

@@ -4,8 +4,9 @@ applied to the HIP output of the previous stage, so integer stages are
 checked bit-exactly on identical fp16 inputs (int4 codes flip on one-ulp
 input changes, which end-to-end comparisons would amplify).  Shapes: a
 reduced layer (hidden 1024, 8 query / 2 or 4 KV heads of 128, FFN 896 =
-28 x 32, so the down-proj rotation is had_28 x H_32) and the config-3 head
-layout (32 / 8 heads) with a reduced FFN.
+28 x 32, so the down-proj rotation is had_28 x H_32), the config-3 head
+layout (32 / 8 heads) with a reduced FFN, and config 3 itself (hidden 4096,
+32 / 8 heads, FFN 14336, batch 32, 4096 cached tokens).
 """
 import numpy as np
 import pytest
@@ -40,9 +41,10 @@ def _run(B, T, hidden, Hq, Hkv, ffn, page, seed):
     rng = np.random.default_rng(seed)
     layer = W4A4LlamaDecodeLayer.random(hidden, Hq, Hkv, D, ffn, layer_idx=1, seed=seed)
     cache = MultiLayerPagedKVCache4Bit(B, page, T + 1, "cuda", 2, Hkv, D, group_size=Hq // Hkv)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
     for li in range(2):  # prefill both layers (init_kv_i4)
-        kv = rng.standard_normal((2, B, T, Hkv, D)).astype(np.float16)
-        cache.update(to_dev(kv[0]), to_dev(kv[1]), li, {})
+        kv = torch.randn((2, B, T, Hkv, D), device="cuda", generator=gen).half()
+        cache.update(kv[0], kv[1], li, {})
     k0 = torch.zeros(B, 1, Hkv, D, dtype=torch.float16, device="cuda")
     cache.update(k0, k0, 0, {})  # layer 0's step: the cache now counts T + 1 tokens
     data, param = to_np(cache.pages).copy(), to_np(cache.scales).copy()
@@ -104,6 +106,9 @@ def _run(B, T, hidden, Hq, Hkv, ffn, page, seed):
     (3, 70, 1024, 8, 2, 896, 32, 1),
     (4, 300, 1024, 8, 4, 896, 64, 2),
     (2, 200, 4096, 32, 8, 896, 64, 3),
+    # config 3 at its full shape: Llama-3-8B layer, batch 32, 4096 cached
+    # tokens in 256-token pages, FFN 14336 (had_28 x H_512)
+    (32, 4096, 4096, 32, 8, 14336, 256, 4),
 ])
 def test_decode_layer_stagewise(B, T, hidden, Hq, Hkv, ffn, page, seed):
     _run(B, T, hidden, Hq, Hkv, ffn, page, seed)

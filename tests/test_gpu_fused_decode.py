@@ -141,26 +141,15 @@ def _prefilled_cache(B, T, Hkv, Hq, page, layers, rng):
     from signrot_amd.transformers import MultiLayerPagedKVCache4Bit
     cache = MultiLayerPagedKVCache4Bit(B, page, T + 2, "cuda", layers, Hkv, 128,
                                        group_size=Hq // Hkv)
+    gen = torch.Generator(device="cuda").manual_seed(int(rng.integers(1 << 30)))
     for li in range(layers):
-        kv = rng.standard_normal((2, B, T, Hkv, 128)).astype(np.float16)
-        cache.update(to_dev(kv[0]), to_dev(kv[1]), li, {})
+        kv = torch.randn((2, B, T, Hkv, 128), device="cuda", generator=gen).half()
+        cache.update(kv[0], kv[1], li, {})
     return cache
 
 
 def _clone_cache(cache):
-    import copy
-    c2 = copy.copy(cache)
-    c2.pages = cache.pages.clone()
-    c2.scales = cache.scales.clone()
-    c2._needs_init = list(cache._needs_init)
-    c2._kv_indices_full = cache._kv_indices_full.clone()
-    c2._last_page_offset = cache._last_page_offset.clone()
-    c2._kv_indptr_buf = cache._kv_indptr_buf.clone()
-    c2._spec_cache = dict(cache._spec_cache, kv_data=c2.pages, kv_param=c2.scales,
-                          kv_indices=c2._kv_indices_full, last_page_offset=c2._last_page_offset,
-                          kv_indptr=c2._kv_indptr_buf)
-    c2._stub = copy.copy(cache._stub)
-    return c2
+    return cache.clone()
 
 
 @pytest.mark.parametrize("B,T,Hq,Hkv,page,cos_batch", [(3, 37, 8, 2, 16, 1), (32, 255, 32, 8, 256, 1),
@@ -199,10 +188,12 @@ def test_qkv_rope_had_append_equals_update_chain(B, T, Hq, Hkv, page, cos_batch)
         assert_bitexact(to_np(out_b), to_np(out_a), f"attention output (layer {li})")
 
 
-@pytest.mark.parametrize("hidden,Hq,Hkv,ffn,T", [(1024, 8, 2, 14336, 40), (4096, 32, 8, 896, 300)])
-def test_fused_decode_layer_equals_op_by_op(hidden, Hq, Hkv, ffn, T):
+@pytest.mark.parametrize("hidden,Hq,Hkv,ffn,T,B,page", [
+    (1024, 8, 2, 14336, 40, 4, 64), (4096, 32, 8, 896, 300, 4, 64),
+    # config 3 at its full shape (what bench.py times)
+    (4096, 32, 8, 14336, 4096, 32, 256)])
+def test_fused_decode_layer_equals_op_by_op(hidden, Hq, Hkv, ffn, T, B, page):
     from signrot_amd.transformers.decode_layer import W4A4LlamaDecodeLayer, rope_cos_sin
-    B, page = 4, 64
     rng = np.random.default_rng(hidden + ffn)
     layers = [W4A4LlamaDecodeLayer.random(hidden, Hq, Hkv, 128, ffn, layer_idx=i, seed=5 + i)
               for i in range(2)]

@@ -102,3 +102,34 @@ def test_matmul_empty(C):
     b = torch.zeros(5, 16, dtype=torch.uint8, device="cuda")
     assert C.matmul(a, b).shape == (0, 5)
 
+
+def _sample_rows(rng, M, n=48):
+    """Edge rows, rows at 128/256-row tile boundaries and random rows."""
+    fixed = {0, 1, 127, 128, 255, 256, M // 2, M - 257, M - 256, M - 2, M - 1}
+    rand = set(rng.choice(M, n, replace=False).tolist())
+    return np.array(sorted(r for r in fixed | rand if 0 <= r < M))
+
+
+@pytest.mark.parametrize("M,N,K,what", [
+    (8192, 4096, 14336, "cfg2 down_proj M=8192"),
+    (4096, 57344, 8192, "cfg4 gate/up (fused) M=4096"),
+    (4096, 8192, 28672, "cfg4 down_proj M=4096"),
+    (2048, 4096, 14336, "cfg2 down_proj M=2048"),
+    (512, 57344, 8192, "cfg4 gate/up M=512"),
+])
+def test_config_shapes_sampled_rows(C, M, N, K, what):
+    """The configs' full GEMM shapes (each kernel at its real tile grid), the
+    int32 product and the fused W4A4 linear checked bit-exactly on sampled
+    rows against the brute-force oracle."""
+    rng = np.random.default_rng(M + N + K)
+    a, b = _rand_packed(rng, M, K), _rand_packed(rng, N, K)
+    sa = (np.abs(rng.standard_normal(M)) * 0.05 + 1e-3).astype(np.float16)
+    sb = (np.abs(rng.standard_normal(N)) * 0.01 + 1e-4).astype(np.float16)
+    da, db = to_dev(a), to_dev(b)
+    c = C.matmul(da, db)
+    out = C.w4a4_linear(da, to_dev(sa), db, to_dev(sb))
+    rows = _sample_rows(rng, M)
+    want_c = oq.matmul_s4s4(a[rows], b)
+    assert_bitexact(to_np(c[torch.from_numpy(rows).cuda()]), want_c, f"{what}: int32 C")
+    want = oq.w4a4_linear(a[rows], sa[rows], b, sb)
+    assert_bitexact(to_np(out[torch.from_numpy(rows).cuda()]), want, f"{what}: fp16 out")

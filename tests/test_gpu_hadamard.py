@@ -87,7 +87,9 @@ def test_online_hadamard_fp32_mode(C):
                                     (11008, 3), (32, 10), (14336, 7), (14336, 3001),
                                     (14336, 1), (14336, 513), (14336, 1024),
                                     (6144, 9), (10240, 13), (28672, 700), (12288, 3),
-                                    (20480, 2)])
+                                    (20480, 2),
+                                    # config 2 at M = 8192, config 4 at M = 4096
+                                    (14336, 8192), (28672, 4096)])
 @pytest.mark.parametrize("use_sign", [False, True])
 def test_had_sign_quant_bitexact(C, n, rows, use_sign):
     rng = np.random.default_rng(n + rows)

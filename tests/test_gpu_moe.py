@@ -204,6 +204,7 @@ BLOCKS = [  # hidden, inter, experts, top_k, norm, tokens
     (256, 768, 16, 4, True, 37),
     (512, 1536, 8, 2, False, 5),
     (4096, 14336, 8, 2, True, 64),
+    (4096, 14336, 8, 2, True, 512),      # config 5 (Mixtral-8x7B shape, 512 tokens)
 ]
 
 
@@ -221,7 +222,18 @@ def test_block_grouped_equals_loop(hidden, inter, experts, top_k, norm, tokens):
     assert torch.isfinite(out).all()
 
 
-@pytest.mark.parametrize("hidden,inter,experts,top_k,norm,tokens", BLOCKS[:2])
+def _check_moe_rows(got, q, s, w, s_w, eid, rows, what):
+    """Oracle W4A4 linear of the given expert-ordered rows, each against its
+    own expert's weights, bit-exact."""
+    got, q, s, eid = to_np(got), to_np(q), to_np(s), to_np(eid)
+    w, s_w = to_np(w), to_np(s_w)
+    for e in np.unique(eid[rows]):
+        r = rows[eid[rows] == e]
+        assert_bitexact(got[r], oq.w4a4_linear(q[r], s[r].reshape(-1), w[e], s_w[e]),
+                        f"{what} (expert {e})")
+
+
+@pytest.mark.parametrize("hidden,inter,experts,top_k,norm,tokens", BLOCKS[:2] + BLOCKS[3:])
 @torch.no_grad()
 def test_block_stagewise_vs_oracle(C, hidden, inter, experts, top_k, norm, tokens):
     """Each stage of the grouped forward against the oracle on the previous
@@ -231,11 +243,24 @@ def test_block_stagewise_vs_oracle(C, hidden, inter, experts, top_k, norm, token
     from oracle import glue as og
     blk = _block(hidden, inter, experts, top_k, norm, seed=7 + tokens)
     x = torch.randn(tokens, hidden, device=DEV, dtype=torch.float16)
-    _, _, perm, counts, flat_e = blk.route(x)
-    tok = perm // top_k
-    eid = flat_e[perm].to(torch.int32)
-    off = torch.zeros(experts + 1, dtype=torch.int32, device=DEV)
-    off[1:] = torch.cumsum(counts, 0)
+    route = blk.route(x)
+    tok = route.order // top_k
+    eid = route.expert
+    off = route.offsets
+    assert torch.equal(off[1:] - off[:-1], route.counts)
+    # the routing rule itself (moe.py:168-185): fp32 softmax, top-k,
+    # renormalised, rows ordered by expert, stable within an expert
+    probs = torch.softmax(route.logits.float(), dim=1)
+    tp, te = torch.topk(probs, top_k, dim=-1)
+    if norm:
+        tp = tp / tp.sum(dim=-1, keepdim=True)
+    assert torch.equal(route.weights, tp.to(x.dtype))
+    flat = te.reshape(-1)
+    assert torch.equal(route.expert.long(), torch.sort(flat, stable=True).values)
+    assert torch.equal(flat[route.order], route.expert.long())
+    for e in range(experts):
+        rows = route.order[off[e]:off[e + 1]]
+        assert torch.all(rows[1:] > rows[:-1])   # stable: increasing within an expert
     q_tok, s_tok = C.sym_quant_dynamic(x, 1.0)
     qw, sw = oq.sym_quant_dynamic(to_np(x))
     assert_bitexact(to_np(q_tok), qw, "token codes")
@@ -243,10 +268,22 @@ def test_block_stagewise_vs_oracle(C, hidden, inter, experts, top_k, norm, token
     gate_h = C.w4a4_linear_moe(q_a, s_a.view(-1), blk.w_gate, blk.s_gate, off)
     up_h = C.w4a4_linear_moe(q_a, s_a.view(-1), blk.w_up, blk.s_up, off)
     offn = to_np(off)
-    assert_bitexact(to_np(gate_h), om.w4a4_linear_moe(to_np(q_a), to_np(s_a), to_np(blk.w_gate),
-                                                       to_np(blk.s_gate), offn), "gate")
-    assert_bitexact(to_np(up_h), om.w4a4_linear_moe(to_np(q_a), to_np(s_a), to_np(blk.w_up),
-                                                     to_np(blk.s_up), offn), "up")
+    nrows = tokens * top_k
+    big = nrows * inter * hidden > 1e9
+    # every row for small blocks; the first, last and 16 random rows of
+    # every expert at the config-5 shape (the float64 oracle is too slow
+    # for all 1024 rows x 14336 x 4096 three times)
+    rng = np.random.default_rng(tokens)
+    rows = np.arange(nrows) if not big else np.unique(np.concatenate(
+        [np.concatenate([[offn[e], offn[e + 1] - 1],
+                         rng.integers(offn[e], offn[e + 1], 16)])
+         for e in range(experts) if offn[e + 1] > offn[e]]).astype(np.int64))
+    if not big:
+        assert_bitexact(to_np(gate_h), om.w4a4_linear_moe(to_np(q_a), to_np(s_a),
+                                                           to_np(blk.w_gate), to_np(blk.s_gate),
+                                                           offn), "gate")
+    _check_moe_rows(gate_h, q_a, s_a, blk.w_gate, blk.s_gate, eid, rows, "gate")
+    _check_moe_rows(up_h, q_a, s_a, blk.w_up, blk.s_up, eid, rows, "up")
     inter_h = C.swiglu(gate_h, up_h)
     np.testing.assert_allclose(to_np(inter_h).astype(np.float32),
                                og.swiglu(to_np(gate_h), to_np(up_h)).astype(np.float32),
@@ -257,8 +294,13 @@ def test_block_stagewise_vs_oracle(C, hidden, inter, experts, top_k, norm, token
     assert_bitexact(to_np(s_d), sdw, "down scale")
     assert_bitexact(to_np(q_d), qdw, "down codes")
     y = C.w4a4_linear_moe(q_d, s_d.view(-1), blk.w_down, blk.s_down, off)
-    assert_bitexact(to_np(y), om.w4a4_linear_moe(qdw, sdw, to_np(blk.w_down), to_np(blk.s_down),
-                                                  offn), "down")
+    _check_moe_rows(y, q_d, s_d, blk.w_down, blk.s_down, eid, rows, "down")
+    # the block's own forward gives these stages' result after the combine
+    out, _ = blk(x.view(1, tokens, hidden))
+    slots = torch.empty_like(y)
+    slots[route.order] = y
+    want = (slots.view(tokens, top_k, hidden) * route.weights.unsqueeze(-1)).sum(dim=1)
+    assert torch.equal(out.view(tokens, hidden), want), "block output"
 
 
 @torch.no_grad()

@@ -55,6 +55,31 @@ def test_prefill_matches_oracle(C, B, T, Hq, Hkv, causal, masked):
     _check(out, q, k, v, mask, causal, f"B={B} T={T} Hq={Hq} Hkv={Hkv} causal={causal}")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_padded_positions_hold_nan_and_inf(C, causal):
+    """Whatever a padded position holds never reaches a live row: NaN and
+    ±inf in the masked q, K and V rows leave the live rows equal to the
+    attention over the unpadded tokens, and the masked rows zero."""
+    B, T, Hq, Hkv = 2, 150, 8, 2
+    q, k, v = _inputs(B, T, Hq, Hkv, seed=91)
+    mask = torch.ones(B, T, dtype=torch.int64)
+    mask[0, :40] = 0                          # left padding
+    mask[1, 3::7] = 0                         # holes
+    dead = mask == 0
+    want = oa.prefill(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), causal)
+    qn, kn, vn = q.clone(), k.clone(), v.clone()
+    for t, fill in ((qn, float("nan")), (kn, float("inf")), (vn, float("nan"))):
+        t[dead] = fill
+    kn[1, 3, 0, :5] = float("-inf")
+    vn[0, 7, 1, 9] = float("inf")
+    out = C.prefill_attention(qn.cuda(), kn.cuda(), vn.cuda(), mask.cuda(), causal)
+    torch.cuda.synchronize()
+    got = to_np(out).astype(np.float64)
+    assert np.all(np.isfinite(got)), "a padded position leaked into the output"
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+    assert np.all(got[dead.numpy()] == 0)
+
+
 def test_prefill_large_logits(C):
     """Logits far above 1 (|q.k| * scale in the hundreds): the running max
     keeps exp2 in range."""
