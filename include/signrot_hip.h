@@ -232,6 +232,23 @@ int srq_batch_decode_i4(void *o, const void *q, const void *kv_data, const void 
                         int64_t page_size, int64_t head_dim, float *tmp, int64_t num_chunks,
                         void *stream);
 
+/* srq_batch_decode_i4 with num_chunks split-KV chunks and no workspace
+ * argument: the partial states go to a fixed device array of the library
+ * (8 MiB per GPU, held until the process ends), so the call allocates
+ * nothing.  No counterpart in the reference: for callers that cannot
+ * allocate or pass a workspace (code under graph capture, serving loops,
+ * hosts that forbid hipMalloc).  Needs batch * num_qo_heads * num_chunks *
+ * (head_dim + 4) * 4 <= 8 MiB (else SRQ_EINVAL); the stream must belong to the
+ * current device.  Every call on one GPU shares that array, so calls that
+ * overlap on one GPU (other streams, other threads) race: serialize them.
+ * Same results as srq_batch_decode_i4 with a workspace, bit for bit. */
+int srq_batch_decode_i4_noalloc(void *o, const void *q, const void *kv_data,
+                                const void *kv_param, const int32_t *kv_indptr,
+                                const int32_t *kv_indices, const int32_t *last_page_offset,
+                                int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
+                                int64_t num_layers, int64_t layer_idx, int64_t page_size,
+                                int64_t head_dim, int64_t num_chunks, void *stream);
+
 /* Decode-step q/k/v post-processing in one launch.  qkv f16 [batch,
  * (n_q_heads + 2 n_kv_heads) * head_dim] is the q/k/v projection output of
  * one new token per request (q heads, then k heads, then v heads); cos, sin

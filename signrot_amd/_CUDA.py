@@ -495,6 +495,28 @@ def batch_decode_i4(o, q, kv_data, kv_param, kv_indptr, kv_indices, last_page_of
           int(layer_idx), P, D, tmp_ptr, chunks, _stream(q))
 
 
+def batch_decode_i4_noalloc(o, q, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset,
+                            layer_idx, num_chunks=1):
+    """batch_decode_i4 split into num_chunks chunks whose partial states go
+    to the library's fixed per-GPU scratch (no workspace, no allocation);
+    same results as batch_decode_i4 with a tmp of that many chunks.  Calls
+    that overlap on one GPU race on the scratch."""
+    L, H, P, D = _check_cache("batch_decode_i4_noalloc", kv_data, kv_param, kv_indptr,
+                              kv_indices, last_page_offset)
+    _check("batch_decode_i4_noalloc", [(o, "o"), (q, "q"), (kv_data, "kv_data")],
+           [torch.float16, torch.float16, None])
+    if o.dim() != 3 or q.dim() != 3 or o.shape != q.shape:
+        raise RuntimeError("batch_decode_i4_noalloc: o and q must be the same [B, N, D] shape")
+    B, Hq = q.shape[0], q.shape[1]
+    if q.shape[2] != D:
+        raise RuntimeError(f"batch_decode_i4_noalloc: q head_dim {q.shape[2]} != {D}")
+    if kv_indptr.shape[0] != B + 1 or last_page_offset.shape[0] != B:
+        raise RuntimeError("batch_decode_i4_noalloc: index tensors do not match the batch")
+    _call("srq_batch_decode_i4_noalloc", _ptr(o), _ptr(q), _ptr(kv_data), _ptr(kv_param),
+          _ptr(kv_indptr), _ptr(kv_indices), _ptr(last_page_offset), B, Hq, H, L,
+          int(layer_idx), P, D, int(num_chunks), _stream(q))
+
+
 # ------------------------------------------------------- decode-layer glue
 
 def rmsnorm(x, eps, mean_dim):

@@ -27,6 +27,8 @@
 //     sum p * v_zero accumulated separately in fp32.
 #include "common.h"
 
+#include <atomic>
+
 #include <math.h>
 
 namespace {
@@ -944,6 +946,95 @@ extern "C" int srq_batch_decode_i4(void *o, const void *q, const void *kv_data,
         SRQ_LAUNCH_CHECK("batch_decode_i4 (merge)");
     }
     return SRQ_OK;
+}
+
+
+// ------------------------------------ allocation-free split-KV decode
+// The split-KV partial states of srq_batch_decode_i4_noalloc live in this
+// file-scope device array instead of a caller workspace.  Each GPU the
+// library runs on holds its own copy (kDecodeScratchBytes) until the process
+// ends.  On the host `scratch` names a host-side stand-in, not device memory:
+// the device address of the current GPU's copy comes from
+// hipGetSymbolAddress, once per device, and only that address is passed on.
+namespace {
+constexpr int64_t kDecodeScratchBytes = 8LL << 20;
+constexpr int kMaxDevices = 64;
+std::atomic<float *> g_scratch_addr[kMaxDevices];
+std::atomic_flag g_scratch_lock = ATOMIC_FLAG_INIT;  // first lookup per device
+}  // namespace
+
+static __device__ __align__(256) float scratch[kDecodeScratchBytes / sizeof(float)];
+
+// Device address of the current device's `scratch` (looked up on the first
+// call per device, with that device current).
+static int decode_scratch(hipStream_t st, float **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        srq_set_error("batch_decode_i4_noalloc: no current HIP device (or index >= %d)",
+                      kMaxDevices);
+        return SRQ_ELAUNCH;
+    }
+    if (st) {
+        hipDevice_t sdev = -1;
+        if (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev) {
+            srq_set_error("batch_decode_i4_noalloc: the stream is not on the current device %d",
+                          dev);
+            return SRQ_EINVAL;
+        }
+    }
+    float *p = g_scratch_addr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        while (g_scratch_lock.test_and_set(std::memory_order_acquire)) {
+        }
+        p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+        hipError_t e = hipSuccess;
+        if (!p) {
+            void *addr = nullptr;
+            e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (e == hipSuccess && addr) {
+                p = static_cast<float *>(addr);
+                g_scratch_addr[dev].store(p, std::memory_order_release);
+            }
+        }
+        g_scratch_lock.clear(std::memory_order_release);
+        if (!p) {
+            srq_set_error("batch_decode_i4_noalloc: hipGetSymbolAddress(scratch) failed on "
+                          "device %d: %s", dev, hipGetErrorString(e));
+            return SRQ_ELAUNCH;
+        }
+    }
+    *out = p;
+    return SRQ_OK;
+}
+
+extern "C" int srq_batch_decode_i4_noalloc(void *o, const void *q, const void *kv_data,
+                                           const void *kv_param, const int32_t *kv_indptr,
+                                           const int32_t *kv_indices,
+                                           const int32_t *last_page_offset, int64_t batch,
+                                           int64_t num_qo_heads, int64_t num_kv_heads,
+                                           int64_t num_layers, int64_t layer_idx,
+                                           int64_t page_size, int64_t head_dim,
+                                           int64_t num_chunks, void *stream) {
+    if (num_chunks <= 1 || batch <= 0)
+        return srq_batch_decode_i4(o, q, kv_data, kv_param, kv_indptr, kv_indices,
+                                   last_page_offset, batch, num_qo_heads, num_kv_heads,
+                                   num_layers, layer_idx, page_size, head_dim, nullptr, 1,
+                                   stream);
+    SRQ_CHECK_ARG(num_qo_heads > 0 && head_dim > 0 && num_chunks <= 1024,
+                  "batch_decode_i4_noalloc: bad heads, head_dim or num_chunks");
+    const int64_t need = batch * num_qo_heads * num_chunks * (head_dim + 4) * (int64_t)sizeof(float);
+    SRQ_CHECK_ARG(need <= kDecodeScratchBytes,
+                  "batch_decode_i4_noalloc: batch %lld x %lld heads x %lld chunks needs %lld "
+                  "bytes of split-KV state, more than the fixed %lld-byte scratch (use fewer "
+                  "chunks or srq_batch_decode_i4 with a workspace)",
+                  (long long)batch, (long long)num_qo_heads, (long long)num_chunks,
+                  (long long)need, (long long)kDecodeScratchBytes);
+    float *tmp = nullptr;
+    const int rc = decode_scratch((hipStream_t)stream, &tmp);
+    if (rc) return rc;
+    return srq_batch_decode_i4(o, q, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset,
+                               batch, num_qo_heads, num_kv_heads, num_layers, layer_idx,
+                               page_size, head_dim, tmp, num_chunks, stream);
 }
 
 
