@@ -55,6 +55,10 @@ def parse():
     p.add_argument("--prefill-attention-only", action="store_true",
                    help="only measure the prefill attention (Llama-70B heads, T = 512, "
                         "2048, 8192) and print its results")
+    p.add_argument("--profile", choices=PROFILE_WORKLOADS, default=None,
+                   help="only run one workload a few times (for rocprofv3 counter passes): "
+                        "the cfg2 QLinear at M = 2048, 128 or 8192, the cfg4 MLP at M = 512, "
+                        "the cfg5 MoE block or the cfg3 decode layer")
     p.add_argument("--cpu-rows", type=int, default=256,
                    help="rows of the CPU baseline sample")
     p.add_argument("--min-bytes", type=float, default=640e6,
@@ -109,13 +113,16 @@ def time_cpu_baseline(args, x, hadk, k, sign, wfq):
     t = sum(times) / len(times)
     sd = (sum((v - t) ** 2 for v in times) / max(1, len(times) - 1)) ** 0.5
     tops = 2.0 * rows * args.N * args.K / t / 1e12
-    return {"value": tops, "unit": "TOPS", "cores": cores, "kind": "port",
+    return {"value": tops, "unit": "TOPS", "cores": cores, "cpu_model": cpu_model(),
+            "kind": "port",
             "sample": (f"{rows} of {args.M} rows of the same QLinear (fp16 fake-quant: "
                        f"matmul_hadU + sign + per-token sym int4 quant-dequant + F.linear), "
                        f"{reps} reps, {t * 1e3:.1f} ms +- {1.96 * sd * 1e3:.1f} ms each")}
 
 
 COPY_BYTES = 1 << 30
+PROFILE_WORKLOADS = ("cfg2_M2048", "cfg2_M128", "cfg2_M8192", "cfg2_M16", "cfg4_M512",
+                     "cfg5_moe", "cfg3_decode")
 
 
 def bench_decode_layer(args, dev):
@@ -466,6 +473,17 @@ def measured_traffic(kernel, M, K, N):
     return entry.get("hbm_bytes")
 
 
+def traffic_commit():
+    """The commit the committed traffic figures were measured at."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "traffic_cfg2.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("measured_at")
+    except (OSError, ValueError):
+        return None
+
+
 def gemm_kernel_name(M, N):
     """Kernel srq_w4a4_linear launches for M x N outputs (gemm.hip dispatch)."""
     if M <= 32:
@@ -491,6 +509,37 @@ def calibrate_copy(dev, reps=3):
     print(json.dumps({"calibrate_copy_bytes": COPY_BYTES, "reps": reps}), flush=True)
 
 
+def profile_workloads(args, dev):
+    """One workload of the committed rocprofv3 summaries, a few launches
+    over weight sets that exceed the MALL."""
+    t0 = time.perf_counter()
+    name = args.profile
+    if name.startswith("cfg2_M"):
+        m = int(name[len("cfg2_M"):])
+        res = bench_qlinear(dev, m, 14336, 4096, args.seed + 20 + m, reps=5, min_bytes=6e8)
+    elif name == "cfg4_M512":
+        res = bench_mlp70b(dev, 512, args.seed + 30 + 512, reps=3, min_bytes=6e8)
+    elif name == "cfg5_moe":
+        res = bench_moe(dev, args.seed + 40, reps=3)
+    else:
+        args.decode_steps, args.decode_layers = 3, 2
+        res = bench_decode_layer(args, dev)
+    print(json.dumps({"profile": name, "result": res,
+                      "wall_s": round(time.perf_counter() - t0, 1)}), flush=True)
+
+
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -509,6 +558,9 @@ def main():
         return
     if args.calibrate_copy:
         calibrate_copy(dev)
+        return
+    if args.profile:
+        profile_workloads(args, dev)
         return
     from signrot_amd import _CUDA
 
@@ -619,6 +671,7 @@ def main():
                      "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / PEAK_INT8_TOPS, 4),
                      "traffic": measured_traffic(gemm_kernel_name(M, N).split()[0], M, K, N),
+                     "traffic_measured_at": traffic_commit(),
                      "kernel": gemm_kernel_name(M, N),
                      "algorithmic_ops": ops, "avg_launch_us": round(gemm_ms * 1e3, 2)},
         "kernels": {
