@@ -3,12 +3,14 @@
 // FFN 14336 = had_28 ⊗ H_512, Llama-3-70B FFN 28672 = had_28 ⊗ H_1024),
 // optionally fused with the SignRot sign and the per-token int4 quantizer.
 //
-// A block of 4 waves owns one token row at a time (persistent over rows).
-// The row sits in LDS in the lane order of the stage-A A operand; the next
-// row is prefetched into registers (16 bytes per lane per slot) while this
-// one is transformed, and written to LDS after this row's LDS reads are
-// done, so its HBM latency overlaps a whole row of work.  Wave w computes
-// output columns i2 in [32 w, 32 w + 32) of every 128-element segment.
+// A block of 4 waves owns one token row at a time (persistent over rows),
+// with one barrier per row.  Rows are double-buffered in LDS, in the lane
+// order of the stage-A A operand: the next row streams from HBM straight
+// into the other buffer (buffer loads into LDS) while this one is
+// transformed, and the previous row is quantized from its block reduction
+// at the start of this row's iteration, so neither the fetch latency nor
+// the reduction needs a barrier of its own.  Wave w computes output
+// columns i2 in [32 w, 32 w + 32) of every 128-element segment.
 //
 // Stage A (bits 0-6 of the 512-chunk, H_128): fp16 MFMA 32x32x16.  A-operand
 // row rr of a tile is the 128-element segment (chunk 8T + ct, quarter i1)
@@ -22,7 +24,9 @@
 // Stage K (hadK over the K chunks): transposed MFMA out^T[i2][c] =
 // sum_c' y[c'][i1][i2] hadK[c][c'], the A operand built from the lane's own
 // registers (k-slot (g, e) <-> chunk 8(2s + e/4) + 4g + e%4), so lane
-// (c = l%32, g) receives runs of 4 consecutive i2 of chunk c.
+// (c = l%32, g) receives 16 outputs of chunk c; stage A's output columns
+// are permuted (pl below) so that these are the 16 consecutive
+// i2 = 32 nt + 16 g .. + 15, stored directly (no staging through LDS).
 // out = fp16(fp32 sum)                        -- second rounding point
 //
 // H_1024 (P = 2): the row is 2K 512-chunks, chunk j = 2c + h for Hadamard
@@ -37,7 +41,8 @@
 // as an xor of the fp16 sign bit) while the block reduces the row max.
 //
 // Quantizer: s = fp16(amax / 7) (then fp16(s * clip)), r = fl32(1 / s), and
-// per element fp16(x * r) by one v_fma_mix*_f16.  For fp16 x and s that is
+// per element fp16(x * r) by one v_fma_mix*_f16; the SignRot sign is folded
+// into the offset add below (codes of -x are the negated codes of x).  For fp16 x and s that is
 // the correctly rounded fp16(x / s) of the reference's __hdiv whenever the
 // quotient is >= 2^-14, and it yields the same int4 code for every pair
 // (exhaustively checked over all fp16 pairs by tests/c/quot_exact.c).
@@ -92,77 +97,96 @@ struct MfmaRotArgs {
     int64_t n_sign_rows;
 };
 
-// Quantize one row's packed K-mix results w (this lane: chunk ln, i2 runs
-// 32 nt + 8u + 4g .. +3 for u = 0..3, per quarter i1) and write the codes
-// to the row's LDS staging area (qrow: this lane's first code byte there).
+// Stores of one lane's results.  After the K-mix a lane (chunk ln, half g)
+// holds, for each quarter i1, the 16 consecutive outputs i2 = 32 nt + 16 g
+// + 0..15 of chunk ln as 8 packed fp16 pairs w[i1][0..7]: 32 bytes of a
+// rotated row, 8 bytes of its codes (qrow: the lane's first code byte of
+// quarter 0; quarter i1 is 64 bytes further).
+
+// Symmetric int4 codes with the SignRot sign folded into the offset add:
+// sg[i1][p] holds the two elements' signs as fp16 ±1.0, and
+// fp16(q * sign + 1544) rounds the signed quotient half to even (ulp 1 in
+// [1024, 2048)) with the code + 8 in the low nibble.  The codes of a sign-
+// flipped value are the negated codes (round half to even is odd-symmetric),
+// so this equals quantizing x * sign.  CLAMP: the signed quotient is clamped
+// to [-8, 7] in fp16 first.
 template <bool CLAMP>
-SRQ_DEV void quant_store(const u32 (&w)[4][8], float rcp, uint8_t *qrow) {
+SRQ_DEV u32 offset_codes_signed(u32 q, u32 sg) {
+    v2h h = __builtin_bit_cast(v2h, q);
+    const v2h s = __builtin_bit_cast(v2h, sg);
+    if (CLAMP) {
+        h = h * s;
+        h = __builtin_elementwise_min(__builtin_elementwise_max(h, (v2h){-8, -8}), (v2h){7, 7});
+        h = h + (v2h){1544, 1544};
+    } else {
+        h = __builtin_elementwise_fma(h, s, (v2h){1544, 1544});
+    }
+    return __builtin_bit_cast(u32, h);
+}
+
+template <bool CLAMP>
+SRQ_DEV void quant_store(const u32 (&w)[4][8], const u32 (&sg)[4][8], float rcp, uint8_t *qrow) {
 #pragma unroll
-    for (int i1 = 0; i1 < 4; ++i1)
+    for (int i1 = 0; i1 < 4; ++i1) {
+        u32 c[8];
 #pragma unroll
-        for (int u = 0; u < 4; u += 2) {
-            const u32 a = offset_codes<CLAMP>(quot2(w[i1][2 * u], rcp));
-            const u32 b = offset_codes<CLAMP>(quot2(w[i1][2 * u + 1], rcp));
-            const u32 c = offset_codes<CLAMP>(quot2(w[i1][2 * u + 2], rcp));
-            const u32 d = offset_codes<CLAMP>(quot2(w[i1][2 * u + 3], rcp));
-            const u32 r = pack8(a, b, c, d);
-            // runs u and u + 1 are 8 elements (4 bytes) apart
-            uint8_t *p = qrow + i1 * 64 + 4 * u;
-            *reinterpret_cast<uint16_t *>(p) = (uint16_t)r;
-            *reinterpret_cast<uint16_t *>(p + 4) = (uint16_t)(r >> 16);
-        }
+        for (int p = 0; p < 8; ++p) c[p] = offset_codes_signed<CLAMP>(quot2(w[i1][p], rcp), sg[i1][p]);
+        uint2 r;
+        r.x = pack8(c[0], c[1], c[2], c[3]);
+        r.y = pack8(c[4], c[5], c[6], c[7]);
+        *reinterpret_cast<uint2 *>(qrow + i1 * 64) = r;
+    }
 }
 
 // The same codes for a row holding a NaN or inf (after the rotation), by the
 // exact per-element arithmetic: the quotient of the packed route is NaN there
 // and would not give the reference's code 0.  r = 1 / s is inf for s == 0
 // and 0 for s == inf, so x * r behaves as the reference's x / s.
-SRQ_DEV void quant_store_exact(const u32 (&w)[4][8], float s, uint8_t *qrow) {
+SRQ_DEV void quant_store_exact(const u32 (&w)[4][8], const u32 (&sg)[4][8], float s,
+                               uint8_t *qrow) {
     const float r = sym_recip(s);
 #pragma unroll
-    for (int i1 = 0; i1 < 4; ++i1)
+    for (int i1 = 0; i1 < 4; ++i1) {
+        u32 c[2] = {0, 0};
 #pragma unroll
-        for (int u = 0; u < 4; u += 2) {
-            u32 c = 0;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const v2h pr = __builtin_bit_cast(v2h, w[i1][2 * u + e / 2]);
-                c |= (u32)(sym_code_r((float)pr[e & 1], r) & 0xF) << (4 * e);
-            }
-            uint8_t *p = qrow + i1 * 64 + 4 * u;
-            *reinterpret_cast<uint16_t *>(p) = (uint16_t)c;
-            *reinterpret_cast<uint16_t *>(p + 4) = (uint16_t)(c >> 16);
+        for (int e = 0; e < 16; ++e) {
+            const v2h pr = __builtin_bit_cast(v2h, w[i1][e / 2]);
+            const v2h sp = __builtin_bit_cast(v2h, sg[i1][e / 2]);
+            const float x = (float)pr[e & 1] * (float)sp[e & 1];  // exact sign flip
+            c[e / 8] |= (u32)(sym_code_r(x, r) & 0xF) << (4 * (e % 8));
         }
+        *reinterpret_cast<uint2 *>(qrow + i1 * 64) = (uint2){c[0], c[1]};
+    }
 }
 
-// Asymmetric uint4 codes of the same values (MODE 2), same staging layout:
+// Asymmetric uint4 codes of the same values (MODE 2, w already signed):
 // FAST, the packed route (finite row, s > 0, |zi| <= 511); otherwise each
 // code by the exact per-element arithmetic (asym_code).
 template <bool FAST>
 SRQ_DEV void quant_store_asym(const u32 (&w)[4][8], float rcp, v2h lo, v2h hi, v2h zo,
                               float s, int zi, uint8_t *qrow) {
 #pragma unroll
-    for (int i1 = 0; i1 < 4; ++i1)
+    for (int i1 = 0; i1 < 4; ++i1) {
+        u32 r[2];
 #pragma unroll
-        for (int u = 0; u < 4; u += 2) {
-            u32 r;
+        for (int hlf = 0; hlf < 2; ++hlf) {
+            const int u = 4 * hlf;
             if constexpr (FAST) {
-                r = pack8_raw(asym_offset_codes(quot2(w[i1][2 * u], rcp), lo, hi, zo),
-                              asym_offset_codes(quot2(w[i1][2 * u + 1], rcp), lo, hi, zo),
-                              asym_offset_codes(quot2(w[i1][2 * u + 2], rcp), lo, hi, zo),
-                              asym_offset_codes(quot2(w[i1][2 * u + 3], rcp), lo, hi, zo));
+                r[hlf] = pack8_raw(asym_offset_codes(quot2(w[i1][u], rcp), lo, hi, zo),
+                                   asym_offset_codes(quot2(w[i1][u + 1], rcp), lo, hi, zo),
+                                   asym_offset_codes(quot2(w[i1][u + 2], rcp), lo, hi, zo),
+                                   asym_offset_codes(quot2(w[i1][u + 3], rcp), lo, hi, zo));
             } else {
-                r = 0;
+                r[hlf] = 0;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const v2h pr = __builtin_bit_cast(v2h, w[i1][2 * u + e / 2]);
-                    r |= (u32)(asym_code((float)pr[e & 1], s, zi, 0, 15) & 0xF) << (4 * e);
+                    const v2h pr = __builtin_bit_cast(v2h, w[i1][u + e / 2]);
+                    r[hlf] |= (u32)(asym_code((float)pr[e & 1], s, zi, 0, 15) & 0xF) << (4 * e);
                 }
             }
-            uint8_t *p = qrow + i1 * 64 + 4 * u;
-            *reinterpret_cast<uint16_t *>(p) = (uint16_t)r;
-            *reinterpret_cast<uint16_t *>(p + 4) = (uint16_t)(r >> 16);
         }
+        *reinterpret_cast<uint2 *>(qrow + i1 * 64) = (uint2){r[0], r[1]};
+    }
 }
 
 // MODE: 0 rotation (fp16 out), 1 + symmetric int4 quantizer, 2 + asymmetric
@@ -175,29 +199,33 @@ SRQ_DEV void quant_store_asym(const u32 (&w)[4][8], float rcp, v2h lo, v2h hi, v
 template <int NT, int MODE, bool SW, int P>
 __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had512_mfma_kernel(
     MfmaRotArgs a) {
-    // The staged row: 128-element segment (chunk c, quarter i1) at
-    // rowbuf + 256 (4c + i1) bytes, its 16-byte piece p at position
-    // p ^ 2h(c, i1), h = i1 | ((c >> 2) & 1) << 2.  The swizzle makes both
-    // the row writes (8 lanes: 8 pieces of one segment) and the stage-A
-    // reads (8 lanes: one piece of 8 segments with distinct h) hit distinct
-    // LDS banks.  Chunks K .. 8 NT - 1 stay zero.
-    __shared__ v4i rowbuf[NT * 8 * 64];
-    // codes of one row for coalesced stores: chunk c's 256 bytes at 272 c
-    __shared__ v4i cbuf[MODE >= 1 ? NT * 8 * 17 : 1];
+    // The staged rows, double-buffered (row r of the block's sequence in
+    // rowbuf[r & 1]): 128-element segment (chunk c, quarter i1) at
+    // + 256 (4c + i1) bytes, its 16-byte piece p at position p ^ 2h(c, i1),
+    // h = i1 | ((c >> 2) & 1) << 2.  The swizzle makes the stage-A reads
+    // (8 lanes: one piece of 8 segments with distinct h) hit distinct LDS
+    // banks.  Chunks K .. 8 NT - 1 stay zero.
+    __shared__ v4i rowbuf[2][NT * 8 * 64];
     // row reduction, double-buffered by row parity: MODE 1 max |x| and the
     // non-finite flag per wave; MODE 2 min, max and the non-finite flag
     __shared__ float red[2][MODE == 2 ? 12 : 8];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int nt = wave;
+    const int nt = threadIdx.x >> 6;  // the wave
     const int g = lane >> 5;
     const int ln = lane & 31;
     const int nc = a.KC * P;  // 512-chunks in the row
     const int n = nc * 512;
 
     // ---- constants
+    // Output column permutation: MFMA column ln of this n-tile computes i2 =
+    // 32 nt + pl, pl = perm(ln) moving bit 2 of ln to bit 4 and bits 3-4 to
+    // bits 2-3.  The MFMA output rows a lane holds (8 j + 4 g + r, r < 4) then
+    // become the K-mix rows of the 16 consecutive i2 = 32 nt + 16 g + 4 j + r,
+    // so each lane ends with 16 adjacent outputs per quarter and stores them
+    // directly (32 bytes of fp16, 8 bytes of codes).
+    const int pl = (ln & 3) | (((ln >> 3) & 3) << 2) | (((ln >> 2) & 1) << 4);
     // H_128 B operand for this n-tile, k-steps 0..7: entry e of step ks is
-    // (-1)^(parity((16 (ks & 1) + 8 g + e) & ln) ^ parity((ks >> 1) & nt)).
+    // (-1)^(parity((16 (ks & 1) + 8 g + e) & pl) ^ parity((ks >> 1) & nt)).
     // The low 3 bits of the row index are e alone, so the parity splits into
     // an 8-entry pattern in e (shared by all steps) and one sign per step.
     union BkU {
@@ -207,10 +235,10 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
     {
         BkU pat;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pat.h[e] = parity(e & ln) ? (f16)-1 : (f16)1;
+        for (int e = 0; e < 8; ++e) pat.h[e] = parity(e & pl) ? (f16)-1 : (f16)1;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
-            const u32 flip = (parity((16 * (ks & 1) + 8 * g) & ln) ^ parity((ks >> 1) & nt))
+            const u32 flip = (parity((16 * (ks & 1) + 8 * g) & pl) ^ parity((ks >> 1) & nt))
                                  ? 0x80008000u : 0u;
 #pragma unroll
             for (int i = 0; i < 4; ++i) Bk[ks].w[i] = pat.w[i] ^ flip;
@@ -254,55 +282,150 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
                 }
         }
     }
-    // msk[h][i1]: sign xor masks of the outputs of Hadamard chunk ln, half h
+    // msk[h][i1][p]: the signs of this lane's outputs (Hadamard chunk ln,
+    // half h, quarter i1, elements 2p and 2p + 1 of its 16): MODE 0 and 2 as
+    // fp16 sign-bit xor masks, MODE 1 as fp16 ±1.0 pairs (the quantizer
+    // folds them into its offset add)
+    constexpr u32 kSignBase = MODE == 1 ? 0x3C003C00u : 0u;
     u32 msk[P][4][8];
 #pragma unroll
     for (int h = 0; h < P; ++h)
 #pragma unroll
         for (int i1 = 0; i1 < 4; ++i1)
 #pragma unroll
-            for (int p = 0; p < 8; ++p) msk[h][i1][p] = 0;
+            for (int p = 0; p < 8; ++p) msk[h][i1][p] = kSignBase;
     const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.sign, a.sign_row ? a.n_sign_rows * n : n);
     // the sign masks of row r's sign row (called before the next row's
     // prefetch is issued, so waiting for them leaves the prefetch in flight)
-    auto load_row_msk = [&](int64_t r) {
+    // The 16 int8 signs of (h, i1) are 16 consecutive bytes of the sign row
+    // (i2 = 32 nt + 16 g .. + 15): one 16-byte load each (a lane per 4-byte
+    // piece would touch a cache line per lane per piece); dword u holds the
+    // signs of elements 4 u .. 4 u + 3, i.e. of pairs 2 u and 2 u + 1.
+    auto load_msk = [&](uint32_t base, bool ok) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < P; ++h)
+#pragma unroll
+            for (int i1 = 0; i1 < 4; ++i1) {
+                const uint32_t off =
+                    ok ? base + (uint32_t)(ln * 512 * P + h * 512 + i1 * 128 + 32 * nt + 16 * g)
+                       : kOob;
+                const v4i s16 = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            sr, off, 0, 0));
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const u32 sw = (u32)s16[u];
+                    msk[h][i1][2 * u] = kSignBase | ((sw & 0x80u) << 8) | ((sw & 0x8000u) << 16);
+                    msk[h][i1][2 * u + 1] =
+                        kSignBase | ((sw & 0x800000u) >> 8) | (sw & 0x80000000u);
+                }
+            }
+    };
+    auto load_row_msk = [&](int64_t r) __attribute__((always_inline)) {
         const int64_t e = a.sign_row[r];
         const bool ok = e >= 0 && e < a.n_sign_rows && ln < a.KC;
-#pragma unroll
-        for (int h = 0; h < P; ++h)
-#pragma unroll
-            for (int i1 = 0; i1 < 4; ++i1)
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const uint32_t off =
-                        ok ? (uint32_t)(e * n + ln * 512 * P + h * 512 + i1 * 128 + 32 * nt +
-                                        8 * u + 4 * g)
-                           : kOob;
-                    const u32 sw = __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
-                    msk[h][i1][2 * u] = ((sw & 0x80u) << 8) | ((sw & 0x8000u) << 16);
-                    msk[h][i1][2 * u + 1] = ((sw & 0x800000u) >> 8) | (sw & 0x80000000u);
-                }
+        load_msk(ok ? (uint32_t)(e * n) : 0u, ok);
     };
-    if (a.sign && !a.sign_row) {
+    if (a.sign && !a.sign_row) load_msk(0u, ln < a.KC);
+
+    // A-operand row of this lane in stage A: segment (chunk 8T + cta,
+    // quarter i1a), piece 2 ks + g.
+    const int i1a = ln & 3;
+    const int cta = ((ln >> 3) & 3) | (((ln >> 2) & 1) << 2);
+    const int ha = i1a | (((cta >> 2) & 1) << 2);
+    const int rdbase = (cta * 4 + i1a) * 256 + 16 * g;
+    // Row fetch: instruction j of wave w moves chunk c = 4j + w whole (1 KB),
+    // K / 4 instructions per wave.  Plain rows go straight from HBM to LDS
+    // (buffer loads into LDS: lane L = 16 i1 + p' writes LDS piece p' of
+    // segment (c, i1) and so reads global piece p' ^ 2h(c, i1)).  SwiGLU rows
+    // are loaded to registers (gate and up), combined, and stored.
+    const int64_t xbytes = a.rows > 0 ? ((a.rows - 1) * a.ld + n) * 2 : 0;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, xbytes);
+    const __amdgpu_buffer_rsrc_t ur = make_rsrc(SW ? a.up : a.x, xbytes);
+    const int cpw = nc / 4;
+    const int wi1 = lane >> 4, wp = lane & 15;
+    uint32_t dma_off[2];
 #pragma unroll
-        for (int h = 0; h < P; ++h)
+    for (int b = 0; b < 2; ++b) dma_off[b] = wi1 * 256 + 16 * (wp ^ (2 * (wi1 | (b << 2))));
+    v4i pre[SW ? NT * 2 : 1];
+    v4i preu[SW ? NT * 2 : 1];
+    // SwiGLU rows move in halves (PART 0: j < NT, 1: j >= NT) or whole (-1)
+    auto in_part = [](int j, auto part) __attribute__((always_inline)) {
+        constexpr int PART = decltype(part)::value;
+        return PART < 0 || (PART == 0 ? j < NT : j >= NT);
+    };
+    using Whole = std::integral_constant<int, -1>;
+    auto fetch = [&](int64_t r, int buf, auto part) __attribute__((always_inline)) {
+        const uint32_t rb = (uint32_t)(r * a.ld * 2);
+        if constexpr (!SW) {
+            const uint32_t lb = (uint32_t)(uintptr_t)&rowbuf[buf][0];
 #pragma unroll
-            for (int i1 = 0; i1 < 4; ++i1)
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    // int8 signs of i2 = 32 nt + 8u + 4g .. +3: bit 7 of each byte
-                    const uint32_t off =
-                        ln < a.KC ? (uint32_t)(ln * 512 * P + h * 512 + i1 * 128 + 32 * nt +
-                                               8 * u + 4 * g)
-                                  : kOob;
-                    const u32 sw = __builtin_amdgcn_raw_buffer_load_b32(sr, off, 0, 0);
-                    msk[h][i1][2 * u] = ((sw & 0x80u) << 8) | ((sw & 0x8000u) << 16);
-                    msk[h][i1][2 * u + 1] = ((sw & 0x800000u) >> 8) | (sw & 0x80000000u);
+            for (int j = 0; j < NT * 2; ++j)
+                if (j < cpw) {
+                    const int c = 4 * j + nt;
+                    dma16(xr, rb + c * 1024 + dma_off[(c >> 2) & 1], lb + c * 1024);
                 }
+        } else {
+            const uint32_t lr = rb + (uint32_t)(nt * 1024 + lane * 16);
+#pragma unroll
+            for (int j = 0; j < NT * 2; ++j)
+                if (j < cpw && in_part(j, part)) {
+                    pre[j] = __builtin_bit_cast(
+                        v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, lr + j * 4096, 0, 0));
+                    preu[j] = __builtin_bit_cast(
+                        v4i, __builtin_amdgcn_raw_buffer_load_b128(ur, lr + j * 4096, 0, 0));
+                }
+        }
+    };
+    // SwiGLU rows: combine the fetched gate / up pieces into rowbuf[buf]
+    auto sw_store = [&](int buf, auto part) __attribute__((always_inline)) {
+        if constexpr (SW) {
+#pragma unroll
+            for (int j = 0; j < NT * 2; ++j) {
+                if (j >= cpw || !in_part(j, part)) continue;
+                const int c = 4 * j + nt;
+                const int h = wi1 | (((c >> 2) & 1) << 2);
+                const v8h g8 = __builtin_bit_cast(v8h, pre[j]);
+                const v8h u8 = __builtin_bit_cast(v8h, preu[j]);
+                v8h o;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = swiglu1((float)g8[e], (float)u8[e]);
+                rowbuf[buf][(c * 4 + wi1) * 16 + (wp ^ (2 * h))] = __builtin_bit_cast(v4i, o);
+            }
+        }
+    };
+    for (int i = threadIdx.x; i < (NT * 8 - nc) * 64; i += 256) {
+        rowbuf[0][nc * 64 + i] = (v4i){0, 0, 0, 0};
+        rowbuf[1][nc * 64 + i] = (v4i){0, 0, 0, 0};
     }
 
-    // Settle the prologue loads here: the empty asm consumes HB and msk,
-    // so the wait for their loads is placed once, before the row loop.
+    // Row loop, one barrier per row: iteration it transforms row `row` (in
+    // rowbuf[it & 1], its block reduction into red[it & 1]) and finishes the
+    // previous row (quantization from red[(it - 1) & 1]), while the next
+    // row streams into rowbuf[(it + 1) & 1].
+    const int64_t step = gridDim.x;
+    int64_t row = blockIdx.x;
+    // SwiGLU rows of H_1024 are fetched and combined in two halves: the
+    // gate / up registers of a whole 2K-chunk row would not fit beside the
+    // transform's
+    auto fetch_sw_now = [&](int64_t r, int buf) __attribute__((always_inline)) {
+        using H0 = std::integral_constant<int, 0>;
+        using H1 = std::integral_constant<int, 1>;
+        fetch(r, buf, H0{});
+        sw_store(buf, H0{});
+        fetch(r, buf, H1{});
+        sw_store(buf, H1{});
+    };
+    if (row < a.rows) {
+        if constexpr (SW && P == 2) {
+            fetch_sw_now(row, 0);
+        } else {
+            fetch(row, 0, Whole{});
+            if constexpr (SW) sw_store(0, Whole{});
+        }
+    }
+    // Settle the prologue loads here, after the first row's fetch is issued
+    // (their latencies overlap): the empty asm consumes HB and msk, so the
+    // wait for their loads is placed once, before the row loop.
     // Otherwise the wait-count pass, unable to prove across the loop's back
     // edge that these loads are done, waits for them inside every row --
     // and, counting in order, for the next row's prefetch as well.
@@ -320,69 +443,80 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
 #pragma unroll
             for (int p = 0; p < 8; ++p) asm volatile("" : "+v"(msk[h][i1][p]));
 
-    // A-operand row of this lane in stage A: segment (chunk 8T + cta,
-    // quarter i1a), piece 2 ks + g.
-    const int i1a = ln & 3;
-    const int cta = ((ln >> 3) & 3) | (((ln >> 2) & 1) << 2);
-    const int ha = i1a | (((cta >> 2) & 1) << 2);
-    const uint8_t *rowb = reinterpret_cast<const uint8_t *>(rowbuf);
-    const int rdbase = (cta * 4 + i1a) * 256 + 16 * g;
-    // Row fetch: instruction j of wave w reads chunk c = 4j + w whole (1 KB,
-    // lane l: piece l % 16 of quarter l / 16), K / 4 instructions per wave.
-    const int64_t xbytes = a.rows > 0 ? ((a.rows - 1) * a.ld + n) * 2 : 0;
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.x, xbytes);
-    const __amdgpu_buffer_rsrc_t ur = make_rsrc(SW ? a.up : a.x, xbytes);
-    const int cpw = nc / 4;
-    const int wi1 = lane >> 4, wp = lane & 15;
-    v4i pre[NT * 2];
-    v4i preu[SW ? NT * 2 : 1];
-    auto gload = [&](int64_t r) {
-        const uint32_t rb = (uint32_t)(r * a.ld * 2) + (uint32_t)(wave * 1024 + lane * 16);
+    // SwiGLU rows of H_1024 quantize each row in its own iteration, after a
+    // second barrier: holding the previous row's outputs next to the gate /
+    // up prefetch of a 2K-chunk row would exceed the register file
+    constexpr bool kDefer = !(SW && P == 2);
+    u32 wprev[kDefer ? P : 1][4][8];
+    int64_t prev = -1;
+    // Quantize the previous row r (its K-mix outputs wprev) from its block
+    // reduction in red[par] and store its codes: MODE 1 symmetric int4 with
+    // the sign folded into the offset add, MODE 2 asymmetric uint4 (wprev is
+    // already signed).
+    auto finish_row = [&](int64_t r, int par, auto &wq) __attribute__((always_inline)) {
+        // this lane's first code byte: chunk ln, i2 = 32 nt + 16 g (quarter 0)
+        uint8_t *qlane = a.q + r * (n / 2) + (ln * 512 * P + 32 * nt + 16 * g) / 2;
+        const float *rr = red[par];
+        if constexpr (MODE == 1) {
+            if (a.sign && a.sign_row) load_row_msk(r);
+            const float amx = round16(fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3])));
+            const bool bad =
+                __builtin_amdgcn_readfirstlane((rr[4] + rr[5] + rr[6] + rr[7]) != 0.f);
+            f16 s16 = f16_rn(amx / 7.f);
+            if (a.clip != 1.f) s16 = f16_rn((float)s16 * a.clip);
+            // quotient divisor: s itself, or 2^-126 when s == 0 -- then every
+            // nonzero x overflows to ±inf and clamps to 7 / -8, and x == 0
+            // gives 0, which is what x / 0 yields after the reference's
+            // __half2int_rn (saturation, NaN -> 0)
+            const float sq = fmaxf((float)s16, 0x1p-126f);
+            const float rcp = 1.0f / sq;
+            if (threadIdx.x == 0) a.qscale[r] = s16;
+            // row-uniform: can any |x / s| round beyond ±7?
+            const bool clampit = __builtin_amdgcn_readfirstlane(!(amx <= 7.25f * sq));
+            if (ln < a.KC) {
 #pragma unroll
-        for (int j = 0; j < NT * 2; ++j)
-            if (j < cpw) {
-                pre[j] = __builtin_bit_cast(
-                    v4i, __builtin_amdgcn_raw_buffer_load_b128(xr, rb + j * 4096, 0, 0));
-                if constexpr (SW)
-                    preu[j] = __builtin_bit_cast(
-                        v4i, __builtin_amdgcn_raw_buffer_load_b128(ur, rb + j * 4096, 0, 0));
+                for (int h = 0; h < P; ++h) {
+                    uint8_t *qrow = qlane + h * 256;
+                    if (bad) quant_store_exact(wq[h], msk[h], (float)s16, qrow);
+                    else if (clampit) quant_store<true>(wq[h], msk[h], rcp, qrow);
+                    else quant_store<false>(wq[h], msk[h], rcp, qrow);
+                }
             }
-    };
-    auto lstore = [&]() {
-#pragma unroll
-        for (int j = 0; j < NT * 2; ++j) {
-            if (j >= cpw) continue;
-            const int c = 4 * j + wave;
-            const int h = wi1 | (((c >> 2) & 1) << 2);
-            v4i val = pre[j];
-            if constexpr (SW) {
-                const v8h g8 = __builtin_bit_cast(v8h, pre[j]);
-                const v8h u8 = __builtin_bit_cast(v8h, preu[j]);
-                v8h o;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) o[e] = swiglu1((float)g8[e], (float)u8[e]);
-                val = __builtin_bit_cast(v4i, o);
+        } else {
+            const float vmin = fminf(fminf(rr[0], rr[1]), fminf(rr[2], rr[3]));
+            const float vmax = fmaxf(fmaxf(rr[4], rr[5]), fmaxf(rr[6], rr[7]));
+            const bool bad = (rr[8] + rr[9] + rr[10] + rr[11]) != 0.f;
+            f16 sh, zh;
+            asym_row_params(vmin, vmax, a.clip, sh, zh);
+            if (threadIdx.x == 0) {
+                a.qscale[r] = sh;
+                a.qzero[r] = zh;
             }
-            rowbuf[(c * 4 + wi1) * 16 + (wp ^ (2 * h))] = val;
+            const float sf = (float)sh;
+            const int zi = h2i_rn((float)zh);
+            const bool fast = __builtin_amdgcn_readfirstlane(!bad && sf > 0.f && zi >= -511 &&
+                                                             zi <= 511);
+            const float rcp = 1.0f / fmaxf(sf, 0x1p-126f);
+            const v2h lo2 = (v2h){(f16)(float)(-zi), (f16)(float)(-zi)};
+            const v2h hi2 = (v2h){(f16)(float)(15 - zi), (f16)(float)(15 - zi)};
+            const v2h zo2 = (v2h){(f16)(float)zi, (f16)(float)zi};
+            if (ln < a.KC) {
+#pragma unroll
+                for (int h = 0; h < P; ++h) {
+                    uint8_t *qrow = qlane + h * 256;
+                    if (fast) quant_store_asym<true>(wq[h], rcp, lo2, hi2, zo2, sf, zi, qrow);
+                    else quant_store_asym<false>(wq[h], rcp, lo2, hi2, zo2, sf, zi, qrow);
+                }
+            }
         }
     };
-    for (int i = threadIdx.x; i < (NT * 8 - nc) * 64; i += 256)
-        rowbuf[nc * 64 + i] = (v4i){0, 0, 0, 0};
-
-    const int64_t step = gridDim.x;
-    int64_t row = blockIdx.x;
-    if (row < a.rows) {
-        gload(row);
-        lstore();
-    }
-    for (int it = 0; row < a.rows; row += step, ++it) {
-        // every wave's LDS writes of this row are done
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        const bool more = row + step < a.rows;
-        if (a.sign && a.sign_row) load_row_msk(row);
-        if (more) gload(row + step);
+    // Transform row `row` from rowbuf[buf]: stages A and B, the K-mix
+    // into w (packed fp16), MODE 0 stores, MODE 1 / 2 partial row
+    // reductions into red[par].
+    auto transform = [&](int64_t row, int buf, int par, u32 (&w)[P][4][8])
+                         __attribute__((always_inline)) {
+        const uint8_t *rowb = reinterpret_cast<const uint8_t *>(&rowbuf[buf][0]);
+        if (a.sign && a.sign_row && MODE != 1) load_row_msk(row);
 
         // ---- stage A (H_128 over i2, this wave's 32 output columns) and
         // stage B (H_4 over i1), y = fp16(FWHT * 1/sqrt(n)) into the K-mix
@@ -405,7 +539,7 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
         // T (left to itself the scheduler puts each read just before its
         // MFMA and exposes every LDS round trip).
         v8h xk[2][8];
-        auto rd = [&](int T, int ks) {
+        auto rd = [&](int T, int ks) __attribute__((always_inline)) {
             return *reinterpret_cast<const v8h *>(rowb + T * 8192 + rdbase + 32 * (ks ^ ha));
         };
         // Stage B (+ the bit-9 stage for P = 2) and the first rounding
@@ -413,7 +547,7 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
         // [v%4] element 4 (T%2) + v/4, the pairs (v, v + 4) adjacent
         // elements.  P = 2: registers (4h + i1, 4h + i1 + 8) -> ka[T/4][h]
         // [i1] elements 2 (T%4), 2 (T%4) + 1.
-        auto finish = [&](v16f d, int T) {
+        auto finish = [&](v16f d, int T) __attribute__((always_inline)) {
 #pragma unroll
             for (int v = 0; v < 16; v += 4) {
                 const float a0 = d[v], a1 = d[v + 1], a2 = d[v + 2], a3 = d[v + 3];
@@ -478,13 +612,15 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
         }
         finish(dprev, NT - 1);
 
-        // ---- K-mix: round to fp16, apply the sign, keep; row max of |out|
-        // (NaN-ignoring, as the reference's fmaxf).  MODE 2: packed min and
-        // max of the signed fp16 values (NaN-ignoring, as fminf / fmaxf).
-        // MODE 1 and 2: a NaN-propagating max of |x| that flags rows with a
-        // NaN or inf; lanes past the K chunks hold no outputs and stay out.
-        u32 w[P][4][8];
-        float amax = 0.f;
+        // ---- K-mix: round to fp16 and keep (MODE 0 and 2 apply the sign
+        // here; MODE 1 folds it into the quantizer).  MODE 1: row max of |out|
+        // (NaN-ignoring, as the reference's fmaxf) and a NaN-propagating max of
+        // |out| in fp32, which flags rows holding a NaN or an output that
+        // rounds to inf (|out| >= 65520).  MODE 2: packed min and max of the
+        // signed fp16 values (NaN-ignoring, as fminf / fmaxf) and the packed
+        // NaN-propagating max of |x|.  Lanes past the K chunks hold no outputs
+        // and stay out of the flags.
+        float amax = 0.f, anan = 0.f;
         v2h mn2 = (v2h){(f16)__builtin_inff(), (f16)__builtin_inff()};
         v2h mx2 = -mn2, ab2 = (v2h){0, 0};
 #pragma unroll
@@ -496,14 +632,19 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
                 if (NS > 1) z = mfma32(ka[NS > 1 ? 1 : 0][h][i1].h, HB[1], z);
 #pragma unroll
                 for (int p = 0; p < 8; ++p) {
-                    if (MODE != 2) amax = absmax3(amax, z[2 * p], z[2 * p + 1]);
-                    w[h][i1][p] = pk16(z[2 * p], z[2 * p + 1]) ^ msk[h][i1][p];
-                    if (MODE >= 1 && ln < a.KC) {
+                    if (MODE == 1) {
+                        amax = absmax3(amax, z[2 * p], z[2 * p + 1]);
+                        anan = __builtin_elementwise_maximum(
+                            __builtin_elementwise_maximum(anan, fabsf(z[2 * p])),
+                            fabsf(z[2 * p + 1]));
+                        w[h][i1][p] = pk16(z[2 * p], z[2 * p + 1]);
+                    } else {
+                        w[h][i1][p] = pk16(z[2 * p], z[2 * p + 1]) ^ msk[h][i1][p];
+                    }
+                    if (MODE == 2 && ln < a.KC) {
                         const v2h v = __builtin_bit_cast(v2h, w[h][i1][p]);
-                        if (MODE == 2) {
-                            mn2 = __builtin_elementwise_min(mn2, v);
-                            mx2 = __builtin_elementwise_max(mx2, v);
-                        }
+                        mn2 = __builtin_elementwise_min(mn2, v);
+                        mx2 = __builtin_elementwise_max(mx2, v);
                         ab2 = __builtin_elementwise_maximum(ab2, __builtin_elementwise_abs(v));
                     }
                 }
@@ -514,71 +655,32 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
                 for (int h = 0; h < P; ++h)
 #pragma unroll
                     for (int i1 = 0; i1 < 4; ++i1) {
-                        // runs of 4 fp16 (8 bytes) at i2 = 32 nt + 8u + 4g
+                        // 16 fp16 (32 bytes) at i2 = 32 nt + 16 g
                         f16 *orow = a.out + row * n + ln * 512 * P + h * 512 + i1 * 128 +
-                                    32 * nt + 4 * g;
+                                    32 * nt + 16 * g;
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            uint2 pk;
-                            pk.x = w[h][i1][2 * u];
-                            pk.y = w[h][i1][2 * u + 1];
-                            *reinterpret_cast<uint2 *>(orow + 8 * u) = pk;
+                        for (int hh = 0; hh < 2; ++hh) {
+                            uint4 pk;
+                            pk.x = w[h][i1][4 * hh];
+                            pk.y = w[h][i1][4 * hh + 1];
+                            pk.z = w[h][i1][4 * hh + 2];
+                            pk.w = w[h][i1][4 * hh + 3];
+                            *reinterpret_cast<uint4 *>(orow + 8 * hh) = pk;
                         }
                     }
             }
-            if (more) {
-                // every wave is done reading this row from LDS
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                __builtin_amdgcn_s_barrier();
-                asm volatile("" ::: "memory");
-                lstore();
-            }
-            continue;
         }
-
         if constexpr (MODE == 1) {
-            // ---- block row max (this barrier also ends every wave's LDS
-            // reads of the row, so the prefetched row may be written after)
+            // partial row max |x| and non-finite flag of this wave
             amax = wave_max_dpp(amax);
-            const bool badl = !((float)ab2[0] <= 65504.f) || !((float)ab2[1] <= 65504.f);
+            const bool badl = ln < a.KC && !(anan < 65520.f);
             const bool wbad = __builtin_amdgcn_ballot_w64(badl) != 0;
             if (lane == 0) {
-                red[it & 1][wave] = amax;
-                red[it & 1][4 + wave] = wbad ? 1.f : 0.f;
+                red[par][nt] = amax;
+                red[par][4 + nt] = wbad ? 1.f : 0.f;
             }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            const float *rr = red[it & 1];
-            amax = round16(fmaxf(fmaxf(rr[0], rr[1]), fmaxf(rr[2], rr[3])));
-            const bool bad =
-                __builtin_amdgcn_readfirstlane((rr[4] + rr[5] + rr[6] + rr[7]) != 0.f);
-
-            f16 s16 = f16_rn(amax / 7.f);
-            if (a.clip != 1.f) s16 = f16_rn((float)s16 * a.clip);
-            // quotient divisor: s itself, or 2^-126 when s == 0 -- then every
-            // nonzero x overflows to ±inf and clamps to 7 / -8, and x == 0
-            // gives 0, which is what x / 0 yields after the reference's
-            // __half2int_rn (saturation, NaN -> 0)
-            const float sq = fmaxf((float)s16, 0x1p-126f);
-            const float rcp = 1.0f / sq;
-            if (threadIdx.x == 0) a.qscale[row] = s16;
-            // row-uniform: can any |x / s| round beyond ±7?
-            const bool clampit = __builtin_amdgcn_readfirstlane(!(amax <= 7.25f * sq));
-
-            if (ln < a.KC) {
-#pragma unroll
-                for (int h = 0; h < P; ++h) {
-                    uint8_t *qrow =
-                        reinterpret_cast<uint8_t *>(cbuf) + (P * ln + h) * 272 + 16 * nt + 2 * g;
-                    if (bad) quant_store_exact(w[h], (float)s16, qrow);
-                    else if (clampit) quant_store<true>(w[h], rcp, qrow);
-                    else quant_store<false>(w[h], rcp, qrow);
-                }
-            }
-        } else {
-            // ---- block row min / max and non-finite flag (the barrier also
-            // ends every wave's LDS reads of the row)
+        } else if constexpr (MODE == 2) {
+            // partial row min / max and non-finite flag of this wave
             float fmn = fminf((float)mn2[0], (float)mn2[1]);
             float fmx = fmaxf((float)mx2[0], (float)mx2[1]);
             const bool badl = !((float)ab2[0] <= 65504.f) || !((float)ab2[1] <= 65504.f);
@@ -586,65 +688,55 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
             fmx = wave_max_dpp(fmx);
             const bool wbad = __builtin_amdgcn_ballot_w64(badl) != 0;
             if (lane == 0) {
-                red[it & 1][wave] = fmn;
-                red[it & 1][4 + wave] = fmx;
-                red[it & 1][8 + wave] = wbad ? 1.f : 0.f;
-            }
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            const float* rr = red[it & 1];
-            const float vmin = fminf(fminf(rr[0], rr[1]), fminf(rr[2], rr[3]));
-            const float vmax = fmaxf(fmaxf(rr[4], rr[5]), fmaxf(rr[6], rr[7]));
-            const bool bad = (rr[8] + rr[9] + rr[10] + rr[11]) != 0.f;
-            f16 sh, zh;
-            asym_row_params(vmin, vmax, a.clip, sh, zh);
-            if (threadIdx.x == 0) {
-                a.qscale[row] = sh;
-                a.qzero[row] = zh;
-            }
-            const float sf = (float)sh;
-            const int zi = h2i_rn((float)zh);
-            const bool fast = __builtin_amdgcn_readfirstlane(!bad && sf > 0.f && zi >= -511 &&
-                                                             zi <= 511);
-            const float rcp = 1.0f / fmaxf(sf, 0x1p-126f);
-            const v2h lo2 = (v2h){(f16)(float)(-zi), (f16)(float)(-zi)};
-            const v2h hi2 = (v2h){(f16)(float)(15 - zi), (f16)(float)(15 - zi)};
-            const v2h zo2 = (v2h){(f16)(float)zi, (f16)(float)zi};
-            if (ln < a.KC) {
-#pragma unroll
-                for (int h = 0; h < P; ++h) {
-                    uint8_t *qrow =
-                        reinterpret_cast<uint8_t *>(cbuf) + (P * ln + h) * 272 + 16 * nt + 2 * g;
-                    if (fast) quant_store_asym<true>(w[h], rcp, lo2, hi2, zo2, sf, zi, qrow);
-                    else quant_store_asym<false>(w[h], rcp, lo2, hi2, zo2, sf, zi, qrow);
-                }
+                red[par][nt] = fmn;
+                red[par][4 + nt] = fmx;
+                red[par][8 + nt] = wbad ? 1.f : 0.f;
             }
         }
-        // the row's codes are staged; write them out 16 bytes per lane
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    };
+    // One row per iteration and one barrier per row: iteration it
+    // transforms row `row` (rowbuf[it & 1], reduction into red[it & 1])
+    // and finishes the previous row, while the next row streams into
+    // rowbuf[(it + 1) & 1].
+    for (int it = 0;; ++it) {
+        const bool have = row < a.rows;
+        // this wave's row fetches (and the previous row's code stores)
+        // are done; after the barrier every wave's are, every wave has
+        // finished the previous iteration's LDS reads, and
+        // red[(it - 1) & 1] is whole
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        {
-            // LDS reads of the codes, then the prefetched row into LDS, then
-            // the global stores: the wait for the prefetch (vmcnt counts in
-            // order) then does not also wait for this row's code stores
-            constexpr int R = (NT * 8 * 16 + 255) / 256;
-            const int pieces = nc * 16;
-            v4i cv[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int pc = threadIdx.x + 256 * r;
-                cv[r] = pc < pieces ? cbuf[(pc >> 4) * 17 + (pc & 15)] : (v4i){};
-            }
-            if (more) lstore();
-            uint8_t *qout = a.q + row * (n / 2);
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const int pc = threadIdx.x + 256 * r;
-                if (pc < pieces) *reinterpret_cast<v4i *>(qout + pc * 16) = cv[r];
+        const bool more = have && row + step < a.rows;
+        if constexpr (SW && P == 2) {
+            // the next row, combined now so its gate / up registers are
+            // free during this row's transform
+            if (more) fetch_sw_now(row + step, (it + 1) & 1);
+        } else {
+            if (more) fetch(row + step, (it + 1) & 1, Whole{});
+        }
+        if constexpr (MODE >= 1 && kDefer) {
+            if (prev >= 0) finish_row(prev, (it - 1) & 1, wprev);
+            prev = -1;
+        }
+        if (!have) break;
+        if constexpr (kDefer) {
+            transform(row, it & 1, it & 1, wprev);
+            prev = row;
+        } else {
+            u32 w[P][4][8];
+            transform(row, it & 1, it & 1, w);
+            if constexpr (MODE >= 1) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                finish_row(row, it & 1, w);
             }
         }
+        if constexpr (SW && P == 1) {
+            if (more) sw_store((it + 1) & 1, Whole{});
+        }
+        row += step;
     }
 }
 
@@ -671,8 +763,8 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     if (ld < n) ld = n;
     if (rows > 0 && ((rows - 1) * ld + n) * 2 >= (int64_t)kOob) return 0;  // 32-bit offsets
     if (!srq_aligned(x, 16) || (up && !srq_aligned(up, 16)) || ld % 8) return 0;
-    if (q && !srq_aligned(q, 16)) return 0;  // 16-byte code stores
-    if (out && !srq_aligned(out, 8)) return 0;
+    if (q && !srq_aligned(q, 8)) return 0;     // 8-byte code stores
+    if (out && !srq_aligned(out, 16)) return 0;  // 16-byte fp16 stores
     MfmaRotArgs a{};
     a.x = (const f16 *)x;
     a.rows = rows;
