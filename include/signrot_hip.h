@@ -117,6 +117,42 @@ int srq_w4a4_linear_residual(const void *A, const void *a_scale, const void *B,
                              const void *b_scale, const void *bias, const void *residual,
                              int64_t M, int64_t N, int64_t K, void *out, void *stream);
 
+/* ------------------------------------------------------------ bf6 GEMM
+ * The same int4 x int4 products on gfx950's 6-bit-operand MFMA
+ * (v_mfma_scale_f32_32x32x64_f8f6f4, e3m2 operands), twice the int8 MFMA
+ * rate and bit-identical: every int4 code is an exact e3m2 value and the fp32
+ * accumulator holds the integer sums exactly (|sum| <= 64 K < 2^24).
+ * Operands are in the bf6 block layout: for an R x K code matrix (K % 128
+ * == 0, rows padded to a multiple of 32 with zero codes), 32 x 128 blocks of
+ * 3072 bytes, block (rb, kb) at byte (rb * K / 128 + kb) * 3072; for MFMA
+ * k-slice q (0, 1), lane l = r + 32 h of a block carries codes
+ * 128 kb + 64 q + 32 h + j (j < 32) of row 32 rb + r as e3m2 bit fields j
+ * (bits 6 j .. 6 j + 5) of 192 bits, bytes 0-15 at 1024 q + 16 l and bytes
+ * 16-23 at 2048 + 16 l + 8 q.  No reference counterpart: an
+ * execution layout for the products of srq_matmul_s4s4 / srq_w4a4_linear
+ * (signrot/kernels/gemm.cu:7-45, quant.cu:84-87), e.g. for a weight
+ * converted once at load. */
+
+/* Bytes of the bf6 block layout of a [rows, K] code matrix, or -1 if
+ * K % 128 != 0 or a size is negative. */
+int64_t srq_bf6_bytes(int64_t rows, int64_t K);
+
+/* Packed int4 rows (the reference's layout) src u8 [rows, K/2] -> dst in the
+ * bf6 block layout (srq_bf6_bytes(rows, K) bytes).  K % 128 == 0; src and dst
+ * 16-byte aligned. */
+int srq_i4_to_bf6(const void *src, int64_t rows, int64_t K, void *dst, void *stream);
+
+/* C int32 [M, N] = A @ B^T from bf6-layout A6 (M rows) and B6 (N rows);
+ * equal to srq_matmul_s4s4 on the int4 operands.  K % 128 == 0, K < 131072. */
+int srq_matmul_bf6(const void *A6, const void *B6, int64_t M, int64_t N, int64_t K,
+                   int32_t *C, void *stream);
+
+/* srq_w4a4_linear from bf6-layout operands: out f16 [M, N] =
+ * fp16((float(C) * a_scale[m]) * b_scale[n]) (+ bias[n]), bit-identical. */
+int srq_w4a4_linear_bf6(const void *A6, const void *a_scale, const void *B6,
+                        const void *b_scale, const void *bias, int64_t M, int64_t N,
+                        int64_t K, void *out, void *stream);
+
 /* --------------------------------------------------------------- Hadamard */
 
 /* Walsh-Hadamard transform (Sylvester order) over the last dim, times scale.
@@ -148,6 +184,18 @@ int srq_online_hadamard(const void *x, void *out, int64_t rows, int64_t n, int64
 int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_t K,
                        const void *hadK, const int8_t *sign, int fp32_had,
                        float clip_ratio, void *q, void *scale, void *stream);
+
+/* srq_had_sign_quant writing the codes in the bf6 block layout of
+ * srq_i4_to_bf6 (rows of n codes) for srq_w4a4_linear_bf6: q6 u8
+ * [srq_bf6_bytes(rows, n)] (the code fields of rows past `rows` in the last
+ * 32-row block are left unwritten), scale f16 [rows].  The same codes and
+ * scales as srq_had_sign_quant.  Needs the MFMA rotation (K % 4 == 0,
+ * n = K * 512 or K * 1024, 9 <= K <= 32), else SRQ_EUNSUPPORTED.  No
+ * reference counterpart (an execution layout of OnlineHadamard + Quantizer,
+ * signrot/nn/hadamard.py:26-42, nn/quantization.py:11-40). */
+int srq_had_sign_quant_bf6(const void *x, int64_t rows, int64_t n, int64_t K,
+                           const void *hadK, const int8_t *sign, float clip_ratio,
+                           void *q6, void *scale, void *stream);
 
 /* Rotation + sign of srq_had_sign_quant followed by the per-token asymmetric
  * uint4 quantizer of srq_asym_quant_dynamic (row min/max of the rotated,

@@ -132,6 +132,75 @@ def w4a4_linear(A, a_scale, B, b_scale, bias=None):
     return out
 
 
+# ------------------------------------------------------------- bf6 GEMM
+# The same W4A4 products on the 6-bit-operand MFMA (twice the int8 rate),
+# from operands in the bf6 block layout (srq_i4_to_bf6 in
+# include/signrot_hip.h): a weight is converted once, the product is
+# bit-identical to matmul / w4a4_linear on the packed int4 operands.
+
+def bf6_bytes(rows, K):
+    """Bytes of the bf6 block layout of a [rows, K] code matrix (K % 128 == 0)."""
+    if K % 128:
+        raise RuntimeError(f"bf6_bytes: K={K} must be a multiple of 128")
+    return -(-rows // 32) * (K // 128) * 3072
+
+
+def i4_to_bf6(W):
+    """Packed int4 rows u8 [R, K/2] -> the bf6 block layout, u8 [bf6_bytes(R, K)]."""
+    _check("i4_to_bf6", [(W, "W")], [torch.uint8])
+    if W.dim() != 2:
+        raise RuntimeError(f"i4_to_bf6: expected [R, K/2], got {tuple(W.shape)}")
+    R, K = W.shape[0], W.shape[1] * 2
+    out = torch.empty(bf6_bytes(R, K), dtype=torch.uint8, device=W.device)
+    _call("srq_i4_to_bf6", _ptr(W), R, K, _ptr(out), _stream(W))
+    return out
+
+
+def had_sign_quant_bf6(x, hadK, K, sign=None, clip_ratio=1.0):
+    """had_sign_quant with the codes in the bf6 block layout: (q6 u8
+    [bf6_bytes(rows, n)], scale f16 [..., 1]); the same codes and scales."""
+    _check("had_sign_quant_bf6", [(x, "x"), (hadK, "hadK"), (sign, "sign")],
+           [torch.float16, torch.float16, torch.int8])
+    n = x.shape[-1]
+    _check_had("had_sign_quant_bf6", n, hadK, K, sign, False)
+    rows = x.numel() // n if n else 0
+    q6 = torch.empty(bf6_bytes(rows, n), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((*x.shape[:-1], 1), dtype=torch.float16, device=x.device)
+    if rows:
+        _call("srq_had_sign_quant_bf6", _ptr(x), rows, n, int(K), _ptr(hadK), _ptr(sign),
+              float(clip_ratio), _ptr(q6), _ptr(scale), _stream(x))
+    return q6, scale
+
+
+def _bf6_operands(name, A6, B6, M, N, K):
+    _check(name, [(A6, "A6"), (B6, "B6")], [torch.uint8, torch.uint8])
+    if A6.numel() < bf6_bytes(M, K) or B6.numel() < bf6_bytes(N, K):
+        raise RuntimeError(f"{name}: A6 / B6 hold fewer bytes than bf6_bytes(M or N, K)")
+
+
+def matmul_bf6(A6, B6, M, N, K):
+    """int32 [M, N] = A @ B^T from bf6-layout operands (== matmul on int4)."""
+    _bf6_operands("matmul_bf6", A6, B6, M, N, K)
+    C = torch.empty((M, N), dtype=torch.int32, device=A6.device)
+    _call("srq_matmul_bf6", _ptr(A6), _ptr(B6), M, N, K, _ptr(C), _stream(A6))
+    return C
+
+
+def w4a4_linear_bf6(A6, a_scale, B6, b_scale, M, N, K, bias=None):
+    """w4a4_linear from bf6-layout operands: out f16 [M, N], bit-identical."""
+    _bf6_operands("w4a4_linear_bf6", A6, B6, M, N, K)
+    _check("w4a4_linear_bf6", [(a_scale, "a_scale"), (b_scale, "b_scale"), (bias, "bias")],
+           [torch.float16, torch.float16, torch.float16])
+    if a_scale.numel() != M or b_scale.numel() != N:
+        raise RuntimeError("w4a4_linear_bf6: a_scale must have M and b_scale N elements")
+    if bias is not None and bias.numel() != N:
+        raise RuntimeError("w4a4_linear_bf6: bias must have N elements")
+    out = torch.empty((M, N), dtype=torch.float16, device=A6.device)
+    _call("srq_w4a4_linear_bf6", _ptr(A6), _ptr(a_scale), _ptr(B6), _ptr(b_scale), _ptr(bias),
+          M, N, K, _ptr(out), _stream(A6))
+    return out
+
+
 # ------------------------------------------------------------------ quant
 
 def w4a4_linear_residual(A, a_scale, B, b_scale, residual, bias=None, out=None):

@@ -32,6 +32,10 @@ SIGNATURES = {
     "srq_asym_quant": [_p, _p, _p, _i64, _i64, _i32, _p, _p],
     "srq_sum_i4": [_p, _i64, _i64, _i32, _p, _p],
     "srq_matmul_colrow_i8_i32": [_p, _p, _i64, _i64, _p, _p],
+    "srq_i4_to_bf6": [_p, _i64, _i64, _p, _p],
+    "srq_had_sign_quant_bf6": [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _p, _p],
+    "srq_matmul_bf6": [_p, _p, _i64, _i64, _i64, _p, _p],
+    "srq_w4a4_linear_bf6": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_swiglu_had_sign_quant_moe": [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _f32,
                                       _p, _p, _p],
     "srq_hadamard_transform": [_p, _p, _i64, _i64, _f32, _i32, _p],
@@ -82,6 +86,8 @@ def lib():
         handle.srq_last_error.argtypes = []
         handle.srq_abi_version.restype = ctypes.c_int
         handle.srq_abi_version.argtypes = []
+        handle.srq_bf6_bytes.restype = ctypes.c_int64
+        handle.srq_bf6_bytes.argtypes = [_i64, _i64]
         for name, args in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = args

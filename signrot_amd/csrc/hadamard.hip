@@ -404,7 +404,7 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
                     hipStream_t st, const void *up = nullptr, int64_t ld = 0,
                     const int32_t *sign_row = nullptr, int64_t n_sign_rows = 0,
-                    void *qzero = nullptr);
+                    void *qzero = nullptr, int bf6 = 0);
 
 extern "C" int srq_hadamard_transform(const void *x, void *out, int64_t rows, int64_t n,
                                       float scale, int dtype, void *stream) {
@@ -536,6 +536,25 @@ extern "C" int srq_swiglu_had_sign_quant_moe(const void *gate, const void *up, i
     }
     srq_set_error("swiglu_had_sign_quant_moe: needs n = K * 512 with 9 <= K <= 32, K %% 4 == 0 "
                   "(n=%lld, K=%lld)", (long long)n, (long long)K);
+    return SRQ_EUNSUPPORTED;
+}
+
+extern "C" int srq_had_sign_quant_bf6(const void *x, int64_t rows, int64_t n, int64_t K,
+                                      const void *hadK, const int8_t *sign, float clip_ratio,
+                                      void *q6, void *scale, void *stream) {
+    int rc = check_rotation("had_sign_quant_bf6", x, rows, n, K, hadK);
+    if (rc) return rc;
+    if (rows == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(q6 && scale, "had_sign_quant_bf6: null output");
+    SRQ_CHECK_ARG(srq_aligned(x, 16) && srq_aligned(q6, 16),
+                  "had_sign_quant_bf6: x and q6 must be 16-byte aligned");
+    if (srq_had512_mfma(x, rows, n, K, hadK, sign, clip_ratio, q6, scale, nullptr,
+                        (hipStream_t)stream, nullptr, 0, nullptr, 0, nullptr, 1)) {
+        SRQ_LAUNCH_CHECK("had_sign_quant_bf6");
+        return SRQ_OK;
+    }
+    srq_set_error("had_sign_quant_bf6: needs K %% 4 == 0 and n = K * 512 or K * 1024 with "
+                  "9 <= K <= 32 (n=%lld, K=%lld)", (long long)n, (long long)K);
     return SRQ_EUNSUPPORTED;
 }
 

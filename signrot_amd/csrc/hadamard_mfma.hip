@@ -95,6 +95,9 @@ struct MfmaRotArgs {
     // [n_sign_rows, n] sign table (ids outside the table: sign +1)
     const int32_t *sign_row;
     int64_t n_sign_rows;
+    // MODE 1: write the codes in the bf6 block layout of srq_i4_to_bf6
+    // (rows of n codes, n % 128 == 0) instead of packed int4
+    int bf6;
 };
 
 // Stores of one lane's results.  After the K-mix a lane (chunk ln, half g)
@@ -156,6 +159,75 @@ SRQ_DEV void quant_store_exact(const u32 (&w)[4][8], const u32 (&sg)[4][8], floa
             c[e / 8] |= (u32)(sym_code_r(x, r) & 0xF) << (4 * (e % 8));
         }
         *reinterpret_cast<uint2 *>(qrow + i1 * 64) = (uint2){c[0], c[1]};
+    }
+}
+
+// bf6 output (MODE 1 with MfmaRotArgs::bf6): the codes of a lane's 16
+// consecutive outputs i2 = 32 nt + 16 g + e of one quarter are fields
+// j = 16 g + e of MFMA lane (row % 32) + 32 (nt % 2), k slice nt / 2, of
+// the quarter's 32 x 128 block: 96 bits, written as three dwords -- g = 0 to
+// bytes 0-11 of the slice's 16-byte run X, g = 1 to bytes 12-15 of X and
+// the slice's 8 bytes of the shared run Y.
+typedef _Float16 v32h __attribute__((ext_vector_type(32)));
+typedef int v6i __attribute__((ext_vector_type(6)));
+
+// Two quarters' codes per conversion: c[0] (quarter i1) and c[1] (i1 + 1),
+// 16 each -> 192 bits, the first 96 for quarter i1.
+SRQ_DEV void store_bf6_pair(const v2h (&c)[2][8], uint8_t *const *X, uint8_t *const *Y, int g) {
+    v32h v;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            v[16 * t + 2 * p] = c[t][p][0];
+            v[16 * t + 2 * p + 1] = c[t][p][1];
+        }
+    const v6i o = __builtin_amdgcn_cvt_scalef32_pk32_bf6_f16(v, 1.0f);  // exact integers
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        u32 *d0 = reinterpret_cast<u32 *>(g ? X[t] + 12 : X[t]);
+        u32 *d1 = reinterpret_cast<u32 *>(g ? Y[t] : X[t] + 4);
+        u32 *d2 = reinterpret_cast<u32 *>(g ? Y[t] + 4 : X[t] + 8);
+        *d0 = (u32)o[3 * t];
+        *d1 = (u32)o[3 * t + 1];
+        *d2 = (u32)o[3 * t + 2];
+    }
+}
+
+template <bool CLAMP>
+SRQ_DEV void quant_store_bf6(const u32 (&w)[4][8], const u32 (&sg)[4][8], float rcp,
+                             uint8_t *const (&X)[4], uint8_t *const (&Y)[4], int g) {
+#pragma unroll
+    for (int i0 = 0; i0 < 4; i0 += 2) {
+        v2h c[2][8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int p = 0; p < 8; ++p)
+                c[t][p] = __builtin_bit_cast(v2h, offset_codes_signed<CLAMP>(
+                                                      quot2(w[i0 + t][p], rcp), sg[i0 + t][p])) -
+                          (v2h){1544, 1544};  // the signed code, exact
+        store_bf6_pair(c, X + i0, Y + i0, g);
+    }
+}
+
+// the exact per-element codes (rows holding a NaN or inf), bf6 output
+SRQ_DEV void quant_store_bf6_exact(const u32 (&w)[4][8], const u32 (&sg)[4][8], float s,
+                                   uint8_t *const (&X)[4], uint8_t *const (&Y)[4], int g) {
+    const float r = sym_recip(s);
+#pragma unroll
+    for (int i0 = 0; i0 < 4; i0 += 2) {
+        v2h c[2][8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const v2h pr = __builtin_bit_cast(v2h, w[i0 + t][e / 2]);
+                const v2h sp = __builtin_bit_cast(v2h, sg[i0 + t][e / 2]);
+                c[t][e / 2][e & 1] =
+                    (f16)(float)sym_code_r((float)pr[e & 1] * (float)sp[e & 1], r);
+            }
+        store_bf6_pair(c, X + i0, Y + i0, g);
     }
 }
 
@@ -473,13 +545,30 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
             if (threadIdx.x == 0) a.qscale[r] = s16;
             // row-uniform: can any |x / s| round beyond ±7?
             const bool clampit = __builtin_amdgcn_readfirstlane(!(amx <= 7.25f * sq));
-            if (ln < a.KC) {
+            if (ln < a.KC && !a.bf6) {
 #pragma unroll
                 for (int h = 0; h < P; ++h) {
                     uint8_t *qrow = qlane + h * 256;
                     if (bad) quant_store_exact(wq[h], msk[h], (float)s16, qrow);
                     else if (clampit) quant_store<true>(wq[h], msk[h], rcp, qrow);
                     else quant_store<false>(wq[h], msk[h], rcp, qrow);
+                }
+            } else if (ln < a.KC) {
+                // 32 x 128 block (r / 32, kb) with kb = 4 (P ln + h) + i1
+                const int lm = (int)(r & 31) + 32 * (nt & 1);
+                uint8_t *rowblk = a.q + (r >> 5) * (int64_t)(n / 128) * 3072;
+#pragma unroll
+                for (int h = 0; h < P; ++h) {
+                    uint8_t *X[4], *Y[4];
+#pragma unroll
+                    for (int i1 = 0; i1 < 4; ++i1) {
+                        uint8_t *blk = rowblk + (int64_t)(4 * (P * ln + h) + i1) * 3072;
+                        X[i1] = blk + 1024 * (nt >> 1) + 16 * lm;
+                        Y[i1] = blk + 2048 + 16 * lm + 8 * (nt >> 1);
+                    }
+                    if (bad) quant_store_bf6_exact(wq[h], msk[h], (float)s16, X, Y, g);
+                    else if (clampit) quant_store_bf6<true>(wq[h], msk[h], rcp, X, Y, g);
+                    else quant_store_bf6<false>(wq[h], msk[h], rcp, X, Y, g);
                 }
             }
         } else {
@@ -747,7 +836,7 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
 int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
                     const int8_t *sign, float clip, void *q, void *qscale, void *out,
                     hipStream_t st, const void *up, int64_t ld, const int32_t *sign_row,
-                    int64_t n_sign_rows, void *qzero) {
+                    int64_t n_sign_rows, void *qzero, int bf6) {
     // K % 4 == 0: the row fetch moves 4 chunks per instruction and the hadK
     // loads take runs of 2 or 4 table entries (every Hadamard order above 2
     // is a multiple of 4)
@@ -760,6 +849,7 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     // row: it fits the register file up to K = 28 (K = 32 would spill)
     if (up && P == 2 && K > 28) return 0;
     if (qzero && (up || !q)) return 0;  // asymmetric codes: plain rows only
+    if (bf6 && (!q || qzero || n % 128 || !srq_aligned(q, 16))) return 0;
     if (ld < n) ld = n;
     if (rows > 0 && ((rows - 1) * ld + n) * 2 >= (int64_t)kOob) return 0;  // 32-bit offsets
     if (!srq_aligned(x, 16) || (up && !srq_aligned(up, 16)) || ld % 8) return 0;
@@ -781,6 +871,7 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
     a.sign_row = sign_row;
     a.n_sign_rows = n_sign_rows;
     a.qzero = (f16 *)qzero;
+    a.bf6 = bf6;
     // persistent blocks of 4 waves, up to 2 per CU (256 CUs; 1 with the
     // SwiGLU input, H_1024 chunks or the asymmetric quantizer), one row each
     // at a time
