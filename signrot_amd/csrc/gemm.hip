@@ -149,123 +149,6 @@ SRQ_DEV void store_block(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t
 }
 
 // ---------------------------------------------------------------------------
-// Tile kernel: BM x BN block per workgroup of 4 waves (2 x 2), each wave
-// (BM/2) x (BN/2) made of 16x16 MFMA blocks; BK = 256 int4 (128 bytes) per
-// main-loop step.  Global -> registers (prefetch of the next step) ->
-// LDS (one buffer, rows padded to 144 bytes so the 16 rows an MFMA fragment
-// reads land on distinct banks) -> registers -> MFMA.
-
-constexpr int kBK = 256;             // int4 elements per step
-constexpr int kBKB = kBK / 2;        // bytes per row per step
-constexpr int kLdsRow = kBKB + 16;   // padded LDS row stride (bytes)
-
-template <int BM, int BN, bool UA>
-__global__ __launch_bounds__(256) void gemm_tile_kernel(const uint8_t *__restrict__ A,
-                                                        const uint8_t *__restrict__ B,
-                                                        int64_t M, int64_t N, int64_t K,
-                                                        Epi e) {
-    constexpr int WM = BM / 2, WN = BN / 2;      // per-wave tile
-    constexpr int FM = WM / 16, FN = WN / 16;    // MFMA blocks per wave
-    constexpr int A_CHUNKS = BM * kBKB / 16 / 256;  // 16-byte chunks per thread
-    constexpr int B_CHUNKS = BN * kBKB / 16 / 256;
-    __shared__ __attribute__((aligned(16))) uint8_t As[BM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[BN * kLdsRow];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-
-    // XCD-aware tile order: consecutive workgroups land on different XCDs
-    // (round-robin dispatch), so give each XCD a contiguous range of tiles.
-    const int64_t tiles_n = (N + BN - 1) / BN;
-    const int64_t tiles = ((M + BM - 1) / BM) * tiles_n;
-    int64_t t = blockIdx.x;
-    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
-    const int64_t m0 = (t / tiles_n) * BM;
-    const int64_t n0 = (t % tiles_n) * BN;
-
-    const int64_t KB = K / 2;  // bytes per row
-    const int steps = (int)((K + kBK - 1) / kBK);
-
-    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
-    v4i ra[A_CHUNKS], rb[B_CHUNKS];
-    auto gload = [&](int s) {
-        const int64_t kb0 = (int64_t)s * kBKB;
-#pragma unroll
-        for (int i = 0; i < A_CHUNKS; ++i) {
-            const int c = tid + 256 * i;
-            const int r = c / (kBKB / 16), col = (c % (kBKB / 16)) * 16;
-            ra[i] = bload16(ar, chunk_off(m0 + r, M, kb0 + col, KB));
-        }
-#pragma unroll
-        for (int i = 0; i < B_CHUNKS; ++i) {
-            const int c = tid + 256 * i;
-            const int r = c / (kBKB / 16), col = (c % (kBKB / 16)) * 16;
-            rb[i] = bload16(br, chunk_off(n0 + r, N, kb0 + col, KB));
-        }
-    };
-    auto sstore = [&]() {
-#pragma unroll
-        for (int i = 0; i < A_CHUNKS; ++i) {
-            const int c = tid + 256 * i;
-            const int r = c / (kBKB / 16), col = (c % (kBKB / 16)) * 16;
-            *reinterpret_cast<v4i *>(As + r * kLdsRow + col) = ra[i];
-        }
-#pragma unroll
-        for (int i = 0; i < B_CHUNKS; ++i) {
-            const int c = tid + 256 * i;
-            const int r = c / (kBKB / 16), col = (c % (kBKB / 16)) * 16;
-            *reinterpret_cast<v4i *>(Bs + r * kLdsRow + col) = rb[i];
-        }
-    };
-
-    v4i acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = (v4i){0, 0, 0, 0};
-
-    const int frow = lane & 15;
-    const int fk = (lane >> 4) * 8;  // byte offset of this lane's 16 codes
-
-    gload(0);
-    for (int s = 0; s < steps; ++s) {
-        __syncthreads();  // previous step's LDS reads are done
-        sstore();
-        __syncthreads();
-        if (s + 1 < steps) gload(s + 1);
-        uint2 wa[2][FM], wb[2][FN];
-        auto fetch = [&](int kk, int slot) {
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-                wa[slot][i] = *reinterpret_cast<const uint2 *>(
-                    As + (wm * WM + i * 16 + frow) * kLdsRow + kk * 32 + fk);
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-                wb[slot][j] = *reinterpret_cast<const uint2 *>(
-                    Bs + (wn * WN + j * 16 + frow) * kLdsRow + kk * 32 + fk);
-        };
-        fetch(0, 0);
-#pragma unroll
-        for (int kk = 0; kk < kBKB / 32; ++kk) {
-            if (kk + 1 < kBKB / 32) fetch(kk + 1, (kk + 1) & 1);
-            v4i fa[FM], fb[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) fa[i] = unpack8a<UA>(wa[kk & 1][i].x, wa[kk & 1][i].y);
-#pragma unroll
-            for (int j = 0; j < FN; ++j) fb[j] = unpack8(wb[kk & 1][j].x, wb[kk & 1][j].y);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(fa[i], fb[j], acc[i][j]);
-        }
-    }
-
-    store_block<FM, FN>(e, M, N, m0 + wm * WM, n0 + wn * WN, acc, lane);
-}
-
-// ---------------------------------------------------------------------------
 // Large-M kernel: 256 x 128 block per workgroup, split into two kinds of
 // waves.  Producer waves (NPROD) only move data: K advances KBB bytes
 // (2 KBB codes) per step through an NSTG-stage LDS ring filled by buffer ->
@@ -628,6 +511,151 @@ __global__ __launch_bounds__(512, 1) void gemm_sq_kernel(const uint8_t *__restri
         big_compute<FM, FN, KBB, kSqBM, UA>(smem + (s % NSTG) * kStage, wm, wn, lane, acc);
     }
     store_block32<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Ring kernel for mid-size M: BM x BN tile per workgroup, 4 compute waves
+// (2 x 2) of 16x16x64 int8 MFMA blocks and 2 producer waves moving the
+// tile's rows through an NSTG-stage LDS ring (buffer -> LDS DMA, 128 bytes =
+// 256 codes per row per step, 8 rows per 1 KiB DMA block).  A small tile
+// does little MFMA work per loaded byte, so the kernel is bound by data
+// movement; the deep ring keeps NSTG - 1 steps in flight to cover the
+// HBM latency of the weight stream.  Stage layout and swizzle are the
+// large-M kernel's (16-byte chunk j of row r at j ^ swz(r)); out-of-range
+// rows and the K tail read as zeros.
+
+constexpr int kRingKBB = 128;
+
+// this wave's DMA of step s is done while `later` more of its steps (PER
+// DMA instructions each) may stay in flight; vmcnt takes an immediate
+template <int PER, int MAXL>
+SRQ_DEV void ring_wait(int later) {
+    if constexpr (MAXL > 0) {
+        if (later >= MAXL) {
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(MAXL * PER) : "memory");
+            return;
+        }
+        ring_wait<PER, MAXL - 1>(later);
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+}
+
+template <int BM, int BN, int NSTG, int NPROD, bool UA>
+__global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_ring_kernel(const uint8_t *__restrict__ A,
+                                                           const uint8_t *__restrict__ B,
+                                                           int64_t M, int64_t N, int64_t K,
+                                                           Epi e) {
+    constexpr int KBB = kRingKBB;
+    constexpr int kRows = BM + BN;
+    constexpr int kStage = kRows * KBB;
+    constexpr int kDma = kRows / 8;  // 1 KiB DMA blocks per stage
+    constexpr int kPer = kDma / NPROD;
+    static_assert(kPer * NPROD == kDma && kRows % 8 == 0, "DMA split");
+    static_assert((NSTG - 2) * kPer <= 63, "vmcnt range");
+    static_assert(NSTG * kStage <= 160 * 1024, "LDS ring");
+    constexpr int WM = BM / 2, WN = BN / 2, FM = WM / 16, FN = WN / 16;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTG * kStage];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // XCD-aware tile order: consecutive workgroups land on different XCDs
+    // (round-robin dispatch), so give each XCD a contiguous range of tiles
+    const int64_t tiles_n = (N + BN - 1) / BN;
+    const int64_t tiles = ((M + BM - 1) / BM) * tiles_n;
+    int64_t t = blockIdx.x;
+    if (tiles % 8 == 0) t = (t % 8) * (tiles / 8) + t / 8;
+    const int64_t m0 = (t / tiles_n) * BM, n0 = (t % tiles_n) * BN;
+    const int64_t KB = K / 2;
+    const int steps = (int)((KB + KBB - 1) / KBB);
+
+    if (wave >= 4) {
+        // ---- producer pw: DMA blocks i = kPer pw + q, stage rows 8 i .. 8 i
+        // + 7; lane l fetches chunk (l % 8) ^ swz(r) of row r = 8 i + l / 8
+        const int pw = wave - 4;
+        const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
+        const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)smem;
+        uint32_t roff[kPer];
+        int jc[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = pw * kPer + q;
+            const int r = 8 * i + lane / 8;
+            jc[q] = ((lane % 8) ^ swz<KBB>(r)) * 16;
+            const bool isa = 8 * i < BM;
+            const int64_t row = isa ? m0 + r : n0 + r - BM;
+            roff[q] = row < (isa ? M : N) ? (uint32_t)(row * KB) : kOob;
+        }
+        auto issue = [&](int st) __attribute__((always_inline)) {
+            const int64_t kb0 = (int64_t)st * KBB;
+            const bool tail = kb0 + KBB > KB;
+            const uint32_t dst0 = lds0 + (st % NSTG) * kStage;
+#pragma unroll
+            for (int q = 0; q < kPer; ++q) {
+                const int i = pw * kPer + q;
+                uint32_t off = roff[q] == kOob ? kOob : roff[q] + (uint32_t)kb0 + jc[q];
+                if (tail && kb0 + jc[q] >= KB) off = kOob;
+                dma16(8 * i < BM ? ar : br, off, dst0 + i * 1024);
+            }
+        };
+#pragma unroll
+        for (int s = 0; s < NSTG - 1; ++s)
+            if (s < steps) issue(s);
+        for (int s = 0; s < steps; ++s) {
+            // this wave's DMA of step s is done; every producer's after the
+            // barrier, and every compute wave is done with step s - 1's stage
+            const int later = steps - 1 - s < NSTG - 2 ? steps - 1 - s : NSTG - 2;
+            ring_wait<kPer, NSTG - 2>(later);
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (s + NSTG - 1 < steps) issue(s + NSTG - 1);
+        }
+        return;  // the compute waves meet no barrier after their K loop
+    }
+
+    // ---- compute wave (wm, wn): FM x FN blocks of 16 x 16; lane reads 8
+    // bytes (16 codes) of row (lane & 15) at byte 32 kk + 8 (lane >> 4)
+    const int wm = wave >> 1, wn = wave & 1;
+    v4i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = (v4i){0, 0, 0, 0};
+    const int frow = lane & 15;
+    const int fsub = ((lane >> 4) & 1) * 8;  // byte inside the 16-byte chunk
+    const int fch = lane >> 5;                // chunk 2 kk + fch
+    auto rd = [&](const uint8_t *stage, int r, int kk) __attribute__((always_inline)) {
+        return *reinterpret_cast<const uint2 *>(
+            stage + r * KBB + (((2 * kk + fch) ^ swz<KBB>(r)) << 4) + fsub);
+    };
+    for (int s = 0; s < steps; ++s) {
+        // step s has landed; every wave is done with step s - 1
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        const uint8_t *stage = smem + (s % NSTG) * kStage;
+        uint2 wa[2][FM], wb[2][FN];
+        auto fetch = [&](int kk, int slot) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) wa[slot][i] = rd(stage, wm * WM + i * 16 + frow, kk);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) wb[slot][j] = rd(stage, BM + wn * WN + j * 16 + frow, kk);
+        };
+        fetch(0, 0);
+#pragma unroll
+        for (int kk = 0; kk < KBB / 32; ++kk) {
+            if (kk + 1 < KBB / 32) fetch(kk + 1, (kk + 1) & 1);
+            v4i fa[FM], fb[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) fa[i] = unpack8a<UA>(wa[kk & 1][i].x, wa[kk & 1][i].y);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) fb[j] = unpack8(wb[kk & 1][j].x, wb[kk & 1][j].y);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(fa[i], fb[j], acc[i][j]);
+        }
+    }
+    store_block<FM, FN>(e, M, N, m0 + wm * WM, n0 + wn * WN, acc, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -1211,23 +1239,28 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         // enough 256 x 256 tiles to cover the 256 CUs
         const int64_t tiles = srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN);
         gemm_sq_kernel<128, 2, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(a, b, M, N, K, e);
-    } else if (M >= 1024) {
+    } else if (M >= 1024 || srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) >= 512) {
         const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
         // 4 compute waves (128 x 64 each) + 4 producer waves
         gemm_big_kernel<4, 2, 2, 4, 2, 128, 3, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
     } else {
         // mid-size M: the tile shrinks with M so the grid still covers the
-        // 256 CUs (at N = 4096: 256 workgroups for M = 128, 256, 512)
-        auto tile = [&](auto bm, auto bn) {
+        // 256 CUs (at N = 4096: 256 workgroups for M = 128, 256, 512); the
+        // smaller the tile, the deeper the DMA ring
+        auto ring = [&](auto bm, auto bn, auto nstg) {
             constexpr int BM = decltype(bm)::value, BN = decltype(bn)::value;
+            constexpr int NP = 4;  // 4 producers: measured 28.5 vs 31.8 us for 2 at M = 128
             const int64_t tiles = srq_cdiv(M, BM) * srq_cdiv(N, BN);
-            gemm_tile_kernel<BM, BN, UA><<<dim3((unsigned)tiles), dim3(256), 0, st>>>(a, b, M, N, K, e);
+            gemm_ring_kernel<BM, BN, decltype(nstg)::value, NP, UA>
+                <<<dim3((unsigned)tiles), dim3(64 * (4 + NP)), 0, st>>>(a, b, M, N, K, e);
         };
-        if (M <= 128) tile(std::integral_constant<int, 64>{}, std::integral_constant<int, 32>{});
-        else if (M <= 256) tile(std::integral_constant<int, 64>{}, std::integral_constant<int, 64>{});
-        else if (M <= 512) tile(std::integral_constant<int, 128>{}, std::integral_constant<int, 64>{});
-        else tile(std::integral_constant<int, 128>{}, std::integral_constant<int, 128>{});
+        using I32 = std::integral_constant<int, 32>;
+        using I64 = std::integral_constant<int, 64>;
+        using I128 = std::integral_constant<int, 128>;
+        if (M <= 128) ring(I64{}, I32{}, std::integral_constant<int, 12>{});
+        else if (M <= 256) ring(I64{}, I64{}, std::integral_constant<int, 9>{});
+        else ring(I128{}, I64{}, std::integral_constant<int, 6>{});
     }
 }
 
