@@ -220,6 +220,100 @@ SRQ_DEV void store_block32(const Epi &e, int64_t M, int64_t N, int64_t mb, int64
         }
 }
 
+// fp16 epilogue through LDS: the wave's (32 FM) x (32 FN) block is
+// dequantized (and bias added) into its private LDS area `tile` (row stride
+// 32 FN halves), then stored row-wise, each lane 16 bytes (8 outputs), with
+// the residual read the same way.  The MFMA layout stores would write 2
+// bytes per lane; this cuts the store instructions 8-fold (the epilogue of
+// the M = 2048 GEMM took 20 of its 108 us).  Same arithmetic as store_one.
+template <int FM, int FN, bool CHECK>
+SRQ_DEV void store_block32_lds_impl(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t nb,
+                                    const v16i (&acc)[FM][FN], int lane, f16 *tile) {
+    constexpr int W = 32 * FN;
+    float sbv[FN], bv[FN];
+    int64_t gnv[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        gnv[j] = nb + j * 32 + (lane & 31);
+        const bool on = !CHECK || gnv[j] < N;
+        sbv[j] = on ? (float)e.sb[gnv[j]] : 0.f;
+        bv[j] = on && e.bias ? (float)e.bias[gnv[j]] : 0.f;
+    }
+    // the row scales first, all loads in flight together
+    float sav[FM][16];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t gm = mb + i * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+            sav[i][v] = !CHECK || gm < M ? (float)e.sa[gm] : 0.f;
+        }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int lr = i * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+            const int64_t gm = mb + lr;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                int val = acc[i][j][v] >> (e.ua ? 4 : 8);
+                if (e.zr) {  // (uniform) asymmetric activations
+                    const bool on = !CHECK || (gm < M && gnv[j] < N);
+                    val = on ? epi_val(e, acc[i][j][v], gm, gnv[j]) : 0;
+                }
+                f16 o = f16_rn((float)val * sav[i][v] * sbv[j]);
+                if (e.bias) o = f16_rn((float)o + bv[j]);
+                tile[lr * W + j * 32 + (lane & 31)] = o;
+            }
+        }
+    constexpr int LPR = W / 8;     // lanes per row (16 bytes each)
+    constexpr int RPI = 64 / LPR;  // rows per store instruction
+    const int c8 = (lane % LPR) * 8;
+    const int64_t gn0 = nb + c8;
+    const bool vec = N % 8 == 0 && ((uintptr_t)e.out % 16 == 0) &&
+                     (!e.res || (uintptr_t)e.res % 16 == 0);
+#pragma unroll
+    for (int r0 = 0; r0 < 32 * FM; r0 += RPI) {
+        const int lr = r0 + lane / LPR;
+        const int64_t gm = mb + lr;
+        if (CHECK && gm >= M) continue;
+        v8h o = *reinterpret_cast<const v8h *>(tile + lr * W + c8);
+        if (vec && (!CHECK || gn0 + 8 <= N)) {
+            if (e.res) {
+                const v8h rv = *reinterpret_cast<const v8h *>(e.res + gm * N + gn0);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) o[k] = f16_rn((float)o[k] + (float)rv[k]);
+            }
+            *reinterpret_cast<v8h *>(e.out + gm * N + gn0) = o;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (gn0 + k >= N) break;
+                f16 ok = o[k];
+                if (e.res) ok = f16_rn((float)ok + (float)e.res[gm * N + gn0 + k]);
+                e.out[gm * N + gn0 + k] = ok;
+            }
+        }
+    }
+}
+
+// fp16 epilogue through LDS: the wave's (32 FM) x (32 FN) block is
+// dequantized (and bias added) into its private LDS area `tile` (row stride
+// 32 FN halves), then stored row-wise, each lane 16 bytes (8 outputs), with
+// the residual read the same way.  The MFMA layout stores would write 2
+// bytes per lane, 8 times the store instructions.  Blocks wholly inside the
+// matrix take a branch-free path (per-element bounds checks made the
+// unrolled epilogue hundreds of divergent branches: 20 of the M = 2048
+// GEMM's 108 us).  Same arithmetic as store_one.
+template <int FM, int FN>
+SRQ_DEV void store_block32_lds(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t nb,
+                               const v16i (&acc)[FM][FN], int lane, f16 *tile) {
+    if (mb + 32 * FM <= M && nb + 32 * FN <= N)
+        store_block32_lds_impl<FM, FN, false>(e, M, N, mb, nb, acc, lane, tile);
+    else
+        store_block32_lds_impl<FM, FN, true>(e, M, N, mb, nb, acc, lane, tile);
+}
+
 // One K step of a compute wave: the stage holds BM A rows then the B rows.
 template <int FM, int FN, int KBB, int BM = kBigBM, bool UA = false>
 SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {
@@ -397,7 +491,20 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
         sl = sl == 2 ? 0 : sl + 1;
     }
 
-    store_block32<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane);
+    if (e.C) {
+        store_block32<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane);
+    } else {
+        // every wave has passed the last step's barrier, so only the stage
+        // of step steps - 1 can still be read: the other two hold the
+        // waves' output tiles (32 FM x 32 FN halves each)
+        constexpr int kTile = 32 * FM * 32 * FN * 2;
+        static_assert(kCompute * kTile <= 2 * kStage, "epilogue tiles");
+        uint8_t *fr0 = smem + (steps % 3) * kStage, *fr1 = smem + ((steps + 1) % 3) * kStage;
+        const int per0 = kStage / kTile;
+        uint8_t *t = wave < per0 ? fr0 + wave * kTile : fr1 + (wave - per0) * kTile;
+        store_block32_lds<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane,
+                                  reinterpret_cast<f16 *>(t));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1241,7 +1348,8 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         gemm_sq_kernel<128, 2, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(a, b, M, N, K, e);
     } else if (M >= 1024 || srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) >= 512) {
         const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
-        // 4 compute waves (128 x 64 each) + 4 producer waves
+        // 4 compute waves (128 x 64 each) + 4 producer waves (8 compute
+        // waves of 64 x 64, two per SIMD, measured no faster)
         gemm_big_kernel<4, 2, 2, 4, 2, 128, 3, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
     } else {
