@@ -226,33 +226,41 @@ SRQ_DEV void store_block32(const Epi &e, int64_t M, int64_t N, int64_t mb, int64
 // the residual read the same way.  The MFMA layout stores would write 2
 // bytes per lane; this cuts the store instructions 8-fold (the epilogue of
 // the M = 2048 GEMM took 20 of its 108 us).  Same arithmetic as store_one.
-template <int FM, int FN, bool CHECK>
-SRQ_DEV void store_block32_lds_impl(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t nb,
-                                    const v16i (&acc)[FM][FN], int lane, f16 *tile) {
-    constexpr int W = 32 * FN;
+// Row of accumulator element v of a BS x BS MFMA block held by `lane`
+// (column lane % BS): 32x32 -> 8 (v / 4) + 4 (lane / 32) + v % 4,
+// 16x16 -> 4 (lane / 16) + v.
+template <int BS>
+SRQ_DEV int frag_row(int v, int lane) {
+    if constexpr (BS == 32) return 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+    else return 4 * (lane >> 4) + v;
+}
+
+template <int BS, int FM, int FN, bool CHECK, typename AccT>
+SRQ_DEV void store_block_lds_impl(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t nb,
+                                  const AccT (&acc)[FM][FN], int lane, f16 *tile) {
+    constexpr int NV = BS * BS / 64;  // accumulator elements per lane per block
+    constexpr int W = BS * FN;        // tile row stride (halves)
     float sbv[FN], bv[FN];
     int64_t gnv[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-        gnv[j] = nb + j * 32 + (lane & 31);
+        gnv[j] = nb + j * BS + (lane & (BS - 1));
         const bool on = !CHECK || gnv[j] < N;
         sbv[j] = on ? (float)e.sb[gnv[j]] : 0.f;
         bv[j] = on && e.bias ? (float)e.bias[gnv[j]] : 0.f;
     }
-    // the row scales first, all loads in flight together
-    float sav[FM][16];
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i) {
+        // the block's row scales first, all loads in flight together
+        float sav[NV];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t gm = mb + i * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-            sav[i][v] = !CHECK || gm < M ? (float)e.sa[gm] : 0.f;
+        for (int v = 0; v < NV; ++v) {
+            const int64_t gm = mb + i * BS + frag_row<BS>(v, lane);
+            sav[v] = !CHECK || gm < M ? (float)e.sa[gm] : 0.f;
         }
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int lr = i * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+        for (int v = 0; v < NV; ++v) {
+            const int lr = i * BS + frag_row<BS>(v, lane);
             const int64_t gm = mb + lr;
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
@@ -261,19 +269,21 @@ SRQ_DEV void store_block32_lds_impl(const Epi &e, int64_t M, int64_t N, int64_t 
                     const bool on = !CHECK || (gm < M && gnv[j] < N);
                     val = on ? epi_val(e, acc[i][j][v], gm, gnv[j]) : 0;
                 }
-                f16 o = f16_rn((float)val * sav[i][v] * sbv[j]);
+                f16 o = f16_rn((float)val * sav[v] * sbv[j]);
                 if (e.bias) o = f16_rn((float)o + bv[j]);
-                tile[lr * W + j * 32 + (lane & 31)] = o;
+                tile[lr * W + j * BS + (lane & (BS - 1))] = o;
             }
         }
+    }
     constexpr int LPR = W / 8;     // lanes per row (16 bytes each)
     constexpr int RPI = 64 / LPR;  // rows per store instruction
+    static_assert(LPR >= 1 && 64 % LPR == 0 && (BS * FM) % RPI == 0, "row store shape");
     const int c8 = (lane % LPR) * 8;
     const int64_t gn0 = nb + c8;
     const bool vec = N % 8 == 0 && ((uintptr_t)e.out % 16 == 0) &&
                      (!e.res || (uintptr_t)e.res % 16 == 0);
 #pragma unroll
-    for (int r0 = 0; r0 < 32 * FM; r0 += RPI) {
+    for (int r0 = 0; r0 < BS * FM; r0 += RPI) {
         const int lr = r0 + lane / LPR;
         const int64_t gm = mb + lr;
         if (CHECK && gm >= M) continue;
@@ -297,21 +307,23 @@ SRQ_DEV void store_block32_lds_impl(const Epi &e, int64_t M, int64_t N, int64_t 
     }
 }
 
-// fp16 epilogue through LDS: the wave's (32 FM) x (32 FN) block is
-// dequantized (and bias added) into its private LDS area `tile` (row stride
-// 32 FN halves), then stored row-wise, each lane 16 bytes (8 outputs), with
-// the residual read the same way.  The MFMA layout stores would write 2
-// bytes per lane, 8 times the store instructions.  Blocks wholly inside the
-// matrix take a branch-free path (per-element bounds checks made the
-// unrolled epilogue hundreds of divergent branches: 20 of the M = 2048
-// GEMM's 108 us).  Same arithmetic as store_one.
-template <int FM, int FN>
-SRQ_DEV void store_block32_lds(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t nb,
-                               const v16i (&acc)[FM][FN], int lane, f16 *tile) {
-    if (mb + 32 * FM <= M && nb + 32 * FN <= N)
-        store_block32_lds_impl<FM, FN, false>(e, M, N, mb, nb, acc, lane, tile);
+// fp16 epilogue through LDS: the wave's (BS FM) x (BS FN) block of BS x BS
+// MFMA accumulators is dequantized (and bias added) into its private LDS
+// area `tile` (row stride BS FN halves, BS FM rows), then stored row-wise,
+// each lane 16 bytes (8 outputs), with the residual read the same way.  The
+// MFMA layout stores would write 2 bytes per lane, 8 times the store
+// instructions.  Blocks wholly inside the matrix take a branch-free path
+// (per-element bounds checks made the unrolled epilogue hundreds of
+// divergent branches: 20 of the M = 2048 GEMM's 108 us).  Same arithmetic
+// as store_one.  The caller's LDS `tile` must be free of other readers and
+// of in-flight DMA.
+template <int BS, int FM, int FN, typename AccT>
+SRQ_DEV void store_block_lds(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t nb,
+                             const AccT (&acc)[FM][FN], int lane, f16 *tile) {
+    if (mb + BS * FM <= M && nb + BS * FN <= N)
+        store_block_lds_impl<BS, FM, FN, false>(e, M, N, mb, nb, acc, lane, tile);
     else
-        store_block32_lds_impl<FM, FN, true>(e, M, N, mb, nb, acc, lane, tile);
+        store_block_lds_impl<BS, FM, FN, true>(e, M, N, mb, nb, acc, lane, tile);
 }
 
 // One K step of a compute wave: the stage holds BM A rows then the B rows.
@@ -502,7 +514,7 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
         uint8_t *fr0 = smem + (steps % 3) * kStage, *fr1 = smem + ((steps + 1) % 3) * kStage;
         const int per0 = kStage / kTile;
         uint8_t *t = wave < per0 ? fr0 + wave * kTile : fr1 + (wave - per0) * kTile;
-        store_block32_lds<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane,
+        store_block_lds<32, FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane,
                                   reinterpret_cast<f16 *>(t));
     }
 }
@@ -617,7 +629,19 @@ __global__ __launch_bounds__(512, 1) void gemm_sq_kernel(const uint8_t *__restri
         if (s + NSTG - 1 < steps) issue(s + NSTG - 1);
         big_compute<FM, FN, KBB, kSqBM, UA>(smem + (s % NSTG) * kStage, wm, wn, lane, acc);
     }
-    store_block32<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane);
+    if (e.C) {
+        store_block32<FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane);
+    } else {
+        // every wave is past its last step and no DMA is in flight (the
+        // last step waited for vmcnt 0): the whole ring is free for the
+        // waves' epilogue tiles
+        constexpr int kTile = 32 * FM * 32 * FN * 2;
+        static_assert(kWaves * kTile <= NSTG * kStage, "epilogue tiles");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        store_block_lds<32, FM, FN>(e, M, N, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane,
+                                    reinterpret_cast<f16 *>(smem + wave * kTile));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -762,7 +786,18 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_ring_kernel(const ui
                 for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(fa[i], fb[j], acc[i][j]);
         }
     }
-    store_block<FM, FN>(e, M, N, m0 + wm * WM, n0 + wn * WN, acc, lane);
+    if (e.C) {
+        store_block<FM, FN>(e, M, N, m0 + wm * WM, n0 + wn * WN, acc, lane);
+    } else {
+        // after the barrier of the last step no DMA is in flight and the
+        // waves read only that step's stage, (steps - 1) % NSTG; the next
+        // one holds the compute waves' epilogue tiles
+        constexpr int kTile = WM * WN * 2;
+        static_assert(NSTG >= 2 && 4 * kTile <= kStage, "epilogue tiles");
+        uint8_t *fr = smem + (steps % NSTG) * kStage;
+        store_block_lds<16, FM, FN>(e, M, N, m0 + wm * WM, n0 + wn * WN, acc, lane,
+                                    reinterpret_cast<f16 *>(fr + wave * kTile));
+    }
 }
 
 // ---------------------------------------------------------------------------
