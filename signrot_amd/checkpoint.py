@@ -151,3 +151,31 @@ def load_decode_layer(layer, ckpt, prefix):
         if prefix + mlp + "down_proj.had_adj_sign" in ckpt.keys():
             layer.down_sign.copy_(t(mlp + "down_proj.had_adj_sign").to(torch.int8))
     return layer
+
+
+def decode_layer_tensors(layer, prefix):
+    """The inverse of load_decode_layer: a W4A4LlamaDecodeLayer's packed
+    codes and scales under the reference's checkpoint keys
+    (realquant_utils.py:85-142 writes `<prefix>self_attn.q_proj.weight` u8
+    [out, in/2] and `quantizer.<prefix>self_attn.q_proj.scale` fp16
+    [out, 1] per linear, plus `<prefix>mlp.down_proj.had_adj_sign`): the
+    fused q/k/v and gate/up buffers are split back into their projections.
+    Tensors are copied to the CPU."""
+    hd = layer.head_dim
+    nq, nkv = layer.n_heads * hd, layer.n_kv * hd
+    att, mlp = prefix + "self_attn.", prefix + "mlp."
+    parts = {
+        att + "q_proj": (layer.w_qkv[:nq], layer.s_qkv[:nq]),
+        att + "k_proj": (layer.w_qkv[nq:nq + nkv], layer.s_qkv[nq:nq + nkv]),
+        att + "v_proj": (layer.w_qkv[nq + nkv:], layer.s_qkv[nq + nkv:]),
+        att + "o_proj": (layer.w_o, layer.s_o),
+        mlp + "gate_proj": (layer.w_gu[:layer.ffn], layer.s_gu[:layer.ffn]),
+        mlp + "up_proj": (layer.w_gu[layer.ffn:], layer.s_gu[layer.ffn:]),
+        mlp + "down_proj": (layer.w_down, layer.s_down),
+    }
+    out = {}
+    for key, (w, s) in parts.items():
+        out[key + ".weight"] = w.detach().cpu().contiguous()
+        out[f"quantizer.{key}.scale"] = s.detach().cpu().reshape(-1, 1).contiguous()
+    out[mlp + "down_proj.had_adj_sign"] = layer.down_sign.detach().cpu().contiguous()
+    return out

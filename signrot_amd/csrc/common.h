@@ -283,17 +283,22 @@ SRQ_DEV void kv_row_params(float vmax, float vmin, f16 &scale, f16 &zero) {
 // Rotary embedding of one rotate_half pair (x0 at i, x1 at i + D/2) with
 // per-op fp16 rounding, as the three-op torch expression
 // x * cos + rotate_half(x) * sin evaluates it in fp16 (fused.cu:316-362).
-// Products of two fp16 values are exact in fp32, so each rounds once.
-SRQ_DEV f16 rope_lo(float x0, float x1, float c, float s) {
-    const f16 a = (f16)(x0 * c);
-    const f16 b = (f16)(-x1 * s);
-    return (f16)((float)a + (float)b);
+// Written in fp16 arithmetic: a correctly rounded fp16 product or sum equals
+// the fp32 one rounded to fp16 (products of two fp16 values are exact in
+// fp32; fp32 has the 2p + 2 bits that make the double rounding of a sum
+// innocuous), and it keeps the sign of zero.  The fp32 form let the
+// compiler round x1 * s through fma(x1, s, +0), which turns a -0 product
+// into +0 and gave rope_lo -0 where the reference gives +0.
+SRQ_DEV f16 rope_lo(f16 x0, f16 x1, f16 c, f16 s) {
+    const f16 a = x0 * c;
+    const f16 b = (-x1) * s;
+    return a + b;
 }
 
-SRQ_DEV f16 rope_hi(float x0, float x1, float c, float s) {
-    const f16 a = (f16)(x1 * c);
-    const f16 b = (f16)(x0 * s);
-    return (f16)((float)a + (float)b);
+SRQ_DEV f16 rope_hi(f16 x0, f16 x1, f16 c, f16 s) {
+    const f16 a = x1 * c;
+    const f16 b = x0 * s;
+    return a + b;
 }
 
 // ----------------------------------------------- packed-fp16 int4 quantizer

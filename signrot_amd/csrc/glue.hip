@@ -119,9 +119,9 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(f16 *__restrict__ q, f16 *
         const int64_t ct = cos_batch == 1 ? tok % seq_len : tok;
         const f16 *c = cs + ct * (2 * half);
         const f16 *s = sn + ct * (2 * half);
-        const float x0 = (float)base[i], x1 = (float)base[i + half];
-        base[i] = rope_lo(x0, x1, (float)c[i], (float)s[i]);
-        base[i + half] = rope_hi(x0, x1, (float)c[i + half], (float)s[i + half]);
+        const f16 x0 = base[i], x1 = base[i + half];
+        base[i] = rope_lo(x0, x1, c[i], s[i]);
+        base[i + half] = rope_hi(x0, x1, c[i + half], s[i + half]);
     }
 }
 

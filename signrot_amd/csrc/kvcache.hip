@@ -151,8 +151,9 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvArgs a, Paged p) {
         for (int e = 0; e < 8; ++e) {
             const float o = xor_lane(v[e], 8);
             const int i = 8 * l + e;
-            const float c = (float)a.cs[ct * D + i], sn = (float)a.sn[ct * D + i];
-            y[e] = (float)(l < 8 ? rope_lo(v[e], o, c, sn) : rope_hi(o, v[e], c, sn));
+            const f16 c = a.cs[ct * D + i], sn = a.sn[ct * D + i];
+            const f16 xe = (f16)v[e], xo = (f16)o;  // exact: both came from fp16
+            y[e] = (float)(l < 8 ? rope_lo(xe, xo, c, sn) : rope_hi(xo, xe, c, sn));
         }
         if (kind != 2) {
 #pragma unroll

@@ -87,18 +87,21 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         return _CUDA.w4a4_linear(q.view(-1, q.shape[-1]), s.view(-1), getattr(self, f"w_{name}"),
                                  getattr(self, f"s_{name}"))
 
-    def forward(self, hidden_states, cache, cos, sin, trace=None, fused=True):
+    def forward(self, hidden_states, cache, cos, sin, trace=None, fused=True,
+                attention_mask=None):
         """hidden_states fp16 [B, 1, hidden]; cos/sin fp16 [1 or B, 1, head_dim]
         for the new position; returns fp16 [B, 1, hidden].  The cache must
         already hold this layer's context (its first update was a prefill).
-        With a dict `trace`, the intermediates are stored in it (checkers) and
-        the op-by-op path runs; otherwise (fused=True) the fused kernels run,
-        with bit-identical results."""
+        attention_mask: after a left-padded prefill, HF's mask extended by a
+        1 per decoded token ([B, prompt + steps]; it gives each request's
+        length), else None.  With a dict `trace`, the intermediates are
+        stored in it (checkers) and the op-by-op path runs; otherwise
+        (fused=True) the fused kernels run, with bit-identical results."""
         if fused and trace is None:
-            return self._forward_fused(hidden_states, cache, cos, sin)
-        return self._forward_ops(hidden_states, cache, cos, sin, trace)
+            return self._forward_fused(hidden_states, cache, cos, sin, attention_mask)
+        return self._forward_ops(hidden_states, cache, cos, sin, trace, attention_mask)
 
-    def _forward_fused(self, hidden_states, cache, cos, sin):
+    def _forward_fused(self, hidden_states, cache, cos, sin, attention_mask=None):
         """The decode step in 11 launches: rmsnorm_quant -> q/k/v GEMM ->
         qkv_rope_had_append (RoPE, K/q Hadamard, KV quantize + append) ->
         batch_decode_i4 (+ split-KV merge) -> head_had_quant (head-axis
@@ -109,7 +112,8 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         n1, n2 = self.input_layernorm, self.post_attention_layernorm
         q1, s1 = _CUDA.rmsnorm_quant(x2, n1.eps, n1.mean_dim)
         qkv = _CUDA.w4a4_linear(q1, s1.view(-1), self.w_qkv, self.s_qkv)
-        q_rot = cache.update_qkv_fused(qkv, cos, sin, self.layer_idx, self.n_heads)
+        q_rot = cache.update_qkv_fused(qkv, cos, sin, self.layer_idx, self.n_heads,
+                                       attention_mask)
         attn = cache.decode_rotated(q_rot, self.layer_idx)     # [B, Hq, D]
         qa, sa = _CUDA.head_had_quant(attn, _inv_sqrt_f32(self.n_heads))
         x2 = _CUDA.w4a4_linear_residual(qa, sa.view(-1), self.w_o, self.s_o, x2)
@@ -124,15 +128,12 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         out = _CUDA.w4a4_linear_residual(qd, sd.view(-1), self.w_down, self.s_down, x2, out=x2)
         return out.view(B, 1, self.hidden)
 
-    def _forward_ops(self, hidden_states, cache, cos, sin, trace=None):
+    def _forward_ops(self, hidden_states, cache, cos, sin, trace=None, attention_mask=None):
         """Op-by-op decode step (the reference's sequence of ops)."""
         B = hidden_states.shape[0]
         D, Hq, Hk = self.head_dim, self.n_heads, self.n_kv
         x2 = hidden_states.view(B, self.hidden)
-
-        def keep(name, t):
-            if trace is not None:
-                trace[name] = t.clone()
+        keep = self._keeper(trace)
 
         # ---- attention
         h = self.input_layernorm(x2)
@@ -145,19 +146,70 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         kernel.rope_qk(q, k, cos, sin)
         keep("q_rope", q)
         keep("k_rope", k)
-        attend = cache.update(k, v, self.layer_idx, {"attention_mask": None})
+        attend = cache.update(k, v, self.layer_idx, {"attention_mask": attention_mask})
         attn = attend(q)                                      # [B, 1, Hq, D]
         keep("attn", attn)
-        # head-axis Hadamard of o_proj (modeling_llama.py:94, 117)
-        attn = attn.transpose(-1, -2).contiguous()            # [B, 1, D, Hq]
+        x2 = self._attn_out(attn, x2, keep)
+        return self._mlp(x2, keep).view(B, 1, self.hidden)
+
+    def prefill(self, hidden_states, cache, cos, sin, attention_mask=None, trace=None):
+        """The layer's first update: T tokens per request
+        (modeling_llama.py:26-100 with the cache's first update,
+        kv_cache.py:295-395).  hidden_states fp16 [B, T, hidden]; cos/sin
+        fp16 [1 or B, T, head_dim] (left-padded rows take the positions of
+        their real tokens, as HF's position_ids do); attention_mask int
+        [B, T] (1 = token, 0 = left padding) or None.  K/V are quantized into
+        the cache (only the mask's 1-positions), the attention runs causal
+        over the fp16 q/k/v (the flash-attn 2 call it replaces), then o_proj
+        and the MLP as in decode.  Returns fp16 [B, T, hidden]; rows at
+        padding positions are computed but carry no meaning."""
+        B, T, _ = hidden_states.shape
+        D, Hq, Hk = self.head_dim, self.n_heads, self.n_kv
+        x2 = hidden_states.reshape(B * T, self.hidden)
+        keep = self._keeper(trace)
+        h = self.input_layernorm(x2)
+        qkv = self._linear(kernel.PackedQuantizedTensor(*kernel.sym_quant_dynamic(h)), "qkv")
+        keep("norm1", h)
+        keep("qkv", qkv)
+        q = qkv[:, : Hq * D].reshape(B, T, Hq, D).contiguous()
+        k = qkv[:, Hq * D: (Hq + Hk) * D].reshape(B, T, Hk, D).contiguous()
+        v = qkv[:, (Hq + Hk) * D:].reshape(B, T, Hk, D).contiguous()
+        kernel.rope_qk(q, k, cos, sin)
+        keep("q_rope", q)
+        keep("k_rope", k)
+        out = cache.update(k, v, self.layer_idx, {"attention_mask": attention_mask})
+        if not isinstance(out, tuple):
+            raise RuntimeError("prefill: the cache already holds this layer's context")
+        k_f, v_f = out
+        attn = _CUDA.prefill_attention(q, k_f, v_f, attention_mask, causal=True)
+        keep("attn", attn)
+        x2 = self._attn_out(attn.reshape(B * T, Hq, D), x2, keep)
+        return self._mlp(x2, keep).view(B, T, self.hidden)
+
+    @staticmethod
+    def _keeper(trace):
+        def keep(name, t):
+            if trace is not None:
+                trace[name] = t.clone()
+        return keep
+
+    def _attn_out(self, attn, x2, keep):
+        """x2 + o_proj(head-axis Hadamard(attn)); attn [R, ..., Hq, D] over
+        the R rows of x2 [R, hidden] (modeling_llama.py:94-96)."""
+        R = x2.shape[0]
+        attn = attn.reshape(R, 1, self.n_heads, self.head_dim)
+        attn = attn.transpose(-1, -2).contiguous()            # [R, 1, D, Hq]
         attn = matmul_hadU_cuda(attn, None, 1)
-        attn = attn.transpose(-1, -2).reshape(B, self.hidden)
+        attn = attn.transpose(-1, -2).reshape(R, self.hidden)
         keep("attn_rot", attn)
         o = self._linear(kernel.PackedQuantizedTensor(*kernel.sym_quant_dynamic(attn)), "o")
         x2 = x2 + o
         keep("resid1", x2)
+        return x2
 
-        # ---- MLP
+    def _mlp(self, x2, keep):
+        """x2 + down(OnlineHadamard(SwiGLU(gate/up(RMSNorm(x2)))))
+        (modeling_llama.py:119-142)."""
         h = self.post_attention_layernorm(x2)
         gu = self._linear(kernel.PackedQuantizedTensor(*kernel.sym_quant_dynamic(h)), "gu")
         keep("norm2", h)
@@ -169,7 +221,7 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         keep("down_s", s_a)
         d = _CUDA.w4a4_linear(q_a, s_a.view(-1), self.w_down, self.s_down)
         keep("down", d)
-        return (x2 + d).view(B, 1, self.hidden)
+        return x2 + d
 
     def unpacked(self):
         """Host copies of the weights for checkers: {name: (codes u8, scales

@@ -306,14 +306,15 @@ class MultiLayerPagedKVCache4Bit(object):
                      k_param=kp.view(B, H, 2), v_param=vp.view(B, H, 2), layer_idx=layer_idx)
         return _LayerAttention(self._decoder, spec, layer_idx)
 
-    def update_qkv_fused(self, qkv, cos, sin, layer_idx, num_q_heads):
+    def update_qkv_fused(self, qkv, cos, sin, layer_idx, num_q_heads, attention_mask=None):
         """Decode-step form of update() plus the decode query's rotation, one
         kernel: qkv f16 [B, (Hq + 2 H) D] is the q/k/v projection output of
         the new token; q and k get RoPE (cos/sin [1 or B, 1, D]) and the
         head-dim Hadamard, k and v are quantized into the cache.  Returns the
         rotated q [B, Hq, D] for decode_rotated.  Bit for bit the same as
         rope_qk + update() + the query rotation.  The layer must hold its
-        prefill already."""
+        prefill already.  attention_mask as for update() (the extended HF
+        mask after a left-padded prefill) or None."""
         if not self._filled[layer_idx]:
             raise RuntimeError("update_qkv_fused: the layer has no prefill yet")
         if qkv.shape[0] != self.batch_size:
@@ -321,7 +322,7 @@ class MultiLayerPagedKVCache4Bit(object):
         if layer_idx == 0:
             self._reserve(self.length + 1)
             self.length += 1
-        spec = self.get_cache_specs_for_flash_infer(None)
+        spec = self.get_cache_specs_for_flash_infer(attention_mask)
         return _CUDA.qkv_rope_had_append(qkv, cos.contiguous(), sin.contiguous(), num_q_heads,
                                          self.num_heads, **spec, layer_idx=layer_idx,
                                          had_scale=1 / math.sqrt(self.head_dim),

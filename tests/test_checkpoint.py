@@ -93,3 +93,24 @@ def test_load_decode_layer(tmp_path):
     assert torch.equal(layer.w_o, t[p + "self_attn.o_proj.weight"])
     assert torch.equal(layer.w_down, t[p + "mlp.down_proj.weight"])
     assert torch.equal(layer.down_sign, t[p + "mlp.down_proj.had_adj_sign"])
+
+
+def test_decode_layer_export_round_trip(tmp_path):
+    """decode_layer_tensors writes the reference's per-projection keys
+    (q/k/v and gate/up split out of the fused buffers, scales as [out, 1]);
+    saving them and loading them into a fresh layer restores every buffer."""
+    from signrot_amd.transformers.decode_layer import W4A4LlamaDecodeLayer
+    hidden, heads, kv, hd, ffn = 256, 4, 2, 64, 512
+    src = W4A4LlamaDecodeLayer.random(hidden, heads, kv, hd, ffn, seed=3, device="cpu")
+    p = "model.layers.5."
+    t = ck.decode_layer_tensors(src, p)
+    assert t[p + "self_attn.k_proj.weight"].shape == (kv * hd, hidden // 2)
+    assert t[f"quantizer.{p}mlp.up_proj.scale"].shape == (ffn, 1)
+    assert torch.equal(t[p + "mlp.up_proj.weight"], src.w_gu[ffn:])
+    ck.save_packed_checkpoint(str(tmp_path), t, QCFG, max_shard_bytes=40000)
+    dst = W4A4LlamaDecodeLayer(hidden, heads, kv, hd, ffn)
+    ck.load_decode_layer(dst, ck.PackedCheckpoint(str(tmp_path)), p)
+    want = dict(src.named_buffers())
+    for name, b in dst.named_buffers():
+        if b is not None:
+            assert torch.equal(b, want[name]), name

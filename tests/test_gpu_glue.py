@@ -63,6 +63,24 @@ def test_rope_bitexact(C, b, t, hq, hk, d):
         assert_bitexact(to_np(dk), kw, f"k cos_b={cb}")
 
 
+def test_rope_signed_zeros(C):
+    """Zeros of both signs, fp16 underflow and their sums in every (x0, x1,
+    cos, sin) combination: the kernel's output bits, the sign of zero
+    included, are the oracle's (a multiply rounded through fma(x, y, +0)
+    once turned -0 products into +0 here)."""
+    vals = np.array([0.0, -0.0, 1e-7, -1e-7, 6e-8, -6e-8, 0.5, -0.5, 3.0, -3.0], np.float16)
+    n = len(vals)
+    x0, x1, c, s = np.meshgrid(vals, vals, vals, vals, indexing="ij")
+    q = np.stack([x0.reshape(-1), x1.reshape(-1)], -1).reshape(1, n ** 4, 1, 2)
+    cos = np.stack([c.reshape(-1)] * 2, -1).reshape(1, n ** 4, 2)
+    sin = np.stack([s.reshape(-1)] * 2, -1).reshape(1, n ** 4, 2)
+    qw, _ = glue.rope_qk(q, q, cos, sin)
+    dq, dk = to_dev(q), to_dev(q.copy())
+    C.rope_qk(dq, dk, to_dev(cos), to_dev(sin))
+    assert_bitexact(to_np(dq), qw, "rope q signed zeros")
+    assert_bitexact(to_np(dk), qw, "rope k signed zeros")
+
+
 @pytest.mark.parametrize("shape", [(1, 11008), (16, 11008), (2048, 11008), (32, 14336), (7,)])
 def test_swiglu(C, shape):
     rng = np.random.default_rng(sum(shape))

@@ -30,6 +30,27 @@ def test_rope_matches_hf_apply_rotary_pos_emb(b, t, hq, hk, d):
         assert np.array_equal(_bits(ko), _bits(kr.numpy()))
 
 
+def test_rope_signed_zeros_match_hf():
+    """Signed zeros in x, cos and sin (the products that are exactly -0 or
+    +0, their sums, and fp16 underflow) bit for bit as HF's fp16 expression
+    gives them: the sign of a zero output is part of the bit-exact contract
+    (x1 = +0 with sin < 0 and x0 * cos = -0 gives +0)."""
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+    vals = torch.tensor([0.0, -0.0, 1e-7, -1e-7, 6e-8, -6e-8, 0.5, -0.5, 3.0, -3.0],
+                        dtype=torch.float16)
+    n = len(vals)
+    # every (x0, x1, cos, sin) combination of the values, one pair per row
+    x0, x1, c, s = torch.meshgrid(vals, vals, vals, vals, indexing="ij")
+    q = torch.stack([x0.reshape(-1), x1.reshape(-1)], dim=-1).view(1, n ** 4, 1, 2)
+    cos = torch.stack([c.reshape(-1), c.reshape(-1)], dim=-1).view(1, n ** 4, 2)
+    sin = torch.stack([s.reshape(-1), s.reshape(-1)], dim=-1).view(1, n ** 4, 2)
+    qr, _ = apply_rotary_pos_emb(q, q, cos, sin, unsqueeze_dim=2)
+    qo, _ = glue.rope_qk(q.numpy(), q.numpy(), cos.numpy(), sin.numpy())
+    assert np.array_equal(_bits(qo), _bits(qr.numpy()))
+    neg_zero = _bits(qr.numpy()) == 0x8000
+    assert neg_zero.any() and (_bits(qr.numpy()) == 0).any()
+
+
 def test_rope_identity_and_quarter_turn():
     rng = np.random.default_rng(0)
     q = rng.standard_normal((1, 2, 3, 8)).astype(np.float16)
