@@ -326,6 +326,77 @@ SRQ_DEV void store_block_lds(const Epi &e, int64_t M, int64_t N, int64_t mb, int
         store_block_lds_impl<BS, FM, FN, true>(e, M, N, mb, nb, acc, lane, tile);
 }
 
+// fp16 epilogue through an int32 LDS tile, for kernels with little register
+// room: the wave's raw accumulators go to its LDS area `tile` first (row
+// stride BS FN words; a row pass reads whole 256-byte LDS rows), which
+// frees them, then each lane dequantizes 8 consecutive outputs of a row
+// (column scales loaded once per lane, one row scale per row) and stores
+// them as 16 bytes.  Same arithmetic as store_one; `tile` must be free of
+// other readers and of in-flight DMA, 4 BS FN BS FM bytes.
+template <int BS, int FM, int FN, typename AccT>
+SRQ_DEV void store_block_lds32(const Epi &e, int64_t M, int64_t N, int64_t mb, int64_t nb,
+                               const AccT (&acc)[FM][FN], int lane, int32_t *tile) {
+    constexpr int NV = BS * BS / 64;
+    constexpr int W = BS * FN;   // outputs per row
+    constexpr int WS = W;        // row stride (words)
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int lr = i * BS + frag_row<BS>(v, lane);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) tile[lr * WS + j * BS + (lane & (BS - 1))] = acc[i][j][v];
+        }
+    constexpr int LPR = W / 8;     // lanes per row
+    constexpr int RPI = 64 / LPR;  // rows per pass
+    static_assert(LPR >= 1 && 64 % LPR == 0 && (BS * FM) % RPI == 0, "row pass shape");
+    const int c8 = (lane % LPR) * 8;
+    const int64_t gn0 = nb + c8;
+    const bool full_n = gn0 + 8 <= N;
+    float sbv[8], bv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const bool on = gn0 + k < N;
+        sbv[k] = on ? (float)e.sb[gn0 + k] : 0.f;
+        bv[k] = on && e.bias ? (float)e.bias[gn0 + k] : 0.f;
+    }
+    const bool vec = full_n && N % 8 == 0 && ((uintptr_t)e.out % 16 == 0) &&
+                     (!e.res || (uintptr_t)e.res % 16 == 0);
+    for (int r0 = 0; r0 < BS * FM; r0 += RPI) {
+        const int lr = r0 + lane / LPR;
+        const int64_t gm = mb + lr;
+        if (gm >= M || gn0 >= N) continue;
+        const v4i a0 = *reinterpret_cast<const v4i *>(tile + lr * WS + c8);
+        const v4i a1 = *reinterpret_cast<const v4i *>(tile + lr * WS + c8 + 4);
+        const float sa = (float)e.sa[gm];
+        v8h o;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int a = k < 4 ? a0[k] : a1[k - 4];
+            const int val = epi_val(e, a, gm, gn0 + k < N ? gn0 + k : gn0);
+            f16 x = f16_rn((float)val * sa * sbv[k]);
+            if (e.bias) x = f16_rn((float)x + bv[k]);
+            o[k] = x;
+        }
+        if (vec) {
+            if (e.res) {
+                const v8h rv = *reinterpret_cast<const v8h *>(e.res + gm * N + gn0);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) o[k] = f16_rn((float)o[k] + (float)rv[k]);
+            }
+            *reinterpret_cast<v8h *>(e.out + gm * N + gn0) = o;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (gn0 + k >= N) break;
+                f16 ok = o[k];
+                if (e.res) ok = f16_rn((float)ok + (float)e.res[gm * N + gn0 + k]);
+                e.out[gm * N + gn0 + k] = ok;
+            }
+        }
+    }
+}
+
 // One K step of a compute wave: the stage holds BM A rows then the B rows.
 template <int FM, int FN, int KBB, int BM = kBigBM, bool UA = false>
 SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {
@@ -1130,6 +1201,9 @@ bool launch_stream(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int
 
 constexpr int kGrpBM = 128, kGrpBN = 128;
 constexpr int kGrpRows = kGrpBM + kGrpBN;
+// 128-byte K steps in a 3-stage ring (4 stages measured the same: the
+// kernel is not bound by DMA latency)
+constexpr int kGrpKBB = 128, kGrpStages = 3;
 
 struct GroupedArgs {
     int P;
@@ -1196,15 +1270,22 @@ SRQ_DEV int64_t grouped_tiles(const GroupedProb &r) {
     return ((r.m + kGrpBM - 1) / kGrpBM) * ((r.n + kGrpBN - 1) / kGrpBN);
 }
 
-template <int NPROD, bool UA>
+template <int NPROD, bool UA, int NSTG = kGrpStages>
 __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(GroupedArgs g) {
-    constexpr int WGN = 2, FM = 2, FN = 2, KBB = 128, NSTG = 3;
+    constexpr int WGN = 2, FM = 2, FN = 2, KBB = kGrpKBB;
+    static_assert(KBB == 128, "stage layout validated for 128-byte steps only");
     constexpr int kCompute = 4;
     constexpr int kStage = kGrpRows * KBB;
-    constexpr int kDma = kGrpRows / 8;
+    constexpr int C = KBB / 16;           // 16-byte chunks per row
+    constexpr int R = 1024 / KBB;         // rows per 1 KiB DMA block
+    constexpr int kDma = kGrpRows / R;
     constexpr int kDmaPerWave = kDma / NPROD;
     static_assert(kDmaPerWave * NPROD == kDma, "DMA split");
+    static_assert(NSTG >= 2 && (NSTG - 2) * kDmaPerWave <= 63, "vmcnt range");
+    constexpr int kEpiTile = 4 * 32 * FN * 32 * FM;  // a compute wave's int32 block
+    static_assert(NSTG * kStage + kCompute * kEpiTile <= 160 * 1024, "LDS ring");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTG * kStage];
+    __shared__ __attribute__((aligned(16))) uint8_t epi_lds[kCompute * kEpiTile];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1241,9 +1322,9 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
 #pragma unroll
             for (int q = 0; q < kDmaPerWave; ++q) {
                 const int i = pw * kDmaPerWave + q;
-                const int r = 8 * i + lane / 8;
-                jc[q] = ((lane % 8) ^ swz<KBB>(r)) * 16;
-                const bool isa = 8 * i < kGrpBM;
+                const int r = R * i + lane / C;
+                jc[q] = ((lane % C) ^ swz<KBB>(r)) * 16;
+                const bool isa = R * i < kGrpBM;
                 const int64_t row = isa ? m0 + r : n0 + r - kGrpBM;
                 roff[q] = row < (isa ? pr.m : pr.n)
                               ? (uint32_t)(row * (isa ? pr.lda_b : pr.ldb_b)) : kOob;
@@ -1257,22 +1338,20 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                     const uint32_t dst = lds0 + sl * kStage + i * 1024;
                     uint32_t off = roff[q] == kOob ? kOob : roff[q] + (uint32_t)kb0 + jc[q];
                     if (tail && kb0 + jc[q] >= KB) off = kOob;
-                    dma16(8 * i < kGrpBM ? ar : br, off, dst);
+                    dma16(R * i < kGrpBM ? ar : br, off, dst);
                 }
             };
-            if (steps > 0) issue(0, 0);
-            if (steps > 1) issue(1, 1);
-            int sl = 0;
+#pragma unroll
+            for (int q = 0; q < NSTG - 1; ++q)
+                if (q < steps) issue(q, q);
             for (int s = 0; s < steps; ++s) {
-                if (s + 1 < steps) {
-                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave) : "memory");
-                } else {
-                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                }
+                // this wave's DMA of step s is done (later steps may fly);
+                // after the barrier every wave's is, and step s - 1's stage
+                // is free for step s + NSTG - 1
+                ring_wait<kDmaPerWave, NSTG - 2>(min(NSTG - 2, steps - 1 - s));
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
-                if (s + 2 < steps) issue(s + 2, sl == 0 ? 2 : sl - 1);
-                sl = sl == 2 ? 0 : sl + 1;
+                if (s + NSTG - 1 < steps) issue(s + NSTG - 1, (s + NSTG - 1) % NSTG);
             }
             // end of tile: every compute wave is done with every stage
             __builtin_amdgcn_s_barrier();
@@ -1285,26 +1364,36 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){};
-        int sl = 0;
         for (int s = 0; s < steps; ++s) {
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
-            big_compute<FM, FN, KBB, kGrpBM, UA>(smem + sl * kStage, wm, wn, lane, acc);
-            sl = sl == 2 ? 0 : sl + 1;
+            big_compute<FM, FN, KBB, kGrpBM, UA>(smem + (s % NSTG) * kStage, wm, wn, lane, acc);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
 
-        // 32x32 accumulator layout: lane holds column lane & 31, rows
-        // 8 (v / 4) + 4 (lane / 32) + v % 4
-        float sbv[FN];
-        int64_t gnv[FN];
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            gnv[j] = n0 + wn * (FN * 32) + j * 32 + (lane & 31);
-            sbv[j] = (g.out && gnv[j] < pr.n) ? (float)g.sb[(int64_t)p * g.N + gnv[j]] : 0.f;
+        if (g.out) {
+            // fp16 (expert-offset form): rows row0 + m of the [R, N] output,
+            // through the wave's own LDS tile (the ring's stages already
+            // take the next tile's DMA); the sym_dequant_moe zero correction
+            // is epi_val's
+            Epi e{};
+            e.out = g.out + pr.row0 * g.N;
+            e.sa = g.sa + pr.row0;
+            e.sb = g.sb + (int64_t)p * g.N;
+            e.ua = UA;
+            if (g.zr) {
+                e.zr = g.zr + pr.row0;
+                e.ws = g.ws + (int64_t)p * g.N;
+            }
+            store_block_lds32<32, FM, FN>(e, pr.m, pr.n, m0 + wm * (FM * 32),
+                                          n0 + wn * (FN * 32), acc, lane,
+                                          reinterpret_cast<int32_t *>(epi_lds + wave * kEpiTile));
+            continue;
         }
+        // int32 (pointer-array form): 32x32 accumulator layout, lane holds
+        // column lane & 31, rows 8 (v / 4) + 4 (lane / 32) + v % 4
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -1312,20 +1401,10 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                 const int64_t gm =
                     m0 + wm * (FM * 32) + i * 32 + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
                 if (gm >= pr.m) continue;
-                const float sa = g.out ? (float)g.sa[pr.row0 + gm] : 0.f;
 #pragma unroll
                 for (int j = 0; j < FN; ++j) {
-                    if (gnv[j] >= pr.n) continue;
-                    int val = acc[i][j][v] >> (UA ? 4 : 8);
-                    if (g.zr)  // the sym_dequant_moe zero correction, int32 wrapping
-                        val = (int)((u32)val - (u32)(int)g.zr[pr.row0 + gm] *
-                                                   (u32)g.ws[(int64_t)p * g.N + gnv[j]]);
-                    if (g.out) {
-                        const float a = (float)val * sa;
-                        g.out[(pr.row0 + gm) * g.N + gnv[j]] = f16_rn(a * sbv[j]);
-                    } else {
-                        pr.c[gm * pr.ldc + gnv[j]] = val;
-                    }
+                    const int64_t gn = n0 + wn * (FN * 32) + j * 32 + (lane & 31);
+                    if (gn < pr.n) pr.c[gm * pr.ldc + gn] = acc[i][j][v] >> (UA ? 4 : 8);
                 }
             }
     }
