@@ -121,13 +121,21 @@ SRQ_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *p, int64_t bytes) {
 // load; the caller waits with an explicit s_waitcnt before reading the LDS.
 // The LDS base goes in M0 as a "{m0}" operand, so the compiler sets M0 itself
 // and knows the register is taken (nothing it keeps in M0 is overwritten).
+// The leading s_nop 4 supplies the wait states the hardware needs between
+// the compiler's writes of the operands and this instruction's reads of
+// them, which the compiler's hazard pass cannot see inside the asm: an SALU
+// write of M0 before an LDS-DMA read of M0 (1), and a VALU write of an SGPR
+// (v_readlane restoring a spilled descriptor or M0 source) before a VMEM read
+// of it (5).  Without it the DMA could take the previous M0 and land in the
+// wrong LDS stage: a grouped-GEMM build whose scheduler put
+// "s_mov_b32 m0, s33" right before the load returned wrong products.
 SRQ_DEV void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
-    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                  :: "v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 
 SRQ_DEV void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t lds) {
-    asm volatile("buffer_load_dword %0, %1, 0 offen lds"
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, 0 offen lds"
                  :: "v"(voff), "s"(r), "{m0}"(lds) : "memory");
 }
 
