@@ -457,6 +457,45 @@ int srq_w4a4_linear_moe(const void *A, const void *a_scale, const void *B, const
                         const int32_t *expert_offsets, int64_t num_experts, int64_t rows,
                         int64_t N, int64_t K, void *out, void *stream);
 
+/* The gate and up projections of the MoE block in one launch: two
+ * srq_w4a4_linear_moe calls over the same A rows (expert e's rows
+ * expert_offsets[e] .. expert_offsets[e + 1]), B_gate / B_up
+ * [num_experts, N, K/2] with scales s_gate / s_up [num_experts, N], into
+ * out_gate / out_up [rows, N].  Each output is bit-identical to its
+ * srq_w4a4_linear_moe call; the launch interleaves an expert's gate and up
+ * tiles so both read its A rows while they are in L2.  Replaces the two
+ * _gemm_dequant_grouped calls of SignRotMoEBlock.forward
+ * (signrot/nn/moe.py:187-190). */
+int srq_w4a4_linear_moe_gate_up(const void *A, const void *a_scale, const void *B_gate,
+                                const void *s_gate, const void *B_up, const void *s_up,
+                                const int32_t *expert_offsets, int64_t num_experts,
+                                int64_t rows, int64_t N, int64_t K, void *out_gate,
+                                void *out_up, void *stream);
+
+/* Routing of the MoE block in one launch (signrot/nn/moe.py:168-185 plus
+ * the expert sort of 175-180): logits fp16 [tokens, num_experts]
+ * (num_experts <= 64, top_k <= 8) -> weights fp16 [tokens, top_k] (fp32
+ * softmax, top-k with ties to the lower expert, renormalized when norm,
+ * cast to fp16, as torch's softmax / topk / div / to compute them),
+ * choice int32 [tokens * top_k] (expert of row t * top_k + j), and the rows
+ * stably sorted by expert: order [R] (sorted position -> row), inv [R]
+ * (row -> position), expert [R] and token [R] (= order / top_k) per
+ * sorted position, counts [num_experts], offsets [num_experts + 1].
+ * Replaces the softmax, topk, argsort, index_add_ and cumsum ops there. */
+int srq_moe_route(const void *logits, int64_t tokens, int64_t num_experts, int64_t top_k,
+                  int norm, void *weights, int32_t *choice, int32_t *order, int32_t *inv,
+                  int32_t *expert, int32_t *token, int32_t *counts, int32_t *offsets,
+                  void *stream);
+
+/* The MoE block's combine (signrot/nn/moe.py:226-230): out fp16 [tokens,
+ * hidden] = sum over j of fp16(y[inv[t * top_k + j]] * weights[t, j]),
+ * accumulated in fp32 in order of j and rounded to fp16, y fp16 [tokens *
+ * top_k, hidden] in expert order (the un-permute, product and sum of
+ * torch's y[inv].view(T, k, H) * w.unsqueeze(-1)).sum(dim=1)).  hidden % 8
+ * == 0. */
+int srq_moe_combine(const void *y, const int32_t *inv, const void *weights, int64_t tokens,
+                    int64_t top_k, int64_t hidden, void *out, void *stream);
+
 /* srq_w4a4_linear_moe for asymmetric activations: A holds uint4 codes, and
  * before the dequant each int32 product becomes v - a_zero[row] *
  * b_sum[e, col] (wrapping), a_zero int8 [rows], b_sum int32 [num_experts, N]

@@ -893,6 +893,70 @@ def w4a4_linear_moe(A, a_scale, B, b_scale, expert_offsets):
     return out
 
 
+def w4a4_linear_moe_gate_up(A, a_scale, B_gate, s_gate, B_up, s_up, expert_offsets):
+    """The MoE block's gate and up projections in one launch: (out_gate,
+    out_up), each bit-identical to w4a4_linear_moe with its B / scales (the
+    two _gemm_dequant_grouped calls of moe.py:187-190)."""
+    name = "w4a4_linear_moe_gate_up"
+    _check(name, [(A, "A"), (a_scale, "a_scale"), (B_gate, "B_gate"), (s_gate, "s_gate"),
+                  (B_up, "B_up"), (s_up, "s_up"), (expert_offsets, "expert_offsets")],
+           [torch.uint8, torch.float16, torch.uint8, torch.float16, torch.uint8, torch.float16,
+            torch.int32])
+    if A.dim() != 2 or B_gate.dim() != 3 or B_gate.shape[2] != A.shape[1]:
+        raise RuntimeError(f"{name}: expected A [R, K/2] and B [E, N, K/2], got "
+                           f"{tuple(A.shape)} and {tuple(B_gate.shape)}")
+    if tuple(B_up.shape) != tuple(B_gate.shape) or tuple(s_up.shape) != tuple(s_gate.shape):
+        raise RuntimeError(f"{name}: gate and up weights must have the same shapes")
+    R, E, N, K = A.shape[0], B_gate.shape[0], B_gate.shape[1], A.shape[1] * 2
+    if a_scale.numel() != R or tuple(s_gate.shape) != (E, N):
+        raise RuntimeError(f"{name}: a_scale must have R entries and the scales be [E, N]")
+    if expert_offsets.numel() != E + 1:
+        raise RuntimeError(f"{name}: expert_offsets must have num_experts + 1 entries")
+    out_g = torch.empty((R, N), dtype=torch.float16, device=A.device)
+    out_u = torch.empty((R, N), dtype=torch.float16, device=A.device)
+    _call("srq_w4a4_linear_moe_gate_up", _ptr(A), _ptr(a_scale), _ptr(B_gate), _ptr(s_gate),
+          _ptr(B_up), _ptr(s_up), _ptr(expert_offsets), E, R, N, K, _ptr(out_g), _ptr(out_u),
+          _stream(A))
+    return out_g, out_u
+
+
+def moe_route(logits, top_k, norm_topk_prob):
+    """Routing of the MoE block in one launch (moe.py:168-185): returns
+    (weights fp16 [T, k], order, inv, expert, token int32 [T k], counts int32
+    [E], offsets int32 [E + 1]); see srq_moe_route."""
+    name = "moe_route"
+    _check(name, [(logits, "logits")], [torch.float16])
+    if logits.dim() != 2:
+        raise RuntimeError(f"{name}: logits must be [tokens, num_experts]")
+    T, E = logits.shape
+    dev = logits.device
+    R = T * top_k
+    weights = torch.empty((T, top_k), dtype=torch.float16, device=dev)
+    ints = torch.empty((5, R), dtype=torch.int32, device=dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    choice, order, inv, expert, token = ints.unbind(0)
+    _call("srq_moe_route", _ptr(logits), T, E, top_k, 1 if norm_topk_prob else 0, _ptr(weights),
+          _ptr(choice), _ptr(order), _ptr(inv), _ptr(expert), _ptr(token), _ptr(counts),
+          _ptr(offsets), _stream(logits))
+    return weights, order, inv, expert, token, counts, offsets
+
+
+def moe_combine(y, inv, weights):
+    """out [T, H] = sum_j fp16(y[inv[t k + j]] * weights[t, j]) in fp32,
+    rounded to fp16 (moe.py:226-230)."""
+    name = "moe_combine"
+    _check(name, [(y, "y"), (inv, "inv"), (weights, "weights")],
+           [torch.float16, torch.int32, torch.float16])
+    T, k = weights.shape
+    if y.dim() != 2 or y.shape[0] != T * k or inv.numel() != T * k:
+        raise RuntimeError(f"{name}: y must be [T k, H] and inv [T k] for weights [T, k]")
+    out = torch.empty((T, y.shape[1]), dtype=torch.float16, device=y.device)
+    _call("srq_moe_combine", _ptr(y), _ptr(inv), _ptr(weights), T, k, y.shape[1], _ptr(out),
+          _stream(y))
+    return out
+
+
 def w4a4_linear_moe_asym(A, a_scale, a_zero, B, b_scale, b_sum, expert_offsets):
     """w4a4_linear_moe for asymmetric (uint4) activation codes: the int32
     product minus a_zero[row] * b_sum[e, col] before the dequant; a_zero int8

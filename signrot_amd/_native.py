@@ -61,6 +61,10 @@ SIGNATURES = {
     "srq_swiglu": [_p, _p, _i64, _p, _p],
     "srq_matmul_grouped": [_p, _p, _p, _p, _p, _p, _p, _i64, _i32, _p],
     "srq_w4a4_linear_moe": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
+    "srq_w4a4_linear_moe_gate_up": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p,
+                                    _p],
+    "srq_moe_route": [_p, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    "srq_moe_combine": [_p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_sym_quant_dynamic_moe": [_p, _p, _p, _i64, _i64, _i64, _f32, _p, _p, _p],
     "srq_sym_dequant_moe": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
 }

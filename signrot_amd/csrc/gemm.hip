@@ -1225,6 +1225,14 @@ struct GroupedArgs {
     // row [R] and per-expert weight row sums [P, N]
     const int8_t *zr;
     const int32_t *ws;
+    // paired expert-offset form (srq_w4a4_linear_moe_gate_up): 2 P problems,
+    // problem q = expert q / 2 times B (q even) or B2 (q odd), into out /
+    // out2 with sb / sb2 (and ws / ws2); both share the expert's A rows
+    int pair;
+    const uint8_t *B2;
+    const f16 *sb2;
+    f16 *out2;
+    const int32_t *ws2;
 };
 
 struct GroupedProb {
@@ -1252,13 +1260,14 @@ SRQ_DEV GroupedProb grouped_prob(const GroupedArgs &g, int p) {
         r.ldc = uni(g.ldc[p]);
         r.row0 = 0;
     } else {
-        r.row0 = uni(g.offsets[p]);
-        r.m = uni(g.offsets[p + 1]) - r.row0;
+        const int e = g.pair ? p >> 1 : p;
+        r.row0 = uni(g.offsets[e]);
+        r.m = uni(g.offsets[e + 1]) - r.row0;
         r.n = g.N;
         r.k = g.K;
         r.lda_b = r.ldb_b = g.K / 2;
         r.a = g.A + r.row0 * r.lda_b;
-        r.b = g.B + (int64_t)p * g.N * r.ldb_b;
+        r.b = ((g.pair && (p & 1)) ? g.B2 : g.B) + (int64_t)e * g.N * r.ldb_b;
         r.c = nullptr;
         r.ldc = g.N;
     }
@@ -1378,14 +1387,16 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             // through the wave's own LDS tile (the ring's stages already
             // take the next tile's DMA); the sym_dequant_moe zero correction
             // is epi_val's
+            const bool second = g.pair && (p & 1);
+            const int64_t ex = g.pair ? p >> 1 : p;
             Epi e{};
-            e.out = g.out + pr.row0 * g.N;
+            e.out = (second ? g.out2 : g.out) + pr.row0 * g.N;
             e.sa = g.sa + pr.row0;
-            e.sb = g.sb + (int64_t)p * g.N;
+            e.sb = (second ? g.sb2 : g.sb) + ex * g.N;
             e.ua = UA;
             if (g.zr) {
                 e.zr = g.zr + pr.row0;
-                e.ws = g.ws + (int64_t)p * g.N;
+                e.ws = (second ? g.ws2 : g.ws) + ex * g.N;
             }
             store_block_lds32<32, FM, FN>(e, pr.m, pr.n, m0 + wm * (FM * 32),
                                           n0 + wn * (FN * 32), acc, lane,
@@ -1630,6 +1641,44 @@ extern "C" int srq_w4a4_linear_moe(const void *A, const void *a_scale, const voi
     g.out = (f16 *)out;
     gemm_grouped_kernel<4, false><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
     SRQ_LAUNCH_CHECK("w4a4_linear_moe");
+    return SRQ_OK;
+}
+
+extern "C" int srq_w4a4_linear_moe_gate_up(const void *A, const void *a_scale,
+                                           const void *B_gate, const void *s_gate,
+                                           const void *B_up, const void *s_up,
+                                           const int32_t *expert_offsets, int64_t num_experts,
+                                           int64_t rows, int64_t N, int64_t K, void *out_gate,
+                                           void *out_up, void *stream) {
+    SRQ_CHECK_ARG(num_experts >= 0 && num_experts <= 0x3fffffffLL && rows >= 0 && N >= 0 &&
+                      K >= 0, "w4a4_linear_moe_gate_up: bad shape");
+    SRQ_CHECK_ARG(K % 32 == 0 && K < 131072, "w4a4_linear_moe_gate_up: K=%lld must be a "
+                  "multiple of 32 and < 131072", (long long)K);
+    if (num_experts == 0 || rows == 0 || N == 0) return SRQ_OK;
+    if (rows * (K / 2) >= 0xFFFFFFF0LL || N * (K / 2) >= 0xFFFFFFF0LL) {
+        srq_set_error("w4a4_linear_moe_gate_up: operand larger than 4 GiB");
+        return SRQ_EUNSUPPORTED;
+    }
+    SRQ_CHECK_ARG(A && a_scale && B_gate && s_gate && B_up && s_up && expert_offsets &&
+                      out_gate && out_up, "w4a4_linear_moe_gate_up: null pointer");
+    SRQ_CHECK_ARG(srq_aligned(A, 16) && srq_aligned(B_gate, 16) && srq_aligned(B_up, 16),
+                  "w4a4_linear_moe_gate_up: A and B must be 16-byte aligned");
+    GroupedArgs g{};
+    g.P = 2 * (int)num_experts;
+    g.pair = 1;
+    g.offsets = expert_offsets;
+    g.A = (const uint8_t *)A;
+    g.B = (const uint8_t *)B_gate;
+    g.B2 = (const uint8_t *)B_up;
+    g.N = N;
+    g.K = K;
+    g.sa = (const f16 *)a_scale;
+    g.sb = (const f16 *)s_gate;
+    g.sb2 = (const f16 *)s_up;
+    g.out = (f16 *)out_gate;
+    g.out2 = (f16 *)out_up;
+    gemm_grouped_kernel<4, false><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
+    SRQ_LAUNCH_CHECK("w4a4_linear_moe_gate_up");
     return SRQ_OK;
 }
 

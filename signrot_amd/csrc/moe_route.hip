@@ -1,0 +1,237 @@
+// Routing and combine of the MoE block (signrot/nn/moe.py:168-185 routing,
+// 226-230 combine), for gfx950.
+//
+// moe_route: per token, the fp32 softmax of its E fp16 router logits, the
+// top-k experts by probability, the optional renormalization of the k
+// probabilities, the weights cast to fp16; then the T * k (token, choice)
+// rows ordered by expert, stable in the row index t * k + j.  Arithmetic
+// follows torch's ops step by step:
+//   * softmax (softmax_warp_forward for E <= 64): x in fp32, m = max x,
+//     e_i = exp(x_i - m), the sum of the e_i over E padded with zeros to a
+//     power of two P by the shuffle butterfly v_i + v_{i ^ o} for
+//     o = P/2, ..., 1, then p_i = e_i / sum;
+//   * top-k by value, ties to the lower expert; the k values in descending
+//     order;
+//   * renormalization: p_j / (p_0 + p_1 + ... ) summed in order;
+//   * weights: fp16 round of the fp32 values.
+// The sort is a counting sort: per-expert counts, offsets = their
+// exclusive sum, and each row's rank among the earlier rows of its expert
+// from wave ballots (no atomics on global memory: deterministic).
+//
+// moe_combine: out[t, :] = fp16(sum_j fp32(fp16(y[inv[t k + j], :] *
+// w[t, j]))), j in order from 0: the fp16 product and the fp32 sum of
+// torch's (y[inv].view(T, k, H) * w.unsqueeze(-1)).sum(dim=1).
+#include "common.h"
+
+namespace {
+
+constexpr int kRouteThreads = 256;  // one wave per SIMD: the per-token arrays fit in VGPRs
+constexpr int kRouteMaxE = 64;
+constexpr int kRouteMaxK = 8;
+
+SRQ_DEV int pow2_ceil(int n) {
+    int p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
+    const f16 *__restrict__ logits, int T, int E, int K, int norm, f16 *__restrict__ weights,
+    int32_t *__restrict__ choice, int32_t *__restrict__ order, int32_t *__restrict__ inv,
+    int32_t *__restrict__ eid, int32_t *__restrict__ tok, int32_t *__restrict__ counts,
+    int32_t *__restrict__ offsets) {
+    constexpr int kWaves = kRouteThreads / 64;
+    __shared__ int s_count[kRouteMaxE];
+    __shared__ int s_base[kRouteMaxE];      // rows of expert e placed so far
+    __shared__ int s_wave[kWaves][kRouteMaxE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < kRouteMaxE) s_count[tid] = 0;
+    // a wave that sees no row of an expert leaves its slot untouched, so
+    // every slot starts at zero (and is cleared again after each chunk)
+    for (int i = tid; i < kWaves * kRouteMaxE; i += kRouteThreads) (&s_wave[0][0])[i] = 0;
+    __syncthreads();
+
+    // ---- per token: softmax, top-k, weights
+    const int P = pow2_ceil(E);
+    for (int t = tid; t < T; t += kRouteThreads) {
+        float v[kRouteMaxE];
+        float m = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < kRouteMaxE; ++i) {
+            v[i] = i < E ? (float)logits[(int64_t)t * E + i] : -__builtin_inff();
+            if (i < E) m = v[i] > m ? v[i] : m;
+        }
+        float s[kRouteMaxE];
+#pragma unroll
+        for (int i = 0; i < kRouteMaxE; ++i) {
+            v[i] = i < E ? expf(v[i] - m) : 0.f;
+            s[i] = v[i];
+        }
+        // butterfly: after the level with offset o, s[i] = s[i] + s[i ^ o];
+        // lane 0's value is the sum every lane ends with
+#pragma unroll
+        for (int o = kRouteMaxE / 2; o > 0; o >>= 1) {
+            if (o < P) {
+#pragma unroll
+                for (int i = 0; i < o; ++i) s[i] = s[i] + s[i + o];
+            }
+        }
+        const float sum = s[0];
+        float pk[kRouteMaxK];
+        int ek[kRouteMaxK];
+        unsigned long long taken = 0;
+#pragma unroll
+        for (int j = 0; j < kRouteMaxK; ++j) {
+            if (j >= K) break;
+            float best = -1.f;
+            int bi = 0;
+#pragma unroll
+            for (int i = 0; i < kRouteMaxE; ++i) {
+                if (i >= E || ((taken >> i) & 1)) continue;
+                const float p = v[i] / sum;
+                if (p > best) {  // strict: ties keep the lower expert
+                    best = p;
+                    bi = i;
+                }
+            }
+            taken |= 1ull << bi;
+            pk[j] = best;
+            ek[j] = bi;
+        }
+        float den = 0.f;
+        if (norm) {
+#pragma unroll
+            for (int j = 0; j < kRouteMaxK; ++j)
+                if (j < K) den += pk[j];
+        }
+#pragma unroll
+        for (int j = 0; j < kRouteMaxK; ++j) {
+            if (j >= K) break;
+            const float w = norm ? pk[j] / den : pk[j];
+            weights[(int64_t)t * K + j] = (f16)w;
+            choice[(int64_t)t * K + j] = ek[j];
+            atomicAdd(&s_count[ek[j]], 1);  // LDS: integer, order-free
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0;
+        for (int e = 0; e < E; ++e) {
+            offsets[e] = acc;
+            counts[e] = s_count[e];
+            s_base[e] = acc;
+            acc += s_count[e];
+        }
+        offsets[E] = acc;
+    }
+    __syncthreads();
+
+    // ---- stable counting sort of the T K rows by expert, a block at a time
+    const int rows = T * K;
+    for (int c0 = 0; c0 < rows; c0 += kRouteThreads) {
+        const int f = c0 + tid;
+        const int e = f < rows ? choice[f] : -1;
+        // rank among the earlier lanes of this wave with the same expert
+        int rank = 0;
+        unsigned long long left = __ballot(e >= 0);
+        while (left) {
+            const int leader = __builtin_ctzll(left);
+            const int le = __shfl(e, leader);
+            const unsigned long long same = __ballot(e == le);
+            if (e == le) rank = __popcll(same & ((1ull << lane) - 1));
+            if (lane == leader) s_wave[wave][le] = __popcll(same);
+            left &= ~same;
+        }
+        __syncthreads();
+        // per expert: running base + the earlier waves of this chunk
+        if (tid < E) {
+            int acc = s_base[tid];
+            for (int w = 0; w < kWaves; ++w) {
+                const int n = s_wave[w][tid];
+                s_wave[w][tid] = acc;
+                acc += n;
+            }
+            s_base[tid] = acc;
+        }
+        __syncthreads();
+        if (e >= 0) {
+            const int pos = s_wave[wave][e] + rank;
+            order[pos] = f;
+            inv[f] = pos;
+            eid[pos] = e;
+            tok[pos] = f / K;
+        }
+        __syncthreads();
+        // clear this chunk's wave counts
+        for (int i = tid; i < kWaves * kRouteMaxE; i += kRouteThreads)
+            (&s_wave[0][0])[i] = 0;
+        __syncthreads();
+    }
+}
+
+// One thread per 8 consecutive outputs of a token (16-byte loads/stores).
+__global__ __launch_bounds__(256) void moe_combine_kernel(const f16 *__restrict__ y,
+                                                          const int32_t *__restrict__ inv,
+                                                          const f16 *__restrict__ w, int64_t T,
+                                                          int K, int64_t H,
+                                                          f16 *__restrict__ out) {
+    const int64_t per_tok = H / 8;
+    const int64_t total = T * per_tok;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 256) {
+        const int64_t t = i / per_tok, h = (i % per_tok) * 8;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < K; ++j) {
+            const int64_t r = inv[t * K + j];
+            const float wj = (float)w[t * K + j];
+            const v8h yv = *reinterpret_cast<const v8h *>(y + r * H + h);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[k] += (float)f16_rn((float)yv[k] * wj);
+        }
+        v8h o;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] = f16_rn(acc[k]);
+        *reinterpret_cast<v8h *>(out + t * H + h) = o;
+    }
+}
+
+}  // namespace
+
+extern "C" int srq_moe_route(const void *logits, int64_t tokens, int64_t num_experts,
+                             int64_t top_k, int norm, void *weights, int32_t *choice,
+                             int32_t *order, int32_t *inv, int32_t *expert, int32_t *token,
+                             int32_t *counts, int32_t *offsets, void *stream) {
+    SRQ_CHECK_ARG(num_experts >= 1 && num_experts <= kRouteMaxE,
+                  "moe_route: num_experts=%lld must be in [1, %d]", (long long)num_experts,
+                  kRouteMaxE);
+    SRQ_CHECK_ARG(top_k >= 1 && top_k <= num_experts && top_k <= kRouteMaxK,
+                  "moe_route: top_k=%lld must be in [1, min(num_experts, %d)]",
+                  (long long)top_k, kRouteMaxK);
+    SRQ_CHECK_ARG(tokens >= 0 && tokens * top_k < 0x7fffffffLL, "moe_route: bad token count");
+    SRQ_CHECK_ARG(logits || tokens == 0, "moe_route: null logits");
+    SRQ_CHECK_ARG(counts && offsets, "moe_route: null counts / offsets");
+    SRQ_CHECK_ARG(tokens == 0 || (weights && choice && order && inv && expert && token),
+                  "moe_route: null output");
+    moe_route_kernel<<<dim3(1), dim3(kRouteThreads), 0, (hipStream_t)stream>>>(
+        (const f16 *)logits, (int)tokens, (int)num_experts, (int)top_k, norm, (f16 *)weights,
+        choice, order, inv, expert, token, counts, offsets);
+    SRQ_LAUNCH_CHECK("moe_route");
+    return SRQ_OK;
+}
+
+extern "C" int srq_moe_combine(const void *y, const int32_t *inv, const void *weights,
+                               int64_t tokens, int64_t top_k, int64_t hidden, void *out,
+                               void *stream) {
+    SRQ_CHECK_ARG(tokens >= 0 && top_k >= 1 && hidden >= 0, "moe_combine: bad shape");
+    SRQ_CHECK_ARG(hidden % 8 == 0, "moe_combine: hidden=%lld must be a multiple of 8",
+                  (long long)hidden);
+    if (tokens == 0 || hidden == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(y && inv && weights && out, "moe_combine: null pointer");
+    SRQ_CHECK_ARG(srq_aligned(y, 16) && srq_aligned(out, 16),
+                  "moe_combine: y and out must be 16-byte aligned");
+    const int64_t blocks = std::min<int64_t>(srq_cdiv(tokens * (hidden / 8), 256), 4096);
+    moe_combine_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(
+        (const f16 *)y, inv, (const f16 *)weights, tokens, (int)top_k, hidden, (f16 *)out);
+    SRQ_LAUNCH_CHECK("moe_combine");
+    return SRQ_OK;
+}

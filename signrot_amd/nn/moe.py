@@ -38,14 +38,18 @@ from ..functional.hadamard import get_hadK, matmul_hadU_cuda
 class MoERouting(NamedTuple):
     """Routing of one batch: `logits` [T, E]; `weights` [T, k] in the input
     dtype; row r of the expert-ordered batch is (token, choice) row
-    `order[r]` (= token * k + choice), expert `expert[r]` (int32); the rows of
-    expert e are `offsets[e] : offsets[e + 1]` (int32 [E + 1]); `counts` [E]."""
+    `order[r]` (= token * k + choice), of token `token[r]`, expert
+    `expert[r]` (int32); `inv` maps a (token, choice) row to its position;
+    the rows of expert e are `offsets[e] : offsets[e + 1]` (int32 [E + 1]);
+    `counts` [E]."""
     logits: torch.Tensor
     weights: torch.Tensor
     order: torch.Tensor
     expert: torch.Tensor
     counts: torch.Tensor
     offsets: torch.Tensor
+    inv: torch.Tensor
+    token: torch.Tensor
 
 
 class _Codes(NamedTuple):
@@ -190,9 +194,16 @@ class SignRotMoEBlock(torch.nn.Module):
     def route(self, x) -> MoERouting:
         """Router probabilities in fp32, top-k (renormalised when
         norm_topk_prob), weights in x's dtype (moe.py:168-185); rows ordered
-        by expert with fixed-shape device ops only (a stable sort and a
-        scatter-add for the counts: no host reads)."""
+        by expert, stable.  fp16 logits of at most 64 experts (top_k <= 8):
+        one srq_moe_route launch; otherwise the same steps as torch ops (a
+        stable sort and a scatter-add for the counts: no host reads)."""
         logits = self.gate(x)
+        if (logits.dtype == torch.float16 and logits.is_cuda and self.num_experts <= 64
+                and self.top_k <= 8):
+            w, order, inv, expert, token, counts, offsets = _CUDA.moe_route(
+                logits.contiguous(), self.top_k, self.norm_topk_prob)
+            return MoERouting(logits, w.to(x.dtype), order, expert, counts, offsets, inv,
+                              token)
         probs = torch.softmax(logits, dim=1, dtype=torch.float)
         top_p, top_e = torch.topk(probs, self.top_k, dim=-1)
         if self.norm_topk_prob:
@@ -204,16 +215,26 @@ class SignRotMoEBlock(torch.nn.Module):
         offsets = torch.zeros(self.num_experts + 1, dtype=torch.int32, device=x.device)
         torch.cumsum(counts, 0, out=offsets[1:])
         return MoERouting(logits, top_p.to(x.dtype), order, choice[order].to(torch.int32),
-                          counts, offsets)
+                          counts, offsets, torch.argsort(order), order // self.top_k)
 
     def forward(self, hidden_states: torch.Tensor):
         shape = hidden_states.shape
         x = hidden_states.reshape(-1, shape[-1])
         route = self.route(x)
-        codes = self._quant(x.to(torch.float16)).rows(route.order // self.top_k)
-        gate_h = self._project(codes, route, "gate")
-        up_h = self._project(codes, route, "up")
+        codes = self._quant(x.to(torch.float16)).rows(route.token)
+        if self.use_grouped and codes.zero is None:
+            # both projections in one launch (bit-identical to two)
+            gate_h, up_h = _CUDA.w4a4_linear_moe_gate_up(
+                codes.q, codes.scale, self.w_gate, self.s_gate, self.w_up, self.s_up,
+                route.offsets)
+        else:
+            gate_h = self._project(codes, route, "gate")
+            up_h = self._project(codes, route, "up")
         y = self._project(self._down_input(gate_h, up_h, route), route, "down")
+        if x.dtype == torch.float16 and shape[-1] % 8 == 0:
+            # un-permute, weight and sum in one launch (bit-identical)
+            out = _CUDA.moe_combine(y, route.inv.to(torch.int32), route.weights)
+            return out.view(shape), route.logits
         # back to (token, choice) order by a scatter through the permutation
         # (no atomics: a replayed graph gives the same bits), then the
         # weighted sum over each token's k choices

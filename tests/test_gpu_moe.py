@@ -172,6 +172,92 @@ def test_w4a4_linear_moe(C, counts, n, k):
         assert_bitexact(to_np(out), want, "fp16 out")
 
 
+@pytest.mark.parametrize("counts,n,k", [([3, 0, 5, 1], 300, 768),
+                                        ([123, 127, 123, 122, 123, 126, 136, 144], 14336, 4096),
+                                        ([0, 0], 128, 128), ([1], 4096, 1024)])
+def test_w4a4_linear_moe_gate_up_equals_two_calls(C, counts, n, k):
+    """The paired launch gives each projection bit for bit what its own
+    w4a4_linear_moe call gives (the oracle pins that call above)."""
+    torch.manual_seed(sum(counts) + n + 1)
+    a, bg = _grouped_inputs(None, counts, n, k)
+    _, bu = _grouped_inputs(None, counts, n, k)
+    e, rows = len(counts), a.shape[0]
+    sa = (torch.rand(rows, device=DEV) * 0.05 + 1e-3).half()
+    sg = (torch.rand(e, n, device=DEV) * 0.01 + 1e-4).half()
+    su = (torch.rand(e, n, device=DEV) * 0.01 + 1e-4).half()
+    off = torch.tensor(om.expert_offsets(counts), dtype=torch.int32, device=DEV)
+    g, u = C.w4a4_linear_moe_gate_up(a, sa, bg, sg, bu, su, off)
+    assert torch.equal(g, C.w4a4_linear_moe(a, sa, bg, sg, off))
+    assert torch.equal(u, C.w4a4_linear_moe(a, sa, bu, su, off))
+    if rows:
+        assert not torch.equal(g, u)
+
+
+@pytest.mark.parametrize("T,E,k,norm", [(512, 8, 2, True), (37, 8, 2, False),
+                                        (300, 64, 8, True), (5, 4, 4, True),
+                                        (1000, 60, 6, False), (700, 16, 1, True),
+                                        (0, 8, 2, True)])
+def test_moe_route_matches_torch(C, T, E, k, norm):
+    """srq_moe_route against the reference's torch ops (moe.py:168-185):
+    softmax in fp32, topk, renormalization and the fp16 cast bit for bit;
+    the same experts chosen except where the k-th and (k+1)-th
+    probabilities tie (then the lower expert wins); rows ordered by expert,
+    stable; counts, offsets, inv and token consistent with the order."""
+    g = torch.Generator(device=DEV).manual_seed(T + E + k)
+    logits = torch.randn(T, E, generator=g, device=DEV).half()
+    if T > 10:  # exact ties inside rows
+        logits[::5, 1] = logits[::5, 0]
+        logits[::7, E - 1] = logits[::7, E // 2]
+    w, order, inv, expert, token, counts, offsets = C.moe_route(logits, k, norm)
+    probs = torch.softmax(logits, dim=1, dtype=torch.float)
+    tp, te = torch.topk(probs, k, dim=-1)
+    if norm:
+        tp = tp / tp.sum(dim=-1, keepdim=True)
+    assert torch.equal(w, tp.half())
+    # our choice per row: expert[inv] in (token, choice) order
+    ours = expert[inv.long()].view(T, k).long() if T else te
+    same = (torch.sort(ours, 1).values == torch.sort(te, 1).values).all(1)
+    if T and not same.all():
+        bad = (~same).nonzero().flatten()
+        srt = torch.sort(probs[bad], 1, descending=True).values
+        assert k < E and torch.equal(srt[:, k - 1], srt[:, k]), "choice differs without a tie"
+    # our value order: descending, ties to the lower expert
+    pv = probs.gather(1, ours) if T else tp
+    assert (pv[:, :-1] >= pv[:, 1:]).all()
+    tie = pv[:, :-1] == pv[:, 1:]
+    assert (ours[:, :-1][tie] < ours[:, 1:][tie]).all()
+    flat = ours.reshape(-1)
+    assert torch.equal(expert.long(), torch.sort(flat, stable=True).values)
+    assert torch.equal(flat[order.long()], expert.long())
+    assert torch.equal(inv[order.long()], torch.arange(T * k, device=DEV, dtype=torch.int32))
+    assert torch.equal(token, order // k)
+    assert torch.equal(counts.long(), torch.bincount(flat, minlength=E))
+    assert offsets[0] == 0 and torch.equal(offsets[1:] - offsets[:-1], counts)
+    for e in range(E):
+        r = order[offsets[e]:offsets[e + 1]]
+        assert torch.all(r[1:] > r[:-1])
+
+
+@pytest.mark.parametrize("T,k,H", [(512, 2, 4096), (33, 1, 64), (7, 2, 8), (100, 4, 256),
+                                   (0, 2, 64)])
+def test_moe_combine_matches_torch(C, T, k, H):
+    """srq_moe_combine against (y[inv].view(T, k, H) * w.unsqueeze(-1)).sum(1)
+    in torch fp16 (moe.py:226-230): bit for bit for k <= 2 (fp32 sums of
+    two products are order-free); for k = 4 within one fp16 ulp (torch's
+    reduction order is its own)."""
+    g = torch.Generator(device=DEV).manual_seed(T * k + H)
+    y = torch.randn(T * k, H, generator=g, device=DEV).half()
+    w = torch.rand(T, k, generator=g, device=DEV).half()
+    inv = torch.randperm(T * k, generator=g, device=DEV).to(torch.int32)
+    got = C.moe_combine(y, inv, w)
+    want = (y[inv.long()].view(T, k, H) * w.unsqueeze(-1)).sum(dim=1)
+    if k <= 2:
+        assert torch.equal(got, want)
+    else:
+        ulp = torch.finfo(torch.float16).eps * want.float().abs().clamp(min=6.1e-5)
+        assert ((got.float() - want.float()).abs() <= ulp).all()
+
+
 # ------------------------------------------------------------------ block
 
 def _block(hidden, inter, experts, top_k, norm, seed, with_sign=True):
