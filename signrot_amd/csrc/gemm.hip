@@ -353,13 +353,9 @@ SRQ_DEV void store_block_lds32(const Epi &e, int64_t M, int64_t N, int64_t mb, i
     const int c8 = (lane % LPR) * 8;
     const int64_t gn0 = nb + c8;
     const bool full_n = gn0 + 8 <= N;
-    float sbv[8], bv[8];
+    float sbv[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const bool on = gn0 + k < N;
-        sbv[k] = on ? (float)e.sb[gn0 + k] : 0.f;
-        bv[k] = on && e.bias ? (float)e.bias[gn0 + k] : 0.f;
-    }
+    for (int k = 0; k < 8; ++k) sbv[k] = gn0 + k < N ? (float)e.sb[gn0 + k] : 0.f;
     const bool vec = full_n && N % 8 == 0 && ((uintptr_t)e.out % 16 == 0) &&
                      (!e.res || (uintptr_t)e.res % 16 == 0);
     for (int r0 = 0; r0 < BS * FM; r0 += RPI) {
@@ -375,7 +371,8 @@ SRQ_DEV void store_block_lds32(const Epi &e, int64_t M, int64_t N, int64_t mb, i
             const int a = k < 4 ? a0[k] : a1[k - 4];
             const int val = epi_val(e, a, gm, gn0 + k < N ? gn0 + k : gn0);
             f16 x = f16_rn((float)val * sa * sbv[k]);
-            if (e.bias) x = f16_rn((float)x + bv[k]);
+            // bias read per row pass (cached), not held in 8 more registers
+            if (e.bias && gn0 + k < N) x = f16_rn((float)x + (float)e.bias[gn0 + k]);
             o[k] = x;
         }
         if (vec) {
@@ -1204,6 +1201,8 @@ constexpr int kGrpRows = kGrpBM + kGrpBN;
 // 128-byte K steps in a 3-stage ring (4 stages measured the same: the
 // kernel is not bound by DMA latency)
 constexpr int kGrpKBB = 128, kGrpStages = 3;
+// Persistent grid of the grouped kernel: one workgroup per CU (256 CUs).
+constexpr int kGroupedGrid = 256;
 
 struct GroupedArgs {
     int P;
@@ -1233,6 +1232,11 @@ struct GroupedArgs {
     const f16 *sb2;
     f16 *out2;
     const int32_t *ws2;
+    // dense form (the DENSE instantiation): one problem, A [M, K/2] times
+    // B [N, K/2], fp16 out [M, N] with the dense epilogue's bias [N] and
+    // residual [M, N] (either may be null)
+    int64_t M;
+    const f16 *bias, *res;
 };
 
 struct GroupedProb {
@@ -1246,8 +1250,21 @@ SRQ_DEV int64_t uni(int64_t v) {
                      (uint32_t)__builtin_amdgcn_readfirstlane((int)v));
 }
 
+template <bool DENSE>
 SRQ_DEV GroupedProb grouped_prob(const GroupedArgs &g, int p) {
     GroupedProb r;
+    if constexpr (DENSE) {
+        r.row0 = 0;
+        r.m = g.M;
+        r.n = g.N;
+        r.k = g.K;
+        r.lda_b = r.ldb_b = g.K / 2;
+        r.a = g.A;
+        r.b = g.B;
+        r.c = nullptr;
+        r.ldc = g.N;
+        return r;
+    }
     if (g.sizes) {
         r.m = uni(g.sizes[3 * p]);
         r.n = uni(g.sizes[3 * p + 1]);
@@ -1279,7 +1296,7 @@ SRQ_DEV int64_t grouped_tiles(const GroupedProb &r) {
     return ((r.m + kGrpBM - 1) / kGrpBM) * ((r.n + kGrpBN - 1) / kGrpBN);
 }
 
-template <int NPROD, bool UA, int NSTG = kGrpStages>
+template <int NPROD, bool UA, bool DENSE = false, int NSTG = kGrpStages>
 __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(GroupedArgs g) {
     constexpr int WGN = 2, FM = 2, FN = 2, KBB = kGrpKBB;
     static_assert(KBB == 128, "stage layout validated for 128-byte steps only");
@@ -1305,14 +1322,14 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
 
     int p = 0;
     int64_t pstart = 0;
-    GroupedProb pr = grouped_prob(g, 0);
+    GroupedProb pr = grouped_prob<DENSE>(g, 0);
     int64_t ptiles = grouped_tiles(pr);
     for (int64_t t = blockIdx.x;; t += gridDim.x) {
         while (p < g.P && t >= pstart + ptiles) {
             pstart += ptiles;
             ++p;
             if (p < g.P) {
-                pr = grouped_prob(g, p);
+                pr = grouped_prob<DENSE>(g, p);
                 ptiles = grouped_tiles(pr);
             }
         }
@@ -1387,8 +1404,8 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             // through the wave's own LDS tile (the ring's stages already
             // take the next tile's DMA); the sym_dequant_moe zero correction
             // is epi_val's
-            const bool second = g.pair && (p & 1);
-            const int64_t ex = g.pair ? p >> 1 : p;
+            const bool second = !DENSE && g.pair && (p & 1);
+            const int64_t ex = DENSE ? 0 : g.pair ? p >> 1 : p;
             Epi e{};
             e.out = (second ? g.out2 : g.out) + pr.row0 * g.N;
             e.sa = g.sa + pr.row0;
@@ -1397,6 +1414,10 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             if (g.zr) {
                 e.zr = g.zr + pr.row0;
                 e.ws = (second ? g.ws2 : g.ws) + ex * g.N;
+            }
+            if constexpr (DENSE) {
+                e.bias = g.bias;
+                e.res = g.res;
             }
             store_block_lds32<32, FM, FN>(e, pr.m, pr.n, m0 + wm * (FM * 32),
                                           n0 + wn * (FN * 32), acc, lane,
@@ -1471,6 +1492,29 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         // enough 256 x 256 tiles to cover the 256 CUs
         const int64_t tiles = srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN);
         gemm_sq_kernel<128, 2, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(a, b, M, N, K, e);
+    } else if (M < 1024 && !e.C && srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN) >= 192 &&
+               srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) < 512) {
+        // mid-size M with enough 128 x 128 tiles to fill the CUs: the grouped
+        // kernel's dense form (64 x 64 32x32-MFMA tiles per compute wave,
+        // MFMA-bound where the ring kernel's small tiles are bound by the
+        // nibble unpacking: 188 -> 113 us at M = 512, N = 8192, K = 28672)
+        GroupedArgs g{};
+        g.P = 1;
+        g.M = M;
+        g.A = a;
+        g.B = b;
+        g.N = N;
+        g.K = K;
+        g.sa = e.sa;
+        g.sb = e.sb;
+        g.out = e.out;
+        g.bias = e.bias;
+        g.res = e.res;
+        g.zr = e.zr;
+        g.ws = e.ws;
+        const int64_t tiles = srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN);
+        gemm_grouped_kernel<4, UA, true>
+            <<<dim3((unsigned)std::min<int64_t>(tiles, kGroupedGrid)), dim3(512), 0, st>>>(g);
     } else if (M >= 1024 || srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) >= 512) {
         const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
         // 4 compute waves (128 x 64 each) + 4 producer waves (8 compute
@@ -1582,9 +1626,6 @@ extern "C" int srq_w4a4_linear_residual(const void *A, const void *a_scale, cons
     e.res = (const f16 *)residual;
     return run_gemm("w4a4_linear_residual", A, B, M, N, K, e, (hipStream_t)stream);
 }
-
-// Persistent grid of the grouped kernel: one workgroup per CU (256 CUs).
-static constexpr int kGroupedGrid = 256;
 
 extern "C" int srq_matmul_grouped(const int32_t *problem_sizes, const int64_t *ptr_A,
                                   const int64_t *ptr_B, const int64_t *ptr_C,

@@ -134,7 +134,7 @@ def test_matmul_ui4_si4_extremes(C):
 
 @pytest.mark.parametrize("M,N,K,bias", [(1, 4096, 4096, False), (32, 4096, 14336, True),
                                         (130, 512, 2048, False), (2048, 4096, 2048, True),
-                                        (4096, 4096, 512, False)])
+                                        (4096, 4096, 512, False), (300, 8192, 1024, True)])
 def test_w4a4_linear_asym(C, M, N, K, bias):
     rng = np.random.default_rng(M + N + K)
     x = outlier_input(rng, M, K, mag=30.0) + np.float16(0.5)

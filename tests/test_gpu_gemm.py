@@ -69,7 +69,11 @@ def test_matmul_extreme_values(C):
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 4096, 4096), (33, 300, 768),
                                    (128, 4096, 14336), (2048, 4096, 14336), (7, 5, 64),
                                    (32, 6144, 4096), (32, 28672, 4096), (32, 4096, 14336),
-                                   (13, 4100, 8192), (4096, 4096, 2048)])
+                                   (13, 4100, 8192), (4096, 4096, 2048),
+                                   # mid-size M with >= 192 tiles of 128 x 128: the
+                                   # grouped kernel's dense form (ragged M and N,
+                                   # N not a multiple of 8)
+                                   (300, 8192, 1024), (700, 4100, 2048), (129, 28672, 512)])
 @pytest.mark.parametrize("bias", [False, True])
 def test_w4a4_linear_bitexact(C, M, N, K, bias):
     rng = np.random.default_rng(M + N + K + bias)
@@ -86,6 +90,27 @@ def test_w4a4_linear_bitexact(C, M, N, K, bias):
     if bias:
         unf = unf + to_dev(bs)
     assert torch.equal(out, unf)
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 8192, 1024), (700, 4104, 512)])
+def test_w4a4_linear_residual_dense_grouped(C, M, N, K):
+    """The residual (and bias) epilogue of the grouped kernel's dense form:
+    linear + residual equals the oracle-checked linear plus the residual in
+    fp16, in place too."""
+    rng = np.random.default_rng(M + N)
+    a, b = _rand_packed(rng, M, K), _rand_packed(rng, N, K)
+    sa = to_dev((np.abs(rng.standard_normal(M)) * 0.05 + 1e-3).astype(np.float16))
+    sb = to_dev((np.abs(rng.standard_normal(N)) * 0.01 + 1e-4).astype(np.float16))
+    bs = to_dev((rng.standard_normal(N) * 0.5).astype(np.float16))
+    res = to_dev((rng.standard_normal((M, N)) * 3.0).astype(np.float16))
+    da, db = to_dev(a), to_dev(b)
+    for bias in (None, bs):
+        out = C.w4a4_linear_residual(da, sa, db, sb, res, bias=bias)
+        want = C.w4a4_linear(da, sa, db, sb, bias) + res
+        assert torch.equal(out, want)
+    inplace = res.clone()
+    C.w4a4_linear_residual(da, sa, db, sb, inplace, out=inplace)
+    assert torch.equal(inplace, C.w4a4_linear(da, sa, db, sb) + res)
 
 
 def test_matmul_rejects_bad_k(C):
