@@ -85,6 +85,26 @@ int srq_w4a4_linear(const void *A, const void *a_scale, const void *B,
                     const void *b_scale, const void *bias, int64_t M, int64_t N,
                     int64_t K, void *out, void *stream);
 
+/* Workspace form of srq_w4a4_linear (and of srq_w4a4_linear_residual
+ * below, with residual): bit-identical outputs.  For mid-size M (65 ..
+ * 1023) whose 128 x 128 output tiles are too few to fill the GPU, the
+ * product is split over K into int32 partials in `workspace` (device
+ * memory, srq_w4a4_linear_ws_bytes(M, N, K) bytes, 0 when the shape is not
+ * split) and summed by a second pass before the epilogue; with a smaller
+ * workspace the call runs as srq_w4a4_linear.  No counterpart in the
+ * reference (whose GEMM takes no workspace); for callers that can hand
+ * over scratch memory, such as the PyTorch layer, which takes it from its
+ * caching allocator.  Calls sharing one workspace must not overlap. */
+int64_t srq_w4a4_linear_ws_bytes(int64_t M, int64_t N, int64_t K);
+int srq_w4a4_linear_ws(const void *A, const void *a_scale, const void *B,
+                       const void *b_scale, const void *bias, int64_t M, int64_t N,
+                       int64_t K, void *out, void *workspace, int64_t ws_bytes,
+                       void *stream);
+int srq_w4a4_linear_residual_ws(const void *A, const void *a_scale, const void *B,
+                                const void *b_scale, const void *bias, const void *residual,
+                                int64_t M, int64_t N, int64_t K, void *out, void *workspace,
+                                int64_t ws_bytes, void *stream);
+
 /* int4 GEMM with unsigned A: C i32 [M, N] = A · Bᵀ, A u8 [M, K/2] of uint4
  * codes (0..15, the asymmetric activation quantizer's), B u8 [N, K/2] of
  * two's-complement int4; same shape rules as srq_matmul_s4s4.

@@ -23,6 +23,8 @@ Added ops (no reference counterpart, fused forms of reference chains):
   qkv_rope_had_append   = rope_qk + K/q Hadamard + kv_quant_pack + append_kv_i4
                                                               kv_cache.py:144-170, 295-415
 """
+import functools
+
 import torch
 
 from . import _native
@@ -127,9 +129,27 @@ def w4a4_linear(A, a_scale, B, b_scale, bias=None):
     if bias is not None and bias.numel() != N:
         raise RuntimeError("w4a4_linear: bias must have N elements")
     out = torch.empty((M, N), dtype=torch.float16, device=A.device)
-    _call("srq_w4a4_linear", _ptr(A), _ptr(a_scale), _ptr(B), _ptr(b_scale), _ptr(bias),
-          M, N, K, _ptr(out), _stream(A))
+    ws = _splitk_workspace(M, N, K, A.device)
+    if ws is None:
+        _call("srq_w4a4_linear", _ptr(A), _ptr(a_scale), _ptr(B), _ptr(b_scale), _ptr(bias),
+              M, N, K, _ptr(out), _stream(A))
+    else:
+        _call("srq_w4a4_linear_ws", _ptr(A), _ptr(a_scale), _ptr(B), _ptr(b_scale), _ptr(bias),
+              M, N, K, _ptr(out), _ptr(ws), ws.numel(), _stream(A))
     return out
+
+
+@functools.lru_cache(maxsize=512)
+def _splitk_bytes(M, N, K):
+    return int(_native.lib().srq_w4a4_linear_ws_bytes(M, N, K))
+
+
+def _splitk_workspace(M, N, K, device):
+    """The int32 split-K partials' workspace the library asks for at this
+    shape (mid-size M with too few output tiles to fill the GPU), from
+    torch's caching allocator (graph-capture safe), or None."""
+    n = _splitk_bytes(M, N, K)
+    return torch.empty(n, dtype=torch.uint8, device=device) if n else None
 
 
 # ------------------------------------------------------------- bf6 GEMM
@@ -225,8 +245,14 @@ def w4a4_linear_residual(A, a_scale, B, b_scale, residual, bias=None, out=None):
         out = torch.empty((M, N), dtype=torch.float16, device=A.device)
     elif out.numel() != M * N:
         raise RuntimeError(f"w4a4_linear_residual: out must have {M} x {N} elements")
-    _call("srq_w4a4_linear_residual", _ptr(A), _ptr(a_scale), _ptr(B), _ptr(b_scale), _ptr(bias),
-          _ptr(residual), M, N, K, _ptr(out), _stream(A))
+    ws = _splitk_workspace(M, N, K, A.device)
+    if ws is None:
+        _call("srq_w4a4_linear_residual", _ptr(A), _ptr(a_scale), _ptr(B), _ptr(b_scale),
+              _ptr(bias), _ptr(residual), M, N, K, _ptr(out), _stream(A))
+    else:
+        _call("srq_w4a4_linear_residual_ws", _ptr(A), _ptr(a_scale), _ptr(B), _ptr(b_scale),
+              _ptr(bias), _ptr(residual), M, N, K, _ptr(out), _ptr(ws), ws.numel(),
+              _stream(A))
     return out
 
 

@@ -23,6 +23,9 @@ SIGNATURES = {
     "srq_matmul_s4s4": [_p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_residual": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
+    "srq_w4a4_linear_ws": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _p],
+    "srq_w4a4_linear_residual_ws": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64,
+                                    _p],
     "srq_matmul_u4s4": [_p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_asym": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_moe_asym": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
@@ -92,6 +95,8 @@ def lib():
         handle.srq_abi_version.argtypes = []
         handle.srq_bf6_bytes.restype = ctypes.c_int64
         handle.srq_bf6_bytes.argtypes = [_i64, _i64]
+        handle.srq_w4a4_linear_ws_bytes.restype = ctypes.c_int64
+        handle.srq_w4a4_linear_ws_bytes.argtypes = [_i64, _i64, _i64]
         for name, args in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.argtypes = args

@@ -1237,7 +1237,14 @@ struct GroupedArgs {
     // residual [M, N] (either may be null)
     int64_t M;
     const f16 *bias, *res;
+    // split-K form (the SPLITK instantiation): problem p is the dense
+    // product over K codes [p Kc, min((p + 1) Kc, K)), its int32 partial
+    // (shifted down like the dense accumulator) at ws_c + p M N
+    int64_t Kc;
+    int32_t *ws_c;
 };
+
+constexpr int kFormGeneral = 0, kFormDense = 1, kFormSplitK = 2;
 
 struct GroupedProb {
     const uint8_t *a, *b;
@@ -1250,10 +1257,23 @@ SRQ_DEV int64_t uni(int64_t v) {
                      (uint32_t)__builtin_amdgcn_readfirstlane((int)v));
 }
 
-template <bool DENSE>
+template <int FORM>
 SRQ_DEV GroupedProb grouped_prob(const GroupedArgs &g, int p) {
     GroupedProb r;
-    if constexpr (DENSE) {
+    if constexpr (FORM == kFormSplitK) {
+        const int64_t kc0 = (int64_t)p * g.Kc;
+        r.row0 = 0;
+        r.m = g.M;
+        r.n = g.N;
+        r.k = g.K - kc0 < g.Kc ? g.K - kc0 : g.Kc;
+        r.lda_b = r.ldb_b = g.K / 2;
+        r.a = g.A + kc0 / 2;
+        r.b = g.B + kc0 / 2;
+        r.c = g.ws_c + (int64_t)p * g.M * g.N;
+        r.ldc = g.N;
+        return r;
+    }
+    if constexpr (FORM == kFormDense) {
         r.row0 = 0;
         r.m = g.M;
         r.n = g.N;
@@ -1296,7 +1316,7 @@ SRQ_DEV int64_t grouped_tiles(const GroupedProb &r) {
     return ((r.m + kGrpBM - 1) / kGrpBM) * ((r.n + kGrpBN - 1) / kGrpBN);
 }
 
-template <int NPROD, bool UA, bool DENSE = false, int NSTG = kGrpStages>
+template <int NPROD, bool UA, int FORM = kFormGeneral, int NSTG = kGrpStages>
 __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(GroupedArgs g) {
     constexpr int WGN = 2, FM = 2, FN = 2, KBB = kGrpKBB;
     static_assert(KBB == 128, "stage layout validated for 128-byte steps only");
@@ -1322,14 +1342,14 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
 
     int p = 0;
     int64_t pstart = 0;
-    GroupedProb pr = grouped_prob<DENSE>(g, 0);
+    GroupedProb pr = grouped_prob<FORM>(g, 0);
     int64_t ptiles = grouped_tiles(pr);
     for (int64_t t = blockIdx.x;; t += gridDim.x) {
         while (p < g.P && t >= pstart + ptiles) {
             pstart += ptiles;
             ++p;
             if (p < g.P) {
-                pr = grouped_prob<DENSE>(g, p);
+                pr = grouped_prob<FORM>(g, p);
                 ptiles = grouped_tiles(pr);
             }
         }
@@ -1404,6 +1424,7 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             // through the wave's own LDS tile (the ring's stages already
             // take the next tile's DMA); the sym_dequant_moe zero correction
             // is epi_val's
+            constexpr bool DENSE = FORM == kFormDense;
             const bool second = !DENSE && g.pair && (p & 1);
             const int64_t ex = DENSE ? 0 : g.pair ? p >> 1 : p;
             Epi e{};
@@ -1470,10 +1491,70 @@ __global__ void fill_zero_epilogue(int64_t M, int64_t N, Epi e) {
         store_one(e, N, i / N, i % N, 0);
 }
 
-// Kernel choice by shape; UA: A holds unsigned nibbles (Epi::ua).
+// Split-K epilogue: out (m, n) from the sum of the S int32 partials, each
+// shifted down like the dense accumulator (exact: every product is a
+// multiple of the shift), scaled back up so store_one's arithmetic is the
+// dense path's (|sum a w| <= 64 K: the shifted-up value fits in int32).
+// Four consecutive outputs per thread (16-byte partial loads; M N % 4 == 0
+// is the caller's condition, else one per thread).
+template <int V>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t *__restrict__ ws,
+                                                            int S, int64_t M, int64_t N,
+                                                            Epi e) {
+    const int64_t MN = M * N;
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V; i < MN;
+         i += (int64_t)gridDim.x * 256 * V) {
+        int acc[V] = {};
+        for (int s = 0; s < S; ++s) {
+            if constexpr (V == 4) {
+                const v4i p = *reinterpret_cast<const v4i *>(ws + s * MN + i);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) acc[k] += p[k];
+            } else {
+                acc[0] += ws[s * MN + i];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < V; ++k)
+            store_one(e, N, (i + k) / N, (i + k) % N, (int)((u32)acc[k] << (e.ua ? 4 : 8)));
+    }
+}
+
+// Split-K plan for mid-size M whose 128 x 128 tiles cannot fill the CUs:
+// S K-chunks of Kc codes (a multiple of 256) so that tiles * S ~ 256, each
+// chunk at least 7 K steps and tiles * S >= 128 (shorter chunks or fewer
+// workgroups lose to the ring kernel: M = 128, N = 4096, K = 4096 took 19
+// us split 4 ways against 10.5 unsplit; K = 14336 split 8 ways: 24 against
+// 28).  S = 0: no split.
+struct SplitK {
+    int S = 0;
+    int64_t Kc = 0;
+};
+SplitK splitk_plan(int64_t M, int64_t N, int64_t K, bool fp16_out) {
+    SplitK p;
+    if (!fp16_out || M <= 64 || M >= 1024 || K < 2048) return p;
+    const int64_t tiles = srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN);
+    if (tiles >= 192 || srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) >= 512) return p;
+    int64_t S = std::min<int64_t>(256 / tiles, K / 1792);
+    if (S < 2 || tiles * S < 128) return p;
+    const int64_t Kc = srq_cdiv(srq_cdiv(K, S), 256) * 256;
+    p.S = (int)srq_cdiv(K, Kc);
+    p.Kc = Kc;
+    if (p.S < 2) p.S = 0;
+    return p;
+}
+int64_t splitk_bytes(int64_t M, int64_t N, int64_t K, bool fp16_out) {
+    const SplitK p = splitk_plan(M, N, K, fp16_out);
+    return p.S ? (int64_t)p.S * M * N * 4 : 0;
+}
+
+// Kernel choice by shape; UA: A holds unsigned nibbles (Epi::ua).  With a
+// workspace of at least splitk_bytes, mid-size M shapes with few tiles run
+// split over K.
 template <bool UA>
 void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64_t K,
-                 const Epi &e, hipStream_t st) {
+                 const Epi &e, hipStream_t st, void *ws = nullptr, int64_t ws_bytes = 0) {
+    const SplitK sk = ws ? splitk_plan(M, N, K, !e.C) : SplitK{};
     if (K == 0) {
         const int64_t blocks = std::min<int64_t>(srq_cdiv(M * N, 256), 4096);
         fill_zero_epilogue<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(M, N, e);
@@ -1492,6 +1573,30 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         // enough 256 x 256 tiles to cover the 256 CUs
         const int64_t tiles = srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN);
         gemm_sq_kernel<128, 2, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(a, b, M, N, K, e);
+    } else if (sk.S && ws_bytes >= (int64_t)sk.S * M * N * 4) {
+        // split-K: S dense problems over K-chunks write int32 partials,
+        // then one pass sums them and runs the epilogue
+        GroupedArgs g{};
+        g.P = sk.S;
+        g.M = M;
+        g.A = a;
+        g.B = b;
+        g.N = N;
+        g.K = K;
+        g.Kc = sk.Kc;
+        g.ws_c = (int32_t *)ws;
+        const int64_t tiles = srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN) * sk.S;
+        gemm_grouped_kernel<4, UA, kFormSplitK>
+            <<<dim3((unsigned)std::min<int64_t>(tiles, kGroupedGrid)), dim3(512), 0, st>>>(g);
+        if ((M * N) % 4 == 0) {
+            const int64_t blocks = std::min<int64_t>(srq_cdiv(M * N / 4, 256), 2048);
+            splitk_reduce_kernel<4><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+                (const int32_t *)ws, sk.S, M, N, e);
+        } else {
+            const int64_t blocks = std::min<int64_t>(srq_cdiv(M * N, 256), 2048);
+            splitk_reduce_kernel<1><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+                (const int32_t *)ws, sk.S, M, N, e);
+        }
     } else if (M < 1024 && !e.C && srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN) >= 192 &&
                srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) < 512) {
         // mid-size M with enough 128 x 128 tiles to fill the CUs: the grouped
@@ -1513,7 +1618,7 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         g.zr = e.zr;
         g.ws = e.ws;
         const int64_t tiles = srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN);
-        gemm_grouped_kernel<4, UA, true>
+        gemm_grouped_kernel<4, UA, kFormDense>
             <<<dim3((unsigned)std::min<int64_t>(tiles, kGroupedGrid)), dim3(512), 0, st>>>(g);
     } else if (M >= 1024 || srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) >= 512) {
         const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
@@ -1542,12 +1647,12 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
 }
 
 int run_gemm(const char *name, const void *A, const void *B, int64_t M, int64_t N, int64_t K,
-             const Epi &e, hipStream_t st) {
+             const Epi &e, hipStream_t st, void *ws = nullptr, int64_t ws_bytes = 0) {
     if (M == 0 || N == 0) return SRQ_OK;
     const uint8_t *a = (const uint8_t *)A;
     const uint8_t *b = (const uint8_t *)B;
-    if (e.ua) launch_gemm<true>(a, b, M, N, K, e, st);
-    else launch_gemm<false>(a, b, M, N, K, e, st);
+    if (e.ua) launch_gemm<true>(a, b, M, N, K, e, st, ws, ws_bytes);
+    else launch_gemm<false>(a, b, M, N, K, e, st, ws, ws_bytes);
     SRQ_LAUNCH_CHECK(name);
     return SRQ_OK;
 }
@@ -1607,6 +1712,51 @@ extern "C" int srq_w4a4_linear(const void *A, const void *a_scale, const void *B
     e.sb = (const f16 *)b_scale;
     e.bias = (const f16 *)bias;
     return run_gemm("w4a4_linear", A, B, M, N, K, e, (hipStream_t)stream);
+}
+
+extern "C" int64_t srq_w4a4_linear_ws_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    return splitk_bytes(M, N, K, true);
+}
+
+extern "C" int srq_w4a4_linear_ws(const void *A, const void *a_scale, const void *B,
+                                  const void *b_scale, const void *bias, int64_t M, int64_t N,
+                                  int64_t K, void *out, void *workspace, int64_t ws_bytes,
+                                  void *stream) {
+    int rc = check_gemm("w4a4_linear_ws", A, B, M, N, K);
+    if (rc) return rc;
+    if (M && N) SRQ_CHECK_ARG(out && a_scale && b_scale, "w4a4_linear_ws: null pointer");
+    SRQ_CHECK_ARG(ws_bytes >= 0 && (ws_bytes == 0 || workspace),
+                  "w4a4_linear_ws: null workspace");
+    Epi e{};
+    e.out = (f16 *)out;
+    e.sa = (const f16 *)a_scale;
+    e.sb = (const f16 *)b_scale;
+    e.bias = (const f16 *)bias;
+    return run_gemm("w4a4_linear_ws", A, B, M, N, K, e, (hipStream_t)stream, workspace,
+                    ws_bytes);
+}
+
+extern "C" int srq_w4a4_linear_residual_ws(const void *A, const void *a_scale, const void *B,
+                                           const void *b_scale, const void *bias,
+                                           const void *residual, int64_t M, int64_t N,
+                                           int64_t K, void *out, void *workspace,
+                                           int64_t ws_bytes, void *stream) {
+    int rc = check_gemm("w4a4_linear_residual_ws", A, B, M, N, K);
+    if (rc) return rc;
+    if (M && N)
+        SRQ_CHECK_ARG(out && a_scale && b_scale && residual,
+                      "w4a4_linear_residual_ws: null pointer");
+    SRQ_CHECK_ARG(ws_bytes >= 0 && (ws_bytes == 0 || workspace),
+                  "w4a4_linear_residual_ws: null workspace");
+    Epi e{};
+    e.out = (f16 *)out;
+    e.sa = (const f16 *)a_scale;
+    e.sb = (const f16 *)b_scale;
+    e.bias = (const f16 *)bias;
+    e.res = (const f16 *)residual;
+    return run_gemm("w4a4_linear_residual_ws", A, B, M, N, K, e, (hipStream_t)stream,
+                    workspace, ws_bytes);
 }
 
 extern "C" int srq_w4a4_linear_residual(const void *A, const void *a_scale, const void *B,

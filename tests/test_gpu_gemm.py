@@ -113,6 +113,45 @@ def test_w4a4_linear_residual_dense_grouped(C, M, N, K):
     assert torch.equal(inplace, C.w4a4_linear(da, sa, db, sb) + res)
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 4096, 14336), (128, 14336, 4096), (200, 4100, 8192),
+                                   (100, 14336, 4640), (512, 4096, 14336), (65, 1032, 28672),
+                                   (99, 1001, 28672)])
+def test_w4a4_linear_split_k(C, M, N, K):
+    """Mid-size M with few output tiles: the workspace entry points split K
+    into int32 partials; the result is bit for bit the plain entry point's
+    (itself pinned against the oracle above), with bias and residual, in
+    place too; a K tail chunk (K = 4640: chunks of 2560 and 2080), M N not
+    a multiple of 4 (99 x 1001: the one-output reduce)."""
+    from signrot_amd import _native
+    rng = np.random.default_rng(M * 7 + N + K)
+    a, b = to_dev(_rand_packed(rng, M, K)), to_dev(_rand_packed(rng, N, K))
+    sa = to_dev((np.abs(rng.standard_normal(M)) * 0.05 + 1e-3).astype(np.float16))
+    sb = to_dev((np.abs(rng.standard_normal(N)) * 0.01 + 1e-4).astype(np.float16))
+    bs = to_dev((rng.standard_normal(N) * 0.5).astype(np.float16))
+    res = to_dev((rng.standard_normal((M, N)) * 3.0).astype(np.float16))
+    nbytes = int(_native.lib().srq_w4a4_linear_ws_bytes(M, N, K))
+    assert nbytes > 0, "shape expected to split"
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    p = lambda t: 0 if t is None else t.data_ptr()
+    for bias in (None, bs):
+        plain = torch.empty(M, N, dtype=torch.float16, device="cuda")
+        split = torch.empty_like(plain)
+        _native.call("srq_w4a4_linear", p(a), p(sa), p(b), p(sb), p(bias), M, N, K, p(plain), st)
+        _native.call("srq_w4a4_linear_ws", p(a), p(sa), p(b), p(sb), p(bias), M, N, K, p(split),
+                     p(ws), nbytes, st)
+        assert torch.equal(plain, split)
+        plain_r = torch.empty_like(plain)
+        _native.call("srq_w4a4_linear_residual", p(a), p(sa), p(b), p(sb), p(bias), p(res), M, N,
+                     K, p(plain_r), st)
+        inplace = res.clone()
+        _native.call("srq_w4a4_linear_residual_ws", p(a), p(sa), p(b), p(sb), p(bias),
+                     p(inplace), M, N, K, p(inplace), p(ws), nbytes, st)
+        assert torch.equal(plain_r, inplace)
+    # the torch wrapper takes the split path and equals the oracle-checked one
+    assert torch.equal(C.w4a4_linear(a, sa, b, sb, bs), split)
+
+
 def test_matmul_rejects_bad_k(C):
     a = torch.zeros(4, 8, dtype=torch.uint8, device="cuda")  # K = 16
     with pytest.raises(RuntimeError):
