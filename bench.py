@@ -250,6 +250,10 @@ def bench_qlinear(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9, reps=2
     sb = [torch.empty(M, dtype=torch.float16, device=dev) for _ in range(len(xs))]
     ob = [torch.empty(M, N, dtype=torch.float16, device=dev) for _ in range(len(xs))]
     hp = hadk.data_ptr() if hadk is not None else None
+    # the split-K workspace the library asks for at this shape (0: none),
+    # allocated once, outside the timed loops
+    ws_bytes = int(_native.lib().srq_w4a4_linear_ws_bytes(M, N, K))
+    wsp = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
 
     def had(i):
         j = i % len(xs)
@@ -258,9 +262,9 @@ def bench_qlinear(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9, reps=2
 
     def gemm(i):
         j = i % len(xs)
-        _native.call("srq_w4a4_linear", qb[j].data_ptr(), sb[j].data_ptr(),
+        _native.call("srq_w4a4_linear_ws", qb[j].data_ptr(), sb[j].data_ptr(),
                      ws[i % nsets].data_ptr(), wsc.data_ptr(), None, M, N, K, ob[j].data_ptr(),
-                     st.cuda_stream)
+                     wsp.data_ptr(), ws_bytes, st.cuda_stream)
 
     def both(i):
         had(i)
@@ -275,7 +279,8 @@ def bench_qlinear(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9, reps=2
            "qlinear": _roof(t_all, ops, M * K * 2 + N * K // 2 + M * N * 2 + M * 2 + N * 2),
            "had_sign_quant": _roof(t_had, 0.0, M * K * 2 + M * K // 2 + M * 2),
            "w4a4_linear": _roof(t_gemm, ops, M * K // 2 + N * K // 2 + M * N * 2 + M * 2 + N * 2)}
-    del xs, ws, qb, sb, ob
+    res["gemm_kernel"] = gemm_kernel_name(M, N, K, ws_bytes > 0)
+    del xs, ws, qb, sb, ob, wsp
     torch.cuda.empty_cache()
     return res
 
@@ -484,17 +489,24 @@ def traffic_commit():
         return None
 
 
-def gemm_kernel_name(M, N):
-    """Kernel srq_w4a4_linear launches for M x N outputs (gemm.hip dispatch)."""
+def gemm_kernel_name(M, N, K=None, split=False):
+    """Kernel srq_w4a4_linear(_ws) launches for M x N outputs (gemm.hip
+    dispatch, fp16 output)."""
+    def cdiv(a, b):
+        return -(-a // b)
     if M <= 32:
         return "gemm_stream_kernel (srq_w4a4_linear)"
     if M <= 64:
         return "gemm_skinny_kernel (srq_w4a4_linear)"
-    if M >= 1024:
-        if -(-M // 256) * -(-N // 256) >= 256:
-            return "gemm_sq_kernel (srq_w4a4_linear, 256 x 256 tiles)"
+    if M >= 1024 and cdiv(M, 256) * cdiv(N, 256) >= 256:
+        return "gemm_sq_kernel (srq_w4a4_linear, 256 x 256 tiles)"
+    if split:
+        return "gemm_grouped_kernel split-K form + splitk_reduce_kernel (srq_w4a4_linear_ws)"
+    if M < 1024 and cdiv(M, 128) * cdiv(N, 128) >= 192 and cdiv(M, 256) * cdiv(N, 128) < 512:
+        return "gemm_grouped_kernel dense form (srq_w4a4_linear, 128 x 128 tiles)"
+    if M >= 1024 or cdiv(M, 256) * cdiv(N, 128) >= 512:
         return "gemm_big_kernel (srq_w4a4_linear, 256 x 128 tiles)"
-    return "gemm_tile_kernel (srq_w4a4_linear)"
+    return "gemm_ring_kernel (srq_w4a4_linear)"
 
 
 def calibrate_copy(dev, reps=3):
