@@ -961,10 +961,11 @@ __global__ __launch_bounds__(KW * 64) void gemm_skinny_kernel(const uint8_t *__r
 //   16-lane quarter-wave fetches two whole 128-byte lines; lane p of a row
 //   fetches logical 16-byte chunk p ^ (row & 7), which makes the MFMA-layout
 //   reads (lane l: row l & 15, chunk 4t + (l >> 4)) bank-conflict-free.
-// * Per column block, each wave's partial sums go into an LDS int32 buffer
-//   with integer atomic adds (exact and order-independent), then one barrier,
-//   then wave (j mod KW) reads, clears and stores the block.  The buffer is
-//   double-buffered on j, so one barrier per block suffices.
+// * Per column block, each wave's partial sums go into that block's LDS
+//   int32 buffer with integer atomic adds (exact and order-independent) and
+//   the wave moves on: no barrier inside the stream (a barrier per block cost
+//   a third of the time at decode shapes).  After the last block, one
+//   barrier, then wave w dequantizes and stores blocks w, w + KW, ...
 constexpr int kStreamKW = 8;
 constexpr int kStreamS = 4;
 constexpr int kStreamMaxCb = 16;   // column blocks per workgroup
@@ -975,7 +976,7 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
     int64_t K, Epi e) {
     constexpr int KW = kStreamKW, S = kStreamS;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[KW * S * 2048];
-    __shared__ int sum[2][MB * 256];
+    __shared__ int sum[kStreamMaxCb][MB * 256];
     __shared__ float sbl[kStreamMaxCb * 16];
     __shared__ float sal[MB * 16];
     const int lane = threadIdx.x & 63;
@@ -990,13 +991,30 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
     const int ncb_mine = (ncb - (int)blockIdx.x + G - 1) / G;
     const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
 
-    for (int t = threadIdx.x; t < 2 * MB * 256; t += KW * 64) (&sum[0][0])[t] = 0;
+    for (int t = threadIdx.x; t < ncb_mine * MB * 256; t += KW * 64) (&sum[0][0])[t] = 0;
     if (!e.C) {
         for (int t = threadIdx.x; t < MB * 16; t += KW * 64) sal[t] = t < M ? (float)e.sa[t] : 0.f;
         for (int t = threadIdx.x; t < ncb_mine * 16; t += KW * 64) {
             const int64_t n = (int64_t)(blockIdx.x + (t >> 4) * G) * 16 + (t & 15);
             sbl[t] = n < N ? (float)e.sb[n] : 0.f;
         }
+    }
+
+    // The residual (and bias) of the first column block this wave stores
+    // (j = wave), fetched now so the epilogue after the stream does not wait
+    // a memory round trip for them.
+    const int rr = lane & 15;
+    f16 res0[MB][4], bias0 = (f16)0;
+    if (!e.C && wave < ncb_mine) {
+        const int64_t gn = (int64_t)(blockIdx.x + wave * G) * 16 + rr;
+        if (e.bias && gn < N) bias0 = e.bias[gn];
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = i * 16 + 4 * (lane >> 4) + r;
+                res0[i][r] = (e.res && m < M && gn < N) ? e.res[m * N + gn] : (f16)0;
+            }
     }
 
     // A: unit s of this wave, row block i, chunk pair t; lane holds row
@@ -1081,7 +1099,6 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
 #pragma unroll
     for (int it = 0; it < S - 1; ++it) issue(it);
 
-    const int rr = lane & 15;
     for (int j = 0; j < ncb_mine; ++j) {
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
@@ -1115,8 +1132,8 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
                 }
             }
         }
-        int *sm = sum[j & 1];
         if (nsub > 0) {
+            int *sm = sum[j];
 #pragma unroll
             for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -1126,31 +1143,32 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
         }
 #pragma unroll
         for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
-        __syncthreads();
-        if (wave == j % KW) {
-            const int64_t gn = (int64_t)(blockIdx.x + j * G) * 16 + rr;
-            const float sbv = e.C ? 0.f : sbl[j * 16 + rr];
+    }
+    __syncthreads();
+    for (int j = wave; j < ncb_mine; j += KW) {
+        const int *sm = sum[j];
+        const int64_t gn = (int64_t)(blockIdx.x + j * G) * 16 + rr;
+        const float sbv = e.C ? 0.f : sbl[j * 16 + rr];
 #pragma unroll
-            for (int i = 0; i < MB; ++i)
+        for (int i = 0; i < MB; ++i)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int m = i * 16 + 4 * (lane >> 4) + r;
-                    const int idx = i * 256 + (4 * (lane >> 4) + r) * 16 + rr;
-                    const int raw = sm[idx];
-                    sm[idx] = 0;
-                    if (m < M && gn < N) {
-                        const int v = epi_val(e, raw, m, gn);
-                        if (e.C) {
-                            e.C[m * N + gn] = v;
-                        } else {
-                            f16 o = f16_rn(((float)v * sal[m]) * sbv);
-                            if (e.bias) o = f16_rn((float)o + (float)e.bias[gn]);
-                            if (e.res) o = f16_rn((float)o + (float)e.res[m * N + gn]);
-                            e.out[m * N + gn] = o;
-                        }
+            for (int r = 0; r < 4; ++r) {
+                const int m = i * 16 + 4 * (lane >> 4) + r;
+                const int raw = sm[i * 256 + (4 * (lane >> 4) + r) * 16 + rr];
+                if (m < M && gn < N) {
+                    const int v = epi_val(e, raw, m, gn);
+                    if (e.C) {
+                        e.C[m * N + gn] = v;
+                    } else {
+                        const bool first = j == wave;
+                        f16 o = f16_rn(((float)v * sal[m]) * sbv);
+                        if (e.bias) o = f16_rn((float)o + (float)(first ? bias0 : e.bias[gn]));
+                        if (e.res)
+                            o = f16_rn((float)o + (float)(first ? res0[i][r] : e.res[m * N + gn]));
+                        e.out[m * N + gn] = o;
                     }
                 }
-        }
+            }
     }
 }
 

@@ -14,9 +14,13 @@
 //     order;
 //   * renormalization: p_j / (p_0 + p_1 + ... ) summed in order;
 //   * weights: fp16 round of the fp32 values.
-// The sort is a counting sort: per-expert counts, offsets = their
-// exclusive sum, and each row's rank among the earlier rows of its expert
-// from wave ballots (no atomics on global memory: deterministic).
+// The sort is a counting sort in one block: thread i owns a contiguous run
+// of tokens (so its rows t * k + j are contiguous and increasing), counts
+// its rows per expert into an LDS histogram laid out [expert][thread], and
+// one exclusive scan of that histogram gives every (expert, thread) its
+// first output position -- the expert offsets are the column-0 entries.
+// Each thread then places its rows in order: stable, no atomics on global
+// memory, deterministic.
 //
 // moe_combine: out[t, :] = fp16(sum_j fp32(fp16(y[inv[t k + j], :] *
 // w[t, j]))), j in order from 0: the fp16 product and the fp32 sum of
@@ -25,74 +29,70 @@
 
 namespace {
 
-constexpr int kRouteThreads = 256;  // one wave per SIMD: the per-token arrays fit in VGPRs
 constexpr int kRouteMaxE = 64;
 constexpr int kRouteMaxK = 8;
+constexpr int kRouteHistInts = 16384;  // at most EP * THREADS: 64 KB of LDS
 
-SRQ_DEV int pow2_ceil(int n) {
-    int p = 1;
-    while (p < n) p <<= 1;
-    return p;
-}
-
-__global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
+// EP: the expert count rounded up to 8, 16, 32 or 64 (register arrays of
+// that size); EP * THREADS <= kRouteHistInts.
+template <int EP, int THREADS>
+__global__ __launch_bounds__(THREADS) void moe_route_kernel(
     const f16 *__restrict__ logits, int T, int E, int K, int norm, f16 *__restrict__ weights,
     int32_t *__restrict__ choice, int32_t *__restrict__ order, int32_t *__restrict__ inv,
     int32_t *__restrict__ eid, int32_t *__restrict__ tok, int32_t *__restrict__ counts,
     int32_t *__restrict__ offsets) {
-    constexpr int kWaves = kRouteThreads / 64;
-    __shared__ int s_count[kRouteMaxE];
-    __shared__ int s_base[kRouteMaxE];      // rows of expert e placed so far
-    __shared__ int s_wave[kWaves][kRouteMaxE];
+    static_assert(EP * THREADS <= kRouteHistInts, "histogram size");
+    constexpr int kWaves = THREADS / 64;
+    __shared__ int s_hist[EP * THREADS];  // [expert][thread]
+    __shared__ int s_wtot[kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid < kRouteMaxE) s_count[tid] = 0;
-    // a wave that sees no row of an expert leaves its slot untouched, so
-    // every slot starts at zero (and is cleared again after each chunk)
-    for (int i = tid; i < kWaves * kRouteMaxE; i += kRouteThreads) (&s_wave[0][0])[i] = 0;
+    for (int i = tid; i < EP * THREADS; i += THREADS) s_hist[i] = 0;
     __syncthreads();
 
-    // ---- per token: softmax, top-k, weights
-    const int P = pow2_ceil(E);
-    for (int t = tid; t < T; t += kRouteThreads) {
-        float v[kRouteMaxE];
+    // ---- per token: softmax, top-k, weights; histogram of this thread's rows
+    const int per = (T + THREADS - 1) / THREADS;
+    const int t0 = min(T, tid * per), t1 = min(T, t0 + per);
+    int P = 1;
+    while (P < E) P <<= 1;
+    for (int t = t0; t < t1; ++t) {
+        float v[EP];
         float m = -__builtin_inff();
 #pragma unroll
-        for (int i = 0; i < kRouteMaxE; ++i) {
+        for (int i = 0; i < EP; ++i) {
             v[i] = i < E ? (float)logits[(int64_t)t * E + i] : -__builtin_inff();
-            if (i < E) m = v[i] > m ? v[i] : m;
+            m = v[i] > m ? v[i] : m;
         }
-        float s[kRouteMaxE];
+        float s[EP];
 #pragma unroll
-        for (int i = 0; i < kRouteMaxE; ++i) {
+        for (int i = 0; i < EP; ++i) {
             v[i] = i < E ? expf(v[i] - m) : 0.f;
             s[i] = v[i];
         }
-        // butterfly: after the level with offset o, s[i] = s[i] + s[i ^ o];
-        // lane 0's value is the sum every lane ends with
+        // butterfly over the P-padded row: after the level with offset o,
+        // s[i] = s[i] + s[i ^ o]; lane 0's value is the sum every lane ends with
 #pragma unroll
-        for (int o = kRouteMaxE / 2; o > 0; o >>= 1) {
+        for (int o = EP / 2; o > 0; o >>= 1) {
             if (o < P) {
 #pragma unroll
                 for (int i = 0; i < o; ++i) s[i] = s[i] + s[i + o];
             }
         }
         const float sum = s[0];
+#pragma unroll
+        for (int i = 0; i < EP; ++i) v[i] = v[i] / sum;  // the softmax output
         float pk[kRouteMaxK];
         int ek[kRouteMaxK];
-        unsigned long long taken = 0;
+        uint64_t taken = 0;
 #pragma unroll
         for (int j = 0; j < kRouteMaxK; ++j) {
             if (j >= K) break;
             float best = -1.f;
             int bi = 0;
 #pragma unroll
-            for (int i = 0; i < kRouteMaxE; ++i) {
-                if (i >= E || ((taken >> i) & 1)) continue;
-                const float p = v[i] / sum;
-                if (p > best) {  // strict: ties keep the lower expert
-                    best = p;
-                    bi = i;
-                }
+            for (int i = 0; i < EP; ++i) {
+                const bool ok = i < E && !((taken >> i) & 1) && v[i] > best;  // strict: ties keep the lower expert
+                best = ok ? v[i] : best;
+                bi = ok ? i : bi;
             }
             taken |= 1ull << bi;
             pk[j] = best;
@@ -110,62 +110,52 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_kernel(
             const float w = norm ? pk[j] / den : pk[j];
             weights[(int64_t)t * K + j] = (f16)w;
             choice[(int64_t)t * K + j] = ek[j];
-            atomicAdd(&s_count[ek[j]], 1);  // LDS: integer, order-free
+            ++s_hist[ek[j] * THREADS + tid];  // this thread's own column
         }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int acc = 0;
-        for (int e = 0; e < E; ++e) {
-            offsets[e] = acc;
-            counts[e] = s_count[e];
-            s_base[e] = acc;
-            acc += s_count[e];
-        }
-        offsets[E] = acc;
     }
     __syncthreads();
 
-    // ---- stable counting sort of the T K rows by expert, a block at a time
+    // ---- exclusive scan of the histogram in [expert][thread] order: each
+    // thread scans EP consecutive entries, then the per-thread totals are
+    // scanned across the block
+    int run = 0;
+#pragma unroll
+    for (int i = 0; i < EP; ++i) {
+        const int c = s_hist[tid * EP + i];
+        s_hist[tid * EP + i] = run;
+        run += c;
+    }
+    int incl = run;  // inclusive scan of the thread totals within the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(incl, o);
+        if (lane >= o) incl += u;
+    }
+    if (lane == 63) s_wtot[wave] = incl;
+    __syncthreads();
+    int base = incl - run;
+    for (int w = 0; w < wave; ++w) base += s_wtot[w];
+#pragma unroll
+    for (int i = 0; i < EP; ++i) s_hist[tid * EP + i] += base;
+    __syncthreads();
     const int rows = T * K;
-    for (int c0 = 0; c0 < rows; c0 += kRouteThreads) {
-        const int f = c0 + tid;
-        const int e = f < rows ? choice[f] : -1;
-        // rank among the earlier lanes of this wave with the same expert
-        int rank = 0;
-        unsigned long long left = __ballot(e >= 0);
-        while (left) {
-            const int leader = __builtin_ctzll(left);
-            const int le = __shfl(e, leader);
-            const unsigned long long same = __ballot(e == le);
-            if (e == le) rank = __popcll(same & ((1ull << lane) - 1));
-            if (lane == leader) s_wave[wave][le] = __popcll(same);
-            left &= ~same;
-        }
-        __syncthreads();
-        // per expert: running base + the earlier waves of this chunk
-        if (tid < E) {
-            int acc = s_base[tid];
-            for (int w = 0; w < kWaves; ++w) {
-                const int n = s_wave[w][tid];
-                s_wave[w][tid] = acc;
-                acc += n;
-            }
-            s_base[tid] = acc;
-        }
-        __syncthreads();
-        if (e >= 0) {
-            const int pos = s_wave[wave][e] + rank;
-            order[pos] = f;
-            inv[f] = pos;
-            eid[pos] = e;
-            tok[pos] = f / K;
-        }
-        __syncthreads();
-        // clear this chunk's wave counts
-        for (int i = tid; i < kWaves * kRouteMaxE; i += kRouteThreads)
-            (&s_wave[0][0])[i] = 0;
-        __syncthreads();
+    if (tid < E) {
+        const int o0 = s_hist[tid * THREADS];
+        const int o1 = tid + 1 < E ? s_hist[(tid + 1) * THREADS] : rows;
+        offsets[tid] = o0;
+        counts[tid] = o1 - o0;
+        if (tid == 0) offsets[E] = rows;
+    }
+    __syncthreads();
+
+    // ---- place this thread's rows, in row order
+    for (int f = t0 * K; f < t1 * K; ++f) {
+        const int e = choice[f];  // written by this thread above
+        const int pos = s_hist[e * THREADS + tid]++;
+        order[pos] = f;
+        inv[f] = pos;
+        eid[pos] = e;
+        tok[pos] = f / K;
     }
 }
 
@@ -212,9 +202,19 @@ extern "C" int srq_moe_route(const void *logits, int64_t tokens, int64_t num_exp
     SRQ_CHECK_ARG(counts && offsets, "moe_route: null counts / offsets");
     SRQ_CHECK_ARG(tokens == 0 || (weights && choice && order && inv && expert && token),
                   "moe_route: null output");
-    moe_route_kernel<<<dim3(1), dim3(kRouteThreads), 0, (hipStream_t)stream>>>(
-        (const f16 *)logits, (int)tokens, (int)num_experts, (int)top_k, norm, (f16 *)weights,
-        choice, order, inv, expert, token, counts, offsets);
+    auto launch = [&](auto kern, int threads) {
+        kern<<<dim3(1), dim3(threads), 0, (hipStream_t)stream>>>(
+            (const f16 *)logits, (int)tokens, (int)num_experts, (int)top_k, norm,
+            (f16 *)weights, choice, order, inv, expert, token, counts, offsets);
+    };
+    if (num_experts <= 8)
+        launch(moe_route_kernel<8, 1024>, 1024);
+    else if (num_experts <= 16)
+        launch(moe_route_kernel<16, 1024>, 1024);
+    else if (num_experts <= 32)
+        launch(moe_route_kernel<32, 512>, 512);
+    else
+        launch(moe_route_kernel<64, 256>, 256);
     SRQ_LAUNCH_CHECK("moe_route");
     return SRQ_OK;
 }

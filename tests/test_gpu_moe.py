@@ -196,7 +196,9 @@ def test_w4a4_linear_moe_gate_up_equals_two_calls(C, counts, n, k):
 @pytest.mark.parametrize("T,E,k,norm", [(512, 8, 2, True), (37, 8, 2, False),
                                         (300, 64, 8, True), (5, 4, 4, True),
                                         (1000, 60, 6, False), (700, 16, 1, True),
-                                        (0, 8, 2, True)])
+                                        (0, 8, 2, True), (5000, 8, 2, True),
+                                        (2049, 9, 3, False), (900, 32, 4, True),
+                                        (3, 1, 1, True), (4100, 64, 2, False)])
 def test_moe_route_matches_torch(C, T, E, k, norm):
     """srq_moe_route against the reference's torch ops (moe.py:168-185):
     softmax in fp32, topk, renormalization and the fp16 cast bit for bit;
