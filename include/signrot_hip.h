@@ -291,8 +291,9 @@ int srq_init_kv_i4(void *kv_data, void *kv_param, const int32_t *kv_indptr,
  * logits q·k̂ / sqrt(128), softmax, o = Σ p v̂ / Σ p.  With tmp != NULL and
  * num_chunks > 1 each request is split into num_chunks slices whose partial
  * states (tmp f32 [batch, num_qo_heads, num_chunks, 132]) are merged by a
- * second kernel.  Replaces _CUDA.batch_decode_i4 (bindings.cpp:508-559,
- * flashinfer.cu:11-55, decode.cuh:493-751). */
+ * second kernel; o may then be NULL, which leaves the partial states in tmp
+ * unmerged (for srq_merge_head_had_quant).  Replaces _CUDA.batch_decode_i4
+ * (bindings.cpp:508-559, flashinfer.cu:11-55, decode.cuh:493-751). */
 int srq_batch_decode_i4(void *o, const void *q, const void *kv_data, const void *kv_param,
                         const int32_t *kv_indptr, const int32_t *kv_indices,
                         const int32_t *last_page_offset, int64_t batch, int64_t num_qo_heads,
@@ -370,6 +371,18 @@ int srq_rmsnorm_quant(const void *x, int64_t rows, int64_t cols, float eps, int6
 int srq_head_had_quant(const void *x, int64_t batch, int64_t n_heads, int64_t head_dim,
                        float scale, float clip_ratio, void *q, void *qscale, void *rot,
                        void *stream);
+
+/* srq_head_had_quant of the attention output that the split-KV partial
+ * states tmp (f32 [batch, n_heads, num_chunks, 132], as srq_batch_decode_i4
+ * leaves them with o = NULL) merge to: bit-identical to the merge kernel
+ * followed by srq_head_had_quant, in one launch.  head_dim must be 128 and
+ * n_heads * num_chunks <= 124 (the block's records are staged in 64 KiB of
+ * LDS); otherwise SRQ_EINVAL.
+ * Replaces the same chain as srq_head_had_quant, with the split-KV merge of
+ * the reference's decode (decode.cuh:726-751) folded in. */
+int srq_merge_head_had_quant(const float *tmp, int64_t batch, int64_t n_heads, int64_t head_dim,
+                             int64_t num_chunks, float scale, float clip_ratio, void *q,
+                             void *qscale, void *rot, void *stream);
 
 /* Causal (or full) grouped-query softmax attention over fp16 q
  * [batch, seq_len, n_q_heads, 128] and k, v [batch, seq_len, n_kv_heads, 128]

@@ -567,13 +567,19 @@ def qkv_rope_had_append(qkv, cos, sin, n_q_heads, n_kv_heads, kv_data, kv_param,
 def batch_decode_i4(o, q, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset,
                     layer_idx, tmp=None, num_chunks=1):
     """Single-query attention over the int4 cache into o [B, Hq, 128]
-    (bindings.cpp:508-559).  Hq may be 1..8 times the cache's head count."""
+    (bindings.cpp:508-559).  Hq may be 1..8 times the cache's head count.
+    o=None with a split (tmp, num_chunks > 1) leaves the partial states in
+    tmp unmerged (see merge_head_had_quant)."""
     L, H, P, D = _check_cache("batch_decode_i4", kv_data, kv_param, kv_indptr, kv_indices,
                               last_page_offset)
-    _check("batch_decode_i4", [(o, "o"), (q, "q"), (kv_data, "kv_data")],
+    if o is None and (tmp is None or num_chunks <= 1):
+        raise RuntimeError("batch_decode_i4: o may be None only with a split (tmp, num_chunks > 1)")
+    _check("batch_decode_i4", [(q if o is None else o, "o"), (q, "q"), (kv_data, "kv_data")],
            [torch.float16, torch.float16, None])
-    if o.dim() != 3 or q.dim() != 3 or o.shape != q.shape:
+    if o is not None and (o.dim() != 3 or q.dim() != 3 or o.shape != q.shape):
         raise RuntimeError("batch_decode_i4: o and q must be the same [B, N, D] shape")
+    if q.dim() != 3:
+        raise RuntimeError("batch_decode_i4: q must be [B, N, D]")
     B, Hq = q.shape[0], q.shape[1]
     if q.shape[2] != D:
         raise RuntimeError(f"batch_decode_i4: q head_dim {q.shape[2]} != cache head_dim {D}")
@@ -638,6 +644,28 @@ def rmsnorm_quant(x, eps, mean_dim, clip_ratio=1.0, return_norm=False):
     _call("srq_rmsnorm_quant", _ptr(x), rows, cols, float(eps), int(mean_dim), float(clip_ratio),
           _ptr(h), _ptr(q), _ptr(scale), _stream(x))
     return (q, scale, h) if return_norm else (q, scale)
+
+
+# H * num_chunks limit of merge_head_had_quant (its records are staged in 64 KiB of LDS)
+MERGE_HHQ_MAX_RECORDS = 65536 // (132 * 4)
+
+
+def merge_head_had_quant(tmp, scale, clip_ratio=1.0, return_rot=False):
+    """head_had_quant of the attention output merged from split-KV partial
+    states tmp f32 [B, H, num_chunks, 132] (batch_decode_i4 with o=None), in
+    one launch: bit-identical to batch_decode_i4's merge then
+    head_had_quant.  H * num_chunks <= MERGE_HHQ_MAX_RECORDS."""
+    _check("merge_head_had_quant", [(tmp, "tmp")], [torch.float32])
+    if tmp.dim() != 4 or tmp.shape[3] != 132:
+        raise RuntimeError("merge_head_had_quant expects tmp [B, H, num_chunks, 132]")
+    B, H, chunks = tmp.shape[:3]
+    D = 128
+    q = torch.empty((B, H * D // 2), dtype=torch.uint8, device=tmp.device)
+    qs = torch.empty((B, 1), dtype=torch.float16, device=tmp.device)
+    rot = torch.empty((B, H * D), dtype=torch.float16, device=tmp.device) if return_rot else None
+    _call("srq_merge_head_had_quant", _ptr(tmp), B, H, D, chunks, float(scale),
+          float(clip_ratio), _ptr(q), _ptr(qs), _ptr(rot), _stream(tmp))
+    return (q, qs, rot) if return_rot else (q, qs)
 
 
 def head_had_quant(x, scale, clip_ratio=1.0, return_rot=False):

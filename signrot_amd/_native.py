@@ -58,6 +58,7 @@ SIGNATURES = {
     "srq_rmsnorm": [_p, _i64, _i64, _f32, _i64, _p, _p],
     "srq_rmsnorm_quant": [_p, _i64, _i64, _f32, _i64, _f32, _p, _p, _p, _p],
     "srq_head_had_quant": [_p, _i64, _i64, _i64, _f32, _f32, _p, _p, _p, _p],
+    "srq_merge_head_had_quant": [_p, _i64, _i64, _i64, _i64, _f32, _f32, _p, _p, _p, _p],
     "srq_qkv_rope_had_append": [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32,
                                 _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p],
     "srq_rope_qk": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p],

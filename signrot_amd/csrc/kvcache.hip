@@ -711,6 +711,10 @@ SRQ_DEV f16 merge_rec(const float *rec, int chunks, int d) {
     return (f16)(dv > 0.f ? ov / dv : 0.f);
 }
 
+// (head, chunk) records one merge_head_had_quant block stages in LDS (64 KiB)
+constexpr int kMergeHhqMaxRecords = 65536 / ((kD + 4) * 4);
+static_assert(kMergeHhqMaxRecords * ((kD + 4) / 4) <= 16 * 256, "record copy: 16 float4 / thread");
+
 __global__ __launch_bounds__(128) void merge_kernel(const float *__restrict__ tmp, f16 *__restrict__ o,
                                                     int64_t Hq, int chunks) {
     const int64_t bh = blockIdx.x;
@@ -726,25 +730,84 @@ __global__ __launch_bounds__(128) void merge_kernel(const float *__restrict__ tm
 // int4, sym_quant_dynamic arithmetic).  One block per b: thread d holds the
 // H values of column d in registers (stages in ascending bit, as the FWHT
 // kernel), the rotated row is staged in LDS as fp16, then packed eight
-// codes per 32-bit word.
-template <int H>
+// codes per 32-bit word.  MERGE: x is not given; the attention output of
+// head h is merged from the split-KV partial states in tmp first (the
+// merge_kernel arithmetic, so the same fp16 values), which saves the merge
+// launch and its round trip through memory.  The block's records (H chunks
+// x 132 floats, contiguous in tmp) are copied to LDS by all threads at once
+// first: merging from global memory per thread would chain H x chunks
+// dependent round trips.
+template <int H, bool MERGE>
 __global__ __launch_bounds__(256) void head_had_quant_kernel(const f16 *__restrict__ x, int D,
                                                              float scale, float clip,
                                                              u32 *__restrict__ q,
                                                              f16 *__restrict__ qscale,
-                                                             f16 *__restrict__ rot) {
+                                                             f16 *__restrict__ rot,
+                                                             const float *__restrict__ tmp,
+                                                             int chunks) {
     __shared__ __attribute__((aligned(16))) f16 buf[H * 256];
     __shared__ float red[4];
     __shared__ int redb[4];
+    extern __shared__ __attribute__((aligned(16))) float recs[];  // MERGE: H chunks records
+    __shared__ float scs[MERGE ? kMergeHhqMaxRecords : 1];  // MERGE: 2^(m_c - m) per (h, c)
+    __shared__ float dvs[MERGE ? H : 1];                     // MERGE: denominators per h
     const int64_t b = blockIdx.x;
-    const f16 *xb = x + b * H * D;
+    const f16 *xb = MERGE ? nullptr : x + b * H * D;
+    if (MERGE) {
+        // at most 64 KiB: 16 float4 per thread, all loads issued before the
+        // first store (a plain copy loop waits for each load in turn)
+        const int n4 = H * chunks * ((kD + 4) / 4);
+        const v4f *src = reinterpret_cast<const v4f *>(tmp + b * H * chunks * (kD + 4));
+        v4f t[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            t[k] = i < n4 ? src[i] : (v4f){};
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < n4) reinterpret_cast<v4f *>(recs)[i] = t[k];
+        }
+        __syncthreads();
+        // per head: the chunk weights and the denominator (merge_rec's
+        // arithmetic and order)
+        if (threadIdx.x < H) {
+            const int h = threadIdx.x;
+            const float *rh = recs + h * chunks * (kD + 4);
+            float mx = -INFINITY;
+            for (int c = 0; c < chunks; ++c) mx = fmaxf(mx, rh[c * (kD + 4) + kD]);
+            float dv = 0.f;
+            for (int c = 0; c < chunks; ++c) {
+                const float mc = rh[c * (kD + 4) + kD];
+                const float sc = mc == -INFINITY ? 0.f : exp2f(mc - mx);
+                scs[h * chunks + c] = sc;
+                dv += rh[c * (kD + 4) + kD + 1] * sc;
+            }
+            dvs[h] = dv;
+        }
+        __syncthreads();
+    }
     float amax = 0.f;
     bool bad = false;
     const int d = threadIdx.x;
     if (d < D) {
         float v[H];
+        if constexpr (MERGE) {
+            // chunks outer, heads inner: H independent sums, each in chunk order
 #pragma unroll
-        for (int h = 0; h < H; ++h) v[h] = (float)xb[h * D + d];
+            for (int h = 0; h < H; ++h) v[h] = 0.f;
+            for (int c = 0; c < chunks; ++c)
+#pragma unroll
+                for (int h = 0; h < H; ++h)
+                    v[h] += recs[(h * chunks + c) * (kD + 4) + d] * scs[h * chunks + c];
+#pragma unroll
+            for (int h = 0; h < H; ++h)
+                v[h] = (float)(f16)(dvs[h] > 0.f ? v[h] / dvs[h] : 0.f);
+        } else {
+#pragma unroll
+            for (int h = 0; h < H; ++h) v[h] = (float)xb[h * D + d];
+        }
         fwht_regs<H>(v);
 #pragma unroll
         for (int h = 0; h < H; ++h) {
@@ -920,9 +983,10 @@ extern "C" int srq_batch_decode_i4(void *o, const void *q, const void *kv_data,
                   "batch_decode_i4: query heads (%lld) must be 1..8 times the KV heads (%lld)",
                   (long long)num_qo_heads, (long long)num_kv_heads);
     if (batch == 0) return SRQ_OK;
-    SRQ_CHECK_ARG(o && q, "batch_decode_i4: null q/o");
-    SRQ_CHECK_ARG(srq_aligned(q, 16), "batch_decode_i4: q must be 16-byte aligned");
     if (num_chunks < 1 || tmp == nullptr) num_chunks = 1;
+    // o == NULL: the split partial states stay in tmp, unmerged
+    SRQ_CHECK_ARG(q && (o || num_chunks > 1), "batch_decode_i4: null q/o");
+    SRQ_CHECK_ARG(srq_aligned(q, 16), "batch_decode_i4: q must be 16-byte aligned");
     SRQ_CHECK_ARG(num_chunks <= 1024, "batch_decode_i4: num_chunks > 1024");
     DecodeArgs a;
     a.p = make_paged((void *)kv_data, (void *)kv_param, kv_indptr, kv_indices, last_page_offset,
@@ -940,7 +1004,7 @@ extern "C" int srq_batch_decode_i4(void *o, const void *q, const void *kv_data,
     rc = launch_decode(a, grid, st);
     if (rc) return rc;
     SRQ_LAUNCH_CHECK("batch_decode_i4");
-    if (num_chunks > 1) {
+    if (num_chunks > 1 && o) {
         merge_kernel<<<dim3((unsigned)(batch * num_qo_heads)), 128, 0, st>>>(tmp, (f16 *)o,
                                                                           num_qo_heads,
                                                                           (int)num_chunks);
@@ -1080,6 +1144,32 @@ extern "C" int srq_qkv_rope_had_append(const void *qkv, const void *cos, const v
     return SRQ_OK;
 }
 
+namespace {
+template <bool MERGE>
+void launch_head_had_quant(const void *x, const float *tmp, int chunks, int64_t batch,
+                           int64_t n_heads, int D, float scale, float clip_ratio, void *q,
+                           void *qscale, void *rot, hipStream_t st) {
+    const dim3 grid((unsigned)batch);
+    const size_t dyn = MERGE ? (size_t)n_heads * chunks * (kD + 4) * sizeof(float) : 0;
+    switch (n_heads) {
+#define SRQ_HHQ(HH)                                                                       \
+    case HH:                                                                              \
+        head_had_quant_kernel<HH, MERGE><<<grid, 256, dyn, st>>>(                         \
+            (const f16 *)x, D, scale, clip_ratio, (u32 *)q, (f16 *)qscale, (f16 *)rot,    \
+            tmp, chunks);                                                                 \
+        break;
+        SRQ_HHQ(1)
+        SRQ_HHQ(2)
+        SRQ_HHQ(4)
+        SRQ_HHQ(8)
+        SRQ_HHQ(16)
+        SRQ_HHQ(32)
+        SRQ_HHQ(64)
+#undef SRQ_HHQ
+    }
+}
+}  // namespace
+
 extern "C" int srq_head_had_quant(const void *x, int64_t batch, int64_t n_heads, int64_t head_dim,
                                   float scale, float clip_ratio, void *q, void *qscale, void *rot,
                                   void *stream) {
@@ -1095,25 +1185,34 @@ extern "C" int srq_head_had_quant(const void *x, int64_t batch, int64_t n_heads,
     SRQ_CHECK_ARG(x && q && qscale, "head_had_quant: null pointer");
     SRQ_CHECK_ARG(srq_aligned(q, 4) && (!rot || srq_aligned(rot, 16)),
                   "head_had_quant: q must be 4-byte and rot 16-byte aligned");
-    const dim3 grid((unsigned)batch);
-    hipStream_t st = (hipStream_t)stream;
-    const int D = (int)head_dim;
-    switch (n_heads) {
-#define SRQ_HHQ(HH)                                                                       \
-    case HH:                                                                              \
-        head_had_quant_kernel<HH><<<grid, 256, 0, st>>>(                                  \
-            (const f16 *)x, D, scale, clip_ratio, (u32 *)q, (f16 *)qscale, (f16 *)rot);   \
-        break;
-        SRQ_HHQ(1)
-        SRQ_HHQ(2)
-        SRQ_HHQ(4)
-        SRQ_HHQ(8)
-        SRQ_HHQ(16)
-        SRQ_HHQ(32)
-        SRQ_HHQ(64)
-#undef SRQ_HHQ
-    }
+    launch_head_had_quant<false>(x, nullptr, 1, batch, n_heads, (int)head_dim, scale, clip_ratio,
+                                 q, qscale, rot, (hipStream_t)stream);
     SRQ_LAUNCH_CHECK("head_had_quant");
+    return SRQ_OK;
+}
+
+extern "C" int srq_merge_head_had_quant(const float *tmp, int64_t batch, int64_t n_heads,
+                                        int64_t head_dim, int64_t num_chunks, float scale,
+                                        float clip_ratio, void *q, void *qscale, void *rot,
+                                        void *stream) {
+    SRQ_CHECK_ARG(batch >= 0 && n_heads > 0, "merge_head_had_quant: bad shape");
+    SRQ_CHECK_ARG(head_dim == kD, "merge_head_had_quant: head_dim must be %d (got %lld)", kD,
+                  (long long)head_dim);
+    SRQ_CHECK_ARG(n_heads <= 64 && (n_heads & (n_heads - 1)) == 0,
+                  "merge_head_had_quant: n_heads=%lld must be a power of two <= 64",
+                  (long long)n_heads);
+    SRQ_CHECK_ARG(num_chunks >= 1 && n_heads * num_chunks <= kMergeHhqMaxRecords,
+                  "merge_head_had_quant: n_heads * num_chunks = %lld outside [1, %d] (the "
+                  "records are staged in LDS)", (long long)(n_heads * num_chunks),
+                  kMergeHhqMaxRecords);
+    SRQ_CHECK_ARG(batch <= 0x7fffffffLL, "merge_head_had_quant: batch > 2^31-1");
+    if (batch == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(tmp && q && qscale, "merge_head_had_quant: null pointer");
+    SRQ_CHECK_ARG(srq_aligned(q, 4) && (!rot || srq_aligned(rot, 16)),
+                  "merge_head_had_quant: q must be 4-byte and rot 16-byte aligned");
+    launch_head_had_quant<true>(nullptr, tmp, (int)num_chunks, batch, n_heads, kD, scale,
+                                clip_ratio, q, qscale, rot, (hipStream_t)stream);
+    SRQ_LAUNCH_CHECK("merge_head_had_quant");
     return SRQ_OK;
 }
 

@@ -102,11 +102,12 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         return self._forward_ops(hidden_states, cache, cos, sin, trace, attention_mask)
 
     def _forward_fused(self, hidden_states, cache, cos, sin, attention_mask=None):
-        """The decode step in 11 launches: rmsnorm_quant -> q/k/v GEMM ->
+        """The decode step in 10 launches: rmsnorm_quant -> q/k/v GEMM ->
         qkv_rope_had_append (RoPE, K/q Hadamard, KV quantize + append) ->
-        batch_decode_i4 (+ split-KV merge) -> head_had_quant (head-axis
-        Hadamard + quantizer) -> o_proj GEMM + residual -> rmsnorm_quant ->
-        gate/up GEMM -> swiglu_had_sign_quant -> down GEMM + residual."""
+        batch_decode_i4 -> merge_head_had_quant (split-KV merge, head-axis
+        Hadamard + quantizer; head_had_quant when unsplit) -> o_proj GEMM +
+        residual -> rmsnorm_quant -> gate/up GEMM -> swiglu_had_sign_quant ->
+        down GEMM + residual."""
         B = hidden_states.shape[0]
         x2 = hidden_states.view(B, self.hidden)
         n1, n2 = self.input_layernorm, self.post_attention_layernorm
@@ -114,8 +115,7 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         qkv = _CUDA.w4a4_linear(q1, s1.view(-1), self.w_qkv, self.s_qkv)
         q_rot = cache.update_qkv_fused(qkv, cos, sin, self.layer_idx, self.n_heads,
                                        attention_mask)
-        attn = cache.decode_rotated(q_rot, self.layer_idx)     # [B, Hq, D]
-        qa, sa = _CUDA.head_had_quant(attn, _inv_sqrt_f32(self.n_heads))
+        qa, sa = cache.decode_rotated_quant(q_rot, self.layer_idx, _inv_sqrt_f32(self.n_heads))
         x2 = _CUDA.w4a4_linear_residual(qa, sa.view(-1), self.w_o, self.s_o, x2)
         q2, s2 = _CUDA.rmsnorm_quant(x2, n2.eps, n2.mean_dim)
         gu = _CUDA.w4a4_linear(q2, s2.view(-1), self.w_gu, self.s_gu)

@@ -153,6 +153,18 @@ class _SplitDecoder:
                         num_chunks=self.num_chunks if split else 1)
         return o
 
+    def attend_head_had_quant(self, q_rot, spec, layer_idx, scale):
+        """head_had_quant(attend(q_rot), scale): the o_proj input codes and
+        scales.  Split: the partial states are merged inside the head-axis
+        kernel (one launch fewer, the same bits)."""
+        Hq = q_rot.shape[1]
+        if (self.tmp is not None and self.tmp.shape[1] == Hq
+                and Hq * self.num_chunks <= _CUDA.MERGE_HHQ_MAX_RECORDS):
+            batch_decode_i4(None, q_rot, **spec, layer_idx=layer_idx, tmp=self.tmp,
+                            num_chunks=self.num_chunks)
+            return _CUDA.merge_head_had_quant(self.tmp, scale)
+        return _CUDA.head_had_quant(self.attend(q_rot, spec, layer_idx), scale)
+
 
 class _LayerAttention:
     """What update() returns after an append: q [B, 1, Hq, D] -> attention
@@ -332,6 +344,11 @@ class MultiLayerPagedKVCache4Bit(object):
         """Decode attention of an already rotated q [B, Hq, D] over this
         layer's cache (after update_qkv_fused) -> [B, Hq, D]."""
         return self._decoder.attend(q_rot, self._spec, layer_idx)
+
+    def decode_rotated_quant(self, q_rot, layer_idx, scale):
+        """decode_rotated followed by the head-axis Hadamard (times scale)
+        and the per-token quantizer: (codes [B, Hq D / 2], scales [B, 1])."""
+        return self._decoder.attend_head_had_quant(q_rot, self._spec, layer_idx, scale)
 
     # ---------------------------------------------------------- index specs
     def specs(self):

@@ -188,6 +188,49 @@ def test_qkv_rope_had_append_equals_update_chain(B, T, Hq, Hkv, page, cos_batch)
         assert_bitexact(to_np(out_b), to_np(out_a), f"attention output (layer {li})")
 
 
+@pytest.mark.parametrize("B,T,Hq,Hkv,chunks", [(32, 4096, 32, 8, 2), (3, 300, 8, 2, 5),
+                                                (1, 40, 16, 16, 3), (4, 1000, 32, 8, 1),
+                                                (2, 700, 4, 4, 31)])
+def test_merge_head_had_quant_equals_merge_then_head_had_quant(B, T, Hq, Hkv, chunks):
+    """The split-KV merge folded into the head-axis Hadamard + quantizer:
+    bit-identical to batch_decode_i4's merged output fed to head_had_quant
+    (chunks = 1 takes the unsplit path of the cache's decoder)."""
+    from signrot_amd.functional.hadamard import _inv_sqrt_f32
+    C = _ops()
+    rng = np.random.default_rng(B * 10 + T + chunks)
+    cache = _prefilled_cache(B, T, Hkv, Hq, 256, 1, rng)
+    spec = cache.specs()
+    q = to_dev((rng.standard_normal((B, Hq, 128)) * 2.0).astype(np.float16))
+    scale = _inv_sqrt_f32(Hq)
+    o = torch.empty_like(q)
+    tmp = torch.empty((B, Hq, chunks, 132), dtype=torch.float32, device="cuda")
+    C.batch_decode_i4(o, q, **spec, layer_idx=0, tmp=tmp, num_chunks=chunks)
+    q_ref, s_ref = C.head_had_quant(o, scale)
+    if chunks > 1:
+        tmp2 = torch.full_like(tmp, float("nan"))
+        C.batch_decode_i4(None, q, **spec, layer_idx=0, tmp=tmp2, num_chunks=chunks)
+        qg, sg, rot = C.merge_head_had_quant(tmp2, scale, return_rot=True)
+        _, _, rot_ref = C.head_had_quant(o, scale, return_rot=True)
+        torch.cuda.synchronize()
+        assert_bitexact(to_np(rot), to_np(rot_ref), "rotated rows")
+    else:
+        with pytest.raises(RuntimeError, match="split"):
+            C.batch_decode_i4(None, q, **spec, layer_idx=0, tmp=tmp, num_chunks=1)
+        from signrot_amd.transformers.kv_cache import _SplitDecoder
+        dec = _SplitDecoder(B, Hq, 128, 1, "cuda", None)
+        qg, sg = dec.attend_head_had_quant(q, spec, 0, scale)
+    torch.cuda.synchronize()
+    assert_bitexact(to_np(qg), to_np(q_ref), "codes")
+    assert_bitexact(to_np(sg), to_np(s_ref), "scales")
+
+
+def test_merge_head_had_quant_rejects_too_many_records():
+    C = _ops()
+    tmp = torch.zeros((1, 32, 4, 132), dtype=torch.float32, device="cuda")  # 128 > 124
+    with pytest.raises(RuntimeError, match="LDS"):
+        C.merge_head_had_quant(tmp, 1.0)
+
+
 @pytest.mark.parametrize("hidden,Hq,Hkv,ffn,T,B,page", [
     (1024, 8, 2, 14336, 40, 4, 64), (4096, 32, 8, 896, 300, 4, 64),
     # config 3 at its full shape (what bench.py times)
