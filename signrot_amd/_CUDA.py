@@ -139,6 +139,37 @@ def w4a4_linear(A, a_scale, B, b_scale, bias=None):
     return out
 
 
+def interleave_gate_up(w, s, ffn):
+    """Gate/up rows [gate (ffn); up (ffn)] (weights [2 ffn, K/2] or scales
+    [2 ffn] / [2 ffn, 1]) rearranged into blocks of 8 gate rows then 8 up
+    rows, the layout w4a4_linear_swiglu reads.  A copy (weight preparation,
+    done once)."""
+    if ffn % 8 or w.shape[0] != 2 * ffn or s.shape[0] != 2 * ffn:
+        raise RuntimeError("interleave_gate_up: expects [2 ffn, ...] rows with ffn % 8 == 0")
+
+    def il(t):
+        rest = t.shape[1:]
+        return t.reshape(2, ffn // 8, 8, *rest).transpose(0, 1).reshape(2 * ffn, *rest).contiguous()
+    return il(w), il(s)
+
+
+def w4a4_linear_swiglu(A, a_scale, B_il, b_scale_il):
+    """swiglu(gate, up) of the gate/up projection in one launch, for M <= 32:
+    B_il / b_scale_il from interleave_gate_up; out f16 [M, N/2]."""
+    _check("w4a4_linear_swiglu", [(A, "A"), (a_scale, "a_scale"), (B_il, "B"),
+                                  (b_scale_il, "b_scale")],
+           [torch.uint8, torch.float16, torch.uint8, torch.float16])
+    if A.dim() != 2 or B_il.dim() != 2 or A.shape[1] != B_il.shape[1]:
+        raise RuntimeError("w4a4_linear_swiglu: expected A [M, K/2] and B [N, K/2]")
+    M, N, K = A.shape[0], B_il.shape[0], A.shape[1] * 2
+    if a_scale.numel() != M or b_scale_il.numel() != N:
+        raise RuntimeError("w4a4_linear_swiglu: a_scale must have M and b_scale N elements")
+    out = torch.empty((M, N // 2), dtype=torch.float16, device=A.device)
+    _call("srq_w4a4_linear_swiglu", _ptr(A), _ptr(a_scale), _ptr(B_il), _ptr(b_scale_il), M, N, K,
+          _ptr(out), _stream(A))
+    return out
+
+
 @functools.lru_cache(maxsize=512)
 def _splitk_bytes(M, N, K):
     return int(_native.lib().srq_w4a4_linear_ws_bytes(M, N, K))

@@ -22,6 +22,7 @@ SIGNATURES = {
     "srq_kv_quant_pack": [_p, _i64, _i64, _p, _p, _p],
     "srq_matmul_s4s4": [_p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
+    "srq_w4a4_linear_swiglu": [_p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_residual": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_ws": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _p],
     "srq_w4a4_linear_residual_ws": [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64,

@@ -87,6 +87,10 @@ struct Epi {
     int ua;            // A holds unsigned nibbles (accumulator = 16 sum, not 256 sum)
     const int8_t *zr;  // asymmetric activations: zero point per row [M] (with ws) or null
     const int32_t *ws; // sum of each weight row's codes [N]
+    // stream kernel only: the N columns are blocks of 8 gate then 8 up
+    // columns and out [M, N / 2] receives swiglu(gate, up) of each pair
+    // (C, bias, res and zr null)
+    int swiglu;
 };
 
 // The int32 product of output (m, n) from the MFMA accumulator: sum(a * w),
@@ -1145,6 +1149,30 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
         for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
     }
     __syncthreads();
+    if (e.swiglu) {
+        // lane rr < 8: output column 8 c + rr of column block c from gate
+        // column 16 c + rr and up column 16 c + rr + 8, each dequantized as
+        // the plain fp16 epilogue does, then swiglu1
+        for (int j = wave; j < ncb_mine; j += KW) {
+            const int *sm = sum[j];
+            const int64_t cb = blockIdx.x + (int64_t)j * G;
+            const int c = rr & 7;
+            const float sbg = sbl[j * 16 + c], sbu = sbl[j * 16 + c + 8];
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = i * 16 + 4 * (lane >> 4) + r;
+                    const int base = i * 256 + (4 * (lane >> 4) + r) * 16;
+                    if (rr < 8 && m < M && cb * 16 + 16 <= N) {
+                        const f16 g = f16_rn(((float)(sm[base + c] >> 8) * sal[m]) * sbg);
+                        const f16 u = f16_rn(((float)(sm[base + c + 8] >> 8) * sal[m]) * sbu);
+                        e.out[m * (N / 2) + cb * 8 + c] = swiglu1((float)g, (float)u);
+                    }
+                }
+        }
+        return;
+    }
     for (int j = wave; j < ncb_mine; j += KW) {
         const int *sm = sum[j];
         const int64_t gn = (int64_t)(blockIdx.x + j * G) * 16 + rr;
@@ -1730,6 +1758,33 @@ extern "C" int srq_w4a4_linear(const void *A, const void *a_scale, const void *B
     e.sb = (const f16 *)b_scale;
     e.bias = (const f16 *)bias;
     return run_gemm("w4a4_linear", A, B, M, N, K, e, (hipStream_t)stream);
+}
+
+extern "C" int srq_w4a4_linear_swiglu(const void *A, const void *a_scale, const void *B,
+                                      const void *b_scale, int64_t M, int64_t N, int64_t K,
+                                      void *out, void *stream) {
+    int rc = check_gemm("w4a4_linear_swiglu", A, B, M, N, K);
+    if (rc) return rc;
+    SRQ_CHECK_ARG(M <= 32, "w4a4_linear_swiglu: M=%lld > 32 (weight-streaming shapes only)",
+                  (long long)M);
+    SRQ_CHECK_ARG(N % 16 == 0, "w4a4_linear_swiglu: N=%lld must be a multiple of 16",
+                  (long long)N);
+    SRQ_CHECK_ARG(K > 0, "w4a4_linear_swiglu: K must be positive");
+    if (M == 0 || N == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(out && a_scale && b_scale, "w4a4_linear_swiglu: null pointer");
+    Epi e{};
+    e.out = (f16 *)out;
+    e.sa = (const f16 *)a_scale;
+    e.sb = (const f16 *)b_scale;
+    e.swiglu = 1;
+    if (!launch_stream<false>((const uint8_t *)A, (const uint8_t *)B, M, N, K, e,
+                              (hipStream_t)stream)) {
+        srq_set_error("w4a4_linear_swiglu: M=%lld N=%lld K=%lld outside the weight-streaming "
+                      "kernel's limits", (long long)M, (long long)N, (long long)K);
+        return SRQ_EUNSUPPORTED;
+    }
+    SRQ_LAUNCH_CHECK("w4a4_linear_swiglu");
+    return SRQ_OK;
 }
 
 extern "C" int64_t srq_w4a4_linear_ws_bytes(int64_t M, int64_t N, int64_t K) {

@@ -82,6 +82,17 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
             getattr(layer, f"s_{name}").copy_(scale)
         return layer.to(device)
 
+    def _gate_up_interleaved(self):
+        """w_gu / s_gu in the blocks-of-8 gate/up layout of
+        w4a4_linear_swiglu: a derived copy (2 ffn x hidden / 2 bytes), made
+        on first use and again whenever w_gu or s_gu changes in place."""
+        key = (self.w_gu.data_ptr(), self.w_gu._version, self.s_gu.data_ptr(),
+               self.s_gu._version)
+        if getattr(self, "_gu_il_key", None) != key:
+            self._gu_il = _CUDA.interleave_gate_up(self.w_gu, self.s_gu, self.ffn)
+            self._gu_il_key = key
+        return self._gu_il
+
     def _linear(self, xq, name):
         q, s = xq.quantized_x, xq.scales_x
         return _CUDA.w4a4_linear(q.view(-1, q.shape[-1]), s.view(-1), getattr(self, f"w_{name}"),
@@ -106,8 +117,9 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         qkv_rope_had_append (RoPE, K/q Hadamard, KV quantize + append) ->
         batch_decode_i4 -> merge_head_had_quant (split-KV merge, head-axis
         Hadamard + quantizer; head_had_quant when unsplit) -> o_proj GEMM +
-        residual -> rmsnorm_quant -> gate/up GEMM -> swiglu_had_sign_quant ->
-        down GEMM + residual."""
+        residual -> rmsnorm_quant -> gate/up GEMM with the SwiGLU in its
+        epilogue (B <= 32; else the GEMM and swiglu_had_sign_quant) ->
+        had_sign_quant -> down GEMM + residual."""
         B = hidden_states.shape[0]
         x2 = hidden_states.view(B, self.hidden)
         n1, n2 = self.input_layernorm, self.post_attention_layernorm
@@ -118,6 +130,14 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         qa, sa = cache.decode_rotated_quant(q_rot, self.layer_idx, _inv_sqrt_f32(self.n_heads))
         x2 = _CUDA.w4a4_linear_residual(qa, sa.view(-1), self.w_o, self.s_o, x2)
         q2, s2 = _CUDA.rmsnorm_quant(x2, n2.eps, n2.mean_dim)
+        if B <= 32 and self.ffn % 8 == 0:
+            # SwiGLU in the gate/up GEMM's epilogue, then the plain rotation
+            w_il, s_il = self._gate_up_interleaved()
+            a = _CUDA.w4a4_linear_swiglu(q2, s2.view(-1), w_il, s_il)
+            qd, sd = _CUDA.had_sign_quant(a, self.down_hadk, self.down_k, self.down_sign)
+            out = _CUDA.w4a4_linear_residual(qd, sd.view(-1), self.w_down, self.s_down, x2,
+                                             out=x2)
+            return out.view(B, 1, self.hidden)
         gu = _CUDA.w4a4_linear(q2, s2.view(-1), self.w_gu, self.s_gu)
         if _CUDA.swiglu_had_fusable(self.ffn, self.down_k):
             qd, sd = _CUDA.swiglu_had_sign_quant(gu, self.down_hadk, self.down_k,

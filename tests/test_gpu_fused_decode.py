@@ -188,6 +188,34 @@ def test_qkv_rope_had_append_equals_update_chain(B, T, Hq, Hkv, page, cos_batch)
         assert_bitexact(to_np(out_b), to_np(out_a), f"attention output (layer {li})")
 
 
+@pytest.mark.parametrize("M,ffn,K", [(32, 14336, 4096), (1, 14336, 4096), (16, 896, 1024),
+                                     (7, 8, 256), (32, 28672, 8192), (20, 1000, 4128)])
+def test_w4a4_linear_swiglu_equals_linear_then_swiglu(M, ffn, K):
+    """The SwiGLU epilogue of the gate/up projection: bit-identical to the
+    fp16 gate/up GEMM outputs fed to srq_swiglu (fused.cu:367-390)."""
+    C = _ops()
+    rng = np.random.default_rng(M * 7 + ffn + K)
+    A = to_dev(rng.integers(0, 256, (M, K // 2)).astype(np.uint8))
+    sa = to_dev((rng.random(M) * 0.05 + 1e-3).astype(np.float16))
+    w = to_dev(rng.integers(0, 256, (2 * ffn, K // 2)).astype(np.uint8))
+    sw = to_dev((rng.random(2 * ffn) * 0.01 + 1e-4).astype(np.float16))
+    gu = C.w4a4_linear(A, sa, w, sw)
+    want = C.swiglu(gu[:, :ffn].contiguous(), gu[:, ffn:].contiguous())
+    w_il, s_il = C.interleave_gate_up(w, sw, ffn)
+    got = C.w4a4_linear_swiglu(A, sa, w_il, s_il)
+    torch.cuda.synchronize()
+    assert_bitexact(to_np(got), to_np(want), "swiglu(gate, up)")
+
+
+def test_w4a4_linear_swiglu_rejects_prefill_rows():
+    C = _ops()
+    A = torch.zeros(33, 128, dtype=torch.uint8, device="cuda")
+    w = torch.zeros(32, 128, dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match="32"):
+        C.w4a4_linear_swiglu(A, torch.ones(33, dtype=torch.float16, device="cuda"), w,
+                             torch.ones(32, dtype=torch.float16, device="cuda"))
+
+
 @pytest.mark.parametrize("B,T,Hq,Hkv,chunks", [(32, 4096, 32, 8, 2), (3, 300, 8, 2, 5),
                                                 (1, 40, 16, 16, 3), (4, 1000, 32, 8, 1),
                                                 (2, 700, 4, 4, 31)])
