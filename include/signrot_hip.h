@@ -271,6 +271,18 @@ int srq_swiglu_had_sign_quant_moe(const void *gate, const void *up, int64_t ld, 
                                   const int32_t *expert_ids, int64_t num_experts,
                                   float clip_ratio, void *q, void *scale, void *stream);
 
+/* srq_swiglu_had_sign_quant_moe of an input already through the SwiGLU
+ * (x f16 [rows, n], e.g. srq_w4a4_linear_moe_swiglu's output): the
+ * rotation, the per-expert sign rows and the quantizer in one launch,
+ * bit-identical to srq_online_hadamard (no sign) then
+ * srq_sym_quant_dynamic_moe.  n = K * 512 or K * 1024 with 9 <= K <= 32,
+ * K % 4 == 0, else SRQ_EUNSUPPORTED.  Replaces matmul_hadU_cuda ->
+ * sym_quant_dynamic_moe of SignRotMoEBlock.forward (signrot/nn/moe.py:
+ * 186-236, kernels/moe.cu:60-101). */
+int srq_had_sign_quant_moe(const void *x, int64_t rows, int64_t n, int64_t K, const void *hadK,
+                           const int8_t *sign, const int32_t *expert_ids, int64_t num_experts,
+                           float clip_ratio, void *q, void *scale, void *stream);
+
 /* ----------------------------------------------------- paged int4 KV cache */
 /* Cache layout (signrot/kernels/include/flashinfer/page.cuh:18-112):
  *   kv_data  u8  [pages, num_layers, 2, num_heads, page_size, head_dim/2]
@@ -519,6 +531,20 @@ int srq_w4a4_linear_moe_gate_up(const void *A, const void *a_scale, const void *
                                 const int32_t *expert_offsets, int64_t num_experts,
                                 int64_t rows, int64_t N, int64_t K, void *out_gate,
                                 void *out_up, void *stream);
+
+/* The gate and up projections of the MoE block with the SwiGLU in the
+ * epilogue: B [num_experts, N, K/2] holds each expert's gate and up rows
+ * interleaved in blocks of 8 (rows 16 c .. 16 c + 7 = gate rows 8 c ..,
+ * rows 16 c + 8 .. = up rows 8 c ..), b_scale [num_experts, N] likewise;
+ * out f16 [rows, N/2] = swiglu(gate, up) of the paired columns (the
+ * srq_swiglu rounding).  Bit-identical to srq_w4a4_linear_moe_gate_up
+ * followed by srq_swiglu.  N % 16 == 0; A, B and out 16-byte aligned.
+ * Replaces the two _gemm_dequant_grouped calls and the SwiGLU of
+ * SignRotMoEBlock.forward (signrot/nn/moe.py:187-192). */
+int srq_w4a4_linear_moe_swiglu(const void *A, const void *a_scale, const void *B,
+                               const void *b_scale, const int32_t *expert_offsets,
+                               int64_t num_experts, int64_t rows, int64_t N, int64_t K,
+                               void *out, void *stream);
 
 /* Routing of the MoE block in one launch (signrot/nn/moe.py:168-185 plus
  * the expert sort of 175-180): logits fp16 [tokens, num_experts]

@@ -1005,6 +1005,68 @@ def w4a4_linear_moe_gate_up(A, a_scale, B_gate, s_gate, B_up, s_up, expert_offse
     return out_g, out_u
 
 
+def interleave_gate_up_experts(w_gate, s_gate, w_up, s_up):
+    """Per-expert gate and up weights [E, ffn, K/2] (scales [E, ffn]) as one
+    [E, 2 ffn, K/2] tensor with the rows interleaved in blocks of 8 (gate
+    rows 8 c .. then up rows 8 c ..), the layout w4a4_linear_moe_swiglu
+    reads; scales likewise.  A copy (weight preparation, done once)."""
+    E, ffn = w_gate.shape[0], w_gate.shape[1]
+    if ffn % 8 or tuple(w_up.shape) != tuple(w_gate.shape):
+        raise RuntimeError("interleave_gate_up_experts: gate/up [E, ffn, ...], ffn % 8 == 0")
+
+    def il(g, u):
+        rest = g.shape[2:]
+        return torch.stack([g.reshape(E, ffn // 8, 8, *rest), u.reshape(E, ffn // 8, 8, *rest)],
+                           dim=2).reshape(E, 2 * ffn, *rest).contiguous()
+    return il(w_gate, w_up), il(s_gate, s_up)
+
+
+def w4a4_linear_moe_swiglu(A, a_scale, B_il, s_il, expert_offsets):
+    """swiglu(gate, up) of the MoE block's gate/up projections in one
+    launch, B_il / s_il from interleave_gate_up_experts: out f16 [R, ffn],
+    bit-identical to w4a4_linear_moe_gate_up then swiglu."""
+    name = "w4a4_linear_moe_swiglu"
+    _check(name, [(A, "A"), (a_scale, "a_scale"), (B_il, "B"), (s_il, "b_scale"),
+                  (expert_offsets, "expert_offsets")],
+           [torch.uint8, torch.float16, torch.uint8, torch.float16, torch.int32])
+    if A.dim() != 2 or B_il.dim() != 3 or B_il.shape[2] != A.shape[1]:
+        raise RuntimeError(f"{name}: expected A [R, K/2] and B [E, N, K/2]")
+    R, E, N, K = A.shape[0], B_il.shape[0], B_il.shape[1], A.shape[1] * 2
+    if a_scale.numel() != R or tuple(s_il.shape) != (E, N):
+        raise RuntimeError(f"{name}: a_scale must have R entries and the scales be [E, N]")
+    if expert_offsets.numel() != E + 1:
+        raise RuntimeError(f"{name}: expert_offsets must have num_experts + 1 entries")
+    out = torch.empty((R, N // 2), dtype=torch.float16, device=A.device)
+    _call("srq_w4a4_linear_moe_swiglu", _ptr(A), _ptr(a_scale), _ptr(B_il), _ptr(s_il),
+          _ptr(expert_offsets), E, R, N, K, _ptr(out), _stream(A))
+    return out
+
+
+def had_sign_quant_moe(x, hadK, K, sign, expert_ids, clip_ratio=1.0):
+    """swiglu_had_sign_quant_moe for an input already through the SwiGLU:
+    x f16 [rows, n] -> online Hadamard (had_K x H_{n/K}) -> per-expert sign
+    -> per-token int4 quantizer, one launch; bit-identical to
+    matmul_hadU_cuda then sym_quant_dynamic_moe.  Returns (q u8 [rows, n/2],
+    scale f16 [rows, 1])."""
+    name = "had_sign_quant_moe"
+    _check(name, [(x, "x"), (hadK, "hadK"), (expert_ids, "expert_ids")],
+           [torch.float16, torch.float16, torch.int32])
+    if x.dim() != 2:
+        raise RuntimeError(f"{name}: x must be 2D")
+    rows, n = x.shape
+    if expert_ids.numel() != rows:
+        raise RuntimeError(f"{name}: expert_ids must have one entry per row")
+    _check_had(name, n, hadK, K, None, False)
+    sign = _moe_sign(name, sign, n)
+    E = sign.shape[0] if sign is not None else 0
+    q = torch.empty((rows, n // 2), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((rows, 1), dtype=torch.float16, device=x.device)
+    if rows:
+        _call("srq_had_sign_quant_moe", _ptr(x), rows, n, int(K), _ptr(hadK), _ptr(sign),
+              _ptr(expert_ids), E, float(clip_ratio), _ptr(q), _ptr(scale), _stream(x))
+    return q, scale
+
+
 def moe_route(logits, top_k, norm_topk_prob):
     """Routing of the MoE block in one launch (moe.py:168-185): returns
     (weights fp16 [T, k], order, inv, expert, token int32 [T k], counts int32

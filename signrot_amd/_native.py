@@ -68,6 +68,8 @@ SIGNATURES = {
     "srq_w4a4_linear_moe": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
     "srq_w4a4_linear_moe_gate_up": [_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p,
                                     _p],
+    "srq_w4a4_linear_moe_swiglu": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p, _p],
+    "srq_had_sign_quant_moe": [_p, _i64, _i64, _i64, _p, _p, _p, _i64, _f32, _p, _p, _p],
     "srq_moe_route": [_p, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p],
     "srq_moe_combine": [_p, _p, _p, _i64, _i64, _i64, _p, _p],
     "srq_sym_quant_dynamic_moe": [_p, _p, _p, _i64, _i64, _i64, _f32, _p, _p, _p],

@@ -398,6 +398,60 @@ SRQ_DEV void store_block_lds32(const Epi &e, int64_t M, int64_t N, int64_t mb, i
     }
 }
 
+// store_block_lds32 for an N whose columns are blocks of 8 gate then 8 up
+// columns (nb and N multiples of 16): each lane dequantizes the 16 columns
+// of one block of a row as store_block_lds32 would (symmetric A, no bias or
+// residual) and stores the 8 swiglu1(gate, up) values as 16 bytes into the
+// [M, N/2] output.  4 BS FN BS FM bytes of `tile`, as store_block_lds32.
+template <int BS, int FM, int FN, typename AccT>
+SRQ_DEV void store_block_lds32_swiglu(const Epi &e, int64_t M, int64_t N, int64_t mb,
+                                      int64_t nb, const AccT (&acc)[FM][FN], int lane,
+                                      int32_t *tile) {
+    constexpr int NV = BS * BS / 64;
+    constexpr int W = BS * FN;   // columns per row of the block
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int lr = i * BS + frag_row<BS>(v, lane);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) tile[lr * W + j * BS + (lane & (BS - 1))] = acc[i][j][v];
+        }
+    constexpr int LPR = W / 16;    // lanes per row
+    constexpr int RPI = 64 / LPR;  // rows per pass
+    static_assert(LPR >= 1 && 64 % LPR == 0 && (BS * FM) % RPI == 0, "row pass shape");
+    const int c16 = (lane % LPR) * 16;
+    const int64_t gn0 = nb + c16;
+    if (gn0 + 16 > N) return;
+    float sbg[8], sbu[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        sbg[k] = (float)e.sb[gn0 + k];
+        sbu[k] = (float)e.sb[gn0 + 8 + k];
+    }
+    for (int r0 = 0; r0 < BS * FM; r0 += RPI) {
+        const int lr = r0 + lane / LPR;
+        const int64_t gm = mb + lr;
+        if (gm >= M) continue;
+        const int32_t *tr = tile + lr * W + c16;
+        const v4i g0 = *reinterpret_cast<const v4i *>(tr);
+        const v4i g1 = *reinterpret_cast<const v4i *>(tr + 4);
+        const v4i u0 = *reinterpret_cast<const v4i *>(tr + 8);
+        const v4i u1 = *reinterpret_cast<const v4i *>(tr + 12);
+        const float sa = (float)e.sa[gm];
+        v8h o;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int ga = k < 4 ? g0[k] : g1[k - 4];
+            const int ua = k < 4 ? u0[k] : u1[k - 4];
+            const f16 gh = f16_rn((float)(ga >> 8) * sa * sbg[k]);
+            const f16 uh = f16_rn((float)(ua >> 8) * sa * sbu[k]);
+            o[k] = swiglu1((float)gh, (float)uh);
+        }
+        *reinterpret_cast<v8h *>(e.out + gm * (N / 2) + gn0 / 2) = o;
+    }
+}
+
 // One K step of a compute wave: the stage holds BM A rows then the B rows.
 template <int FM, int FN, int KBB, int BM = kBigBM, bool UA = false>
 SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {
@@ -1290,7 +1344,9 @@ struct GroupedArgs {
     int32_t *ws_c;
 };
 
-constexpr int kFormGeneral = 0, kFormDense = 1, kFormSplitK = 2;
+// kFormSwiglu: the expert-offset form over gate/up rows interleaved in
+// blocks of 8, out [R, N/2] = swiglu(gate, up)
+constexpr int kFormGeneral = 0, kFormDense = 1, kFormSplitK = 2, kFormSwiglu = 3;
 
 struct GroupedProb {
     const uint8_t *a, *b;
@@ -1474,7 +1530,7 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             const bool second = !DENSE && g.pair && (p & 1);
             const int64_t ex = DENSE ? 0 : g.pair ? p >> 1 : p;
             Epi e{};
-            e.out = (second ? g.out2 : g.out) + pr.row0 * g.N;
+            e.out = (second ? g.out2 : g.out) + pr.row0 * (FORM == kFormSwiglu ? g.N / 2 : g.N);
             e.sa = g.sa + pr.row0;
             e.sb = (second ? g.sb2 : g.sb) + ex * g.N;
             e.ua = UA;
@@ -1486,9 +1542,14 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                 e.bias = g.bias;
                 e.res = g.res;
             }
-            store_block_lds32<32, FM, FN>(e, pr.m, pr.n, m0 + wm * (FM * 32),
-                                          n0 + wn * (FN * 32), acc, lane,
-                                          reinterpret_cast<int32_t *>(epi_lds + wave * kEpiTile));
+            if constexpr (FORM == kFormSwiglu)
+                store_block_lds32_swiglu<32, FM, FN>(
+                    e, pr.m, pr.n, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane,
+                    reinterpret_cast<int32_t *>(epi_lds + wave * kEpiTile));
+            else
+                store_block_lds32<32, FM, FN>(e, pr.m, pr.n, m0 + wm * (FM * 32),
+                                              n0 + wn * (FN * 32), acc, lane,
+                                              reinterpret_cast<int32_t *>(epi_lds + wave * kEpiTile));
             continue;
         }
         // int32 (pointer-array form): 32x32 accumulator layout, lane holds
@@ -1905,6 +1966,41 @@ extern "C" int srq_w4a4_linear_moe(const void *A, const void *a_scale, const voi
     g.out = (f16 *)out;
     gemm_grouped_kernel<4, false><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
     SRQ_LAUNCH_CHECK("w4a4_linear_moe");
+    return SRQ_OK;
+}
+
+extern "C" int srq_w4a4_linear_moe_swiglu(const void *A, const void *a_scale, const void *B,
+                                          const void *b_scale, const int32_t *expert_offsets,
+                                          int64_t num_experts, int64_t rows, int64_t N,
+                                          int64_t K, void *out, void *stream) {
+    SRQ_CHECK_ARG(num_experts >= 0 && num_experts <= 0x7fffffffLL && rows >= 0 && N >= 0 &&
+                      K >= 0, "w4a4_linear_moe_swiglu: bad shape");
+    SRQ_CHECK_ARG(K % 32 == 0 && K < 131072, "w4a4_linear_moe_swiglu: K=%lld must be a "
+                  "multiple of 32 and < 131072", (long long)K);
+    SRQ_CHECK_ARG(N % 16 == 0, "w4a4_linear_moe_swiglu: N=%lld must be a multiple of 16",
+                  (long long)N);
+    if (num_experts == 0 || rows == 0 || N == 0) return SRQ_OK;
+    if (rows * (K / 2) >= 0xFFFFFFF0LL || N * (K / 2) >= 0xFFFFFFF0LL) {
+        srq_set_error("w4a4_linear_moe_swiglu: operand larger than 4 GiB");
+        return SRQ_EUNSUPPORTED;
+    }
+    SRQ_CHECK_ARG(A && a_scale && B && b_scale && expert_offsets && out,
+                  "w4a4_linear_moe_swiglu: null pointer");
+    SRQ_CHECK_ARG(srq_aligned(A, 16) && srq_aligned(B, 16) && srq_aligned(out, 16),
+                  "w4a4_linear_moe_swiglu: A, B and out must be 16-byte aligned");
+    GroupedArgs g{};
+    g.P = (int)num_experts;
+    g.offsets = expert_offsets;
+    g.A = (const uint8_t *)A;
+    g.B = (const uint8_t *)B;
+    g.N = N;
+    g.K = K;
+    g.sa = (const f16 *)a_scale;
+    g.sb = (const f16 *)b_scale;
+    g.out = (f16 *)out;
+    gemm_grouped_kernel<4, false, kFormSwiglu>
+        <<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
+    SRQ_LAUNCH_CHECK("w4a4_linear_moe_swiglu");
     return SRQ_OK;
 }
 

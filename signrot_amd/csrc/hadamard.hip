@@ -539,6 +539,29 @@ extern "C" int srq_swiglu_had_sign_quant_moe(const void *gate, const void *up, i
     return SRQ_EUNSUPPORTED;
 }
 
+extern "C" int srq_had_sign_quant_moe(const void *x, int64_t rows, int64_t n, int64_t K,
+                                      const void *hadK, const int8_t *sign,
+                                      const int32_t *expert_ids, int64_t num_experts,
+                                      float clip_ratio, void *q, void *scale, void *stream) {
+    int rc = check_rotation("had_sign_quant_moe", x, rows, n, K, hadK);
+    if (rc) return rc;
+    if (rows == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(q && scale, "had_sign_quant_moe: null pointer");
+    SRQ_CHECK_ARG(!sign || (expert_ids && num_experts > 0),
+                  "had_sign_quant_moe: sign needs expert_ids and num_experts > 0");
+    SRQ_CHECK_ARG(srq_aligned(x, 16) && srq_aligned(q, 16),
+                  "had_sign_quant_moe: x and q must be 16-byte aligned");
+    if (srq_had512_mfma(x, rows, n, K, hadK, sign, clip_ratio, q, scale, nullptr,
+                        (hipStream_t)stream, nullptr, n, sign ? expert_ids : nullptr,
+                        num_experts)) {
+        SRQ_LAUNCH_CHECK("had_sign_quant_moe");
+        return SRQ_OK;
+    }
+    srq_set_error("had_sign_quant_moe: needs n = K * 512 or K * 1024 with 9 <= K <= 32, "
+                  "K %% 4 == 0 (n=%lld, K=%lld)", (long long)n, (long long)K);
+    return SRQ_EUNSUPPORTED;
+}
+
 extern "C" int srq_had_sign_quant_bf6(const void *x, int64_t rows, int64_t n, int64_t K,
                                       const void *hadK, const int8_t *sign, float clip_ratio,
                                       void *q6, void *scale, void *stream) {

@@ -222,6 +222,15 @@ class SignRotMoEBlock(torch.nn.Module):
         x = hidden_states.reshape(-1, shape[-1])
         route = self.route(x)
         codes = self._quant(x.to(torch.float16)).rows(route.token)
+        if self._swiglu_epilogue(codes):
+            # SwiGLU in the gate/up launch's epilogue, then the plain
+            # rotation + per-expert sign + quantizer (bit-identical)
+            w_il, s_il = self._gate_up_interleaved()
+            a = _CUDA.w4a4_linear_moe_swiglu(codes.q, codes.scale, w_il, s_il, route.offsets)
+            q, s = _CUDA.had_sign_quant_moe(a, self.had_K, self.K, self.sign_down, route.expert,
+                                            self.clip_ratio)
+            y = self._project(_Codes(q, s, None), route, "down")
+            return self._combine(x, shape, y, route)
         if self.use_grouped and codes.zero is None:
             # both projections in one launch (bit-identical to two)
             gate_h, up_h = _CUDA.w4a4_linear_moe_gate_up(
@@ -231,6 +240,31 @@ class SignRotMoEBlock(torch.nn.Module):
             gate_h = self._project(codes, route, "gate")
             up_h = self._project(codes, route, "up")
         y = self._project(self._down_input(gate_h, up_h, route), route, "down")
+        return self._combine(x, shape, y, route)
+
+    def _swiglu_epilogue(self, codes: _Codes) -> bool:
+        """Whether the gate/up launch can end in the SwiGLU: grouped,
+        symmetric, fp16 rotation with an MFMA form for this size."""
+        inter, K = self.intermediate_size, self.K
+        return (self.fuse_down and self.use_grouped and codes.zero is None and not self.fp32_had
+                and self.had_K is not None and inter % 8 == 0 and K % 4 == 0 and 9 <= K <= 32
+                and inter in (K * 512, K * 1024))
+
+    def _gate_up_interleaved(self):
+        """w_gate / w_up (and scales) as one [E, 2 inter, hidden/2] tensor in
+        the blocks-of-8 layout of w4a4_linear_moe_swiglu: a derived copy,
+        made on first use and again whenever a source buffer changes in
+        place."""
+        src = (self.w_gate, self.s_gate, self.w_up, self.s_up)
+        key = tuple((t.data_ptr(), t._version) for t in src)
+        if getattr(self, "_gu_il_key", None) != key:
+            self._gu_il = _CUDA.interleave_gate_up_experts(*src)
+            self._gu_il_key = key
+        return self._gu_il
+
+    def _combine(self, x, shape, y, route: MoERouting):
+        """Expert-ordered rows y back to tokens, weighted and summed over
+        each token's k choices."""
         if x.dtype == torch.float16 and shape[-1] % 8 == 0:
             # un-permute, weight and sum in one launch (bit-identical)
             out = _CUDA.moe_combine(y, route.inv.to(torch.int32), route.weights)

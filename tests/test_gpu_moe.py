@@ -439,6 +439,49 @@ def test_swiglu_had_sign_quant_moe(C, rows, n, K, experts, clip, with_sign):
     assert torch.equal(q, q2), "codes"
 
 
+@pytest.mark.parametrize("counts,n,k", [([3, 0, 5, 1], 304, 768), ([0, 0], 64, 256),
+                                       ([123, 127, 123, 122, 123, 126, 136, 144], 14336, 4096),
+                                       ([700, 1], 1024, 2048)])
+def test_w4a4_linear_moe_swiglu_equals_gate_up_then_swiglu(C, counts, n, k):
+    """The SwiGLU epilogue of the grouped gate/up launch over interleaved
+    weights: bit-identical to the two projections followed by srq_swiglu."""
+    torch.manual_seed(sum(counts) + n)
+    a, bg = _grouped_inputs(None, counts, n, k)
+    _, bu = _grouped_inputs(None, counts, n, k)
+    e, rows = len(counts), a.shape[0]
+    sa = (torch.rand(rows, device=DEV) * 0.05 + 1e-3).half()
+    sg = (torch.rand(e, n, device=DEV) * 0.01 + 1e-4).half()
+    su = (torch.rand(e, n, device=DEV) * 0.01 + 1e-4).half()
+    off = torch.tensor(om.expert_offsets(counts), dtype=torch.int32, device=DEV)
+    g, u = C.w4a4_linear_moe_gate_up(a, sa, bg, sg, bu, su, off)
+    want = C.swiglu(g, u) if rows else g
+    w_il, s_il = C.interleave_gate_up_experts(bg, sg, bu, su)
+    got = C.w4a4_linear_moe_swiglu(a, sa, w_il, s_il, off)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("rows,n,K,experts,with_sign", [
+    (600, 14336, 28, 8, True), (37, 6144, 12, 16, True), (5, 20480, 20, 4, True),
+    (300, 14336, 28, 8, False)])
+def test_had_sign_quant_moe_equals_rotation_then_moe_quant(C, rows, n, K, experts, with_sign):
+    """The plain MoE down-proj input op (input already through the SwiGLU)
+    equals rotation (no sign) -> sym_quant_dynamic_moe bit for bit, H_512
+    and H_1024 chunks, ids outside the sign table."""
+    from oracle import hadamard as oh
+    rng = np.random.default_rng(rows + n + 1)
+    x = to_dev((rng.standard_normal((rows, n)) * 2).astype(np.float16))
+    eid_np = rng.integers(0, experts, rows).astype(np.int32)
+    eid_np[: min(rows, 3)] = [-1, experts, 1 << 20][: min(rows, 3)]
+    eid = to_dev(eid_np)
+    sign = to_dev(rng.choice([-1, 1], (experts, n)).astype(np.int8)) if with_sign else None
+    hk = to_dev(oh.had_table(K).astype(np.float32)).half()
+    q, s = C.had_sign_quant_moe(x, hk, K, sign, eid)
+    rot = C.online_hadamard(x, hk, K, None)
+    q2, s2 = C.sym_quant_dynamic_moe(rot, sign, eid)
+    assert torch.equal(s, s2), "scales"
+    assert torch.equal(q, q2), "codes"
+
+
 @torch.no_grad()
 def test_block_fused_down_equals_unfused():
     blk = _block(4096, 14336, 8, 2, True, seed=5)
