@@ -51,6 +51,16 @@ int srq_abi_version(void);
 int srq_sym_quant_dynamic(const void *x, int64_t rows, int64_t cols,
                           float clip_ratio, void *q, void *scale, void *stream);
 
+/* srq_sym_quant_dynamic of gathered rows: output row r (of rows) quantizes
+ * row src_row[r] of x f16 [x_rows, cols] (an index outside [0, x_rows)
+ * gives scale 0 and zero codes).  cols % 8 == 0, cols <= 32768, x 16-byte
+ * aligned.  Bit-identical to srq_sym_quant_dynamic followed by a row gather
+ * of its outputs.  Replaces the quantizer + the `x[token]` gather of the
+ * MoE block's expert-sorted rows (signrot/nn/moe.py:186-190). */
+int srq_sym_quant_dynamic_rows(const void *x, int64_t x_rows, const int32_t *src_row,
+                               int64_t rows, int64_t cols, float clip_ratio, void *q, void *scale,
+                               void *stream);
+
 /* Symmetric int4 quantization with a given per-row fp16 scale.
  * Replaces _CUDA.sym_quant (bindings.cpp:208-225, quant.cu:13-62). */
 int srq_sym_quant(const void *x, const void *scale, int64_t rows, int64_t cols,

@@ -339,6 +339,22 @@ def sym_quant_dynamic(x, clip_ratio=1.0):
     return q, scale
 
 
+def sym_quant_dynamic_rows(x, src_row, clip_ratio=1.0):
+    """sym_quant_dynamic(x[src_row]) in one launch (no gathered copy): x f16
+    [rows, cols], src_row int32 [R] -> (q u8 [R, cols/2], scale f16 [R, 1]).
+    Indices outside [0, rows) give zero codes and scale 0."""
+    _check("sym_quant_dynamic_rows", [(x, "x"), (src_row, "src_row")],
+           [torch.float16, torch.int32])
+    if x.dim() != 2 or src_row.dim() != 1:
+        raise RuntimeError("sym_quant_dynamic_rows expects x [rows, cols] and src_row [R]")
+    R, cols = src_row.shape[0], x.shape[1]
+    q = torch.empty((R, cols // 2), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((R, 1), dtype=torch.float16, device=x.device)
+    _call("srq_sym_quant_dynamic_rows", _ptr(x), x.shape[0], _ptr(src_row), R, cols,
+          float(clip_ratio), _ptr(q), _ptr(scale), _stream(x))
+    return q, scale
+
+
 # ------------------------------------------------- asymmetric activations
 
 def asym_quant_dynamic(x, clip_ratio=1.0):

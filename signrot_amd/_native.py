@@ -17,6 +17,7 @@ _p = ctypes.c_void_p
 # name -> argtypes (restype is int for all compute entry points)
 SIGNATURES = {
     "srq_sym_quant_dynamic": [_p, _i64, _i64, _f32, _p, _p, _p],
+    "srq_sym_quant_dynamic_rows": [_p, _i64, _p, _i64, _i64, _f32, _p, _p, _p],
     "srq_sym_quant": [_p, _p, _i64, _i64, _p, _p],
     "srq_sym_dequant": [_p, _p, _p, _i64, _i64, _p, _p],
     "srq_kv_quant_pack": [_p, _i64, _i64, _p, _p, _p],

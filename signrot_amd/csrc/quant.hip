@@ -53,16 +53,25 @@ SRQ_DEV float row_reduce(float v, float *lds) {
 // --------------------------------------------------------------------------
 // sym_quant_dynamic: vector path (cols % 8 == 0, 16-byte aligned rows)
 
+// src_row (optional): output row r quantizes input row src_row[r] of the
+// x_rows rows of x; an index outside [0, x_rows) reads as a zero row.
 template <int TPR, int VPT>
 __global__ __launch_bounds__(256) void sym_quant_dynamic_vec_kernel(
     const f16 *__restrict__ x, int64_t rows, int nvec, float clip,
-    u32 *__restrict__ q, f16 *__restrict__ scale_out) {
+    u32 *__restrict__ q, f16 *__restrict__ scale_out, const int32_t *__restrict__ src_row,
+    int64_t x_rows) {
     constexpr int RPB = 256 / TPR;
     __shared__ float lds[4];
     const int lt = threadIdx.x % TPR;
     const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / TPR;
     const bool valid = row < rows;
-    const v8h *xr = reinterpret_cast<const v8h *>(x) + row * nvec;
+    int64_t srow = row;
+    bool live = valid;
+    if (src_row && valid) {
+        srow = src_row[row];
+        live = srow >= 0 && srow < x_rows;
+    }
+    const v8h *xr = reinterpret_cast<const v8h *>(x) + (live ? srow : 0) * nvec;
 
     v8h v[VPT];
     float amax = 0.f;
@@ -70,7 +79,7 @@ __global__ __launch_bounds__(256) void sym_quant_dynamic_vec_kernel(
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int idx = lt + i * TPR;
-        if (valid && idx < nvec) {
+        if (live && idx < nvec) {
             v[i] = __builtin_nontemporal_load(xr + idx);
         } else {
             v[i] = (v8h){0, 0, 0, 0, 0, 0, 0, 0};
@@ -135,22 +144,24 @@ __global__ __launch_bounds__(256) void sym_quant_dynamic_generic_kernel(
 
 template <int TPR, int VPT>
 static void launch_sqd_vec(const void *x, int64_t rows, int nvec, float clip, void *q,
-                           void *scale, hipStream_t st) {
+                           void *scale, hipStream_t st, const int32_t *src_row,
+                           int64_t x_rows) {
     constexpr int RPB = 256 / TPR;
     const int64_t blocks = srq_cdiv(rows, RPB);
     sym_quant_dynamic_vec_kernel<TPR, VPT><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-        (const f16 *)x, rows, nvec, clip, (u32 *)q, (f16 *)scale);
+        (const f16 *)x, rows, nvec, clip, (u32 *)q, (f16 *)scale, src_row, x_rows);
 }
 
 template <int TPR>
 static bool dispatch_sqd_vpt(const void *x, int64_t rows, int nvec, float clip, void *q,
-                             void *scale, hipStream_t st) {
+                             void *scale, hipStream_t st, const int32_t *src_row = nullptr,
+                             int64_t x_rows = 0) {
     const int vpt = (int)srq_cdiv(nvec, TPR);
-    if (vpt <= 1) launch_sqd_vec<TPR, 1>(x, rows, nvec, clip, q, scale, st);
-    else if (vpt <= 2) launch_sqd_vec<TPR, 2>(x, rows, nvec, clip, q, scale, st);
-    else if (vpt <= 4) launch_sqd_vec<TPR, 4>(x, rows, nvec, clip, q, scale, st);
-    else if (vpt <= 8) launch_sqd_vec<TPR, 8>(x, rows, nvec, clip, q, scale, st);
-    else if (vpt <= 16) launch_sqd_vec<TPR, 16>(x, rows, nvec, clip, q, scale, st);
+    if (vpt <= 1) launch_sqd_vec<TPR, 1>(x, rows, nvec, clip, q, scale, st, src_row, x_rows);
+    else if (vpt <= 2) launch_sqd_vec<TPR, 2>(x, rows, nvec, clip, q, scale, st, src_row, x_rows);
+    else if (vpt <= 4) launch_sqd_vec<TPR, 4>(x, rows, nvec, clip, q, scale, st, src_row, x_rows);
+    else if (vpt <= 8) launch_sqd_vec<TPR, 8>(x, rows, nvec, clip, q, scale, st, src_row, x_rows);
+    else if (vpt <= 16) launch_sqd_vec<TPR, 16>(x, rows, nvec, clip, q, scale, st, src_row, x_rows);
     else return false;
     return true;
 }
@@ -176,6 +187,28 @@ extern "C" int srq_sym_quant_dynamic(const void *x, int64_t rows, int64_t cols,
             (const f16 *)x, rows, cols, clip_ratio, nullptr, (uint8_t *)q, (f16 *)scale);
     }
     SRQ_LAUNCH_CHECK("sym_quant_dynamic");
+    return SRQ_OK;
+}
+
+extern "C" int srq_sym_quant_dynamic_rows(const void *x, int64_t x_rows, const int32_t *src_row,
+                                          int64_t rows, int64_t cols, float clip_ratio, void *q,
+                                          void *scale, void *stream) {
+    SRQ_CHECK_ARG(rows >= 0 && x_rows >= 0 && cols >= 0, "sym_quant_dynamic_rows: bad shape");
+    if (rows == 0) return SRQ_OK;
+    SRQ_CHECK_ARG(rows <= 0x7fffffffLL, "sym_quant_dynamic_rows: rows > 2^31-1");
+    SRQ_CHECK_ARG(x && src_row && q && scale, "sym_quant_dynamic_rows: null pointer");
+    SRQ_CHECK_ARG(cols > 0 && cols % 8 == 0 && cols <= 8 * 256 * 16,
+                  "sym_quant_dynamic_rows: cols=%lld must be a positive multiple of 8 <= 32768",
+                  (long long)cols);
+    SRQ_CHECK_ARG(srq_aligned(x, 16) && srq_aligned(q, 4),
+                  "sym_quant_dynamic_rows: x must be 16-byte and q 4-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    const int nvec = (int)(cols / 8);
+    if (nvec <= 64 * 16 && cols <= 4096)
+        dispatch_sqd_vpt<64>(x, rows, nvec, clip_ratio, q, scale, st, src_row, x_rows);
+    else
+        dispatch_sqd_vpt<256>(x, rows, nvec, clip_ratio, q, scale, st, src_row, x_rows);
+    SRQ_LAUNCH_CHECK("sym_quant_dynamic_rows");
     return SRQ_OK;
 }
 

@@ -221,7 +221,13 @@ class SignRotMoEBlock(torch.nn.Module):
         shape = hidden_states.shape
         x = hidden_states.reshape(-1, shape[-1])
         route = self.route(x)
-        codes = self._quant(x.to(torch.float16)).rows(route.token)
+        xh = x.to(torch.float16)
+        if (not self.asym and xh.shape[1] % 8 == 0 and route.token.dtype == torch.int32
+                and xh.is_contiguous()):
+            # quantize the expert-sorted rows straight from their tokens
+            codes = _Codes(*_CUDA.sym_quant_dynamic_rows(xh, route.token, self.clip_ratio), None)
+        else:
+            codes = self._quant(xh).rows(route.token)
         if self._swiglu_epilogue(codes):
             # SwiGLU in the gate/up launch's epilogue, then the plain
             # rotation + per-expert sign + quantizer (bit-identical)

@@ -482,6 +482,27 @@ def test_had_sign_quant_moe_equals_rotation_then_moe_quant(C, rows, n, K, expert
     assert torch.equal(q, q2), "codes"
 
 
+@pytest.mark.parametrize("rows,cols,R", [(512, 4096, 1024), (37, 768, 100), (5, 8, 3),
+                                        (64, 14336, 130)])
+def test_sym_quant_dynamic_rows_equals_quant_then_gather(C, rows, cols, R):
+    """Quantizing gathered rows in one launch: bit-identical to
+    sym_quant_dynamic then the row gather; out-of-range indices give zero
+    codes and scale 0."""
+    rng = np.random.default_rng(rows + cols + R)
+    x = to_dev((rng.standard_normal((rows, cols)) * 3).astype(np.float16))
+    idx_np = rng.integers(0, rows, R).astype(np.int32)
+    idx_np[: min(R, 2)] = [-1, rows][: min(R, 2)]
+    idx = to_dev(idx_np)
+    q, s = C.sym_quant_dynamic_rows(x, idx)
+    qa, sa = C.sym_quant_dynamic(x)
+    ok = torch.from_numpy((idx_np >= 0) & (idx_np < rows)).to(DEV)
+    safe = torch.where(ok, idx.long(), torch.zeros_like(idx.long()))
+    want_q = torch.where(ok[:, None], qa[safe], torch.zeros_like(qa[safe]))
+    want_s = torch.where(ok[:, None], sa[safe], torch.zeros_like(sa[safe]))
+    assert torch.equal(q, want_q), "codes"
+    assert torch.equal(s, want_s), "scales"
+
+
 @torch.no_grad()
 def test_block_fused_down_equals_unfused():
     blk = _block(4096, 14336, 8, 2, True, seed=5)
