@@ -51,10 +51,15 @@ SRQ_DEV v16f mfma32(v8h a, v8h b, v16f c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// K/V tiles are double-buffered in LDS: the next tile's global loads are
+// issued into registers before this tile's MFMAs and written to the other
+// buffer after them, so one barrier per tile covers both "tile t + 1 is in
+// LDS" and "every wave is done with the buffer tile t + 2 will overwrite",
+// and the load latency hides behind the compute.
 __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
-    __shared__ __align__(16) f16 Ks[KT * KS];
-    __shared__ __align__(16) f16 Vt[HD * VS];
-    __shared__ float kbias[KT];
+    __shared__ __align__(16) f16 Ks_[2][KT * KS];
+    __shared__ __align__(16) f16 Vt_[2][HD * VS];
+    __shared__ float kbias_[2][KT];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -92,104 +97,151 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
     const int kv_end = a.causal ? min(a.T, q0 + QT) : a.T;
     const int ntiles = (kv_end + KT - 1) / KT;
 
-    for (int t = 0; t < ntiles; ++t) {
+    // staging registers of one tile: K row tid / 4, 32 halves from (tid % 4) * 32;
+    // V keys 2 (tid % 32) + {0, 1}, d from 16 (tid / 32); key bias tid (< KT)
+    // (raw loads; the masking selects run at store time, after the MFMAs, so
+    // that no use of a loaded value forces its wait before them)
+    v8h kx[4], vx0[2], vx1[2];
+    bool kok = false, vok0 = false, vok1 = false;
+    float kbv = 0.f;
+    auto load_tile = [&](int t) __attribute__((always_inline)) {
         const int k0 = t * KT;
-        __syncthreads();
-        // K tile, row-major: thread -> row tid / 4, 32 halves from (tid % 4) * 32
         {
             const int r = tid >> 2, d0 = (tid & 3) * 32;
             const int key = k0 + r;
-            const bool ok = key < a.T && (!mb || mb[key] != 0);
-            const f16 *src = kb + (int64_t)(ok ? key : 0) * a.kv_tok + d0;
+            kok = key < a.T && (!mb || mb[key] != 0);
+            const f16 *src = kb + (int64_t)(kok ? key : 0) * a.kv_tok + d0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                v8h x = *reinterpret_cast<const v8h *>(src + 8 * i);
-                *reinterpret_cast<v8h *>(&Ks[r * KS + d0 + 8 * i]) = ok ? x : (v8h)(f16)0;
-            }
+            for (int i = 0; i < 4; ++i) kx[i] = *reinterpret_cast<const v8h *>(src + 8 * i);
         }
-        // V tile, transposed: thread -> keys 2 (tid % 32) + {0, 1}, d from 16 (tid / 32)
         {
             const int kp = tid & 31, d0 = (tid >> 5) * 16;
             const int key = k0 + 2 * kp;
-            const bool ok0 = key < a.T && (!mb || mb[key] != 0);
-            const bool ok1 = key + 1 < a.T && (!mb || mb[key + 1] != 0);
-            const f16 *s0 = vb + (int64_t)(ok0 ? key : 0) * a.kv_tok + d0;
-            const f16 *s1 = vb + (int64_t)(ok1 ? key + 1 : 0) * a.kv_tok + d0;
-            v8h x0[2], x1[2];
+            vok0 = key < a.T && (!mb || mb[key] != 0);
+            vok1 = key + 1 < a.T && (!mb || mb[key + 1] != 0);
+            const f16 *s0 = vb + (int64_t)(vok0 ? key : 0) * a.kv_tok + d0;
+            const f16 *s1 = vb + (int64_t)(vok1 ? key + 1 : 0) * a.kv_tok + d0;
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
-                v8h u0 = *reinterpret_cast<const v8h *>(s0 + 8 * i);
-                v8h u1 = *reinterpret_cast<const v8h *>(s1 + 8 * i);
-                x0[i] = ok0 ? u0 : (v8h)(f16)0;
-                x1[i] = ok1 ? u1 : (v8h)(f16)0;
-            }
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                v2h pr;
-                pr[0] = x0[j / 8][j % 8];
-                pr[1] = x1[j / 8][j % 8];
-                *reinterpret_cast<v2h *>(&Vt[(d0 + j) * VS + 2 * kp]) = pr;
+                vx0[i] = *reinterpret_cast<const v8h *>(s0 + 8 * i);
+                vx1[i] = *reinterpret_cast<const v8h *>(s1 + 8 * i);
             }
         }
         if (tid < KT) {
             const int key = k0 + tid;
             const bool ok = key < a.T && (!mb || mb[key] != 0);
-            kbias[tid] = ok ? 0.f : -INFINITY;
+            kbv = ok ? 0.f : -INFINITY;
         }
-        __syncthreads();
-        if (a.causal && k0 > wave_last) continue;   // no key of this tile is visible
+    };
+    // K row-major, V transposed (V^T rows d, columns keys)
+    auto store_tile = [&](int buf) __attribute__((always_inline)) {
+        {
+            const int r = tid >> 2, d0 = (tid & 3) * 32;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<v8h *>(&Ks_[buf][r * KS + d0 + 8 * i]) =
+                    kok ? kx[i] : (v8h)(f16)0;
+        }
+        {
+            const int kp = tid & 31, d0 = (tid >> 5) * 16;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                v2h pr;
+                pr[0] = vok0 ? vx0[j / 8][j % 8] : (f16)0;
+                pr[1] = vok1 ? vx1[j / 8][j % 8] : (f16)0;
+                *reinterpret_cast<v2h *>(&Vt_[buf][(d0 + j) * VS + 2 * kp]) = pr;
+            }
+        }
+        if (tid < KT) kbias_[buf][tid] = kbv;
+    };
 
-        // S^T, two 32-key blocks
-        v16f s[2];
+    if (ntiles > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < ntiles; ++t) {
+        const int k0 = t * KT;
+        const int buf = t & 1;
+        const f16 *Ks = Ks_[buf];
+        const f16 *Vt = Vt_[buf];
+        const float *kbias = kbias_[buf];
+        if (t + 1 < ntiles) load_tile(t + 1);  // in flight during this tile's MFMAs
+        // this tile's compute (returns early when no key is visible)
+        [&]() __attribute__((always_inline)) {
+            if (a.causal && k0 > wave_last) return;   // no key of this tile is visible
+
+            // S^T, two 32-key blocks
+            v16f s[2];
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-            s[sb] = (v16f)0.f;
-            const f16 *kr = &Ks[(32 * sb + ln) * KS + 8 * g];
+            for (int sb = 0; sb < 2; ++sb) {
+                s[sb] = (v16f)0.f;
+                const f16 *kr = &Ks[(32 * sb + ln) * KS + 8 * g];
 #pragma unroll
-            for (int kk = 0; kk < HD / 16; ++kk)
-                s[sb] = mfma32(*reinterpret_cast<const v8h *>(kr + 16 * kk), qf[kk], s[sb]);
-        }
-        // scale, mask, tile max
-        float mt = -INFINITY;
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int kr = 32 * sb + 8 * (v / 4) + 4 * g + (v % 4);
-                float x = kbias[kr] == 0.f ? s[sb][v] * a.c : -INFINITY;
-                if (a.causal && k0 + kr > qrow) x = -INFINITY;
-                s[sb][v] = x;
-                mt = fmaxf(mt, x);
+                for (int kk = 0; kk < HD / 16; ++kk)
+                    s[sb] = mfma32(*reinterpret_cast<const v8h *>(kr + 16 * kk), qf[kk], s[sb]);
             }
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float mn = fmaxf(m, mt);
-        const float mu = mn == -INFINITY ? 0.f : mn;
-        const float alpha = __builtin_amdgcn_exp2f(m - mu);
-        m = mn;
-        float ps = 0.f;
-        v8h pb[4];
+            // scale, mask, tile max.  A tile with every key live and visible to
+            // every row of the wave (no mask, inside the sequence, below the
+            // causal diagonal) skips the per-key tests: the same values.
+            float mt = -INFINITY;
+            const bool full = !mb && k0 + KT <= a.T && (!a.causal || k0 + KT - 1 <= q0 + wave * 32);
+            if (full) {
 #pragma unroll
-        for (int sb = 0; sb < 2; ++sb)
+                for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const float p = __builtin_amdgcn_exp2f(s[sb][v] - mu);
-                ps += p;
-                pb[2 * sb + v / 8][v % 8] = (f16)p;
+                    for (int v = 0; v < 16; ++v) {
+                        const float x = s[sb][v] * a.c;
+                        s[sb][v] = x;
+                        mt = fmaxf(mt, x);
+                    }
+            } else {
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int kr = 32 * sb + 8 * (v / 4) + 4 * g + (v % 4);
+                        float x = kbias[kr] == 0.f ? s[sb][v] * a.c : -INFINITY;
+                        if (a.causal && k0 + kr > qrow) x = -INFINITY;
+                        s[sb][v] = x;
+                        mt = fmaxf(mt, x);
+                    }
             }
-        l = l * alpha + ps;
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float mn = fmaxf(m, mt);
+            const float mu = mn == -INFINITY ? 0.f : mn;
+            const float alpha = __builtin_amdgcn_exp2f(m - mu);
+            m = mn;
+            float ps = 0.f;
+            v8h pb[4];
 #pragma unroll
-        for (int i = 0; i < HD / 32; ++i) o[i] *= alpha;
-        // O^T += V^T P^T; PV step st covers keys 16 st .. 16 st + 15 of the tile
+            for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
+                for (int v = 0; v < 16; ++v) {
+                    const float p = __builtin_amdgcn_exp2f(s[sb][v] - mu);
+                    ps += p;
+                    pb[2 * sb + v / 8][v % 8] = (f16)p;
+                }
+            l = l * alpha + ps;
+            // alpha is exactly 1 wherever the running max did not move
+            if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-            for (int db = 0; db < HD / 32; ++db) {
-                const f16 *vr = &Vt[(32 * db + ln) * VS + 16 * st + 4 * g];
-                v4h lo = *reinterpret_cast<const v4h *>(vr);
-                v4h hi = *reinterpret_cast<const v4h *>(vr + 8);
-                v8h av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o[db] = mfma32(av, pb[st], o[db]);
+                for (int i = 0; i < HD / 32; ++i) o[i] *= alpha;
             }
+            // O^T += V^T P^T; PV step st covers keys 16 st .. 16 st + 15 of the tile
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+#pragma unroll
+                for (int db = 0; db < HD / 32; ++db) {
+                    const f16 *vr = &Vt[(32 * db + ln) * VS + 16 * st + 4 * g];
+                    v4h lo = *reinterpret_cast<const v4h *>(vr);
+                    v4h hi = *reinterpret_cast<const v4h *>(vr + 8);
+                    v8h av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    o[db] = mfma32(av, pb[st], o[db]);
+                }
+        }();
+        if (t + 1 < ntiles) store_tile(buf ^ 1);
+        __syncthreads();
     }
 
     if (qrow >= a.T) return;
