@@ -406,6 +406,102 @@ int srq_had512_mfma(const void *x, int64_t rows, int64_t n, int64_t K, const voi
                     const int32_t *sign_row = nullptr, int64_t n_sign_rows = 0,
                     void *qzero = nullptr, int bf6 = 0);
 
+// Rotation + sign + quantizer of rows of n = 256 E (a power of two, K = 1:
+// the plain FWHT) for the decode-sized row counts of a q/k/v-shaped
+// QLinear: one 256-thread block per row, thread t holding elements
+// [E t, E t + E) in registers.  The FWHT stages run in ascending index bit
+// as everywhere else, so the fp32 values are those of the LDS kernel:
+// bits below log2 E inside the thread, the next 6 bits across the lanes of
+// a wave (shuffles), the top 2 bits across the 4 waves (one LDS exchange).
+// Then the finish and the quantizer of rotate_kernel (fp16(y * scale) *
+// sign, amax, fp16(amax / 7) (* clip), codes), one 4E-byte store per thread.
+namespace {
+
+constexpr int kPow2Threads = 256;
+
+template <int E>
+__global__ __launch_bounds__(kPow2Threads) void rot_pow2_quant_kernel(RotArgs a) {
+    static_assert(E >= 8 && E <= 32 && (E & (E - 1)) == 0, "E");
+    constexpr int n = kPow2Threads * E;
+    __shared__ float xch[4][E][64];
+    __shared__ float red[4];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
+        const f16 *xr = reinterpret_cast<const f16 *>(a.x) + row * n + E * t;
+        float v[E];
+#pragma unroll
+        for (int j = 0; j < E; j += 8) {
+            const v8h h = *reinterpret_cast<const v8h *>(xr + j);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[j + i] = (float)h[i];
+        }
+        // bits 0 .. log2 E - 1
+#pragma unroll
+        for (int h = 1; h < E; h <<= 1)
+#pragma unroll
+            for (int i = 0; i < E; ++i)
+                if ((i & h) == 0) {
+                    const float x0 = v[i], x1 = v[i + h];
+                    v[i] = x0 + x1;
+                    v[i + h] = x0 - x1;
+                }
+        // the next 6 bits: lane bit s; the lower partner keeps x0 + x1, the
+        // upper x0 - x1 (x0 the lower one's value)
+#pragma unroll
+        for (int sbit = 0; sbit < 6; ++sbit) {
+            const bool upper = (lane >> sbit) & 1;
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const float p = __shfl_xor(v[i], 1 << sbit, 64);
+                v[i] = upper ? p - v[i] : v[i] + p;
+            }
+        }
+        // the top 2 bits: the 4 waves' values of (lane, i), FWHT_4 in order
+#pragma unroll
+        for (int i = 0; i < E; ++i) xch[wave][i][lane] = v[i];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            const float x0 = xch[0][i][lane], x1 = xch[1][i][lane];
+            const float x2 = xch[2][i][lane], x3 = xch[3][i][lane];
+            const float y0 = x0 + x1, y1 = x0 - x1, y2 = x2 + x3, y3 = x2 - x3;
+            const float z0 = y0 + y2, z1 = y1 + y3, z2 = y0 - y2, z3 = y1 - y3;
+            v[i] = wave == 0 ? z0 : wave == 1 ? z1 : wave == 2 ? z2 : z3;
+        }
+        // finish: fp16(y * scale), sign; row amax (NaN-ignoring)
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < E; ++i) {
+            float x = round16(v[i] * a.scale);
+            if (a.sign) x *= (float)a.sign[E * t + i];
+            v[i] = x;
+            amax = fmaxf(amax, fabsf(round16(x)));
+        }
+        amax = wave_max(amax);
+        if (lane == 0) red[wave] = amax;
+        __syncthreads();
+        amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        f16 sc = f16_rn(amax / 7.f);
+        if (a.clip != 1.f) sc = f16_rn((float)sc * a.clip);
+        if (t == 0) a.qscale[row] = sc;
+        const float rs = sym_recip((float)sc);
+        u32 w[E / 8];
+#pragma unroll
+        for (int k = 0; k < E / 8; ++k) {
+            w[k] = 0;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                w[k] |= (u32)(sym_code_r(round16(v[8 * k + e]), rs) & 0xF) << (4 * e);
+        }
+        u32 *qr = a.q + row * (n / 8) + (E / 8) * t;
+#pragma unroll
+        for (int k = 0; k < E / 8; ++k) qr[k] = w[k];
+        __syncthreads();  // xch and red are reused by the next row
+    }
+}
+
+}  // namespace
+
 extern "C" int srq_hadamard_transform(const void *x, void *out, int64_t rows, int64_t n,
                                       float scale, int dtype, void *stream) {
     SRQ_CHECK_ARG(dtype == 0 || dtype == 1, "hadamard_transform: dtype must be 0 (f16) or 1 (f32)");
@@ -484,6 +580,14 @@ extern "C" int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_
     a.qscale = (f16 *)scale;
     if (!fp32_had && srq_had512_mfma(x, rows, n, K, hadK, sign, clip_ratio, q, scale, nullptr,
                                      (hipStream_t)stream)) {
+        SRQ_LAUNCH_CHECK("had_sign_quant");
+        return SRQ_OK;
+    }
+    if (!fp32_had && K == 1 && (n == 2048 || n == 4096 || n == 8192)) {
+        const dim3 grid((unsigned)std::min<int64_t>(rows, 4096)), block(kPow2Threads);
+        if (n == 2048) rot_pow2_quant_kernel<8><<<grid, block, 0, (hipStream_t)stream>>>(a);
+        else if (n == 4096) rot_pow2_quant_kernel<16><<<grid, block, 0, (hipStream_t)stream>>>(a);
+        else rot_pow2_quant_kernel<32><<<grid, block, 0, (hipStream_t)stream>>>(a);
         SRQ_LAUNCH_CHECK("had_sign_quant");
         return SRQ_OK;
     }

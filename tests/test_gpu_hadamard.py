@@ -88,6 +88,10 @@ def test_online_hadamard_fp32_mode(C):
                                     (14336, 1), (14336, 513), (14336, 1024),
                                     (6144, 9), (10240, 13), (28672, 700), (12288, 3),
                                     (20480, 2),
+                                    # the register/shuffle kernel of the plain
+                                    # 2^k rotations (one block per row, grid
+                                    # stride past 4096 rows)
+                                    (4096, 1), (2048, 5), (8192, 7), (8192, 1), (4096, 4200),
                                     # config 2 at M = 8192, config 4 at M = 4096
                                     (14336, 8192), (28672, 4096)])
 @pytest.mark.parametrize("use_sign", [False, True])
