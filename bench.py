@@ -350,9 +350,10 @@ def bench_qlinear_asym(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9):
 
 def bench_mlp70b(dev, M, seed, hidden=8192, ffn=28672, reps=10, min_bytes=2.2e9):
     """Config 4: Llama-3-70B-shape W4A4 MLP block: per-token int4 quant of x,
-    the gate and up W4A4 linears as one GEMM over the concatenated weights
-    (the decode layer's layout), SwiGLU + had_28 x H_1024 rotation + sign +
-    quant in one launch, down W4A4 linear."""
+    the gate and up W4A4 linears as one GEMM over their rows interleaved in
+    blocks of 8 with the SwiGLU in its epilogue (the decode layer's layout),
+    had_28 x H_1024 rotation + sign + quant in one launch, down W4A4
+    linear."""
     from signrot_amd import _CUDA
     from signrot_amd.functional.hadamard import get_hadK
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -364,6 +365,9 @@ def bench_mlp70b(dev, M, seed, hidden=8192, ffn=28672, reps=10, min_bytes=2.2e9)
     Wgu = [_rand_w(2 * ffn, hidden, dev, g) for _ in range(nsets)]
     Wd = [_rand_w(hidden, ffn, dev, g) for _ in range(nsets)]
     sgu = torch.full((2 * ffn,), 1.0 / hidden, dtype=torch.float16, device=dev)
+    # weight preparation (once, untimed): gate/up rows in blocks of 8
+    il = [_CUDA.interleave_gate_up(w, sgu, ffn) for w in Wgu]
+    del Wgu
     sd = torch.full((hidden,), 1.0 / ffn, dtype=torch.float16, device=dev)
     x = torch.randn(M, hidden, device=dev, generator=g)
     ch = torch.randperm(hidden, device=dev, generator=g)[:8]
@@ -373,15 +377,15 @@ def bench_mlp70b(dev, M, seed, hidden=8192, ffn=28672, reps=10, min_bytes=2.2e9)
     def mlp(i):
         j = i % nsets
         q, s = _CUDA.sym_quant_dynamic(x)
-        gu = _CUDA.w4a4_linear(q, s.view(-1), Wgu[j], sgu)
-        qd, sdn = _CUDA.swiglu_had_sign_quant(gu, hadk, k, sign)
+        a = _CUDA.w4a4_linear_swiglu(q, s.view(-1), il[j][0], il[j][1])
+        qd, sdn = _CUDA.had_sign_quant(a, hadk, k, sign)
         return _CUDA.w4a4_linear(qd, sdn.view(-1), Wd[j], sd)
 
     st = torch.cuda.current_stream()
     t = _time_launches(mlp, max(reps, nsets), st) * 1e3
     ops = 2.0 * M * 3 * hidden * ffn
     nbytes = wbytes + M * hidden * 2 * 2
-    del Wgu, Wd
+    del il, Wd
     torch.cuda.empty_cache()
     return {"M": M, "hidden": hidden, "ffn": ffn, "hadamard": f"had_{k} x H_{ffn // k}",
             "weight_sets": nsets, "mlp": _roof(t, ops, nbytes)}

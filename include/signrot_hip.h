@@ -95,17 +95,18 @@ int srq_w4a4_linear(const void *A, const void *a_scale, const void *B,
                     const void *b_scale, const void *bias, int64_t M, int64_t N,
                     int64_t K, void *out, void *stream);
 
-/* Decode-shape gate/up projection with the SwiGLU in the epilogue: B u8
+/* Gate/up projection with the SwiGLU in the epilogue: B u8
  * [N, K/2] holds the gate and up weight rows interleaved in blocks of 8
  * (rows 16 c .. 16 c + 7 = gate rows 8 c .., rows 16 c + 8 .. = up rows
  * 8 c ..), b_scale likewise; out f16 [M, N/2] = swiglu(g, u) element-wise
  * with g, u the srq_w4a4_linear outputs of the paired columns (the
  * fused.cu:367-390 SwiGLU, rounded as srq_swiglu).  Bit-identical to
  * srq_w4a4_linear over the gate and up weights followed by srq_swiglu.
- * M <= 32 and N % 16 == 0 (the weight-streaming kernel), else
- * SRQ_EINVAL / SRQ_EUNSUPPORTED.  Replaces the gate_proj / up_proj
+ * Any M (every kernel of srq_w4a4_linear's dispatch ends in the SwiGLU row
+ * pass; the skinny and split-K forms are not used); N % 16 == 0 and out
+ * 16-byte aligned, else SRQ_EINVAL.  Replaces the gate_proj / up_proj
  * Linear4bit pair and the SwiGLU before the down_proj's online Hadamard
- * (e2e/quantized_llama/modeling_llama.py:125-137) in a decode step. */
+ * (e2e/quantized_llama/modeling_llama.py:125-137). */
 int srq_w4a4_linear_swiglu(const void *A, const void *a_scale, const void *B,
                            const void *b_scale, int64_t M, int64_t N, int64_t K, void *out,
                            void *stream);

@@ -154,7 +154,7 @@ def interleave_gate_up(w, s, ffn):
 
 
 def w4a4_linear_swiglu(A, a_scale, B_il, b_scale_il):
-    """swiglu(gate, up) of the gate/up projection in one launch, for M <= 32:
+    """swiglu(gate, up) of the gate/up projection in one launch (any M):
     B_il / b_scale_il from interleave_gate_up; out f16 [M, N/2]."""
     _check("w4a4_linear_swiglu", [(A, "A"), (a_scale, "a_scale"), (B_il, "B"),
                                   (b_scale_il, "b_scale")],

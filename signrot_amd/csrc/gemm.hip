@@ -279,6 +279,28 @@ SRQ_DEV void store_block_lds_impl(const Epi &e, int64_t M, int64_t N, int64_t mb
             }
         }
     }
+    if (e.swiglu) {
+        // 16 staged columns per lane (8 gate, 8 up: N % 16 == 0, blocks of
+        // 16 aligned) -> 8 swiglu1 outputs of the [M, N/2] output, 16 bytes
+        constexpr int LPS = W / 16;
+        constexpr int RPS = 64 / LPS;
+        static_assert(LPS >= 1 && 64 % LPS == 0, "swiglu row shape");
+        const int c16 = (lane % LPS) * 16;
+        const int64_t gs0 = nb + c16;
+#pragma unroll
+        for (int r0 = 0; r0 < BS * FM; r0 += RPS) {
+            const int lr = r0 + lane / LPS;
+            const int64_t gm = mb + lr;
+            if (lr >= BS * FM || (CHECK && (gm >= M || gs0 + 16 > N))) continue;
+            const v8h gv = *reinterpret_cast<const v8h *>(tile + lr * W + c16);
+            const v8h uv = *reinterpret_cast<const v8h *>(tile + lr * W + c16 + 8);
+            v8h o;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) o[k] = swiglu1((float)gv[k], (float)uv[k]);
+            *reinterpret_cast<v8h *>(e.out + gm * (N / 2) + gs0 / 2) = o;
+        }
+        return;
+    }
     constexpr int LPR = W / 8;     // lanes per row (16 bytes each)
     constexpr int RPI = 64 / LPR;  // rows per store instruction
     static_assert(LPR >= 1 && 64 % LPR == 0 && (BS * FM) % RPI == 0, "row store shape");
@@ -1337,6 +1359,7 @@ struct GroupedArgs {
     // residual [M, N] (either may be null)
     int64_t M;
     const f16 *bias, *res;
+    int swiglu;  // dense form: the columns are blocks of 8 gate, 8 up; out [M, N/2]
     // split-K form (the SPLITK instantiation): problem p is the dense
     // product over K codes [p Kc, min((p + 1) Kc, K)), its int32 partial
     // (shifted down like the dense accumulator) at ws_c + p M N
@@ -1530,7 +1553,8 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             const bool second = !DENSE && g.pair && (p & 1);
             const int64_t ex = DENSE ? 0 : g.pair ? p >> 1 : p;
             Epi e{};
-            e.out = (second ? g.out2 : g.out) + pr.row0 * (FORM == kFormSwiglu ? g.N / 2 : g.N);
+            const bool sw = FORM == kFormSwiglu || (DENSE && g.swiglu);
+            e.out = (second ? g.out2 : g.out) + pr.row0 * (sw ? g.N / 2 : g.N);
             e.sa = g.sa + pr.row0;
             e.sb = (second ? g.sb2 : g.sb) + ex * g.N;
             e.ua = UA;
@@ -1542,7 +1566,7 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                 e.bias = g.bias;
                 e.res = g.res;
             }
-            if constexpr (FORM == kFormSwiglu)
+            if (sw)
                 store_block_lds32_swiglu<32, FM, FN>(
                     e, pr.m, pr.n, m0 + wm * (FM * 32), n0 + wn * (FN * 32), acc, lane,
                     reinterpret_cast<int32_t *>(epi_lds + wave * kEpiTile));
@@ -1667,20 +1691,20 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         fill_zero_epilogue<<<dim3((unsigned)blocks), dim3(256), 0, st>>>(M, N, e);
     } else if (launch_stream<UA>(a, b, M, N, K, e, st)) {
         // M <= 32: persistent weight-streaming kernel
-    } else if (M <= 16) {
+    } else if (M <= 16 && !e.swiglu) {
         gemm_skinny_kernel<1, 8, 4, UA><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
-    } else if (M <= 32) {
+    } else if (M <= 32 && !e.swiglu) {
         gemm_skinny_kernel<2, 8, 4, UA><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
-    } else if (M <= 64) {
+    } else if (M <= 64 && !e.swiglu) {
         gemm_skinny_kernel<4, 8, 2, UA><<<dim3((unsigned)srq_cdiv(N, 16), 1), dim3(512), 0, st>>>(
             a, b, M, N, K, e);
     } else if (M >= 1024 && srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN) >= 256) {
         // enough 256 x 256 tiles to cover the 256 CUs
         const int64_t tiles = srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN);
         gemm_sq_kernel<128, 2, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(a, b, M, N, K, e);
-    } else if (sk.S && ws_bytes >= (int64_t)sk.S * M * N * 4) {
+    } else if (sk.S && !e.swiglu && ws_bytes >= (int64_t)sk.S * M * N * 4) {
         // split-K: S dense problems over K-chunks write int32 partials,
         // then one pass sums them and runs the epilogue
         GroupedArgs g{};
@@ -1724,6 +1748,7 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         g.res = e.res;
         g.zr = e.zr;
         g.ws = e.ws;
+        g.swiglu = e.swiglu;
         const int64_t tiles = srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN);
         gemm_grouped_kernel<4, UA, kFormDense>
             <<<dim3((unsigned)std::min<int64_t>(tiles, kGroupedGrid)), dim3(512), 0, st>>>(g);
@@ -1826,24 +1851,20 @@ extern "C" int srq_w4a4_linear_swiglu(const void *A, const void *a_scale, const 
                                       void *out, void *stream) {
     int rc = check_gemm("w4a4_linear_swiglu", A, B, M, N, K);
     if (rc) return rc;
-    SRQ_CHECK_ARG(M <= 32, "w4a4_linear_swiglu: M=%lld > 32 (weight-streaming shapes only)",
-                  (long long)M);
     SRQ_CHECK_ARG(N % 16 == 0, "w4a4_linear_swiglu: N=%lld must be a multiple of 16",
                   (long long)N);
     SRQ_CHECK_ARG(K > 0, "w4a4_linear_swiglu: K must be positive");
     if (M == 0 || N == 0) return SRQ_OK;
     SRQ_CHECK_ARG(out && a_scale && b_scale, "w4a4_linear_swiglu: null pointer");
+    SRQ_CHECK_ARG(srq_aligned(out, 16), "w4a4_linear_swiglu: out must be 16-byte aligned");
     Epi e{};
     e.out = (f16 *)out;
     e.sa = (const f16 *)a_scale;
     e.sb = (const f16 *)b_scale;
     e.swiglu = 1;
-    if (!launch_stream<false>((const uint8_t *)A, (const uint8_t *)B, M, N, K, e,
-                              (hipStream_t)stream)) {
-        srq_set_error("w4a4_linear_swiglu: M=%lld N=%lld K=%lld outside the weight-streaming "
-                      "kernel's limits", (long long)M, (long long)N, (long long)K);
-        return SRQ_EUNSUPPORTED;
-    }
+    // every kernel of the dispatch but the skinny and split-K forms (which
+    // it then skips) ends in the swiglu row pass
+    launch_gemm<false>((const uint8_t *)A, (const uint8_t *)B, M, N, K, e, (hipStream_t)stream);
     SRQ_LAUNCH_CHECK("w4a4_linear_swiglu");
     return SRQ_OK;
 }

@@ -118,7 +118,7 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         batch_decode_i4 -> merge_head_had_quant (split-KV merge, head-axis
         Hadamard + quantizer; head_had_quant when unsplit) -> o_proj GEMM +
         residual -> rmsnorm_quant -> gate/up GEMM with the SwiGLU in its
-        epilogue (B <= 32; else the GEMM and swiglu_had_sign_quant) ->
+        epilogue (ffn % 8 == 0; else the GEMM and swiglu_had_sign_quant) ->
         had_sign_quant -> down GEMM + residual."""
         B = hidden_states.shape[0]
         x2 = hidden_states.view(B, self.hidden)
@@ -130,7 +130,7 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         qa, sa = cache.decode_rotated_quant(q_rot, self.layer_idx, _inv_sqrt_f32(self.n_heads))
         x2 = _CUDA.w4a4_linear_residual(qa, sa.view(-1), self.w_o, self.s_o, x2)
         q2, s2 = _CUDA.rmsnorm_quant(x2, n2.eps, n2.mean_dim)
-        if B <= 32 and self.ffn % 8 == 0:
+        if self.ffn % 8 == 0:
             # SwiGLU in the gate/up GEMM's epilogue, then the plain rotation
             w_il, s_il = self._gate_up_interleaved()
             a = _CUDA.w4a4_linear_swiglu(q2, s2.view(-1), w_il, s_il)

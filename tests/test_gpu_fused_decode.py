@@ -188,11 +188,17 @@ def test_qkv_rope_had_append_equals_update_chain(B, T, Hq, Hkv, page, cos_batch)
         assert_bitexact(to_np(out_b), to_np(out_a), f"attention output (layer {li})")
 
 
-@pytest.mark.parametrize("M,ffn,K", [(32, 14336, 4096), (1, 14336, 4096), (16, 896, 1024),
-                                     (7, 8, 256), (32, 28672, 8192), (20, 1000, 4128)])
+@pytest.mark.parametrize("M,ffn,K", [
+    (32, 14336, 4096), (1, 14336, 4096), (16, 896, 1024), (7, 8, 256), (32, 28672, 8192),
+    (20, 1000, 4128),
+    # every other kernel of the dispatch: ring (the skinny kernel is skipped),
+    # dense grouped, big, 256 x 256 square tiles
+    (48, 896, 1024), (70, 256, 256), (600, 512, 2048), (128, 14336, 4096), (300, 4096, 1024),
+    (1100, 1504, 1024), (4096, 4096, 512), (2048, 14336, 512)])
 def test_w4a4_linear_swiglu_equals_linear_then_swiglu(M, ffn, K):
-    """The SwiGLU epilogue of the gate/up projection: bit-identical to the
-    fp16 gate/up GEMM outputs fed to srq_swiglu (fused.cu:367-390)."""
+    """The SwiGLU epilogue of the gate/up projection, on every kernel the
+    shape dispatches to: bit-identical to the fp16 gate/up GEMM outputs fed
+    to srq_swiglu (fused.cu:367-390)."""
     C = _ops()
     rng = np.random.default_rng(M * 7 + ffn + K)
     A = to_dev(rng.integers(0, 256, (M, K // 2)).astype(np.uint8))
@@ -207,13 +213,13 @@ def test_w4a4_linear_swiglu_equals_linear_then_swiglu(M, ffn, K):
     assert_bitexact(to_np(got), to_np(want), "swiglu(gate, up)")
 
 
-def test_w4a4_linear_swiglu_rejects_prefill_rows():
+def test_w4a4_linear_swiglu_rejects_unpaired_columns():
     C = _ops()
     A = torch.zeros(33, 128, dtype=torch.uint8, device="cuda")
-    w = torch.zeros(32, 128, dtype=torch.uint8, device="cuda")
-    with pytest.raises(RuntimeError, match="32"):
+    w = torch.zeros(40, 128, dtype=torch.uint8, device="cuda")
+    with pytest.raises(RuntimeError, match="16"):
         C.w4a4_linear_swiglu(A, torch.ones(33, dtype=torch.float16, device="cuda"), w,
-                             torch.ones(32, dtype=torch.float16, device="cuda"))
+                             torch.ones(40, dtype=torch.float16, device="cuda"))
 
 
 @pytest.mark.parametrize("B,T,Hq,Hkv,chunks", [(32, 4096, 32, 8, 2), (3, 300, 8, 2, 5),
