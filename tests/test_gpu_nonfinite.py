@@ -156,6 +156,39 @@ def test_swiglu_had_sign_quant_moe_nonfinite(C):
     assert_bitexact(to_np(q), to_np(q2), "codes")
 
 
+@pytest.mark.parametrize("n,K", [(14336, 28), (28672, 28)])
+def test_had_sign_quant_moe_nonfinite(C, n, K):
+    """The plain MoE down-proj input op (rotation + per-expert sign rows +
+    quantizer) on rows holding NaN / inf: equal to the rotation then
+    sym_quant_dynamic_moe."""
+    rows, experts = 27, 8
+    rng = np.random.default_rng(n + 1)
+    x = to_dev(_special_rows(rng, rows, n, 2.0))
+    eid = to_dev(rng.integers(0, experts, rows).astype(np.int32))
+    sign = to_dev(rng.choice([-1, 1], (experts, n)).astype(np.int8))
+    hk = _hadk(K)
+    q, s = C.had_sign_quant_moe(x, hk, K, sign, eid, 1.0)
+    rot = C.online_hadamard(x, hk, K, None)
+    q2, s2 = C.sym_quant_dynamic_moe(rot, sign, eid, 1.0)
+    torch.cuda.synchronize()
+    assert_bitexact(to_np(s), to_np(s2), "scales")
+    assert_bitexact(to_np(q), to_np(q2), "codes")
+
+
+def test_sym_quant_dynamic_rows_nonfinite(C):
+    """Rows holding NaN / inf quantized straight from gathered token rows:
+    equal to sym_quant_dynamic of the gathered rows."""
+    rows, cols = 27, 4096
+    rng = np.random.default_rng(11)
+    x = to_dev(_special_rows(rng, rows, cols, 3.0))
+    idx = to_dev(rng.integers(0, rows, 54).astype(np.int32))
+    q, s = C.sym_quant_dynamic_rows(x, idx)
+    q2, s2 = C.sym_quant_dynamic(x[idx.long()].contiguous())
+    torch.cuda.synchronize()
+    assert_bitexact(to_np(s), to_np(s2), "scales")
+    assert_bitexact(to_np(q), to_np(q2), "codes")
+
+
 @pytest.mark.parametrize("rows,cols", [(27, 4096), (18, 8192), (9, 1024)])
 def test_rmsnorm_quant_nonfinite(C, rows, cols):
     """A NaN makes the sum of squares NaN (the whole row NaN: scale 0); an
