@@ -702,14 +702,17 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
         finish(dprev, NT - 1);
 
         // ---- K-mix: round to fp16 and keep (MODE 0 and 2 apply the sign
-        // here; MODE 1 folds it into the quantizer).  MODE 1: row max of |out|
-        // (NaN-ignoring, as the reference's fmaxf) and a NaN-propagating max of
-        // |out| in fp32, which flags rows holding a NaN or an output that
-        // rounds to inf (|out| >= 65520).  MODE 2: packed min and max of the
-        // signed fp16 values (NaN-ignoring, as fminf / fmaxf) and the packed
-        // NaN-propagating max of |x|.  Lanes past the K chunks hold no outputs
-        // and stay out of the flags.
-        float amax = 0.f, anan = 0.f;
+        // here; MODE 1 folds it into the quantizer).  MODE 1: NaN-propagating
+        // packed max and min of the rounded outputs (v_pk_maximum3 /
+        // v_pk_minimum3, four values per instruction); rounding is monotone
+        // and odd-symmetric, so max(mx, -mn) is fp16(max |out|) for a row
+        // free of NaN, and inf or NaN flags a row holding a NaN or an output
+        // that rounds to inf (|out| >= 65520).  A wave holding such a lane
+        // recomputes its NaN-ignoring max (the reference's fmaxf) from the
+        // kept values.  MODE 2: packed min and max of the signed fp16 values
+        // (NaN-ignoring, as fminf / fmaxf) and the packed NaN-propagating max
+        // of |x|.  Lanes past the K chunks hold no outputs and stay out of
+        // the reductions and flags.
         v2h mn2 = (v2h){(f16)__builtin_inff(), (f16)__builtin_inff()};
         v2h mx2 = -mn2, ab2 = (v2h){0, 0};
 #pragma unroll
@@ -722,11 +725,15 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
 #pragma unroll
                 for (int p = 0; p < 8; ++p) {
                     if (MODE == 1) {
-                        amax = absmax3(amax, z[2 * p], z[2 * p + 1]);
-                        anan = __builtin_elementwise_maximum(
-                            __builtin_elementwise_maximum(anan, fabsf(z[2 * p])),
-                            fabsf(z[2 * p + 1]));
                         w[h][i1][p] = pk16(z[2 * p], z[2 * p + 1]);
+                        if (p & 1) {
+                            const v2h v0 = __builtin_bit_cast(v2h, w[h][i1][p - 1]);
+                            const v2h v1 = __builtin_bit_cast(v2h, w[h][i1][p]);
+                            mx2 = __builtin_elementwise_maximum(
+                                __builtin_elementwise_maximum(mx2, v0), v1);
+                            mn2 = __builtin_elementwise_minimum(
+                                __builtin_elementwise_minimum(mn2, v0), v1);
+                        }
                     } else {
                         w[h][i1][p] = pk16(z[2 * p], z[2 * p + 1]) ^ msk[h][i1][p];
                     }
@@ -761,9 +768,32 @@ __global__ __launch_bounds__(256, (SW || P == 2 || MODE == 2) ? 1 : 2) void had5
         }
         if constexpr (MODE == 1) {
             // partial row max |x| and non-finite flag of this wave
-            amax = wave_max_dpp(amax);
-            const bool badl = ln < a.KC && !(anan < 65520.f);
+            float al = __builtin_elementwise_maximum(
+                __builtin_elementwise_maximum((float)mx2[0], (float)mx2[1]),
+                -__builtin_elementwise_minimum((float)mn2[0], (float)mn2[1]));
+            if (ln >= a.KC) al = 0.f;
+            const bool badl = !(al <= 65504.f);
             const bool wbad = __builtin_amdgcn_ballot_w64(badl) != 0;
+            if (wbad) {
+                // NaN-ignoring max |x| of this lane's kept outputs
+                al = 0.f;
+                if (ln < a.KC) {
+#pragma unroll
+                    for (int h = 0; h < P; ++h)
+#pragma unroll
+                        for (int i1 = 0; i1 < 4; ++i1)
+#pragma unroll
+                            for (int p = 0; p < 8; ++p) {
+                                // through an empty asm, so this rare-path
+                                // work stays behind the branch
+                                u32 t = w[h][i1][p];
+                                asm volatile("" : "+v"(t));
+                                const v2h v = __builtin_bit_cast(v2h, t);
+                                al = absmax3(al, (float)v[0], (float)v[1]);
+                            }
+                }
+            }
+            const float amax = wave_max_dpp(al);
             if (lane == 0) {
                 red[par][nt] = amax;
                 red[par][4 + nt] = wbad ? 1.f : 0.f;
