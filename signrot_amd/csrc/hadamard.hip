@@ -426,6 +426,30 @@ __global__ __launch_bounds__(kPow2Threads) void rot_pow2_quant_kernel(RotArgs a)
     __shared__ float xch[4][E][64];
     __shared__ float red[4];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // this thread's E signs (the same for every row), loaded once up front
+    // so no row waits a memory round trip for them after its transform
+    // (the host passes a 16-byte aligned sign vector)
+    float sgn[E];
+    if (a.sign) {
+        const int8_t *sp = a.sign + E * t;
+        u32 raw[E / 4];
+        if constexpr (E == 8) {
+            const uint2 r2 = *reinterpret_cast<const uint2 *>(sp);
+            raw[0] = r2.x;
+            raw[1] = r2.y;
+        } else {
+#pragma unroll
+            for (int j = 0; j < E / 16; ++j) {
+                const uint4 r4 = *reinterpret_cast<const uint4 *>(sp + 16 * j);
+                raw[4 * j] = r4.x;
+                raw[4 * j + 1] = r4.y;
+                raw[4 * j + 2] = r4.z;
+                raw[4 * j + 3] = r4.w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < E; ++i) sgn[i] = (float)(int8_t)(raw[i / 4] >> (8 * (i % 4)));
+    }
     for (int64_t row = blockIdx.x; row < a.rows; row += gridDim.x) {
         const f16 *xr = reinterpret_cast<const f16 *>(a.x) + row * n + E * t;
         float v[E];
@@ -473,7 +497,7 @@ __global__ __launch_bounds__(kPow2Threads) void rot_pow2_quant_kernel(RotArgs a)
 #pragma unroll
         for (int i = 0; i < E; ++i) {
             float x = round16(v[i] * a.scale);
-            if (a.sign) x *= (float)a.sign[E * t + i];
+            if (a.sign) x *= sgn[i];
             v[i] = x;
             amax = fmaxf(amax, fabsf(round16(x)));
         }
@@ -583,7 +607,8 @@ extern "C" int srq_had_sign_quant(const void *x, int64_t rows, int64_t n, int64_
         SRQ_LAUNCH_CHECK("had_sign_quant");
         return SRQ_OK;
     }
-    if (!fp32_had && K == 1 && (n == 2048 || n == 4096 || n == 8192)) {
+    if (!fp32_had && K == 1 && (n == 2048 || n == 4096 || n == 8192) &&
+        (!sign || srq_aligned(sign, 16))) {
         const dim3 grid((unsigned)std::min<int64_t>(rows, 4096)), block(kPow2Threads);
         if (n == 2048) rot_pow2_quant_kernel<8><<<grid, block, 0, (hipStream_t)stream>>>(a);
         else if (n == 4096) rot_pow2_quant_kernel<16><<<grid, block, 0, (hipStream_t)stream>>>(a);

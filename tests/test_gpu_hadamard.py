@@ -121,6 +121,22 @@ def test_had_sign_quant_bitexact(C, n, rows, use_sign):
     assert np.mean(got.view(np.uint16) != want.view(np.uint16)) < 5e-3
 
 
+@pytest.mark.parametrize("n", [2048, 4096, 8192])
+def test_had_sign_quant_pow2_unaligned_sign(C, n):
+    # a sign vector that is not 16-byte aligned takes the generic kernel:
+    # the same codes and scales as the aligned one
+    rng = np.random.default_rng(n)
+    x = to_dev(outlier_input(rng, 9, n, n_out=8, mag=100.0))
+    sign_np = rng.choice([-1, 1], n).astype(np.int8)
+    buf = torch.empty(n + 16, dtype=torch.int8, device="cuda")
+    buf[3:n + 3] = to_dev(sign_np)
+    unaligned = buf[3:n + 3]
+    assert unaligned.data_ptr() % 16 != 0
+    q1, s1 = C.had_sign_quant(x, None, 1, to_dev(sign_np))
+    q2, s2 = C.had_sign_quant(x, None, 1, unaligned)
+    assert torch.equal(q1, q2) and torch.equal(s1, s2)
+
+
 def test_zero_sign_raises_in_module():
     from signrot_amd.nn import OnlineHadamard
     m = OnlineHadamard(4096, had_adj=True).cuda()
