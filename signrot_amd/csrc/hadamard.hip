@@ -17,6 +17,8 @@
 // vector stores (fp16 out) or goes straight into the quantizer (fused).
 #include "common.h"
 
+#include <type_traits>
+
 #include <math.h>
 
 namespace {
@@ -419,6 +421,14 @@ namespace {
 
 constexpr int kPow2Threads = 256;
 
+// lane i receives lane sel(i)'s value, sel given by the DPP control CTRL
+// (all rows and banks, every lane's source in range)
+template <int CTRL>
+SRQ_DEV float dpp_f32(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
 template <int E>
 __global__ __launch_bounds__(kPow2Threads) void rot_pow2_quant_kernel(RotArgs a) {
     static_assert(E >= 8 && E <= 32 && (E & (E - 1)) == 0, "E");
@@ -470,16 +480,29 @@ __global__ __launch_bounds__(kPow2Threads) void rot_pow2_quant_kernel(RotArgs a)
                     v[i + h] = x0 - x1;
                 }
         // the next 6 bits: lane bit s; the lower partner keeps x0 + x1, the
-        // upper x0 - x1 (x0 the lower one's value)
-#pragma unroll
-        for (int sbit = 0; sbit < 6; ++sbit) {
-            const bool upper = (lane >> sbit) & 1;
+        // upper x0 - x1 (x0 the lower one's value).  The partner's value
+        // (lane ^ 2^s) moves by DPP for bits 0, 1 and 3 (quad permutations,
+        // a row rotation by 8: no LDS round trip), by ds_bpermute for bits
+        // 2, 4 and 5.
+        auto stage = [&](auto sb) __attribute__((always_inline)) {
+            constexpr int SB = decltype(sb)::value;
+            const bool upper = (lane >> SB) & 1;
 #pragma unroll
             for (int i = 0; i < E; ++i) {
-                const float p = __shfl_xor(v[i], 1 << sbit, 64);
+                float p;
+                if constexpr (SB == 0) p = dpp_f32<0xB1>(v[i]);        // quad_perm [1,0,3,2]
+                else if constexpr (SB == 1) p = dpp_f32<0x4E>(v[i]);   // quad_perm [2,3,0,1]
+                else if constexpr (SB == 3) p = dpp_f32<0x128>(v[i]);  // row_ror:8
+                else p = __shfl_xor(v[i], 1 << SB, 64);
                 v[i] = upper ? p - v[i] : v[i] + p;
             }
-        }
+        };
+        stage(std::integral_constant<int, 0>{});
+        stage(std::integral_constant<int, 1>{});
+        stage(std::integral_constant<int, 2>{});
+        stage(std::integral_constant<int, 3>{});
+        stage(std::integral_constant<int, 4>{});
+        stage(std::integral_constant<int, 5>{});
         // the top 2 bits: the 4 waves' values of (lane, i), FWHT_4 in order
 #pragma unroll
         for (int i = 0; i < E; ++i) xch[wave][i][lane] = v[i];
