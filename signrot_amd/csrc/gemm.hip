@@ -1883,6 +1883,9 @@ extern "C" int srq_w4a4_linear_ws(const void *A, const void *a_scale, const void
     if (M && N) SRQ_CHECK_ARG(out && a_scale && b_scale, "w4a4_linear_ws: null pointer");
     SRQ_CHECK_ARG(ws_bytes >= 0 && (ws_bytes == 0 || workspace),
                   "w4a4_linear_ws: null workspace");
+    // the split-K partials are written and read with 16-byte vector accesses
+    SRQ_CHECK_ARG(ws_bytes == 0 || srq_aligned(workspace, 16),
+                  "w4a4_linear_ws: workspace must be 16-byte aligned");
     Epi e{};
     e.out = (f16 *)out;
     e.sa = (const f16 *)a_scale;
@@ -1904,6 +1907,9 @@ extern "C" int srq_w4a4_linear_residual_ws(const void *A, const void *a_scale, c
                       "w4a4_linear_residual_ws: null pointer");
     SRQ_CHECK_ARG(ws_bytes >= 0 && (ws_bytes == 0 || workspace),
                   "w4a4_linear_residual_ws: null workspace");
+    // the split-K partials are written and read with 16-byte vector accesses
+    SRQ_CHECK_ARG(ws_bytes == 0 || srq_aligned(workspace, 16),
+                  "w4a4_linear_residual_ws: workspace must be 16-byte aligned");
     Epi e{};
     e.out = (f16 *)out;
     e.sa = (const f16 *)a_scale;

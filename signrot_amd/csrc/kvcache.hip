@@ -1085,6 +1085,10 @@ extern "C" int srq_batch_decode_i4_noalloc(void *o, const void *q, const void *k
                                    last_page_offset, batch, num_qo_heads, num_kv_heads,
                                    num_layers, layer_idx, page_size, head_dim, nullptr, 1,
                                    stream);
+    // with chunks and no o the workspace form leaves the unmerged partial
+    // states in tmp, which here is the library's private scratch: refuse
+    SRQ_CHECK_ARG(o, "batch_decode_i4_noalloc: null output (the split-KV partial states "
+                     "would stay in the library's private scratch)");
     SRQ_CHECK_ARG(num_qo_heads > 0 && head_dim > 0 && num_chunks <= 1024,
                   "batch_decode_i4_noalloc: bad heads, head_dim or num_chunks");
     const int64_t need = batch * num_qo_heads * num_chunks * (head_dim + 4) * (int64_t)sizeof(float);

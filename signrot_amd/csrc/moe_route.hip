@@ -86,12 +86,20 @@ __global__ __launch_bounds__(THREADS) void moe_route_kernel(
 #pragma unroll
         for (int j = 0; j < kRouteMaxK; ++j) {
             if (j >= K) break;
+            // NaN ranks above every number (torch.topk's order); a row with
+            // a NaN or inf logit has all-NaN probabilities, so its k picks
+            // are k distinct experts with NaN weights.  Strict comparisons:
+            // ties, NaN ones included, keep the lower expert.
             float best = -1.f;
-            int bi = 0;
+            bool best_nan = false;
+            int bi = -1;
 #pragma unroll
             for (int i = 0; i < EP; ++i) {
-                const bool ok = i < E && !((taken >> i) & 1) && v[i] > best;  // strict: ties keep the lower expert
+                const bool vn = v[i] != v[i];
+                const bool above = vn ? !best_nan : (!best_nan && v[i] > best);
+                const bool ok = i < E && !((taken >> i) & 1) && (bi < 0 || above);
                 best = ok ? v[i] : best;
+                best_nan = ok ? vn : best_nan;
                 bi = ok ? i : bi;
             }
             taken |= 1ull << bi;

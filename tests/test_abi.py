@@ -63,6 +63,17 @@ def test_abi_version(lib):
      "negative"),
     (lambda L: L.srq_sym_dequant_moe(None, None, None, None, ctypes.c_void_p(8), None, 4, 4, 4,
                                      None, None), "together"),
+    # split-K workspaces are read and written 16 bytes at a time
+    (lambda L: L.srq_w4a4_linear_ws(*[ctypes.c_void_p(256)] * 4, None, 256, 256, 1024,
+                                    ctypes.c_void_p(256), ctypes.c_void_p(264), 64, None),
+     "16-byte aligned"),
+    (lambda L: L.srq_w4a4_linear_residual_ws(*[ctypes.c_void_p(256)] * 4, None,
+                                             ctypes.c_void_p(256), 256, 256, 1024,
+                                             ctypes.c_void_p(256), ctypes.c_void_p(8), 64, None),
+     "16-byte aligned"),
+    # the no-allocation decode has nowhere to leave unmerged split-KV states
+    (lambda L: L.srq_batch_decode_i4_noalloc(None, *[ctypes.c_void_p(256)] * 6, 2, 32, 8, 1, 0,
+                                             64, 128, 4, None), "null output"),
 ])
 def test_argument_errors(lib, call, msg):
     rc = call(lib)

@@ -240,6 +240,65 @@ def test_moe_route_matches_torch(C, T, E, k, norm):
         assert torch.all(r[1:] > r[:-1])
 
 
+@pytest.mark.parametrize("E,k,norm", [(8, 2, True), (8, 2, False), (16, 4, True)])
+def test_moe_route_nonfinite_rows(C, E, k, norm):
+    """Rows whose logits hold a NaN, a +inf or only -inf have all-NaN fp32
+    softmax probabilities in torch; torch.topk ranks NaN above every number,
+    so such a token gets k distinct experts with NaN weights (and a NaN block
+    output).  Here: NaN ranks first, NaN ties go to the lower expert, each
+    expert at most once; finite rows (a partly -inf row among them) are
+    unchanged and equal torch's ops bit for bit."""
+    g = torch.Generator(device=DEV).manual_seed(E * 10 + k)
+    T = 24
+    logits = torch.randn(T, E, generator=g, device=DEV).half()
+    nan, inf = float("nan"), float("inf")
+    logits[3, 1] = nan
+    logits[5, E - 1] = inf
+    logits[7, :] = -inf
+    logits[9, 2] = inf
+    logits[9, 4] = -inf
+    logits[11, ::2] = -inf  # partly -inf: finite probabilities
+    bad = torch.tensor([3, 5, 7, 9], device=DEV)
+    w, order, inv, expert, token, counts, offsets = C.moe_route(logits, k, norm)
+    probs = torch.softmax(logits, dim=1, dtype=torch.float)
+    assert torch.isnan(probs[bad]).all()  # the premise: torch's rows are all NaN
+    ours = expert[inv.long()].view(T, k).long()
+    wv = w.view(T, k)
+    assert torch.isnan(wv[bad]).all(), "non-finite rows must carry NaN weights"
+    for t in bad.tolist():
+        assert ours[t].tolist() == list(range(k)), "NaN ties: the lower experts, once each"
+    good = torch.ones(T, dtype=torch.bool, device=DEV)
+    good[bad] = False
+    tp, te = torch.topk(probs[good], k, dim=-1)
+    if norm:
+        tp = tp / tp.sum(dim=-1, keepdim=True)
+    assert torch.equal(wv[good], tp.half())
+    assert torch.isfinite(wv[good]).all()
+    assert torch.equal(torch.sort(ours[good], 1).values, torch.sort(te, 1).values)
+    flat = ours.reshape(-1)
+    assert torch.equal(counts.long(), torch.bincount(flat, minlength=E))
+    assert torch.equal(expert.long(), torch.sort(flat, stable=True).values)
+
+
+@torch.no_grad()
+def test_block_nan_token():
+    """One token with a NaN activation through SignRotMoEBlock.forward: its
+    router logits are NaN, so (as with torch's softmax / topk) its output row
+    is all NaN; every other token's output equals the clean run's bit for
+    bit (grouping by expert does not change a row's arithmetic)."""
+    blk = _block(256, 768, 16, 4, True, seed=11)
+    x = torch.randn(1, 37, 256, device=DEV, dtype=torch.float16)
+    out, _ = blk(x)
+    xn = x.clone()
+    xn[0, 3, 5] = float("nan")
+    outn, logits = blk(xn)
+    assert torch.isnan(logits[3]).all()
+    assert torch.isnan(outn[0, 3]).all()
+    keep = torch.ones(37, dtype=torch.bool, device=DEV)
+    keep[3] = False
+    assert torch.equal(outn[0, keep], out[0, keep])
+
+
 @pytest.mark.parametrize("T,k,H", [(512, 2, 4096), (33, 1, 64), (7, 2, 8), (100, 4, 256),
                                    (0, 2, 64)])
 def test_moe_combine_matches_torch(C, T, k, H):
