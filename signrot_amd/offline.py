@@ -231,14 +231,15 @@ def head_axis_hadamard(x, num_heads):
 def attach_online_rotations(model, signs=None):
     """Forward pre-hooks that apply the deployed path's online rotations in
     the model's float dtype: the full Hadamard on every down_proj input
-    (then that layer's calibrated sign, if `signs` holds one) and the
-    head-axis Hadamard on every o_proj input.  Returns the hook handles."""
+    (then that layer's calibrated sign, if `signs` holds one; an MoE
+    layer's entry is an ExpertSigns, one sign per expert) and the head-axis
+    Hadamard on every o_proj input.  Returns the hook handles."""
     heads = model.config.num_attention_heads
     handles = []
     for i, layer in enumerate(_layers(model)):
-        sign = None if signs is None else signs.get(i)
+        entry = None if signs is None else signs.get(i)
 
-        def down_hook(_, inp, sign=sign):
+        def down_hook(_, inp, sign=None):
             x = matmul_hadU(inp[0])
             if sign is not None:
                 x = x * sign.to(device=x.device, dtype=x.dtype)
@@ -247,8 +248,10 @@ def attach_online_rotations(model, signs=None):
         def o_hook(_, inp):
             return (head_axis_hadamard(inp[0], heads),) + inp[1:]
 
-        for down in _down_projs(layer):
-            handles.append(down.register_forward_pre_hook(down_hook))
+        for e, down in enumerate(_down_projs(layer)):
+            sign = entry.sign[e] if isinstance(entry, ExpertSigns) else entry
+            handles.append(down.register_forward_pre_hook(
+                lambda m, inp, sign=sign: down_hook(m, inp, sign)))
         handles.append(layer.self_attn.o_proj.register_forward_pre_hook(o_hook))
     return handles
 
@@ -256,42 +259,86 @@ def attach_online_rotations(model, signs=None):
 # --------------------------------------------------------- sign calibration
 
 
+class ExpertSigns:
+    """The SignRot signs of an MoE layer's expert down_projs: `sign` int8
+    [E, n] (all ones for an expert that received no calibration token, the
+    identity adjustment the reference leaves in place, quant_utils.py:
+    225-236) and `calibrated` bool [E] (whether the expert's sign was taken
+    from a token and folded into its weight).  `sign` is the sign_down
+    tensor of SignRotMoEBlock."""
+
+    def __init__(self, sign, calibrated):
+        self.sign, self.calibrated = sign, calibrated
+
+    def folded(self, e):
+        """Expert e's folded sign, or None if it kept the identity."""
+        return self.sign[e] if bool(self.calibrated[e]) else None
+
+
+def _folded_sign(signs, i, name):
+    """The sign folded into target `name` of layer i (a down_proj), or None."""
+    if signs is None or i not in signs or not name.endswith("down_proj"):
+        return None
+    entry = signs[i]
+    if isinstance(entry, ExpertSigns):
+        return entry.folded(int(name.split(".")[2]))  # mlp.experts.<e>.down_proj
+    return entry
+
+
 @torch.no_grad()
 def calibrate_down_proj_signs(model, input_ids):
-    """The SignRot sign of every layer's down_proj (adjust_hadamard,
-    gptq_utils.py:539-638, with the rule of quant_utils.py:362-367): one
-    calibration forward with the rotations of a rotated model attached;
-    each down_proj's rotated input picks the sign of its massive-outlier
-    token (batch 0), and the sign is folded into the down_proj weight's
-    columns (W <- W diag(s)).  With those signs applied to the rotated
-    input at run time the function is unchanged.  Dense layers only (an
-    MoE layer's experts each need their own sign).  Returns {layer: int8
-    sign}."""
-    if any(_is_moe(layer) for layer in _layers(model)):
-        raise NotImplementedError("sign calibration of MoE experts")
-    signs = {}
+    """The SignRot sign of every down_proj (adjust_hadamard, gptq_utils.py:
+    539-638, with the rule of quant_utils.py:362-367): one calibration
+    forward with the rotations of a rotated model attached; each down_proj
+    takes the sign pattern of its first call's massive-outlier token (batch
+    0 of a [B, T, n] input, all rows of an expert's [rows, n] input) and the
+    sign is folded into its weight's columns (W <- W diag(s)).  With those
+    signs applied to the rotated input at run time the function is
+    unchanged.  MoE layers calibrate every expert separately on the rows
+    routed to it; an expert that receives no row keeps the all-ones sign
+    (nothing folded).  Returns {layer: int8 [n] sign} for dense layers and
+    {layer: ExpertSigns} for MoE layers."""
+    found = {}          # (layer, expert) -> sign
     handles = []
     heads = model.config.num_attention_heads
     for i, layer in enumerate(_layers(model)):
-        def down_hook(mod, inp, i=i):
-            x = matmul_hadU(inp[0])
-            if i not in signs:
-                signs[i] = adj_sign_from_rotated(x).cpu()
-                w = mod.weight.data
-                mod.weight.data = w * signs[i].to(device=w.device, dtype=w.dtype)
-            return (x * signs[i].to(device=x.device, dtype=x.dtype),) + inp[1:]
+        for e, down in enumerate(_down_projs(layer)):
+            def down_hook(mod, inp, key=(i, e)):
+                x = matmul_hadU(inp[0])
+                rows = x.reshape(-1, x.shape[-1]).shape[0]
+                if key not in found and rows > 0:
+                    found[key] = adj_sign_from_rotated(x).cpu()
+                    w = mod.weight.data
+                    mod.weight.data = w * found[key].to(device=w.device, dtype=w.dtype)
+                if key in found:
+                    x = x * found[key].to(device=x.device, dtype=x.dtype)
+                return (x,) + inp[1:]
+
+            handles.append(down.register_forward_pre_hook(down_hook))
 
         def o_hook(_, inp):
             return (head_axis_hadamard(inp[0], heads),) + inp[1:]
 
-        for down in _down_projs(layer):
-            handles.append(down.register_forward_pre_hook(down_hook))
         handles.append(layer.self_attn.o_proj.register_forward_pre_hook(o_hook))
     try:
         model(input_ids, use_cache=False)
     finally:
         for h in handles:
             h.remove()
+    signs = {}
+    for i, layer in enumerate(_layers(model)):
+        downs = _down_projs(layer)
+        if not _is_moe(layer):
+            if (i, 0) in found:
+                signs[i] = found[(i, 0)]
+            continue
+        n = downs[0].weight.shape[1]
+        sign = torch.ones(len(downs), n, dtype=torch.int8)
+        cal = torch.zeros(len(downs), dtype=torch.bool)
+        for e in range(len(downs)):
+            if (i, e) in found:
+                sign[e], cal[e] = found[(i, e)], True
+        signs[i] = ExpertSigns(sign, cal)
     return signs
 
 
@@ -432,8 +479,11 @@ class GPTQ:
         if actorder:
             perm = torch.argsort(torch.diagonal(H), descending=True)
             W, H = W[:, perm], H[perm][:, perm]
+        # in place, as the reference adds it (H[diag, diag] += damp): a
+        # Hessian object shared with another linear (an MoE expert's gate and
+        # up projections) is seen damped by the next one
         damp = percdamp * torch.mean(torch.diagonal(H))
-        H = H + damp * torch.eye(cols, dtype=H.dtype, device=H.device)
+        H.diagonal().add_(damp)
         Hinv = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(H)), upper=True)
         Q = torch.zeros_like(W)
         for b0 in range(0, cols, blocksize):
@@ -505,9 +555,9 @@ def rtn_quantize(model, bits=4, sym=True, mse=False, signs=None):
     quantizers = {}
     for i, layer in enumerate(_layers(model)):
         for name, lin in _quant_targets(layer):
-            sign = None
-            if signs is not None and i in signs and name.endswith("down_proj"):
-                sign = signs[i].to(device=lin.weight.device, dtype=lin.weight.dtype)
+            sign = _folded_sign(signs, i, name)
+            if sign is not None:
+                sign = sign.to(device=lin.weight.device, dtype=lin.weight.dtype)
             w = lin.weight.data
             if sign is not None:
                 w = w * sign
@@ -563,25 +613,39 @@ def gptq_quantize(model, input_ids, bits=4, sym=True, mse=False, percdamp=0.01,
     quantizers = {}
     calls = _layer_inputs(model, input_ids)
     hidden = [args[0] if args else kw["hidden_states"] for args, kw in calls]
-    for i, layer in enumerate(_layers(model)):
+
+    def run_layer(layer):
+        outs = []
+        for x, (args, kw) in zip(hidden, calls):
+            kw = {k: v for k, v in kw.items() if k != "hidden_states"}
+            out = layer(x, *args[1:], **kw)
+            outs.append(out[0] if isinstance(out, tuple) else out)
+        return outs
+
+    def quantize_group(i, layer, names, hooked):
+        """GPTQ of the linears `names` of layer i, which share one input: the
+        Hessian is recorded on `hooked` (the first of them) over the
+        calibration batches, copied to the others, then each is quantized."""
         targets = dict(_quant_targets(layer))
-        if _is_moe(layer):
-            raise NotImplementedError("GPTQ of MoE experts (use rtn_quantize)")
-        stages = [["self_attn.k_proj", "self_attn.v_proj", "self_attn.q_proj"],
-                  ["self_attn.o_proj"], ["mlp.up_proj", "mlp.gate_proj"], ["mlp.down_proj"]]
-        for names in stages:
-            first = targets[names[0]]
-            work = {}
-            for n in names:
-                folded = signs is not None and i in signs and n.endswith("down_proj")
-                work[n] = GPTQ(targets[n], _make_quantizer(n, bits, sym, mse, folded), dtype)
-            h = first.register_forward_pre_hook(lambda _, inp: work[names[0]].add_batch(inp[0]))
-            try:
-                for x, (args, kw) in zip(hidden, calls):
-                    kw = {k: v for k, v in kw.items() if k != "hidden_states"}
-                    layer(x, *args[1:], **kw)
-            finally:
+        work = {n: GPTQ(targets[n], _make_quantizer(n, bits, sym, mse,
+                                                    _folded_sign(signs, i, n) is not None),
+                        dtype) for n in names}
+        handles = [targets[h].register_forward_pre_hook(
+            lambda _, inp, h=h: work[h].add_batch(inp[0])) for h in hooked]
+        try:
+            run_layer(layer)
+        finally:
+            for h in handles:
                 h.remove()
+        return work
+
+    for i, layer in enumerate(_layers(model)):
+        stages = [["self_attn.k_proj", "self_attn.v_proj", "self_attn.q_proj"],
+                  ["self_attn.o_proj"]]
+        if not _is_moe(layer):
+            stages += [["mlp.up_proj", "mlp.gate_proj"], ["mlp.down_proj"]]
+        for names in stages:
+            work = quantize_group(i, layer, names, [names[0]])
             for n in names[1:]:
                 work[n].H = work[names[0]].H.clone()
                 work[n].nsamples = work[names[0]].nsamples
@@ -589,12 +653,34 @@ def gptq_quantize(model, input_ids, bits=4, sym=True, mse=False, percdamp=0.01,
                 quantizers[f"model.layers.{i}.{n}"] = work[n].fasterquant(
                     blocksize=blocksize, percdamp=percdamp, groupsize=groupsize,
                     actorder=actorder)
-        new = []
-        for x, (args, kw) in zip(hidden, calls):
-            kw = {k: v for k, v in kw.items() if k != "hidden_states"}
-            out = layer(x, *args[1:], **kw)
-            new.append(out[0] if isinstance(out, tuple) else out)
-        hidden = new
+        if _is_moe(layer):
+            # _quantize_moe_mlp (gptq_utils.py:161-255): every expert's
+            # gate_proj records the rows routed to it over the same forwards
+            # (its Hessian is shared with up_proj); the down_projs record
+            # their inputs in a second pass, after gate/up are quantized.  An
+            # expert that receives no row has an all-zero Hessian, and GPTQ's
+            # dead-column rule then zeroes its weight, as the reference's does.
+            experts = range(len(layer.mlp.experts))
+            gate_up = [f"mlp.experts.{e}.{p}" for e in experts for p in ("gate_proj", "up_proj")]
+            work = quantize_group(i, layer, gate_up,
+                                  [f"mlp.experts.{e}.gate_proj" for e in experts])
+            for e in experts:
+                # the same tensor, not a copy (gptq_utils.py:203): up_proj's
+                # fasterquant sees the gate's in-place dead-column fix and
+                # damping
+                g, u = f"mlp.experts.{e}.gate_proj", f"mlp.experts.{e}.up_proj"
+                work[u].H, work[u].nsamples = work[g].H, work[g].nsamples
+            for n in gate_up:
+                quantizers[f"model.layers.{i}.{n}"] = work[n].fasterquant(
+                    blocksize=blocksize, percdamp=percdamp, groupsize=groupsize,
+                    actorder=actorder)
+            downs = [f"mlp.experts.{e}.down_proj" for e in experts]
+            work = quantize_group(i, layer, downs, downs)
+            for n in downs:
+                quantizers[f"model.layers.{i}.{n}"] = work[n].fasterquant(
+                    blocksize=blocksize, percdamp=percdamp, groupsize=groupsize,
+                    actorder=actorder)
+        hidden = run_layer(layer)
     return quantizers
 
 
@@ -603,42 +689,64 @@ def gptq_quantize(model, input_ids, bits=4, sym=True, mse=False, percdamp=0.01,
 
 def packed_checkpoint_tensors(model, quantizers, signs=None):
     """The packed-int4 checkpoint of a quantized model
-    (realquant_utils.py:50-82): every quantized weight as int4 codes
-    round(W / scale) packed two per byte, its scale under
-    `quantizer.<layer>.scale` ([out, 1] fp16, plus `.zero` for asymmetric
-    weights), down_proj's calibrated sign under `...down_proj.had_adj_sign`,
-    every other tensor in fp16.  Symmetric 4-bit weights only."""
+    (realquant_utils.py:50-92), in the reference's steps: every quantized
+    weight as its integer codes (sym: round(W / scale) clamped to the
+    quantizer's range; asym: round(W / scale) + zero clamped to [0, maxq])
+    packed two per byte by pack_i4, every other tensor in fp16; then under
+    `quantizer.<layer>.` the quantizer's scale, zero (zeros for a symmetric
+    one) and maxq.  pack_i4 accepts codes in [-8, 7] only (as the reference's
+    does), so codes of an asymmetric or 8-bit quantizer pack only when every
+    one of them lies in that range; otherwise its AssertionError propagates,
+    as the reference's export raises there.  The calibrated signs go under
+    `model.layers.<i>.mlp.down_proj.had_adj_sign` (an MoE layer: one per
+    expert, `mlp.experts.<e>.down_proj.had_adj_sign`, all ones for an
+    expert without a calibration token)."""
     out = {}
     for name, t in model.state_dict().items():
         layer = name.rsplit(".", 1)[0]
         q = quantizers.get(layer)
         if q is not None and name.endswith(".weight"):
-            if not q.sym or q.bits != 4:
-                raise NotImplementedError("packed export of symmetric 4-bit weights only")
             codes = q.codes(t.double() if t.dtype != torch.float16 else t.float())
             out[name] = pack_i4(codes.to(torch.int8)).contiguous()
         else:
             out[name] = t.to(torch.float16).contiguous()
     for layer, q in quantizers.items():
         out[f"quantizer.{layer}.scale"] = q.scale.to(torch.float16).contiguous()
-        if not q.sym:
-            out[f"quantizer.{layer}.zero"] = q.zero.to(torch.float16).contiguous()
+        out[f"quantizer.{layer}.zero"] = q.zero.to(torch.float16).contiguous()
+        out[f"quantizer.{layer}.maxq"] = torch.tensor(q.maxq)
     for i, s in (signs or {}).items():
-        out[f"model.layers.{i}.mlp.down_proj.had_adj_sign"] = s.to(torch.int8).contiguous()
+        if isinstance(s, ExpertSigns):
+            for e in range(s.sign.shape[0]):
+                out[f"model.layers.{i}.mlp.experts.{e}.down_proj.had_adj_sign"] = \
+                    s.sign[e].to(torch.int8).contiguous()
+        else:
+            out[f"model.layers.{i}.mlp.down_proj.had_adj_sign"] = s.to(torch.int8).contiguous()
     return out
 
 
 def export_packed_checkpoint(model, quantizers, path, signs=None, rotate_mode="hadamard",
-                             max_shard_bytes=5 * 2 ** 30):
+                             max_shard_bytes=5 * 2 ** 30, w_quantizer="rtn", a_clip_ratio=1.0,
+                             kv_bits=4, kv_asym=True, kv_groupsize=128, kv_clip_ratio=1.0,
+                             fp32_had=False, int8_down_proj=False):
     """Write the packed checkpoint directory (realquant_utils.py:17-142):
-    the tensors of packed_checkpoint_tensors, the quantization_config as
-    the first shard's metadata and in config.json."""
+    the tensors of packed_checkpoint_tensors, and the quantization_config
+    (the reference's keys: weight and activation settings, the K/V cache
+    settings, format, rotation, fp32_had, adj_layers, int8_down_proj) as
+    the first shard's metadata and in config.json.  Returns the config."""
     from .checkpoint import save_packed_checkpoint
     any_q = next(iter(quantizers.values()))
-    qcfg = {"quant_method": "SignRot", "w_bits": any_q.bits, "w_asym": not any_q.sym,
-            "w_groupsize": -1, "w_clip": any_q.mse, "w_perchannel": True, "a_bits": 4,
-            "a_asym": False, "format": "packed_int4", "rotate": hasattr(model, "Q"),
-            "rotate_mode": rotate_mode, "adj_layers": ["down_proj"] if signs else []}
+    qcfg = {"quant_method": "SignRot", "w_quantizer": w_quantizer,
+            "w_bits": any_q.bits, "w_asym": not any_q.sym, "w_groupsize": -1,
+            "w_clip": any_q.mse, "w_perchannel": True,
+            "a_bits": 4, "a_asym": False, "a_groupsize": -1, "a_clip_ratio": a_clip_ratio,
+            "k_bits": kv_bits, "k_asym": kv_asym, "k_groupsize": kv_groupsize,
+            "k_clip_ratio": kv_clip_ratio,
+            "v_bits": kv_bits, "v_asym": kv_asym, "v_groupsize": kv_groupsize,
+            "v_clip_ratio": kv_clip_ratio,
+            "format": "packed_int4",
+            "rotate": hasattr(model, "Q"), "rotate_mode": rotate_mode, "fp32_had": fp32_had,
+            "adj_layers": ["down_proj"] if signs else [],
+            "int8_down_proj": int8_down_proj}
     cfg = json.loads(model.config.to_json_string()) if hasattr(model.config, "to_json_string") \
         else {}
     save_packed_checkpoint(path, packed_checkpoint_tensors(model, quantizers, signs), qcfg, cfg,

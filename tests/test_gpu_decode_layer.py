@@ -17,9 +17,9 @@ from tests.gpu_util import to_dev, to_np
 pytestmark = pytest.mark.gpu
 
 
-def _run(B, T, hidden, Hq, Hkv, ffn, page, seed, ckpt_dir=None):
-    """One decode step of a random layer, checked stage by stage.  With
-    ckpt_dir, the layer is written as a packed checkpoint
+def _run(B, T, hidden, Hq, Hkv, ffn, page, seed, ckpt_dir=None, layer=None):
+    """One decode step of a random layer (or of `layer`), checked stage by
+    stage.  With ckpt_dir, the layer is written as a packed checkpoint
     (save_packed_checkpoint), read back into a fresh layer
     (load_decode_layer) and that layer runs the step, while the oracle
     takes the original layer's weights."""
@@ -27,7 +27,8 @@ def _run(B, T, hidden, Hq, Hkv, ffn, page, seed, ckpt_dir=None):
     from signrot_amd.transformers.decode_layer import W4A4LlamaDecodeLayer, rope_cos_sin
     D = 128
     rng = np.random.default_rng(seed)
-    layer = W4A4LlamaDecodeLayer.random(hidden, Hq, Hkv, D, ffn, layer_idx=1, seed=seed)
+    if layer is None:
+        layer = W4A4LlamaDecodeLayer.random(hidden, Hq, Hkv, D, ffn, layer_idx=1, seed=seed)
     w = layer.unpacked()
     if ckpt_dir is not None:
         from signrot_amd import checkpoint as ck
@@ -76,3 +77,46 @@ def test_decode_layer_from_checkpoint(tmp_path, B, T, hidden, Hq, Hkv, ffn, page
     key remap, fused into the decode layer's q/k/v and gate/up buffers)
     decodes one step as the oracle does with the original weights."""
     _run(B, T, hidden, Hq, Hkv, ffn, page, seed, ckpt_dir=tmp_path)
+
+
+def test_offline_model_export_loads_and_decodes(tmp_path):
+    """The whole offline -> deployed flow (the reference's rotate /
+    adjust_hadamard / rtn_fwrd / realquant export, then modeling_llama.py's
+    load): a float64 HF Llama layer (hidden 1024, 8 query / 2 KV heads of
+    128, FFN 896 = had_28 x 32) has its norms fused, is rotated, has its
+    down_proj sign calibrated and its weights RTN-quantized by offline.py,
+    is exported with export_packed_checkpoint, loaded into the decode layer
+    with load_decode_layer, and decodes one step on the HIP kernels, checked
+    stage by stage against the oracle with the loaded codes and scales,
+    which equal the offline model's fake-quantized weights."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from signrot_amd import checkpoint as ck
+    from signrot_amd import offline as off
+    from signrot_amd.functional.quantization import unpack_i4
+    from signrot_amd.transformers.decode_layer import W4A4LlamaDecodeLayer
+    hidden, Hq, Hkv, ffn = 1024, 8, 2, 896
+    cfg = LlamaConfig(vocab_size=128, hidden_size=hidden, intermediate_size=ffn,
+                      num_hidden_layers=1, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                      head_dim=128, max_position_embeddings=64, tie_word_embeddings=False)
+    torch.manual_seed(21)
+    m = LlamaForCausalLM(cfg).double().eval()
+    with torch.no_grad():
+        m.model.layers[0].input_layernorm.weight.uniform_(0.5, 1.5)
+        m.model.layers[0].post_attention_layernorm.weight.uniform_(0.5, 1.5)
+    off.fuse_layer_norms(m)
+    off.rotate_model(m, seed=7)
+    ids = torch.randint(0, 128, (1, 24), generator=torch.Generator().manual_seed(3))
+    signs = off.calibrate_down_proj_signs(m, ids)
+    quant = off.rtn_quantize(m, signs=signs)
+    off.export_packed_checkpoint(m, quant, str(tmp_path), signs=signs)
+    c = ck.PackedCheckpoint(str(tmp_path))
+    layer = W4A4LlamaDecodeLayer(hidden, Hq, Hkv, 128, ffn, layer_idx=1).to("cuda")
+    ck.load_decode_layer(layer, c, "model.layers.0.")
+    assert torch.equal(layer.down_sign.cpu(), signs[0])
+    for buf, names in {"qkv": ["q_proj", "k_proj", "v_proj"], "o": ["o_proj"]}.items():
+        codes = unpack_i4(getattr(layer, f"w_{buf}").cpu()).double()
+        s64 = torch.cat([quant[f"model.layers.0.self_attn.{n}"].scale for n in names])
+        want = torch.cat([m.get_submodule(f"model.layers.0.self_attn.{n}").weight.data
+                          for n in names])
+        assert torch.allclose(codes * s64, want, rtol=0, atol=1e-12)
+    _run(3, 70, hidden, Hq, Hkv, ffn, 32, 8, layer=layer)

@@ -16,6 +16,7 @@ on a small random HF Llama in float64.  Pins:
 * the packed export: codes and scales read back through load_decode_layer
   reproduce the fake-quantized weights."""
 import copy
+import math
 
 import numpy as np
 import pytest
@@ -324,3 +325,229 @@ def test_export_reads_back_through_load_decode_layer(tmp_path):
         # the fake-quantized weight is code x scale (scale in float64 here)
         s64 = torch.cat([quant["model.layers.0." + n].scale for n in names])
         assert torch.allclose(codes * s64, want_w, rtol=0, atol=1e-12)
+
+
+# ----------------------------------------------------------------- MoE layers
+
+
+class _Expert(torch.nn.Module):
+    def __init__(self, hidden, ffn):
+        super().__init__()
+        self.gate_proj = torch.nn.Linear(hidden, ffn, bias=False)
+        self.up_proj = torch.nn.Linear(hidden, ffn, bias=False)
+        self.down_proj = torch.nn.Linear(ffn, hidden, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(torch.nn.functional.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class _SparseMoE(torch.nn.Module):
+    """The sparse MoE block of the reference's target models (transformers
+    4.57 Qwen3-MoE layout: router `gate`, `experts[e]` with gate/up/down
+    Linears): fp32-style softmax over the router logits, top-k, optional
+    renormalization, each expert called once per forward on the rows routed
+    to it (and not at all when none is)."""
+
+    def __init__(self, hidden, ffn, experts, top_k, norm=True):
+        super().__init__()
+        self.gate = torch.nn.Linear(hidden, experts, bias=False)
+        # added to the router logits: -1e4 makes an expert unreachable (a
+        # buffer, so the offline rotation leaves it alone)
+        self.register_buffer("route_bias", torch.zeros(experts, dtype=torch.float64))
+        self.experts = torch.nn.ModuleList(_Expert(hidden, ffn) for _ in range(experts))
+        self.top_k, self.norm = top_k, norm
+
+    def forward(self, x):
+        shp = x.shape
+        x2 = x.reshape(-1, shp[-1])
+        p = torch.softmax(self.gate(x2) + self.route_bias, dim=-1)
+        w, sel = torch.topk(p, self.top_k, dim=-1)
+        if self.norm:
+            w = w / w.sum(dim=-1, keepdim=True)
+        out = torch.zeros_like(x2)
+        for e, ex in enumerate(self.experts):
+            tok, pos = torch.where(sel == e)
+            if tok.numel() == 0:
+                continue
+            out.index_add_(0, tok, ex(x2[tok]) * w[tok, pos, None])
+        return out.reshape(shp)
+
+
+def _moe_model(seed=0, layers=1, ffn=112, experts=4, top_k=2, dead=None):
+    """A small float64 Llama whose MLPs are sparse MoE blocks; expert `dead`
+    (if given) has a router row that never wins a top-k slot."""
+    m = _model(seed=seed, layers=layers, ffn=ffn)
+    torch.manual_seed(seed + 100)
+    for layer in m.model.layers:
+        moe = _SparseMoE(64, ffn, experts, top_k).double()
+        if dead is not None:
+            moe.route_bias[dead] = -1e4   # never routed
+        layer.mlp = moe
+    return m.eval()
+
+
+def test_moe_rotation_and_sign_calibration_per_expert():
+    """Fusion, rotation and per-expert sign calibration of an MoE model:
+    the function is unchanged with the online rotations and signs attached;
+    each expert's sign follows the rule on the rows routed to it in the
+    calibration forward (recorded independently on an untouched copy) and
+    is folded into its down_proj only; an expert that receives no row keeps
+    the all-ones sign, unfolded, and is reported as not calibrated."""
+    m = _moe_model(seed=12, dead=3)
+    ids = _ids(13, b=1, t=40)
+    want0 = _logits(m, ids)
+    off.fuse_layer_norms(m)
+    # the embedding centring changes the function (reference behaviour);
+    # compare the rotated model against the fused one
+    want = _logits(m, ids)
+    off.rotate_model(m, seed=2)
+    hs = off.attach_online_rotations(m)
+    # (matmul_hadU's fp32 1/sqrt(n) costs ~1e-7)
+    _close(_logits(m, ids), want, 1e-6)
+    want_rot = _logits(m, ids)
+    for h in hs:
+        h.remove()
+    ref = copy.deepcopy(m)
+    rec = {}
+    hs = off.attach_online_rotations(ref)
+    for e, ex in enumerate(ref.model.layers[0].mlp.experts):
+        ex.down_proj.register_forward_pre_hook(
+            lambda _, inp, e=e: rec.setdefault(e, inp[0].clone()))
+    _logits(ref, ids)
+    for h in hs:
+        h.remove()
+    assert 3 not in rec and sorted(rec) == [0, 1, 2]
+    before = [ex.down_proj.weight.clone() for ex in m.model.layers[0].mlp.experts]
+    signs = off.calibrate_down_proj_signs(m, ids)
+    es = signs[0]
+    assert isinstance(es, off.ExpertSigns) and es.sign.shape == (4, 112)
+    assert es.calibrated.tolist() == [True, True, True, False]
+    for e in range(3):
+        assert torch.equal(es.sign[e], adj_sign_from_rotated(rec[e]))
+        assert torch.equal(m.model.layers[0].mlp.experts[e].down_proj.weight,
+                           before[e] * es.sign[e].double())
+    assert torch.equal(es.sign[3], torch.ones(112, dtype=torch.int8))
+    assert torch.equal(m.model.layers[0].mlp.experts[3].down_proj.weight, before[3])
+    assert es.folded(3) is None and torch.equal(es.folded(1), es.sign[1])
+    hs = off.attach_online_rotations(m, signs)
+    _close(_logits(m, ids), want_rot, 1e-12)
+    for h in hs:
+        h.remove()
+    # RTN: calibrated experts' down_proj on the symmetric grid, the others not
+    quant = off.rtn_quantize(copy.deepcopy(m), signs=signs)
+    grid = [quant[f"model.layers.0.mlp.experts.{e}.down_proj"].symmetric_grid for e in range(4)]
+    assert grid == [True, True, True, False]
+    assert want0.shape == want.shape
+
+
+def test_moe_gptq_per_expert_hessians(monkeypatch):
+    """GPTQ of an MoE layer (_quantize_moe_mlp, gptq_utils.py:161-255): each
+    expert's gate_proj Hessian is 2/n sum x x^T over exactly the rows routed
+    to it, one sample per forward (recomputed here from the block's recorded
+    inputs by an independent softmax / top-k); up_proj is quantized with the
+    same Hessian object, after the gate's in-place dead-column fix and
+    damping; every weight ends on its quantizer's grid.  An expert that gets
+    no row has all-zero Hessians: the dead-column rule zeroes its gate_proj
+    and down_proj, while its up_proj, handed the gate's fixed and damped
+    Hessian (1.01 I), is quantized as RTN -- what the reference's shared
+    Hessian object does."""
+    m = _moe_model(seed=14, dead=2)
+    off.fuse_layer_norms(m)
+    off.rotate_model(m, seed=5)
+    hs = off.attach_online_rotations(m)
+    calib = [_ids(40 + i, b=1, t=24) for i in range(3)]
+    seen = {}
+    orig = off.GPTQ.fasterquant
+
+    def spy(self, *a, **k):
+        seen[id(self.linear)] = (self.H.clone(), self.nsamples, id(self.H))
+        return orig(self, *a, **k)
+
+    monkeypatch.setattr(off.GPTQ, "fasterquant", spy)
+    blk_in = []
+    moe = m.model.layers[0].mlp
+    up_before = [ex.up_proj.weight.data.clone() for ex in moe.experts]
+    h_in = moe.register_forward_pre_hook(lambda _, inp: blk_in.append(inp[0].clone()))
+    quant = off.gptq_quantize(m, calib, dtype=torch.float64)
+    h_in.remove()
+    for h in hs:
+        h.remove()
+    assert len(quant) == 4 + 3 * 4
+    for key, q in quant.items():
+        lin = m.get_submodule(key)
+        assert torch.equal(lin.weight.data, q.quantize(lin.weight.data))
+    # block inputs: the o stage's forwards, then the gate/up pass, the down
+    # pass and the final pass: the gate/up pass is forwards 3 * 3 .. 3 * 4
+    gate_up_inputs = blk_in[2 * len(calib):3 * len(calib)]
+    for e, ex in enumerate(moe.experts):
+        H = torch.zeros(64, 64, dtype=torch.float64)
+        n = 0
+        for x in gate_up_inputs:
+            x2 = x.reshape(-1, 64)
+            p = torch.softmax(moe.gate(x2) + moe.route_bias, dim=-1)
+            _, sel = torch.topk(p, moe.top_k, dim=-1)
+            rows = x2[(sel == e).any(-1)]
+            if rows.shape[0] == 0:
+                continue
+            H *= n / (n + 1)
+            n += 1
+            r = math.sqrt(2 / n) * rows.T
+            H += r @ r.T
+        Hg, ng, idg = seen[id(ex.gate_proj)]
+        Hu, nu, idu = seen[id(ex.up_proj)]
+        assert idg == idu and ng == nu == n
+        if n == 0:
+            assert e == 2 and torch.count_nonzero(Hg) == 0
+            assert torch.count_nonzero(ex.gate_proj.weight) == 0
+            assert torch.count_nonzero(ex.down_proj.weight) == 0
+            assert torch.equal(Hu, 1.01 * torch.eye(64, dtype=torch.float64))
+            qu = quant[f"model.layers.0.mlp.experts.{e}.up_proj"]
+            assert torch.equal(ex.up_proj.weight.data, qu.quantize(up_before[e]))
+            continue
+        assert torch.allclose(Hg, H, rtol=1e-12, atol=1e-12)
+        fixed = Hg.clone()
+        dead = torch.diagonal(fixed) == 0
+        fixed[dead, dead] = 1
+        damp = 0.01 * torch.mean(torch.diagonal(fixed))
+        assert torch.equal(Hu, fixed + damp * torch.eye(64, dtype=torch.float64))
+
+
+def test_packed_export_keys_and_config(tmp_path):
+    """The exporter's reference steps (realquant_utils.py:17-142): every
+    quantizer's scale, zero (zeros for symmetric) and maxq; the full
+    quantization_config; an MoE layer's signs per expert; asymmetric codes
+    (0..15) fail pack_i4's [-8, 7] range check as the reference's export
+    does, while symmetric ones round-trip."""
+    from signrot_amd import checkpoint as ck
+    from signrot_amd.functional.quantization import unpack_i4
+    m = _moe_model(seed=15, dead=1)
+    off.fuse_layer_norms(m)
+    off.rotate_model(m, seed=6)
+    signs = off.calibrate_down_proj_signs(m, _ids(16, b=1, t=16))
+    quant = off.rtn_quantize(m, signs=signs)
+    qcfg = off.export_packed_checkpoint(m, quant, str(tmp_path), signs=signs,
+                                        w_quantizer="rtn")
+    c = ck.PackedCheckpoint(str(tmp_path))
+    for key in ("w_quantizer", "a_groupsize", "a_clip_ratio", "k_bits", "k_asym",
+                "k_groupsize", "k_clip_ratio", "v_bits", "v_asym", "v_groupsize",
+                "v_clip_ratio", "fp32_had", "int8_down_proj", "adj_layers"):
+        assert key in c.quantization_config and c.quantization_config[key] == qcfg[key]
+    assert c.quantization_config["fp32_had"] is False
+    assert c.quantization_config["int8_down_proj"] is False
+    for layer, q in quant.items():
+        assert int(c.get_tensor(f"quantizer.{layer}.maxq")) == 7
+        assert torch.count_nonzero(c.get_tensor(f"quantizer.{layer}.zero")) == 0
+        codes = unpack_i4(c.get_tensor(layer + ".weight")).double()
+        assert torch.equal(codes, q.codes(m.get_submodule(layer).weight.data))
+    for e in range(4):
+        s = c.get_tensor(f"model.layers.0.mlp.experts.{e}.down_proj.had_adj_sign")
+        assert torch.equal(s, signs[0].sign[e])
+    assert torch.equal(c.get_tensor("model.layers.0.mlp.experts.1.down_proj.had_adj_sign"),
+                       torch.ones(112, dtype=torch.int8))
+    # asymmetric weights: codes 0..15 with zero points; pack_i4 refuses > 7
+    m2 = _model(seed=17, layers=1)
+    qa = off.rtn_quantize(m2, sym=False)
+    some = next(iter(qa.values()))
+    assert not some.sym and some.maxq == 15
+    with pytest.raises(AssertionError):
+        off.packed_checkpoint_tensors(m2, qa)
