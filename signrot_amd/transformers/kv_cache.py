@@ -27,9 +27,58 @@ import math
 from typing import Any, Dict, Optional
 
 import torch
+from transformers.cache_utils import Cache
 
 from .. import _CUDA
 from ..functional import kernel as signrot_kernel
+
+
+def _init_hf_cache(cache):
+    """Cache's own initializer: transformers 4.x takes no arguments, 5.x
+    wants a (here empty) list of cache layers."""
+    try:
+        Cache.__init__(cache, layers=[])
+    except TypeError:
+        Cache.__init__(cache)
+
+
+def asym_quantize_and_pack_i4(x, clip_factor_a_max=1.0, clip_factor_a_min=1.0, lac=False,
+                              quantize=True):
+    """The reference's torch KV quantizer (kv_cache.py:12-58), in x's dtype
+    (fp16: every op rounds once, as the fused kv_quant_pack kernel does).
+
+    Default (lac=False): per row over the last dim, scale =
+    clamp(max - min, 1e-5) / 15, zero = -min, codes clamp(round((x + zero) /
+    scale), 0, 15).  lac=True (learned activation clipping): the range is
+    widened to include 0 and multiplied by the clip factors, an all-zero
+    range becomes [-1, 1], scale = (max - min) / 15, zero = round(-min /
+    scale), codes clamp(round(x / scale) + zero, 0, 15).
+
+    quantize=True returns (u8 codes [..., D/2], element 2j in the low
+    nibble of byte j; scale [..., 1]; zero [..., 1]).  quantize=False
+    returns (scale * (codes - zero), scale, zero) unpacked -- for the
+    default branch that is the reference's expression as written, not the
+    cache's dequantization codes * scale - zero."""
+    maxq = 15
+    hi = torch.amax(x, dim=-1, keepdim=True)
+    lo = torch.amin(x, dim=-1, keepdim=True)
+    if lac:
+        hi = torch.clamp(hi, min=0) * clip_factor_a_max
+        lo = torch.clamp(lo, max=0) * clip_factor_a_min
+        flat = (lo == 0) & (hi == 0)
+        lo = torch.where(flat, torch.full_like(lo, -1.0), lo)
+        hi = torch.where(flat, torch.full_like(hi, 1.0), hi)
+        scale = (hi - lo) / maxq
+        zero = torch.round(-lo / scale)
+        codes = torch.clamp(torch.round(x / scale) + zero, 0, maxq)
+    else:
+        scale = torch.clamp(hi - lo, min=1e-5) / maxq
+        zero = -lo
+        codes = torch.clamp(torch.round((x + zero) / scale), 0, maxq)
+    if not quantize:
+        return scale * (codes - zero), scale, zero
+    u = codes.to(torch.uint8)
+    return u[..., 0::2] | (u[..., 1::2] << 4), scale, zero
 
 
 def unpack_i4_and_asym_dequantize(q, scale, zero, lac: bool = False):
@@ -185,7 +234,7 @@ class _LayerAttention:
         return self.decoder.attend(q, self.spec, self.layer_idx).unsqueeze(1)
 
 
-class MultiLayerPagedKVCache4Bit(object):
+class MultiLayerPagedKVCache4Bit(Cache):
     """Paged int4 KV cache for all layers of a model (the reference's
     MultiLayerPagedKVCache4Bit, kv_cache.py:173-498).
 
@@ -193,6 +242,11 @@ class MultiLayerPagedKVCache4Bit(object):
     scales f16 [pages, n_layers, 2, num_heads, page_size, 2]  ([scale, zero])
     `num_heads` is the number of KV heads; `group_size` the number of query
     heads per KV head."""
+
+    # transformers' Cache exposes batch_size as a read-only property of its
+    # layer list; this cache keeps its own (a plain class attribute ahead of
+    # the property in the lookup lets __init__ set it)
+    batch_size = None
 
     def __init__(self, batch_size, page_size, max_seq_len, device, n_layers, num_heads,
                  head_dim, disable_quant=False, hadamard_dtype=torch.float16, group_size=1,
@@ -203,6 +257,7 @@ class MultiLayerPagedKVCache4Bit(object):
             raise NotImplementedError("learned activation clipping (lac=True) is not built")
         if head_dim != 128:
             raise ValueError("head_dim must be 128")
+        _init_hf_cache(self)
         self.batch_size = batch_size
         self.page_size = page_size
         self.max_seq_len = max_seq_len
@@ -410,5 +465,45 @@ class MultiLayerPagedKVCache4Bit(object):
     def get_max_length(self) -> Optional[int]:
         return None
 
+    def __len__(self):
+        """The number of layers the cache holds (HF Cache's meaning; also
+        keeps `bool(cache)` true)."""
+        return len(self._filled)
+
+    def get_usable_length(self, new_seq_length: int, layer_idx: Optional[int] = 0) -> int:
+        """Cached tokens the new ones can attend to (HF Cache's rule): all of
+        them, the cache having no maximum length."""
+        prev = self.get_seq_length(layer_idx)
+        cap = self.get_max_length()
+        if cap is not None and prev + new_seq_length > cap:
+            return cap - new_seq_length
+        return prev
+
     def to_legacy_cache(self):
         return self
+
+
+class HFCacheAdapter(Cache):
+    """An HF Cache that forwards to an inner cache object (kv_cache.py:
+    501-520): lets a MultiLayerPagedKVCache4Bit, or any object with the same
+    methods, stand where transformers expects a Cache."""
+
+    def __init__(self, inner):
+        _init_hf_cache(self)
+        self.inner = inner
+
+    def get_usable_length(self, kv_seq_len: int, layer_idx: int) -> int:
+        return self.inner.get_usable_length(kv_seq_len, layer_idx)
+
+    def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
+        return self.inner.get_seq_length()
+
+    def get_max_length(self) -> Optional[int]:
+        return self.inner.get_max_length()
+
+    def update(self, key_states, value_states, layer_idx: int, cache_kwargs=None):
+        return self.inner.update(key_states, value_states, layer_idx, cache_kwargs)
+
+    def to_legacy_cache(self):
+        to_legacy = getattr(self.inner, "to_legacy_cache", None)
+        return to_legacy() if to_legacy is not None else self

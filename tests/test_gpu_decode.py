@@ -210,3 +210,48 @@ def test_cache_module_prefill_then_decode():
     for layer in range(L):
         ref = oa.decode(qr, data, param, indptr, indices, last, layer)
         _close(outs[layer][:, 0], ref, f"layer {layer}")
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 32, 128), (1, 2048, 32, 128), (16, 1, 32, 128),
+                                   (4, 37, 8, 128)])
+def test_asym_quantize_and_pack_i4_equals_kv_quant_pack(shape):
+    """The reference's torch KV quantizer against the fused kernel
+    (benchmarks/test_fused_equivalence.py:76-90): codes, scales and zeros
+    bit for bit, also for constant rows (the 1e-5 clamp)."""
+    from signrot_amd import _CUDA
+    from signrot_amd.transformers import asym_quantize_and_pack_i4
+    g = torch.Generator(device="cuda").manual_seed(sum(shape))
+    x = torch.randn(shape, device="cuda", generator=g).half() * 2
+    x[..., 0, :, :] = 1.5
+    q_f, param = _CUDA.kv_quant_pack(x)
+    q_r, s_r, z_r = asym_quantize_and_pack_i4(x)
+    assert torch.equal(q_f, q_r)
+    assert torch.equal(param[..., 0:1], s_r)
+    assert torch.equal(param[..., 1:2], z_r)
+
+
+def test_hf_cache_adapter_over_the_paged_cache():
+    """HFCacheAdapter around MultiLayerPagedKVCache4Bit: prefill and decode
+    updates through the adapter return what the same calls on a bare cache
+    return (bit for bit), and the lengths track."""
+    from transformers.cache_utils import Cache
+    from signrot_amd.transformers import HFCacheAdapter, MultiLayerPagedKVCache4Bit
+    B, T, H, G, L = 2, 70, 2, 4, 2
+    g = torch.Generator(device="cuda").manual_seed(5)
+    ks = torch.randn((L, B, T + 1, H, 128), device="cuda", generator=g).half()
+    vs = torch.randn((L, B, T + 1, H, 128), device="cuda", generator=g).half()
+    q = torch.randn((B, 1, H * G, 128), device="cuda", generator=g).half()
+    outs = []
+    for wrap in (False, True):
+        inner = MultiLayerPagedKVCache4Bit(B, 32, 128, "cuda", L, H, 128, group_size=G)
+        cache = HFCacheAdapter(inner) if wrap else inner
+        assert isinstance(cache, Cache) and len(inner) == L and bool(inner)
+        for layer in range(L):
+            k_ret, v_ret = cache.update(ks[layer, :, :T], vs[layer, :, :T], layer, {})
+            assert torch.equal(k_ret, ks[layer, :, :T]) and torch.equal(v_ret, vs[layer, :, :T])
+        assert cache.get_seq_length() == T and cache.get_usable_length(1, 0) == T
+        res = [cache.update(ks[layer, :, T:], vs[layer, :, T:], layer, {})(q)
+               for layer in range(L)]
+        assert cache.get_seq_length() == T + 1
+        outs.append(torch.stack(res))
+    assert torch.equal(outs[0], outs[1])
