@@ -213,6 +213,36 @@ def _time_launches(launch, n, stream):
     return e0.elapsed_time(e1) / n
 
 
+def _time_graph(launch, n, reps=3):
+    """Average ms of `launch(i)`, i = 0 .. n-1, captured once into a HIP
+    graph and replayed `reps` times (HIP events around the replays): the
+    launches' GPU time without the host's per-call cost, which is of the
+    order of the small-M kernels themselves.  `launch` must issue its work
+    on the current stream."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(2):
+            launch(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(n):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    del graph
+    return e0.elapsed_time(e1) / (reps * n)
+
+
 def _roof(us, ops, nbytes):
     tops = ops / (us * 1e-6) / 1e12
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -229,7 +259,9 @@ def _rand_w(n, k, dev, g):
 def bench_qlinear(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9, reps=20):
     """One W4A4 QLinear (had_sign_quant + w4a4_linear) at [M, K] x [N, K]:
     whole-QLinear and per-kernel averages over distinct input/weight sets
-    (> min_bytes in total, so weights stream from HBM, not the MALL)."""
+    (> min_bytes in total, so weights stream from HBM, not the MALL), timed
+    as launches replayed from a HIP graph (the serving loop's form; the
+    eager back-to-back time of the whole QLinear is reported beside it)."""
     from signrot_amd import _native
     from signrot_amd.functional.hadamard import get_hadK
     st = torch.cuda.current_stream()
@@ -258,24 +290,27 @@ def bench_qlinear(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9, reps=2
     def had(i):
         j = i % len(xs)
         _native.call("srq_had_sign_quant", xs[j].data_ptr(), M, K, k, hp, sign.data_ptr(), 0,
-                     1.0, qb[j].data_ptr(), sb[j].data_ptr(), st.cuda_stream)
+                     1.0, qb[j].data_ptr(), sb[j].data_ptr(),
+                     torch.cuda.current_stream().cuda_stream)
 
     def gemm(i):
         j = i % len(xs)
         _native.call("srq_w4a4_linear_ws", qb[j].data_ptr(), sb[j].data_ptr(),
                      ws[i % nsets].data_ptr(), wsc.data_ptr(), None, M, N, K, ob[j].data_ptr(),
-                     wsp.data_ptr(), ws_bytes, st.cuda_stream)
+                     wsp.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
 
     def both(i):
         had(i)
         gemm(i)
 
     n = max(reps, min(nsets, 64))
-    t_all = _time_launches(both, n, st) * 1e3
-    t_had = _time_launches(had, n, st) * 1e3
-    t_gemm = _time_launches(gemm, n, st) * 1e3
+    t_eager = _time_launches(both, n, st) * 1e3
+    t_all = _time_graph(both, n) * 1e3
+    t_had = _time_graph(had, n) * 1e3
+    t_gemm = _time_graph(gemm, n) * 1e3
     ops = 2.0 * M * N * K
     res = {"M": M, "K": K, "N": N, "hadamard": f"had_{k} x H_{K // k}", "weight_sets": nsets,
+           "timing": "hip_graph", "qlinear_eager_us": round(t_eager, 2),
            "qlinear": _roof(t_all, ops, M * K * 2 + N * K // 2 + M * N * 2 + M * 2 + N * 2),
            "had_sign_quant": _roof(t_had, 0.0, M * K * 2 + M * K // 2 + M * 2),
            "w4a4_linear": _roof(t_gemm, ops, M * K // 2 + N * K // 2 + M * N * 2 + M * 2 + N * 2)}
@@ -382,13 +417,15 @@ def bench_mlp70b(dev, M, seed, hidden=8192, ffn=28672, reps=10, min_bytes=2.2e9)
         return _CUDA.w4a4_linear(qd, sdn.view(-1), Wd[j], sd)
 
     st = torch.cuda.current_stream()
-    t = _time_launches(mlp, max(reps, nsets), st) * 1e3
+    t_eager = _time_launches(mlp, max(reps, nsets), st) * 1e3
+    t = _time_graph(mlp, max(reps, nsets)) * 1e3
     ops = 2.0 * M * 3 * hidden * ffn
     nbytes = wbytes + M * hidden * 2 * 2
     del il, Wd
     torch.cuda.empty_cache()
     return {"M": M, "hidden": hidden, "ffn": ffn, "hadamard": f"had_{k} x H_{ffn // k}",
-            "weight_sets": nsets, "mlp": _roof(t, ops, nbytes)}
+            "weight_sets": nsets, "timing": "hip_graph", "mlp_eager_us": round(t_eager, 2),
+            "mlp": _roof(t, ops, nbytes)}
 
 
 def bench_moe(dev, seed, tokens=512, hidden=4096, ffn=14336, experts=8, top_k=2, reps=10):

@@ -80,6 +80,85 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const f16 *__restrict__ x,
     }
 }
 
+// Block per row for few rows (decode batches): the 256 threads of a block
+// share one row (VPT vectors of 8 each), so a row's VALU work is spread over
+// four waves instead of one; the sum and the maximum cross the waves through
+// LDS.  The maximum (NaN-skipping fmaxf) and the non-finite flag do not
+// depend on the order; the fp32 sum does, within the fp16 ulp the RMSNorm
+// is specified to.
+template <int VPT, bool QUANT>
+__global__ __launch_bounds__(256) void rmsnorm_row_kernel(const f16 *__restrict__ x, int nvec,
+                                                          float eps, float mean_dim,
+                                                          f16 *__restrict__ out, float clip,
+                                                          u32 *__restrict__ q,
+                                                          f16 *__restrict__ qscale) {
+    __shared__ float s_sum[4], s_max[4];
+    __shared__ int s_bad[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t row = blockIdx.x;
+    const v8h *xr = reinterpret_cast<const v8h *>(x) + row * nvec;
+    v8h v[VPT];
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = tid + 256 * i;
+        v[i] = idx < nvec ? xr[idx] : (v8h){};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = (float)v[i][e];
+            acc = __builtin_fmaf(f, f, acc);
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) s_sum[wave] = acc;
+    __syncthreads();
+    acc = (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]);
+    const float inv = 1.0f / __builtin_sqrtf(acc / mean_dim + eps);
+    float amax = 0.f;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int idx = tid + 256 * i;
+        v8h o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = f16_rn((float)v[i][e] * inv);
+        v[i] = o;
+        if (idx < nvec) {
+            if (out) reinterpret_cast<v8h *>(out)[row * nvec + idx] = o;
+            if (QUANT) amax = absmax8_flag(o, amax, bad);
+        }
+    }
+    if (QUANT) {
+        amax = wave_max(amax);
+        const bool wbad = __builtin_amdgcn_ballot_w64(bad) != 0;
+        if (lane == 0) {
+            s_max[wave] = amax;
+            s_bad[wave] = wbad;
+        }
+        __syncthreads();
+        amax = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
+        const bool anybad = (s_bad[0] | s_bad[1] | s_bad[2] | s_bad[3]) != 0;
+        const f16 s = sym_row_scale(amax, clip);
+        if (tid == 0) qscale[row] = s;
+        u32 *qr = q + row * nvec;
+        if (anybad) {
+            // a non-finite value: the exact per-element quantizer
+            const float sf = (float)s;
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
+                if (tid + 256 * i < nvec) qr[tid + 256 * i] = pack8_sym(v[i], sf);
+        } else {
+            const float rcp = sym_rcp_safe((float)s);
+            const bool clampit = sym_row_needs_clamp(amax, (float)s);
+#pragma unroll
+            for (int i = 0; i < VPT; ++i)
+                if (tid + 256 * i < nvec)
+                    qr[tid + 256 * i] = clampit ? pack8_sym_fast<true>(v[i], rcp)
+                                                : pack8_sym_fast<false>(v[i], rcp);
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_generic_kernel(const f16 *__restrict__ x,
                                                               int64_t rows, int64_t cols,
                                                               float eps, float mean_dim,
@@ -137,10 +216,26 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const f16 *__restrict__ g,
 
 }  // namespace
 
+// Rows below which a block shares each row (rmsnorm_row_kernel); above it
+// one wave per row.  srq_rmsnorm and srq_rmsnorm_quant choose by the same
+// rule, so the fused and the unfused normalization round alike.
+constexpr int64_t kRmsRowSplitRows = 256;
+
 template <bool QUANT>
 static void launch_rmsnorm_vec(const void *x, int64_t rows, int64_t nvec, float eps,
                                float mean_dim, void *out, float clip, void *q, void *qs,
                                hipStream_t st) {
+    if (rows < kRmsRowSplitRows && nvec <= 1024) {
+        auto go_row = [&](auto vt) {
+            constexpr int V = decltype(vt)::value;
+            rmsnorm_row_kernel<V, QUANT><<<dim3((unsigned)rows), 256, 0, st>>>(
+                (const f16 *)x, (int)nvec, eps, mean_dim, (f16 *)out, clip, (u32 *)q, (f16 *)qs);
+        };
+        if (nvec <= 256) go_row(std::integral_constant<int, 1>{});
+        else if (nvec <= 512) go_row(std::integral_constant<int, 2>{});
+        else go_row(std::integral_constant<int, 4>{});
+        return;
+    }
     const dim3 grid((unsigned)srq_cdiv(rows, 4));
     const int vpt = (int)srq_cdiv(nvec, 64);
     auto go = [&](auto vt) {
