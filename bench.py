@@ -28,6 +28,7 @@ import torch
 METRIC = "W4A4 QLinear TOPS (M=2048) + decode µs/layer; % of MI355X roofline"
 PEAK_INT8_TOPS = 5000.0   # MI355X dense int8 MFMA, 5.0 POPS
 PEAK_HBM_GBS = 8000.0     # MI355X HBM3E, 8 TB/s
+PEAK_FP6_TOPS = 10100.0   # MI355X dense fp6 / fp4 MFMA, 10.1 PFLOPS (the bf6 path's MFMA)
 
 
 def parse():
@@ -383,6 +384,64 @@ def bench_qlinear_asym(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9):
     return res
 
 
+def bench_qlinear_bf6(dev, M, K, N, seed, n_out=8, mag=50.0, min_bytes=2.2e9, reps=20):
+    """The cfg2 QLinear on the opt-in bf6 path: had_sign_quant_bf6 (rotation +
+    sign + int4 quantizer writing the codes in the bf6 block layout) and
+    w4a4_linear_bf6 (the int4 codes as exact e3m2 values on the 6-bit-operand
+    MFMA, weights converted once with i4_to_bf6).  Bit-identical to the int8
+    path (checked here on the first set); its GEMM is priced against the
+    fp6 MFMA peak it runs on."""
+    from signrot_amd import _CUDA
+    from signrot_amd.functional.hadamard import get_hadK
+    g = torch.Generator(device=dev).manual_seed(seed)
+    had, k = get_hadK(K)
+    hadk = had.half().to(dev).contiguous()
+    sign = (torch.randint(0, 2, (K,), device=dev, generator=g).to(torch.int8) * 2 - 1)
+    set_bytes = M * K * 2 + _CUDA.bf6_bytes(N, K) + _CUDA.bf6_bytes(M, K) + M * N * 2
+    nsets = max(1, min(64, math.ceil(min_bytes / set_bytes)))
+    x0 = torch.randn(M, K, device=dev, generator=g)
+    ch = torch.randperm(K, device=dev, generator=g)[:n_out]
+    x0[:, ch] *= mag
+    x0 = x0.half()
+    xs = [x0] + [x0.clone() for _ in range(min(nsets, 8) - 1)]
+    w4 = _rand_w(N, K, dev, g)
+    ws6 = [_CUDA.i4_to_bf6(w4) for _ in range(nsets)]
+    wsc = (torch.rand(N, device=dev, generator=g) * 1e-3 + 1e-4).half()
+    q6s = [_CUDA.had_sign_quant_bf6(x, hadk, k, sign) for x in xs]
+    q4, s4 = _CUDA.had_sign_quant(x0, hadk, k, sign)
+    ref = _CUDA.w4a4_linear(q4, s4.view(-1), w4, wsc)
+    got = _CUDA.w4a4_linear_bf6(q6s[0][0], q6s[0][1].view(-1), ws6[0], wsc, M, N, K)
+    assert torch.equal(got, ref), "bf6 path differs from the int8 path"
+    del w4, q4, s4, ref, got
+
+    def had(i):
+        return _CUDA.had_sign_quant_bf6(xs[i % len(xs)], hadk, k, sign)
+
+    def gemm(i):
+        q6, sc = q6s[i % len(xs)]
+        return _CUDA.w4a4_linear_bf6(q6, sc.view(-1), ws6[i % nsets], wsc, M, N, K)
+
+    def both(i):
+        q6, sc = had(i)
+        return _CUDA.w4a4_linear_bf6(q6, sc.view(-1), ws6[i % nsets], wsc, M, N, K)
+
+    n = max(reps, min(nsets, 64))
+    t_all = _time_graph(both, n) * 1e3
+    t_had = _time_graph(had, n) * 1e3
+    t_gemm = _time_graph(gemm, n) * 1e3
+    ops = 2.0 * M * N * K
+    gemm_line = _roof(t_gemm, ops, _CUDA.bf6_bytes(M, K) + _CUDA.bf6_bytes(N, K) + M * N * 2)
+    gemm_line["frac_mfma_fp6"] = round(gemm_line["TOPS"] / PEAK_FP6_TOPS, 4)
+    res = {"M": M, "K": K, "N": N, "hadamard": f"had_{k} x H_{K // k}", "weight_sets": nsets,
+           "timing": "hip_graph",
+           "qlinear": _roof(t_all, ops, M * K * 2 + _CUDA.bf6_bytes(N, K) + M * N * 2),
+           "had_sign_quant_bf6": _roof(t_had, 0.0, M * K * 2 + _CUDA.bf6_bytes(M, K) + M * 2),
+           "w4a4_linear_bf6": gemm_line}
+    del xs, ws6, q6s
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_mlp70b(dev, M, seed, hidden=8192, ffn=28672, reps=10, min_bytes=2.2e9):
     """Config 4: Llama-3-70B-shape W4A4 MLP block: per-token int4 quant of x,
     the gate and up W4A4 linears as one GEMM over their rows interleaved in
@@ -488,13 +547,14 @@ def bench_prefill_attention(dev, B, T, Hq, Hkv, seed, reps=20):
 def bench_configs(args, dev):
     """The BASELINE.json configs other than the headline one, each at its
     own shape (configs[0], the cfg2 M sweep, configs[3], configs[4]), the cfg2
-    QLinear with asymmetric activations, and the prefill attention (Llama-70B
-    heads)."""
+    QLinear with asymmetric activations and on the opt-in bf6 path, and the
+    prefill attention (Llama-70B heads)."""
     out = {"cfg1_qproj_M16": bench_qlinear(dev, 16, 4096, 4096, args.seed + 10, n_out=4,
                                            mag=100.0),
            "cfg2_sweep": [bench_qlinear(dev, m, 14336, 4096, args.seed + 20 + m)
                           for m in (1, 16, 128, 2048, 8192)],
            "cfg2_asym_M2048": bench_qlinear_asym(dev, 2048, 14336, 4096, args.seed + 25),
+           "cfg2_bf6_M2048": bench_qlinear_bf6(dev, 2048, 14336, 4096, args.seed + 26),
            "cfg4_mlp70b": [bench_mlp70b(dev, m, args.seed + 30 + m) for m in (1, 32, 512, 4096)],
            "cfg5_moe": bench_moe(dev, args.seed + 40),
            "prefill_attention": [bench_prefill_attention(dev, 1, t, 64, 8, args.seed + 50 + t)
