@@ -537,11 +537,13 @@ SRQ_DEV void stage_tile(const Paged &p, int64_t np0, int64_t kvh, int64_t tb, in
 // and the chunk's page-table slice fits in LDS, each wave streams its tiles
 // through an S-deep direct-to-LDS ring; otherwise each tile is staged with
 // ordinary loads.
-// The minimum of 3 blocks per CU keeps the compiler from parking the P.V
-// accumulators in AGPRs (171 registers, 2 waves per SIMD without the hint;
-// 148 VGPRs, 3 waves per SIMD with it: 37 vs 41 us at config 3).
+// The 4-wave form asks for a minimum of 3 blocks per CU, which keeps the
+// compiler from parking the P.V accumulators in AGPRs (171 registers, 2
+// waves per SIMD without the hint; 148 VGPRs, 3 waves per SIMD with it: 37
+// vs 41 us at config 3); the 8-wave form compiles to the same 148 VGPRs
+// with a minimum of one block.
 template <int GP, int NW, int S>
-__global__ __launch_bounds__(NW * 64, 3) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(NW * 64, NW == 4 ? 3 : 1) void decode_kernel(DecodeArgs a) {
     using Cfg = DecodeCfg<NW, S>;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     __shared__ float m_s[NW][8], d_s[NW][8], z_s[NW][8];
@@ -936,14 +938,18 @@ extern "C" int srq_init_kv_i4(void *kv_data, void *kv_param, const int32_t *kv_i
 
 namespace {
 
-// waves per block and ring depth of the decode kernel, per padded group
-// size: as many waves as the registers allow (170 / 256 VGPRs for 12 / 8
-// waves per CU), 6 tiles of each SIMD in flight
-template <int GP> struct DecodeShape { static constexpr int nw = 4, s = 2; };
+// Waves per block and ring depth of the decode kernel.  Split launches
+// (chunks > 1) run 4-wave blocks, two per CU; an unsplit launch runs 8-wave
+// blocks, one per CU: the same waves per CU, and when the batch alone fills
+// the CUs (B x KV heads >= CUs) no split is needed, so the partial states
+// need no merge pass (config 3: 36.3 us unsplit with 8 waves against 37.6
+// split in two with 4, and the head-axis quantizer then skips the merge:
+// 39.9 against 42.5 us for both launches).
+constexpr int kDecodeS = 2;
 
-template <int GP>
-int launch_decode_g(const DecodeArgs &a, dim3 grid, hipStream_t st) {
-    constexpr int NW = DecodeShape<GP>::nw, S = DecodeShape<GP>::s;
+template <int GP, int NW>
+int launch_decode_nw(const DecodeArgs &a, dim3 grid, hipStream_t st) {
+    constexpr int S = kDecodeS;
     using Cfg = DecodeCfg<NW, S>;
     auto kern = decode_kernel<GP, NW, S>;
     static_assert(Cfg::lds <= 160 * 1024 - 4096, "decode LDS");
@@ -955,6 +961,11 @@ int launch_decode_g(const DecodeArgs &a, dim3 grid, hipStream_t st) {
     }
     kern<<<grid, NW * 64, Cfg::lds, st>>>(a);
     return SRQ_OK;
+}
+
+template <int GP>
+int launch_decode_g(const DecodeArgs &a, dim3 grid, hipStream_t st) {
+    return a.chunks == 1 ? launch_decode_nw<GP, 8>(a, grid, st) : launch_decode_nw<GP, 4>(a, grid, st);
 }
 
 int launch_decode(const DecodeArgs &a, dim3 grid, hipStream_t st) {

@@ -293,11 +293,15 @@ class MultiLayerPagedKVCache4Bit(Cache):
 
     @staticmethod
     def decode_chunks(batch_size, num_kv_heads, max_seq_len, cu_count):
-        """Split-KV chunks per (request, KV head): enough blocks for about two
-        per CU (the decode kernel's registers leave room for two four-wave
-        blocks per CU, so more chunks only queue), at least 128 tokens per
-        chunk, at most 1024 chunks."""
+        """Split-KV chunks per (request, KV head).  A batch with at least one
+        (request, KV head) per CU is not split (the unsplit launch runs one
+        eight-wave block per CU, and its outputs need no merge); otherwise
+        enough chunks for about two four-wave blocks per CU (the registers
+        leave room for two, so more chunks only queue), at least 128 tokens
+        per chunk, at most 1024 chunks."""
         blocks = max(1, batch_size * num_kv_heads)
+        if blocks >= cu_count:
+            return 1
         want = -(-2 * cu_count // blocks)
         return max(1, min(want, max_seq_len // 128, 1024))
 
