@@ -143,6 +143,14 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvArgs a, Paged p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = (float)x[e];
     }
+    // The new token's cache slot of a k / v row, looked up now: its two
+    // dependent page-table reads then overlap the row load and the
+    // transform instead of following them.
+    int64_t pos = -1, page = 0;
+    if (valid && kind != 0) {
+        pos = seq_len_of(p, b) - 1;
+        if (pos >= 0) page = p.indices[p.indptr[b] + pos / p.page];
+    }
     // RoPE (q and k rows); the shuffles run on every lane of the wave
     {
         const int64_t ct = a.cos_batch == 1 ? 0 : b;
@@ -198,10 +206,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvArgs a, Paged p) {
         vmax = fmaxf(vmax, xor_lane(vmax, m));
         vmin = fminf(vmin, xor_lane(vmin, m));
     }
-    if (!valid || kind == 0) return;
-    const int64_t len = seq_len_of(p, b);
-    const int64_t pos = len - 1;
-    if (pos < 0) return;
+    if (!valid || kind == 0 || pos < 0) return;
     f16 scale, zero;
     kv_row_params(vmax, vmin, scale, zero);
     const float fs = (float)scale, fz = (float)zero;
@@ -210,7 +215,6 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvArgs a, Paged p) {
     for (int e = 0; e < 8; ++e) word |= (u32)kv_code(v[e], fz, fs) << (4 * e);
     const int kv = kind - 1;
     const int64_t h = slot - a.hq - (kind == 2 ? a.hk : 0);
-    const int64_t page = p.indices[p.indptr[b] + pos / p.page];
     const int64_t entry = pos % p.page;
     const int64_t ri = row_index(p, page, kv, h, entry);
     reinterpret_cast<u32 *>(p.data + ri * (D / 2))[l] = word;
