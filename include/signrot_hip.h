@@ -378,6 +378,25 @@ int srq_qkv_rope_had_append(const void *qkv, const void *cos, const void *sin,
                             const int32_t *last_page_offset, int64_t num_layers,
                             int64_t layer_idx, int64_t page_size, void *stream);
 
+/* srq_qkv_rope_had_append followed by srq_batch_decode_i4, in one launch:
+ * each decode block (request, KV head, chunk) computes the rotated q rows of
+ * its query-head group from qkv and keeps them on chip, and the block whose
+ * chunk holds the new token writes that token's k / v codes into the cache
+ * and attends over them directly.  Arguments as the two entry points (q
+ * comes from qkv, so there is no q_out); with tmp and num_chunks > 1 and
+ * o == NULL the partial states stay in tmp for srq_merge_head_had_quant.
+ * Cache bytes and o are bit-identical to the two calls.  Replaces the same
+ * chain as srq_qkv_rope_had_append plus the decode call of the reference's
+ * attention stub (signrot/transformers/kv_cache.py:144-170, 295-415;
+ * bindings.cpp:508-559). */
+int srq_qkv_decode_i4(void *o, const void *qkv, const void *cos, const void *sin,
+                      int64_t cos_batch, float had_scale, int rotate, void *kv_data,
+                      void *kv_param, const int32_t *kv_indptr, const int32_t *kv_indices,
+                      const int32_t *last_page_offset, int64_t batch, int64_t num_qo_heads,
+                      int64_t num_kv_heads, int64_t num_layers, int64_t layer_idx,
+                      int64_t page_size, int64_t head_dim, float *tmp, int64_t num_chunks,
+                      void *stream);
+
 /* ------------------------------------------------------ decode-layer glue */
 
 /* out f16 [rows, cols] = fp16(x * 1/sqrt(Σ x² / mean_dim + eps)), the sum in

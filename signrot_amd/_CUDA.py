@@ -22,6 +22,7 @@ Added ops (no reference counterpart, fused forms of reference chains):
   swiglu_had_sign_quant = swiglu + had_sign_quant              modeling_llama.py:125-137
   qkv_rope_had_append   = rope_qk + K/q Hadamard + kv_quant_pack + append_kv_i4
                                                               kv_cache.py:144-170, 295-415
+  qkv_decode_i4         = qkv_rope_had_append + batch_decode_i4 kv_cache.py:144-170, 295-415
 """
 import functools
 
@@ -641,6 +642,44 @@ def batch_decode_i4(o, q, kv_data, kv_param, kv_indptr, kv_indices, last_page_of
     _call("srq_batch_decode_i4", _ptr(o), _ptr(q), _ptr(kv_data), _ptr(kv_param),
           _ptr(kv_indptr), _ptr(kv_indices), _ptr(last_page_offset), B, Hq, H, L,
           int(layer_idx), P, D, tmp_ptr, chunks, _stream(q))
+
+
+def qkv_decode_i4(o, qkv, cos, sin, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset,
+                  layer_idx, n_q_heads, had_scale, rotate=True, tmp=None, num_chunks=1):
+    """qkv_rope_had_append followed by batch_decode_i4 in one launch: the
+    new token's k / v are quantized into the cache and attended together
+    with the context, q is rotated on chip.  qkv f16 [B, (Hq + 2 Hk) * 128],
+    cos / sin [1 or B, 128]; o f16 [B, Hq, 128] (None with a split: the
+    partial states stay in tmp for merge_head_had_quant).  The cache bytes
+    and o are bit-identical to the two calls."""
+    L, H, P, D = _check_cache("qkv_decode_i4", kv_data, kv_param, kv_indptr, kv_indices,
+                              last_page_offset)
+    _check("qkv_decode_i4", [(qkv, "qkv"), (cos, "cos"), (sin, "sin"), (o, "o")],
+           [torch.float16, torch.float16, torch.float16, torch.float16])
+    B = qkv.shape[0]
+    if qkv.numel() != B * (n_q_heads + 2 * H) * D:
+        raise RuntimeError(f"qkv_decode_i4: qkv must be [B, {(n_q_heads + 2 * H) * D}]")
+    if n_q_heads % H or n_q_heads // H > 8:
+        raise RuntimeError(f"qkv_decode_i4: {n_q_heads} query heads for {H} KV heads")
+    if kv_indptr.shape[0] != B + 1 or last_page_offset.shape[0] != B:
+        raise RuntimeError("qkv_decode_i4: index tensors do not match the batch")
+    cb = cos.numel() // D
+    if cos.numel() != sin.numel() or cos.numel() % D or cb not in (1, B):
+        raise RuntimeError(f"qkv_decode_i4: cos/sin must be [1 or {B}, {D}]")
+    tmp_ptr, chunks = None, 1
+    if tmp is not None and num_chunks > 1:
+        if tmp.dtype != torch.float32 or tmp.numel() < B * n_q_heads * num_chunks * (D + 4):
+            raise RuntimeError("qkv_decode_i4: tmp must be float32 [B, Hq, chunks, D + 4]")
+        tmp_ptr, chunks = _ptr(tmp), int(num_chunks)
+    if o is None and chunks <= 1:
+        raise RuntimeError("qkv_decode_i4: o may be None only with a split (tmp, num_chunks > 1)")
+    if o is not None and tuple(o.shape) != (B, n_q_heads, D):
+        raise RuntimeError(f"qkv_decode_i4: o must be [{B}, {n_q_heads}, {D}]")
+    _call("srq_qkv_decode_i4", _ptr(o), _ptr(qkv), _ptr(cos), _ptr(sin), cb, float(had_scale),
+          1 if rotate else 0, _ptr(kv_data), _ptr(kv_param), _ptr(kv_indptr), _ptr(kv_indices),
+          _ptr(last_page_offset), B, int(n_q_heads), H, L, int(layer_idx), P, D, tmp_ptr, chunks,
+          _stream(qkv))
+    return o
 
 
 def batch_decode_i4_noalloc(o, q, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset,

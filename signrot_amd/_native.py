@@ -53,6 +53,8 @@ SIGNATURES = {
                        _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "srq_batch_decode_i4": [_p, _p, _p, _p, _p, _p, _p,
                             _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
+    "srq_qkv_decode_i4": [_p, _p, _p, _p, _i64, _f32, _i32, _p, _p, _p, _p, _p,
+                          _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _i64, _p],
     "srq_batch_decode_i4_noalloc": [_p, _p, _p, _p, _p, _p, _p,
                                     _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "srq_prefill_attention": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64,

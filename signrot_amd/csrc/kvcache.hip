@@ -127,6 +127,76 @@ struct QkvArgs {
 
 SRQ_DEV float xor_lane(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// The per-row arithmetic, shared by qkv_post_kernel and the fused form of
+// decode_kernel so that both give the same bits.  Lane l (0..15) of a
+// 16-lane group holds dims 8 l .. 8 l + 7 of one D = 128 row in v; kind 0 / 1
+// / 2 = q / k / v row.  Every lane of the wave must call these (shuffles).
+// RoPE (q, k), then FWHT_D * had_scale rounded to fp16 (q, k, when rotate).
+SRQ_DEV void qkv_row_transform(float (&v)[8], int kind, int l, const f16 *cs, const f16 *sn,
+                               int64_t ct, float had_scale, int rotate) {
+    constexpr int D = 128;
+    {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float o = xor_lane(v[e], 8);
+            const int i = 8 * l + e;
+            const f16 c = cs[ct * D + i], s = sn[ct * D + i];
+            const f16 xe = (f16)v[e], xo = (f16)o;  // exact: both came from fp16
+            y[e] = (float)(l < 8 ? rope_lo(xe, xo, c, s) : rope_hi(xo, xe, c, s));
+        }
+        if (kind != 2) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = y[e];
+        }
+    }
+    if (rotate) {
+        float w[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e] = v[e];
+        fwht_regs<8>(w);
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float o = xor_lane(w[e], m);
+                w[e] = (l & m) ? o - w[e] : w[e] + o;
+            }
+        }
+        if (kind != 2) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (float)f16_rn(w[e] * had_scale);
+        }
+    }
+}
+
+// KV int4 quantizer of a transformed row: the row max / min over the 16
+// lanes, [scale, zero], and this lane's 8 codes as one word.
+SRQ_DEV u32 kv_row_codes(const float (&v)[8], f16 &scale, f16 &zero) {
+    float vmax = -INFINITY, vmin = INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        vmax = fmaxf(vmax, v[e]);
+        vmin = fminf(vmin, v[e]);
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) {
+        vmax = fmaxf(vmax, xor_lane(vmax, m));
+        vmin = fminf(vmin, xor_lane(vmin, m));
+    }
+    kv_row_params(vmax, vmin, scale, zero);
+    const float fs = (float)scale, fz = (float)zero;
+    u32 word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) word |= (u32)kv_code(v[e], fz, fs) << (4 * e);
+    return word;
+}
+
+SRQ_DEV uint32_t pack_param(f16 scale, f16 zero) {
+    const f16 pr[2] = {scale, zero};
+    return *reinterpret_cast<const uint32_t *>(pr);
+}
+
 __global__ __launch_bounds__(256) void qkv_post_kernel(QkvArgs a, Paged p) {
     constexpr int D = 128;
     const int lane = threadIdx.x & 63;
@@ -151,41 +221,7 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvArgs a, Paged p) {
         pos = seq_len_of(p, b) - 1;
         if (pos >= 0) page = p.indices[p.indptr[b] + pos / p.page];
     }
-    // RoPE (q and k rows); the shuffles run on every lane of the wave
-    {
-        const int64_t ct = a.cos_batch == 1 ? 0 : b;
-        float y[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float o = xor_lane(v[e], 8);
-            const int i = 8 * l + e;
-            const f16 c = a.cs[ct * D + i], sn = a.sn[ct * D + i];
-            const f16 xe = (f16)v[e], xo = (f16)o;  // exact: both came from fp16
-            y[e] = (float)(l < 8 ? rope_lo(xe, xo, c, sn) : rope_hi(xo, xe, c, sn));
-        }
-        if (kind != 2) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = y[e];
-        }
-    }
-    if (a.rotate) {
-        float w[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) w[e] = v[e];
-        fwht_regs<8>(w);
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float o = xor_lane(w[e], m);
-                w[e] = (l & m) ? o - w[e] : w[e] + o;
-            }
-        }
-        if (kind != 2) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = (float)f16_rn(w[e] * a.had_scale);
-        }
-    }
+    qkv_row_transform(v, kind, l, a.cs, a.sn, a.cos_batch == 1 ? 0 : b, a.had_scale, a.rotate);
     if (kind == 0) {
         if (valid) {
             v8h o;
@@ -194,34 +230,15 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(QkvArgs a, Paged p) {
             *reinterpret_cast<v8h *>(a.q_out + (b * a.hq + slot) * D + 8 * l) = o;
         }
     }
-    // KV quantizer: row max / min over the 16 lanes
-    float vmax = -INFINITY, vmin = INFINITY;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-        vmax = fmaxf(vmax, v[e]);
-        vmin = fminf(vmin, v[e]);
-    }
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) {
-        vmax = fmaxf(vmax, xor_lane(vmax, m));
-        vmin = fminf(vmin, xor_lane(vmin, m));
-    }
-    if (!valid || kind == 0 || pos < 0) return;
     f16 scale, zero;
-    kv_row_params(vmax, vmin, scale, zero);
-    const float fs = (float)scale, fz = (float)zero;
-    u32 word = 0;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) word |= (u32)kv_code(v[e], fz, fs) << (4 * e);
+    const u32 word = kv_row_codes(v, scale, zero);
+    if (!valid || kind == 0 || pos < 0) return;
     const int kv = kind - 1;
     const int64_t h = slot - a.hq - (kind == 2 ? a.hk : 0);
     const int64_t entry = pos % p.page;
     const int64_t ri = row_index(p, page, kv, h, entry);
     reinterpret_cast<u32 *>(p.data + ri * (D / 2))[l] = word;
-    if (l == 0) {
-        f16 pr[2] = {scale, zero};
-        reinterpret_cast<uint32_t *>(p.param)[ri] = *reinterpret_cast<const uint32_t *>(pr);
-    }
+    if (l == 0) reinterpret_cast<uint32_t *>(p.param)[ri] = pack_param(scale, zero);
 }
 
 // --------------------------------------------------------------- decode
@@ -285,7 +302,17 @@ SRQ_DEV float max32(float x) {
 
 struct DecodeArgs {
     Paged p;
-    const f16 *q;      // [B, Hq, D]
+    const f16 *q;      // [B, Hq, D] (unfused form)
+    // fused form (qkv non-null): the q/k/v projection output of the new
+    // token [B, (Hq + 2 H) D]; q and k get RoPE (cos/sin rows [cos_batch, D])
+    // and, when rotate, the head-dim Hadamard times had_scale; k and v are
+    // quantized into the new token's cache slot (the qkv_post_kernel
+    // arithmetic), and q is used without a trip through memory
+    const f16 *qkv = nullptr;
+    const f16 *cs = nullptr, *sn = nullptr;
+    int cos_batch = 1;
+    int rotate = 0;
+    float had_scale = 1.f;
     f16 *o;            // [B, Hq, D]
     float *tmp;        // [B, Hq, chunks, D + 4] or null
     int64_t B, Hq, G;  // G = Hq / H (query heads per KV head), <= 8
@@ -566,6 +593,50 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 3 : 1) void decode_kernel(Decode
     const int64_t t1 = (t0 + per < len) ? t0 + per : len;
     const int64_t np0 = p.indptr[b];
 
+    // ---- fused form: the q rows of this KV group and the new token's k and
+    // v rows, 16 lanes per row (row slot rs: q heads 0 .. G - 1, then k, v).
+    // The block whose chunk holds the new token (position len - 1) writes its
+    // k / v codes to the cache; every block keeps the rotated q in LDS.
+    __shared__ __attribute__((aligned(16))) f16 q_new[GP * kD];
+    __shared__ __attribute__((aligned(16))) u32 kv_new[2][20];  // 16 code words + param
+    const bool fused = a.qkv != nullptr;
+    const int64_t pos_new = len - 1;
+    const bool owns_new = fused && pos_new >= t0 && pos_new < t1;
+    if (fused) {
+        const int rs = threadIdx.x >> 4, l = threadIdx.x & 15;
+        const int kind = rs < G ? 0 : (rs == G ? 1 : 2);
+        const bool act = rs < G + 2;
+        const int64_t hs = a.Hq + 2 * p.H;
+        const int64_t qkv_row = kind == 0 ? kvh * G + rs : (kind == 1 ? a.Hq + kvh : a.Hq + p.H + kvh);
+        float v[8];
+        {
+            const v8h x = act ? *reinterpret_cast<const v8h *>(a.qkv + (b * hs + qkv_row) * kD + 8 * l)
+                              : (v8h){};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = (float)x[e];
+        }
+        int64_t page_new = 0;
+        if (owns_new && act && kind != 0) page_new = p.indices[np0 + pos_new / p.page];
+        qkv_row_transform(v, kind, l, a.cs, a.sn, a.cos_batch == 1 ? 0 : b, a.had_scale, a.rotate);
+        f16 scale, zero;
+        const u32 word = kv_row_codes(v, scale, zero);
+        if (act && kind == 0) {
+            v8h o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (f16)v[e];
+            *reinterpret_cast<v8h *>(q_new + rs * kD + 8 * l) = o;
+        } else if (act) {
+            const int kv = kind - 1;
+            kv_new[kv][l] = word;
+            if (l == 0) kv_new[kv][16] = pack_param(scale, zero);
+            if (owns_new) {
+                const int64_t ri = row_index(p, page_new, kv, kvh, pos_new % p.page);
+                reinterpret_cast<u32 *>(p.data + ri * (kD / 2))[l] = word;
+                if (l == 0) reinterpret_cast<uint32_t *>(p.param)[ri] = pack_param(scale, zero);
+            }
+        }
+    }
+
     // page-table slice of the chunk into LDS
     int *pt = reinterpret_cast<int *>(lds + NW * Cfg::wave_lds);
     const int ipage = (int)p.page;
@@ -577,11 +648,12 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 3 : 1) void decode_kernel(Decode
 
     DecodeState<GP> st;
     // ---- query operand: row m = head (zero for m >= G); k-step ks, half h2
-    // holds dims 64 h2 + 8 ks + [0, 4, 1, 5, 2, 6, 3, 7] (the codes8 order)
+    // holds dims 64 h2 + 8 ks + [0, 4, 1, 5, 2, 6, 3, 7] (the codes8 order).
+    // Unfused: read from q now (the loads overlap the page-table fetch);
+    // fused: from q_new after the barrier below.
     const int m = lane & 31, h2 = lane >> 5;
-    float qpart = 0.f;
-    {
-        const f16 *qrow = a.q + (b * a.Hq + kvh * G + min(m, G - 1)) * kD + 64 * h2;
+    auto build_q = [&](const f16 *qrow) __attribute__((always_inline)) {
+        float qpart = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             v8h raw = *reinterpret_cast<const v8h *>(qrow + 8 * ks);
@@ -593,11 +665,13 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 3 : 1) void decode_kernel(Decode
 #pragma unroll
             for (int e = 0; e < 8; ++e) qpart += (float)raw[e];
         }
-    }
-    qpart += __shfl_xor(qpart, 32, 64);
+        qpart += __shfl_xor(qpart, 32, 64);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st.qs[r] = __shfl(qpart, 4 * h2 + r, 64) * a.sm_scale_log2;
+    };
+    if (!fused) build_q(a.q + (b * a.Hq + kvh * G + min(m, G - 1)) * kD + 64 * h2);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        st.qs[r] = __shfl(qpart, 4 * h2 + r, 64) * a.sm_scale_log2;
         st.m_run[r] = -INFINITY;
         st.d_part[r] = 0.f;
         st.z_part[r] = 0.f;
@@ -611,7 +685,27 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 3 : 1) void decode_kernel(Decode
     const uint32_t wlds_addr = (uint32_t)(uintptr_t)wlds;
     const int64_t stride = NW * kTile;  // a wave's tiles are NW tiles apart
     int64_t tb = t0 + (int64_t)wave * kTile;
-    __syncthreads();  // page-table slice
+    __syncthreads();  // page-table slice (and the fused form's q_new, kv_new)
+    if (fused) build_q(q_new + min(m, G - 1) * kD + 64 * h2);
+    // fused form: the new token's row of the tile staged at sg (its first
+    // token tbj) is replaced by the codes computed above, after the tile
+    // has landed: whatever the tile's loads read from that cache row (the
+    // block's own write may or may not have reached memory) is overwritten.
+    auto put_new = [&](uint8_t *sg, int64_t tbj) __attribute__((always_inline)) {
+        if (!owns_new || pos_new < tbj || pos_new >= tbj + kTile) return;
+        const int r = (int)(pos_new - tbj);
+        if (lane < 8) {
+            const int kv = lane >> 2, c = lane & 3;
+            const v4i w = *reinterpret_cast<const v4i *>(&kv_new[kv][4 * c]);
+            *reinterpret_cast<v4i *>(sg + 2048 * kv + swz(r, c)) = w;
+        } else if (lane < 10) {
+            const int kv = lane - 8;
+            reinterpret_cast<u32 *>(sg + 4096 + 128 * kv)[r] = kv_new[kv][16];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
 
     if (pipe) {
         // iteration j issues tile j + S - 1 into stage (j + S - 1) % S, then
@@ -630,6 +724,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 3 : 1) void decode_kernel(Decode
             for (int j = 0; j < ntiles; ++j) {
                 issue(j + S - 1);
                 asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * (S - 1)) : "memory");
+                put_new(wlds + (j % S) * kStageBytes, tb + (int64_t)j * stride);
                 tile_step<GP>(st, wlds + (j % S) * kStageBytes, tb + (int64_t)j * stride, t1, lane,
                               a.sm_scale_log2, pvt, nib);
             }
@@ -638,6 +733,7 @@ __global__ __launch_bounds__(NW * 64, NW == 4 ? 3 : 1) void decode_kernel(Decode
     } else {
         for (; tb < t1; tb += stride) {
             stage_tile(p, np0, kvh, tb, t1, lane, wlds);
+            put_new(wlds, tb);
             tile_step<GP>(st, wlds, tb, t1, lane, a.sm_scale_log2, pvt, nib);
         }
     }
@@ -1028,6 +1124,59 @@ extern "C" int srq_batch_decode_i4(void *o, const void *q, const void *kv_data,
     return SRQ_OK;
 }
 
+extern "C" int srq_qkv_decode_i4(void *o, const void *qkv, const void *cos, const void *sin,
+                                 int64_t cos_batch, float had_scale, int rotate, void *kv_data,
+                                 void *kv_param, const int32_t *kv_indptr,
+                                 const int32_t *kv_indices, const int32_t *last_page_offset,
+                                 int64_t batch, int64_t num_qo_heads, int64_t num_kv_heads,
+                                 int64_t num_layers, int64_t layer_idx, int64_t page_size,
+                                 int64_t head_dim, float *tmp, int64_t num_chunks, void *stream) {
+    const char *name = "qkv_decode_i4";
+    int rc = check_paged(name, kv_data, kv_param, kv_indptr, kv_indices, last_page_offset,
+                         num_layers, layer_idx, num_kv_heads, page_size, head_dim);
+    if (rc) return rc;
+    SRQ_CHECK_ARG(batch >= 0 && num_qo_heads > 0 && num_kv_heads <= 65535,
+                  "%s: bad batch/heads", name);
+    SRQ_CHECK_ARG(num_qo_heads % num_kv_heads == 0 && num_qo_heads / num_kv_heads <= 8,
+                  "%s: query heads (%lld) must be 1..8 times the KV heads (%lld)", name,
+                  (long long)num_qo_heads, (long long)num_kv_heads);
+    SRQ_CHECK_ARG(cos_batch == 1 || cos_batch == batch, "%s: cos/sin batch must be 1 or B",
+                  name);
+    if (batch == 0) return SRQ_OK;
+    if (num_chunks < 1 || tmp == nullptr) num_chunks = 1;
+    SRQ_CHECK_ARG(qkv && cos && sin && (o || num_chunks > 1), "%s: null pointer", name);
+    SRQ_CHECK_ARG(srq_aligned(qkv, 16), "%s: qkv must be 16-byte aligned", name);
+    SRQ_CHECK_ARG(num_chunks <= 1024, "%s: num_chunks > 1024", name);
+    DecodeArgs a;
+    a.p = make_paged(kv_data, kv_param, kv_indptr, kv_indices, last_page_offset, num_layers,
+                     layer_idx, num_kv_heads, page_size, head_dim);
+    a.q = nullptr;
+    a.qkv = (const f16 *)qkv;
+    a.cs = (const f16 *)cos;
+    a.sn = (const f16 *)sin;
+    a.cos_batch = (int)cos_batch;
+    a.rotate = rotate ? 1 : 0;
+    a.had_scale = had_scale;
+    a.o = (f16 *)o;
+    a.tmp = tmp;
+    a.B = batch;
+    a.Hq = num_qo_heads;
+    a.G = num_qo_heads / num_kv_heads;
+    a.chunks = (int)num_chunks;
+    a.sm_scale_log2 = (1.0f / sqrtf((float)head_dim)) * 1.44269504088896340736f;
+    hipStream_t st = (hipStream_t)stream;
+    const dim3 grid((unsigned)batch, (unsigned)num_kv_heads, (unsigned)num_chunks);
+    rc = launch_decode(a, grid, st);
+    if (rc) return rc;
+    SRQ_LAUNCH_CHECK(name);
+    if (num_chunks > 1 && o) {
+        merge_kernel<<<dim3((unsigned)(batch * num_qo_heads)), 128, 0, st>>>(tmp, (f16 *)o,
+                                                                          num_qo_heads,
+                                                                          (int)num_chunks);
+        SRQ_LAUNCH_CHECK("qkv_decode_i4 (merge)");
+    }
+    return SRQ_OK;
+}
 
 // ------------------------------------ allocation-free split-KV decode
 // The split-KV partial states of srq_batch_decode_i4_noalloc live in this

@@ -113,21 +113,21 @@ class W4A4LlamaDecodeLayer(torch.nn.Module):
         return self._forward_ops(hidden_states, cache, cos, sin, trace, attention_mask)
 
     def _forward_fused(self, hidden_states, cache, cos, sin, attention_mask=None):
-        """The decode step in 10 launches: rmsnorm_quant -> q/k/v GEMM ->
-        qkv_rope_had_append (RoPE, K/q Hadamard, KV quantize + append) ->
-        batch_decode_i4 -> merge_head_had_quant (split-KV merge, head-axis
-        Hadamard + quantizer; head_had_quant when unsplit) -> o_proj GEMM +
-        residual -> rmsnorm_quant -> gate/up GEMM with the SwiGLU in its
-        epilogue (ffn % 8 == 0; else the GEMM and swiglu_had_sign_quant) ->
-        had_sign_quant -> down GEMM + residual."""
+        """The decode step in 9 launches: rmsnorm_quant -> q/k/v GEMM ->
+        qkv_decode_i4 (RoPE, K/q Hadamard, KV quantize + append, and the
+        attention, one kernel) -> head_had_quant (head-axis Hadamard +
+        quantizer; merge_head_had_quant with the split-KV merge folded in
+        when the batch is split) -> o_proj GEMM + residual -> rmsnorm_quant ->
+        gate/up GEMM with the SwiGLU in its epilogue (ffn % 8 == 0; else the
+        GEMM and swiglu_had_sign_quant) -> had_sign_quant -> down GEMM +
+        residual."""
         B = hidden_states.shape[0]
         x2 = hidden_states.view(B, self.hidden)
         n1, n2 = self.input_layernorm, self.post_attention_layernorm
         q1, s1 = _CUDA.rmsnorm_quant(x2, n1.eps, n1.mean_dim)
         qkv = _CUDA.w4a4_linear(q1, s1.view(-1), self.w_qkv, self.s_qkv)
-        q_rot = cache.update_qkv_fused(qkv, cos, sin, self.layer_idx, self.n_heads,
-                                       attention_mask)
-        qa, sa = cache.decode_rotated_quant(q_rot, self.layer_idx, _inv_sqrt_f32(self.n_heads))
+        qa, sa = cache.update_qkv_decode_quant(qkv, cos, sin, self.layer_idx, self.n_heads,
+                                               _inv_sqrt_f32(self.n_heads), attention_mask)
         x2 = _CUDA.w4a4_linear_residual(qa, sa.view(-1), self.w_o, self.s_o, x2)
         q2, s2 = _CUDA.rmsnorm_quant(x2, n2.eps, n2.mean_dim)
         if self.ffn % 8 == 0:

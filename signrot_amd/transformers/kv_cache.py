@@ -215,6 +215,32 @@ class _SplitDecoder:
         return _CUDA.head_had_quant(self.attend(q_rot, spec, layer_idx), scale)
 
 
+    def qkv_attend(self, qkv, cos, sin, spec, layer_idx, n_q_heads, had_scale, rotate):
+        """qkv_decode_i4 with this split: the attention output o [B, Hq, D]
+        of the new token (its k / v quantized into the cache on the way)."""
+        B, D = qkv.shape[0], 128
+        o = torch.empty((B, n_q_heads, D), dtype=torch.float16, device=qkv.device)
+        split = self.tmp is not None and self.tmp.shape[1] == n_q_heads
+        _CUDA.qkv_decode_i4(o, qkv, cos, sin, **spec, layer_idx=layer_idx, n_q_heads=n_q_heads,
+                            had_scale=had_scale, rotate=rotate,
+                            tmp=self.tmp if split else None,
+                            num_chunks=self.num_chunks if split else 1)
+        return o
+
+    def qkv_attend_head_had_quant(self, qkv, cos, sin, spec, layer_idx, n_q_heads, had_scale,
+                                  rotate, scale):
+        """head_had_quant(qkv_attend(...), scale), the split merged inside the
+        head-axis kernel where the records fit (as attend_head_had_quant)."""
+        if (self.tmp is not None and self.tmp.shape[1] == n_q_heads
+                and n_q_heads * self.num_chunks <= _CUDA.MERGE_HHQ_MAX_RECORDS):
+            _CUDA.qkv_decode_i4(None, qkv, cos, sin, **spec, layer_idx=layer_idx,
+                                n_q_heads=n_q_heads, had_scale=had_scale, rotate=rotate,
+                                tmp=self.tmp, num_chunks=self.num_chunks)
+            return _CUDA.merge_head_had_quant(self.tmp, scale)
+        return _CUDA.head_had_quant(
+            self.qkv_attend(qkv, cos, sin, spec, layer_idx, n_q_heads, had_scale, rotate), scale)
+
+
 class _LayerAttention:
     """What update() returns after an append: q [B, 1, Hq, D] -> attention
     over this layer's cache, [B, 1, Hq, D] (the reference's
@@ -386,18 +412,40 @@ class MultiLayerPagedKVCache4Bit(Cache):
         rope_qk + update() + the query rotation.  The layer must hold its
         prefill already.  attention_mask as for update() (the extended HF
         mask after a left-padded prefill) or None."""
+        spec = self._qkv_step(qkv, layer_idx, attention_mask, "update_qkv_fused")
+        return _CUDA.qkv_rope_had_append(qkv, cos.contiguous(), sin.contiguous(), num_q_heads,
+                                         self.num_heads, **spec, layer_idx=layer_idx,
+                                         had_scale=1 / math.sqrt(self.head_dim),
+                                         rotate=self.hadamard_dtype is not None)
+
+    def _qkv_step(self, qkv, layer_idx, attention_mask, name):
         if not self._filled[layer_idx]:
-            raise RuntimeError("update_qkv_fused: the layer has no prefill yet")
+            raise RuntimeError(f"{name}: the layer has no prefill yet")
         if qkv.shape[0] != self.batch_size:
             raise ValueError(f"batch {qkv.shape[0]} != the cache's {self.batch_size}")
         if layer_idx == 0:
             self._reserve(self.length + 1)
             self.length += 1
-        spec = self.get_cache_specs_for_flash_infer(attention_mask)
-        return _CUDA.qkv_rope_had_append(qkv, cos.contiguous(), sin.contiguous(), num_q_heads,
-                                         self.num_heads, **spec, layer_idx=layer_idx,
-                                         had_scale=1 / math.sqrt(self.head_dim),
-                                         rotate=self.hadamard_dtype is not None)
+        return self.get_cache_specs_for_flash_infer(attention_mask)
+
+    def update_qkv_decode(self, qkv, cos, sin, layer_idx, num_q_heads, attention_mask=None):
+        """update_qkv_fused followed by decode_rotated, one kernel: the new
+        token's k / v go into the cache and the attention output o [B, Hq, D]
+        is returned; bit for bit the two calls."""
+        spec = self._qkv_step(qkv, layer_idx, attention_mask, "update_qkv_decode")
+        return self._decoder.qkv_attend(qkv, cos.contiguous(), sin.contiguous(), spec, layer_idx,
+                                        num_q_heads, 1 / math.sqrt(self.head_dim),
+                                        self.hadamard_dtype is not None)
+
+    def update_qkv_decode_quant(self, qkv, cos, sin, layer_idx, num_q_heads, scale,
+                                attention_mask=None):
+        """update_qkv_fused followed by decode_rotated_quant (the o_proj
+        input: codes [B, Hq D / 2], scales [B, 1]) with the q/k/v step and the
+        attention in one kernel; bit for bit the two calls."""
+        spec = self._qkv_step(qkv, layer_idx, attention_mask, "update_qkv_decode_quant")
+        return self._decoder.qkv_attend_head_had_quant(
+            qkv, cos.contiguous(), sin.contiguous(), spec, layer_idx, num_q_heads,
+            1 / math.sqrt(self.head_dim), self.hadamard_dtype is not None, scale)
 
     def decode_rotated(self, q_rot, layer_idx):
         """Decode attention of an already rotated q [B, Hq, D] over this

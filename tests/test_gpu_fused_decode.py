@@ -188,6 +188,73 @@ def test_qkv_rope_had_append_equals_update_chain(B, T, Hq, Hkv, page, cos_batch)
         assert_bitexact(to_np(out_b), to_np(out_a), f"attention output (layer {li})")
 
 
+@pytest.mark.parametrize("B,T,Hq,Hkv,page,cos_batch,chunks,rotate", [
+    (3, 37, 8, 2, 16, 1, 1, True), (32, 255, 32, 8, 256, 1, 1, True), (2, 16, 4, 4, 16, 2, 1, True),
+    (3, 300, 8, 2, 64, 1, 3, True), (4, 100, 8, 1, 32, 1, 1, True), (1, 40, 16, 16, 16, 1, 2, True),
+    (5, 70, 8, 4, 8, 5, 1, True), (3, 37, 8, 2, 16, 1, 1, False),
+    # config 3: unsplit (one eight-wave block per CU) and split in two
+    (32, 4095, 32, 8, 256, 1, 1, True), (32, 4095, 32, 8, 256, 1, 2, True)])
+def test_qkv_decode_i4_equals_append_then_decode(B, T, Hq, Hkv, page, cos_batch, chunks, rotate):
+    """qkv_decode_i4 (the q/k/v step fused into the decode attention) against
+    qkv_rope_had_append followed by batch_decode_i4: the cache bytes, the
+    attention output and the o_proj input codes are bit-identical, split or
+    not, with the new token in the last tile of its chunk (its codes written
+    by the block and attended from LDS) and in the page-table (stage_tile)
+    form for page sizes below 32."""
+    from signrot_amd.functional.hadamard import _inv_sqrt_f32
+    from signrot_amd.transformers.decode_layer import rope_cos_sin
+    from signrot_amd.transformers.kv_cache import _SplitDecoder
+    rng = np.random.default_rng(B * 1000 + T + chunks)
+    cache_a = _prefilled_cache(B, T, Hkv, Hq, page, 2, rng)
+    caches = [cache_a, _clone_cache(cache_a), _clone_cache(cache_a)]
+    for c in caches:
+        if not rotate:
+            c.hadamard_dtype = None
+        c._decoder = _SplitDecoder(B, Hq, 128, chunks, "cuda", c.hadamard_dtype)
+    cache_a, cache_b, cache_c = caches
+    D = 128
+    if cos_batch == 1:
+        cos, sin = rope_cos_sin([T], D, 500000.0, "cuda")
+    else:
+        cos, sin = rope_cos_sin(list(range(T, T + B)), D, 10000.0, "cuda")
+        cos, sin = cos.view(B, 1, D), sin.view(B, 1, D)
+    scale = _inv_sqrt_f32(Hq)
+    for li in (0, 1):
+        qkv = to_dev((rng.standard_normal((B, (Hq + 2 * Hkv) * D)) * 2.0).astype(np.float16))
+        q_rot = cache_a.update_qkv_fused(qkv, cos, sin, li, Hq)
+        o_a = cache_a.decode_rotated(q_rot, li)
+        qa_a, sa_a = cache_a.decode_rotated_quant(q_rot, li, scale)
+        o_b = cache_b.update_qkv_decode(qkv, cos, sin, li, Hq)
+        qa_c, sa_c = cache_c.update_qkv_decode_quant(qkv, cos, sin, li, Hq, scale)
+        torch.cuda.synchronize()
+        assert cache_a.length == cache_b.length == cache_c.length
+        for name, c in (("qkv_decode_i4", cache_b), ("qkv_decode_i4 + quant", cache_c)):
+            assert_bitexact(to_np(c.pages), to_np(cache_a.pages), f"cache codes, {name} (layer {li})")
+            assert_bitexact(to_np(c.scales), to_np(cache_a.scales), f"cache params, {name} (layer {li})")
+        assert_bitexact(to_np(o_b), to_np(o_a), f"attention output (layer {li})")
+        assert_bitexact(to_np(qa_c), to_np(qa_a), f"o_proj input codes (layer {li})")
+        assert_bitexact(to_np(sa_c), to_np(sa_a), f"o_proj input scales (layer {li})")
+
+
+def test_qkv_decode_i4_argument_errors():
+    C = _ops()
+    rng = np.random.default_rng(3)
+    cache = _prefilled_cache(2, 20, 2, 8, 16, 1, rng)
+    spec = cache.specs()
+    qkv = torch.zeros(2, 12 * 128, dtype=torch.float16, device="cuda")
+    cos = torch.zeros(1, 128, dtype=torch.float16, device="cuda")
+    o = torch.empty(2, 8, 128, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="qkv must be"):
+        C.qkv_decode_i4(o, qkv[:, :-128].contiguous(), cos, cos, **spec, layer_idx=0, n_q_heads=8,
+                        had_scale=1.0)
+    with pytest.raises(RuntimeError, match="split"):
+        C.qkv_decode_i4(None, qkv, cos, cos, **spec, layer_idx=0, n_q_heads=8, had_scale=1.0)
+    with pytest.raises(RuntimeError, match="cos/sin"):
+        C.qkv_decode_i4(o, qkv, torch.zeros(3, 128, dtype=torch.float16, device="cuda"),
+                        torch.zeros(3, 128, dtype=torch.float16, device="cuda"), **spec, layer_idx=0,
+                        n_q_heads=8, had_scale=1.0)
+
+
 @pytest.mark.parametrize("M,ffn,K", [
     (32, 14336, 4096), (1, 14336, 4096), (16, 896, 1024), (7, 8, 256), (32, 28672, 8192),
     (20, 1000, 4128),

@@ -249,6 +249,7 @@ def test_qkv_rope_had_append_nonfinite_kv():
     kv = rng.standard_normal((2, B, T, Hkv, D)).astype(np.float16)
     cache_a.update(to_dev(kv[0]), to_dev(kv[1]), 0, {})
     cache_b = _clone_cache(cache_a)
+    cache_c = _clone_cache(cache_a)
     qkv_np = (rng.standard_normal((B, (Hq + 2 * Hkv) * D)) * 2.0).astype(np.float16)
     k0, v0 = Hq * D, (Hq + Hkv) * D
     qkv_np[0, k0 + 5] = NAN                  # K head 0 of request 0
@@ -263,9 +264,12 @@ def test_qkv_rope_had_append_nonfinite_kv():
     kernel.rope_qk(q, k, cos, sin)
     cache_a.update(k, v, 0, {"attention_mask": None})
     cache_b.update_qkv_fused(qkv, cos, sin, 0, Hq)
+    cache_c.update_qkv_decode(qkv, cos, sin, 0, Hq)  # the form fused with the attention
     torch.cuda.synchronize()
     assert_bitexact(to_np(cache_b.pages), to_np(cache_a.pages), "cache codes")
     assert_bitexact(to_np(cache_b.scales), to_np(cache_a.scales), "cache params")
+    assert_bitexact(to_np(cache_c.pages), to_np(cache_a.pages), "cache codes (qkv_decode_i4)")
+    assert_bitexact(to_np(cache_c.scales), to_np(cache_a.scales), "cache params (qkv_decode_i4)")
     # the new token's V rows (no rotation) against the oracle quantizer,
     # located by the page rule of the cache's own index buffers
     from oracle import attention as oa
