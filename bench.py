@@ -491,7 +491,9 @@ def bench_moe(dev, seed, tokens=512, hidden=4096, ffn=14336, experts=8, top_k=2,
     """Config 5: Mixtral-8x7B-shape W4A4 MoE FFN (SignRotMoEBlock, grouped
     path): 8 experts, top-2 routing of 512 tokens (router logits N(0,1)
     seeded through a random router), hidden 4096, FFN 14336, SwiGLU,
-    had_28 x H_512 + per-expert sign on the down-proj input."""
+    had_28 x H_512 + per-expert sign on the down-proj input.  The block has
+    no host synchronization, so it is timed as HIP-graph replays (the eager
+    time, which adds the module's host work between launches, beside it)."""
     from signrot_amd.nn import SignRotMoEBlock
     g = torch.Generator(device=dev).manual_seed(seed)
     gate = torch.nn.Linear(hidden, experts, bias=False, dtype=torch.float16, device=dev)
@@ -512,13 +514,15 @@ def bench_moe(dev, seed, tokens=512, hidden=4096, ffn=14336, experts=8, top_k=2,
     xs = [torch.randn(1, tokens, hidden, device=dev, generator=g).half() for _ in range(4)]
     st = torch.cuda.current_stream()
     with torch.no_grad():
-        t = _time_launches(lambda i: blk(xs[i % len(xs)]), reps, st) * 1e3
+        t_eager = _time_launches(lambda i: blk(xs[i % len(xs)]), reps, st) * 1e3
+        t = _time_graph(lambda i: blk(xs[i % len(xs)]), reps) * 1e3
         counts = blk.route(xs[0].view(-1, hidden)).counts
     rows = tokens * top_k
     ops = 2.0 * rows * 3 * hidden * ffn
     nbytes = 3 * experts * ffn * hidden // 2
     res = {"tokens": tokens, "experts": experts, "top_k": top_k, "hidden": hidden, "ffn": ffn,
-           "rows_per_expert": counts.tolist(), "block": _roof(t, ops, nbytes)}
+           "rows_per_expert": counts.tolist(), "timing": "hip_graph",
+           "block_eager_us": round(t_eager, 2), "block": _roof(t, ops, nbytes)}
     del blk, xs
     torch.cuda.empty_cache()
     return res
