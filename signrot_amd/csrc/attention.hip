@@ -9,9 +9,12 @@
 // whatever a padded position holds, NaN or inf included, cannot reach a
 // live row -- the unpad step of the reference never reads them either.
 //
-// One block = 4 waves = 128 query rows of one (sequence, q head); wave w
-// owns rows [32 w, 32 w + 32).  Everything is computed transposed so that
-// one lane owns one query row (column l % 32 of the MFMA output):
+// One block = NWV waves over QB = 32 NWV / GH query rows of GH q heads of
+// one KV head (sequence b): wave w owns rows [32 (w / GH), + 32) of q head
+// w % GH of the group, so each K/V tile staged in LDS serves all GH heads
+// that share it (GH = the GQA group size up to 8, in 8-wave blocks; a
+// 4-wave block of one head otherwise).  Everything is computed transposed
+// so that one lane owns one query row (column l % 32 of the MFMA output):
 //   S^T[key][q] = K_tile (64 x 128) . Q^T            fp16 MFMA 32x32x16
 //   O^T[d][q]  += V^T (128 x 64)  . P^T               fp16 MFMA 32x32x16
 // The MFMA output layout (lane l, register v -> row 8(v/4) + 4(l/32) + v%4,
@@ -31,7 +34,6 @@
 namespace {
 
 constexpr int HD = 128;          // head dim
-constexpr int QT = 128;          // query rows per block (4 waves x 32)
 constexpr int KT = 64;           // keys per tile
 constexpr int KS = HD + 8;       // Ks row stride (halves)
 constexpr int VS = KT + 8;       // Vt row stride (halves)
@@ -56,7 +58,11 @@ SRQ_DEV v16f mfma32(v8h a, v8h b, v16f c) {
 // buffer after them, so one barrier per tile covers both "tile t + 1 is in
 // LDS" and "every wave is done with the buffer tile t + 2 will overwrite",
 // and the load latency hides behind the compute.
-__global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
+template <int NWV, int GH>
+__global__ void __launch_bounds__(NWV * 64, 8 / NWV) prefill_attn_kernel(AttnArgs a) {
+    constexpr int NT = NWV * 64;              // threads
+    constexpr int QB = 32 * NWV / GH;         // query rows per block
+    static_assert(NWV % GH == 0 && (NT == 256 || NT == 512), "block shape");
     __shared__ __align__(16) f16 Ks_[2][KT * KS];
     __shared__ __align__(16) f16 Vt_[2][HD * VS];
     __shared__ float kbias_[2][KT];
@@ -64,13 +70,14 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, ln = lane & 31;
+    const int rgrp = wave / GH;               // this wave's 32-row group
     // heaviest causal tiles first
     const int qtile = a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    const int hq = blockIdx.y, b = blockIdx.z;
+    const int hq = (int)blockIdx.y * GH + wave % GH, b = blockIdx.z;
     const int hk = hq / a.group;
-    const int q0 = qtile * QT;
-    const int qrow = q0 + wave * 32 + ln;          // this lane's query row
-    const int wave_last = q0 + wave * 32 + 31;     // last row of this wave
+    const int q0 = qtile * QB;
+    const int qrow = q0 + rgrp * 32 + ln;          // this lane's query row
+    const int wave_last = q0 + rgrp * 32 + 31;     // last row of this wave
 
     const f16 *qb = a.q + (int64_t)b * a.q_seq + (int64_t)hq * HD;
     const f16 *kb = a.k + (int64_t)b * a.kv_seq + (int64_t)hk * HD;
@@ -94,35 +101,37 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
     for (int i = 0; i < HD / 32; ++i) o[i] = (v16f)0.f;
     float m = -INFINITY, l = 0.f;
 
-    const int kv_end = a.causal ? min(a.T, q0 + QT) : a.T;
+    const int kv_end = a.causal ? min(a.T, q0 + QB) : a.T;
     const int ntiles = (kv_end + KT - 1) / KT;
 
-    // staging registers of one tile: K row tid / 4, 32 halves from (tid % 4) * 32;
-    // V keys 2 (tid % 32) + {0, 1}, d from 16 (tid / 32); key bias tid (< KT)
-    // (raw loads; the masking selects run at store time, after the MFMAs, so
-    // that no use of a loaded value forces its wait before them)
-    v8h kx[4], vx0[2], vx1[2];
+    // staging registers of one tile, NT threads: K row tid / KR, KH halves
+    // from (tid % KR) * KH; V keys 2 (tid % 32) + {0, 1}, VH dims from
+    // VH (tid / 32); key bias tid (< KT) (raw loads; the masking selects run
+    // at store time, after the MFMAs, so that no use of a loaded value
+    // forces its wait before them)
+    constexpr int KR = NT / KT, KH = HD / KR, VH = HD / (NT / 32);
+    v8h kx[KH / 8], vx0[VH / 8], vx1[VH / 8];
     bool kok = false, vok0 = false, vok1 = false;
     float kbv = 0.f;
     auto load_tile = [&](int t) __attribute__((always_inline)) {
         const int k0 = t * KT;
         {
-            const int r = tid >> 2, d0 = (tid & 3) * 32;
+            const int r = tid / KR, d0 = (tid % KR) * KH;
             const int key = k0 + r;
             kok = key < a.T && (!mb || mb[key] != 0);
             const f16 *src = kb + (int64_t)(kok ? key : 0) * a.kv_tok + d0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) kx[i] = *reinterpret_cast<const v8h *>(src + 8 * i);
+            for (int i = 0; i < KH / 8; ++i) kx[i] = *reinterpret_cast<const v8h *>(src + 8 * i);
         }
         {
-            const int kp = tid & 31, d0 = (tid >> 5) * 16;
+            const int kp = tid & 31, d0 = (tid >> 5) * VH;
             const int key = k0 + 2 * kp;
             vok0 = key < a.T && (!mb || mb[key] != 0);
             vok1 = key + 1 < a.T && (!mb || mb[key + 1] != 0);
             const f16 *s0 = vb + (int64_t)(vok0 ? key : 0) * a.kv_tok + d0;
             const f16 *s1 = vb + (int64_t)(vok1 ? key + 1 : 0) * a.kv_tok + d0;
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < VH / 8; ++i) {
                 vx0[i] = *reinterpret_cast<const v8h *>(s0 + 8 * i);
                 vx1[i] = *reinterpret_cast<const v8h *>(s1 + 8 * i);
             }
@@ -136,16 +145,16 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
     // K row-major, V transposed (V^T rows d, columns keys)
     auto store_tile = [&](int buf) __attribute__((always_inline)) {
         {
-            const int r = tid >> 2, d0 = (tid & 3) * 32;
+            const int r = tid / KR, d0 = (tid % KR) * KH;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < KH / 8; ++i)
                 *reinterpret_cast<v8h *>(&Ks_[buf][r * KS + d0 + 8 * i]) =
                     kok ? kx[i] : (v8h)(f16)0;
         }
         {
-            const int kp = tid & 31, d0 = (tid >> 5) * 16;
+            const int kp = tid & 31, d0 = (tid >> 5) * VH;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
+            for (int j = 0; j < VH; ++j) {
                 v2h pr;
                 pr[0] = vok0 ? vx0[j / 8][j % 8] : (f16)0;
                 pr[1] = vok1 ? vx1[j / 8][j % 8] : (f16)0;
@@ -185,7 +194,7 @@ __global__ void __launch_bounds__(256, 2) prefill_attn_kernel(AttnArgs a) {
             // every row of the wave (no mask, inside the sequence, below the
             // causal diagonal) skips the per-key tests: the same values.
             float mt = -INFINITY;
-            const bool full = !mb && k0 + KT <= a.T && (!a.causal || k0 + KT - 1 <= q0 + wave * 32);
+            const bool full = !mb && k0 + KT <= a.T && (!a.causal || k0 + KT - 1 <= q0 + rgrp * 32);
             if (full) {
 #pragma unroll
                 for (int sb = 0; sb < 2; ++sb)
@@ -305,8 +314,26 @@ extern "C" int srq_prefill_attention(const void *q, const void *k, const void *v
     a.group = (int)(n_q_heads / n_kv_heads);
     a.c = sm_scale * 1.4426950408889634f;
     a.causal = causal ? 1 : 0;
-    dim3 grid((unsigned)srq_cdiv(seq_len, QT), (unsigned)n_q_heads, (unsigned)batch);
-    prefill_attn_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(a);
+    // GQA groups of 2, 4 or 8 q heads share each staged K/V tile in 8-wave
+    // blocks (32 8 / G query rows of the G heads) when that still gives a
+    // block per CU (MI355X: 256); otherwise 4-wave blocks of 128 rows of one
+    // head (Llama-70B heads, T = 8192: 2012 -> 1528 us; T = 512 stays on
+    // the 4-wave form: 25 against 31 us)
+    hipStream_t st = (hipStream_t)stream;
+    auto go = [&](auto kern, int nwv, int gh) {
+        const int qb = 32 * nwv / gh;
+        dim3 grid((unsigned)srq_cdiv(seq_len, qb), (unsigned)(n_q_heads / gh), (unsigned)batch);
+        kern<<<grid, nwv * 64, 0, st>>>(a);
+    };
+    constexpr int64_t kCUs = 256;
+    const bool gqa = (a.group == 2 || a.group == 4 || a.group == 8) &&
+                     srq_cdiv(seq_len, 256 / a.group) * (n_q_heads / a.group) * batch >= kCUs;
+    switch (gqa ? a.group : 1) {
+    case 2: go(prefill_attn_kernel<8, 2>, 8, 2); break;
+    case 4: go(prefill_attn_kernel<8, 4>, 8, 4); break;
+    case 8: go(prefill_attn_kernel<8, 8>, 8, 8); break;
+    default: go(prefill_attn_kernel<4, 1>, 4, 1); break;
+    }
     SRQ_LAUNCH_CHECK("prefill_attention");
     return SRQ_OK;
 }

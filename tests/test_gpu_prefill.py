@@ -39,7 +39,11 @@ def _check(got, q, k, v, mask, causal, what):
 @pytest.mark.parametrize("B,T,Hq,Hkv,causal,masked", [
     (1, 1, 4, 4, True, False), (2, 77, 8, 2, True, True), (1, 128, 4, 1, True, False),
     (1, 129, 2, 2, True, False), (1, 300, 32, 8, True, False), (2, 200, 4, 4, False, True),
-    (1, 1031, 8, 8, True, False), (3, 65, 6, 3, False, False)])
+    (1, 1031, 8, 8, True, False), (3, 65, 6, 3, False, False),
+    # GQA groups of 8, 4 and 2 in 8-wave blocks of 32 / 64 / 128 query rows
+    # (enough blocks for one per CU), and of 3 (4-wave blocks)
+    (4, 333, 64, 8, True, False), (2, 1100, 64, 8, True, True), (4, 700, 32, 8, True, False),
+    (8, 600, 16, 8, False, False), (3, 1031, 32, 16, True, True), (2, 70, 9, 3, True, True)])
 def test_prefill_matches_oracle(C, B, T, Hq, Hkv, causal, masked):
     q, k, v = _inputs(B, T, Hq, Hkv, seed=T * 7 + B)
     mask = None
