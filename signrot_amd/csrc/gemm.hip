@@ -1050,7 +1050,7 @@ constexpr int kStreamKW = 8;
 constexpr int kStreamS = 4;
 constexpr int kStreamMaxCb = 16;   // column blocks per workgroup
 
-template <int MB, int NSUB, bool AUNP, bool UA>
+template <int MB, int NSUB, bool AUNP, bool UA, bool BATCH = false>
 __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
     const uint8_t *__restrict__ A, const uint8_t *__restrict__ B, int64_t M, int64_t N,
     int64_t K, Epi e) {
@@ -1059,6 +1059,9 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
     __shared__ int sum[kStreamMaxCb][MB * 256];
     __shared__ float sbl[kStreamMaxCb * 16];
     __shared__ float sal[MB * 16];
+    // BATCH: the A transposes after the first batch go through this area
+    // (the ring then holds weight items in flight)
+    __shared__ __attribute__((aligned(16))) uint8_t astage[BATCH ? KW * MB * 2048 : 16];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t KB = K / 2;
@@ -1066,6 +1069,9 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
     const int per = (units + KW - 1) / KW;
     const int u0 = wave * per;
     const int nsub = max(0, min(per, units - u0));
+    // BATCH: the wave's units in batches of NSUB (A of one batch in
+    // registers at a time); a batch's units past nsub read as zeros
+    const int nbat = BATCH ? (per + NSUB - 1) / NSUB : 1;
     const int ncb = (int)((N + 15) / 16);
     const int G = gridDim.x;
     const int ncb_mine = (ncb - (int)blockIdx.x + G - 1) / G;
@@ -1097,21 +1103,24 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
             }
     }
 
-    // A: unit s of this wave, row block i, chunk pair t; lane holds row
-    // 16 i + (lane & 15), logical chunk 4 t + (lane >> 4) of the unit
+    // A: unit s of the wave's batch bt, row block i, chunk pair t; lane
+    // holds row 16 i + (lane & 15), logical chunk 4 t + (lane >> 4) of the
+    // unit, read line-friendly and transposed through the wave's staging
+    // area tb
     v4i areg[NSUB][MB][2];
-    {
+    v4i aun[AUNP ? NSUB : 1][MB][2][2];
+    auto load_a = [&](int bt, uint8_t *tb) __attribute__((always_inline)) {
         v4i raw[NSUB][MB][2];
 #pragma unroll
         for (int s = 0; s < NSUB; ++s)
 #pragma unroll
             for (int h = 0; h < 2 * MB; ++h) {
                 const int64_t row = 8 * h + (lane >> 3);
-                const int64_t kb = (int64_t)(u0 + s) * 128 + 16 * (lane & 7);
-                const bool ok = s < nsub && row < M && kb < KB;
+                const int su = bt * NSUB + s;
+                const int64_t kb = (int64_t)(u0 + su) * 128 + 16 * (lane & 7);
+                const bool ok = su < nsub && row < M && kb < KB;
                 raw[s][h >> 1][h & 1] = bload16(ar, ok ? (uint32_t)(row * KB + kb) : kOob);
             }
-        uint8_t *tb = ring + wave * (S * 2048);
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) {
 #pragma unroll
@@ -1130,38 +1139,50 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
             // this wave's reads of unit s land before unit s + 1 overwrites the slot
             __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
         }
-    }
 #pragma unroll
-    for (int s = 0; s < NSUB; ++s)
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-#pragma unroll
-            for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(areg[s][i][t]));
-    v4i aun[AUNP ? NSUB : 1][MB][2][2];
-    if (AUNP) {
-#pragma unroll
-        for (int s = 0; s < (AUNP ? NSUB : 1); ++s)
+        for (int s = 0; s < NSUB; ++s)
 #pragma unroll
             for (int i = 0; i < MB; ++i)
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    aun[s][i][t][0] = unpack8a<UA>((u32)areg[s][i][t][0], (u32)areg[s][i][t][1]);
-                    aun[s][i][t][1] = unpack8a<UA>((u32)areg[s][i][t][2], (u32)areg[s][i][t][3]);
-                }
-    }
+                for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(areg[s][i][t]));
+        if (AUNP) {
+#pragma unroll
+            for (int s = 0; s < (AUNP ? NSUB : 1); ++s)
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        aun[s][i][t][0] = unpack8a<UA>((u32)areg[s][i][t][0], (u32)areg[s][i][t][1]);
+                        aun[s][i][t][1] = unpack8a<UA>((u32)areg[s][i][t][2], (u32)areg[s][i][t][3]);
+                    }
+        }
+    };
+    load_a(0, ring + wave * (S * 2048));
     __syncthreads();
 
-    // item = (column block j, unit s); DMA instruction h covers rows 8 h + (lane >> 3)
+    // item = (batch, column block j, unit s); DMA instruction h covers rows
+    // 8 h + (lane >> 3).  Without batching the items are (j, s < nsub);
+    // with it every batch has NSUB units (those past nsub load zeros).
     const uint32_t ring_w = (uint32_t)(uintptr_t)ring + (uint32_t)wave * (S * 2048);
-    const int total = ncb_mine * nsub;
+    const int per_bat = BATCH ? ncb_mine * NSUB : ncb_mine * nsub;
+    const int total = per_bat * nbat;
     auto issue = [&](int item) {
         const uint32_t lds = ring_w + (item % S) * 2048;
         int64_t nrow0 = 0, kb0 = 0;
-        const bool live = item < total;
+        bool live = item < total;
         if (live) {
-            const int j = item / nsub, s = item - j * nsub;
+            int j, su;
+            if (BATCH) {
+                const int bt = item / per_bat, rem = item - bt * per_bat;
+                j = rem / NSUB;
+                su = bt * NSUB + (rem - j * NSUB);
+                live = su < nsub;
+            } else {
+                j = item / nsub;
+                su = item - j * nsub;
+            }
             nrow0 = (int64_t)(blockIdx.x + j * G) * 16;
-            kb0 = (int64_t)(u0 + s) * 128;
+            kb0 = (int64_t)(u0 + su) * 128;
         }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -1179,51 +1200,58 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
 #pragma unroll
     for (int it = 0; it < S - 1; ++it) issue(it);
 
-    for (int j = 0; j < ncb_mine; ++j) {
+    for (int bt = 0; bt < nbat; ++bt) {
+        // the next batch's A (the items already in flight keep streaming)
+        if (BATCH && bt > 0) load_a(bt, astage + wave * (MB * 2048));
+        for (int j = 0; j < ncb_mine; ++j) {
 #pragma unroll
-        for (int s = 0; s < NSUB; ++s) {
-            if (s >= nsub) break;
-            const int it = j * nsub + s;
-            issue(it + S - 1);  // items past the end load zeros into a free stage
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (S - 1)) : "memory");
-            const uint8_t *st = ring + wave * (S * 2048) + (it % S) * 2048 + 128 * rr;
-            v4i bw[2];
+            for (int s = 0; s < NSUB; ++s) {
+                if (!BATCH && s >= nsub) break;
+                const int it = bt * per_bat + j * (BATCH ? NSUB : nsub) + s;
+                issue(it + S - 1);  // items past the end load zeros into a free stage
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (S - 1)) : "memory");
+                const uint8_t *st = ring + wave * (S * 2048) + (it % S) * 2048 + 128 * rr;
+                v4i bw[2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
-                bw[t] = *(const v4i *)(st + 16 * ((4 * t + (lane >> 4)) ^ (rr & 7)));
+                for (int t = 0; t < 2; ++t)
+                    bw[t] = *(const v4i *)(st + 16 * ((4 * t + (lane >> 4)) ^ (rr & 7)));
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const v4i b0 = unpack8((u32)bw[t][0], (u32)bw[t][1]);
-                const v4i b1 = unpack8((u32)bw[t][2], (u32)bw[t][3]);
+                for (int t = 0; t < 2; ++t) {
+                    const v4i b0 = unpack8((u32)bw[t][0], (u32)bw[t][1]);
+                    const v4i b1 = unpack8((u32)bw[t][2], (u32)bw[t][3]);
 #pragma unroll
-                for (int i = 0; i < MB; ++i) {
-                    v4i a0, a1;
-                    if (AUNP) {
-                        a0 = aun[AUNP ? s : 0][i][t][0];
-                        a1 = aun[AUNP ? s : 0][i][t][1];
-                    } else {
-                        v4i w = areg[s][i][t];
-                        asm volatile("" : "+v"(w));  // unpack per use, not hoisted out of j
-                        a0 = unpack8a<UA>((u32)w[0], (u32)w[1]);
-                        a1 = unpack8a<UA>((u32)w[2], (u32)w[3]);
+                    for (int i = 0; i < MB; ++i) {
+                        v4i a0, a1;
+                        if (AUNP) {
+                            a0 = aun[AUNP ? s : 0][i][t][0];
+                            a1 = aun[AUNP ? s : 0][i][t][1];
+                        } else {
+                            v4i w = areg[s][i][t];
+                            asm volatile("" : "+v"(w));  // unpack per use, not hoisted out of j
+                            a0 = unpack8a<UA>((u32)w[0], (u32)w[1]);
+                            a1 = unpack8a<UA>((u32)w[2], (u32)w[3]);
+                        }
+                        acc[i] = mfma16(a0, b0, acc[i]);
+                        acc[i] = mfma16(a1, b1, acc[i]);
                     }
-                    acc[i] = mfma16(a0, b0, acc[i]);
-                    acc[i] = mfma16(a1, b1, acc[i]);
                 }
             }
+            if (nsub > 0) {
+                int *sm = sum[j];
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        __hip_atomic_fetch_add(&sm[i * 256 + (4 * (lane >> 4) + r) * 16 + rr],
+                                               acc[i][r], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+#pragma unroll
+            for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
         }
-        if (nsub > 0) {
-            int *sm = sum[j];
-#pragma unroll
-            for (int i = 0; i < MB; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    __hip_atomic_fetch_add(&sm[i * 256 + (4 * (lane >> 4) + r) * 16 + rr], acc[i][r],
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        }
-#pragma unroll
-        for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
     }
+    // the zero-fill DMAs of items past the end land before the block ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (e.swiglu) {
         // lane rr < 8: output column 8 c + rr of column block c from gate
@@ -1288,19 +1316,22 @@ bool launch_stream(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int
     const int64_t cb_per = (ncb + 255) / 256;
     if (cb_per > kStreamMaxCb) return false;
     const dim3 grid((unsigned)((ncb + cb_per - 1) / cb_per)), block(kStreamKW * 64);
-#define SRQ_STREAM(MB, NSUB, AUNP) \
-    gemm_stream_kernel<MB, NSUB, AUNP, UA><<<grid, block, 0, st>>>(a, b, M, N, K, e)
+#define SRQ_STREAM(MB, NSUB, AUNP, BATCH) \
+    gemm_stream_kernel<MB, NSUB, AUNP, UA, BATCH><<<grid, block, 0, st>>>(a, b, M, N, K, e)
+    // per > 8 units per wave (K > 16384): A goes through registers in
+    // batches of NSUB units (cfg4 down at M = 1 / 32: 54 us on the skinny
+    // kernel before)
     if (M <= 16) {
-        if (per <= 2) SRQ_STREAM(1, 2, true);
-        else if (per <= 4) SRQ_STREAM(1, 4, true);
-        else if (per <= 8) SRQ_STREAM(1, 8, false);
-        else return false;
+        if (per <= 2) SRQ_STREAM(1, 2, true, false);
+        else if (per <= 4) SRQ_STREAM(1, 4, true, false);
+        else if (per <= 8) SRQ_STREAM(1, 8, false, false);
+        else SRQ_STREAM(1, 8, false, true);
     } else {
-        if (per <= 2) SRQ_STREAM(2, 2, true);
-        else if (per <= 4) SRQ_STREAM(2, 4, false);
-        else if (per <= 7) SRQ_STREAM(2, 7, false);
-        else if (per <= 8) SRQ_STREAM(2, 8, false);
-        else return false;
+        if (per <= 2) SRQ_STREAM(2, 2, true, false);
+        else if (per <= 4) SRQ_STREAM(2, 4, false, false);
+        else if (per <= 7) SRQ_STREAM(2, 7, false, false);
+        else if (per <= 8) SRQ_STREAM(2, 8, false, false);
+        else SRQ_STREAM(2, 7, false, true);
     }
 #undef SRQ_STREAM
     return true;

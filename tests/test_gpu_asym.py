@@ -113,7 +113,8 @@ def test_matmul_colrow(C):
 U4_SHAPES = [  # every kernel of the dispatcher: stream (M <= 32), skinny,
     # tile (64 < M < 1024), 256x128 (M >= 1024), 256x256 (>= 256 tiles)
     (1, 4096, 4096), (16, 4096, 14336), (32, 6144, 4096), (40, 1000, 8192), (64, 2048, 768),
-    (200, 513, 800), (700, 4096, 1024), (2048, 4096, 1024), (4096, 4096, 512), (5, 3, 64)]
+    (200, 513, 800), (700, 4096, 1024), (2048, 4096, 1024), (4096, 4096, 512), (5, 3, 64),
+    (32, 1000, 28672), (3, 700, 20000)]  # the batched stream form (K > 16384)
 
 
 @pytest.mark.parametrize("M,N,K", U4_SHAPES)

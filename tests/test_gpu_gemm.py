@@ -27,6 +27,10 @@ GEMM_SHAPES = [
     (32, 6144, 4096), (32, 28672, 4096), (32, 4096, 14336), (24, 4112, 16384),
     (16, 1000, 8192), (1, 57344, 8192), (3, 17, 4128), (20, 50, 96), (32, 16, 32),
     (9, 4096, 2048), (32, 300, 8320), (2, 70000, 256), (32, 64, 28672),
+    # K > 16384: A through registers in batches of units (exact batches,
+    # a ragged last batch, the cfg4 down-proj shapes)
+    (1, 8192, 28672), (32, 8192, 28672), (16, 520, 20000), (7, 333, 40064),
+    (25, 1000, 30016),
     # 256 x 256 tile kernel (>= 256 such tiles): XCD-aware tile order, ragged
     # M and N with a K tail (row-major order), a grid of two waves of tiles
     (4096, 4096, 1024), (4352, 4160, 4128), (8192, 4096, 640),
@@ -59,17 +63,20 @@ def test_matmul_extreme_values(C):
     b = np.full((4096, K // 2), 0x77, np.uint8)
     c3 = to_np(C.matmul(to_dev(a), to_dev(b)))
     assert np.all(c3 == -56 * K)
-    # the streaming kernel's deepest configuration (M = 32, K = 16384)
-    K = 16384
-    a = np.full((32, K // 2), 0x88, np.uint8)
-    b = np.full((40, K // 2), 0x88, np.uint8)
-    assert np.all(to_np(C.matmul(to_dev(a), to_dev(b))) == 64 * K)
+    # the streaming kernel's deepest register configuration (M = 32, K =
+    # 16384) and its batched form (K = 28672, four batches of A)
+    for K in (16384, 28672):
+        a = np.full((32, K // 2), 0x88, np.uint8)
+        b = np.full((40, K // 2), 0x88, np.uint8)
+        assert np.all(to_np(C.matmul(to_dev(a), to_dev(b))) == 64 * K)
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 4096, 4096), (33, 300, 768),
                                    (128, 4096, 14336), (2048, 4096, 14336), (7, 5, 64),
                                    (32, 6144, 4096), (32, 28672, 4096), (32, 4096, 14336),
                                    (13, 4100, 8192), (4096, 4096, 2048),
+                                   # the batched weight-streaming form (K > 16384)
+                                   (32, 8192, 28672), (5, 1030, 20000),
                                    # mid-size M with >= 192 tiles of 128 x 128: the
                                    # grouped kernel's dense form (ragged M and N,
                                    # N not a multiple of 8)
