@@ -71,6 +71,10 @@ def test_abi_version(lib):
                                              ctypes.c_void_p(256), 256, 256, 1024,
                                              ctypes.c_void_p(256), ctypes.c_void_p(8), 64, None),
      "16-byte aligned"),
+    # the fused q/k/v + decode entry point checks its rotary-table batch
+    (lambda L: L.srq_qkv_decode_i4(None, None, None, None, 3, ctypes.c_float(1.0), 1,
+                                   *[ctypes.c_void_p(256)] * 5, 2, 8, 2, 1, 0, 16, 128, None, 1,
+                                   None), "cos/sin batch"),
     # the no-allocation decode has nowhere to leave unmerged split-KV states
     (lambda L: L.srq_batch_decode_i4_noalloc(None, *[ctypes.c_void_p(256)] * 6, 2, 32, 8, 1, 0,
                                              64, 128, 4, None), "null output"),
