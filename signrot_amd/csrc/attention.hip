@@ -28,7 +28,13 @@
 // when the tile is stored to LDS.
 // Logits are q.k * sm_scale * log2(e); probabilities use exp2, P is rounded
 // to fp16 for the PV product (as flash-attn does), O and the row sum stay
-// fp32, and out = fp16(O / sum).
+// fp32, and out = fp16(O / sum).  The scale c = |sm_scale| log2(e) is applied
+// inside the exponent, p = exp2(fma(s, c, -m)), with the row max taken over
+// the raw s (the sign of sm_scale goes into Q once: -q for a negative scale,
+// 0 for a zero one).  The running max m is moved only when a tile's max
+// exceeds it by more than 8 (log2 units): P then stays below 2^8, which fp16
+// holds at full relative precision, and out = O / sum is the same quotient,
+// while the 64-register rescale of O runs on few tiles instead of most.
 #include "common.h"
 
 namespace {
@@ -37,6 +43,7 @@ constexpr int HD = 128;          // head dim
 constexpr int KT = 64;           // keys per tile
 constexpr int KS = HD + 8;       // Ks row stride (halves)
 constexpr int VS = KT + 8;       // Vt row stride (halves)
+constexpr float kRescale = 8.f;  // move the running max when it grows by more (log2 units)
 
 struct AttnArgs {
     const f16 *q, *k, *v;
@@ -45,7 +52,8 @@ struct AttnArgs {
     int64_t q_tok, q_seq;        // strides (elements) of q: token, sequence
     int64_t kv_tok, kv_seq;      // strides of k and v
     int T, Hq, group;            // group = Hq / Hkv
-    float c;                     // sm_scale * log2(e)
+    float c;                     // |sm_scale| * log2(e), or 1 for a zero scale
+    float qmul;                  // sign of sm_scale (1, -1 or 0), applied to q
     int causal;
 };
 
@@ -89,10 +97,11 @@ __global__ void __launch_bounds__(NWV * 64, 8 / NWV) prefill_attn_kernel(AttnArg
     {
         const bool ok = qrow < a.T && (!mb || mb[qrow] != 0);
         const f16 *qr = qb + (int64_t)(ok ? qrow : 0) * a.q_tok + 8 * g;
+        const f16 qm = (f16)a.qmul;
 #pragma unroll
         for (int kk = 0; kk < HD / 16; ++kk) {
             v8h t = *reinterpret_cast<const v8h *>(qr + 16 * kk);
-            qf[kk] = ok ? t : (v8h)(f16)0;
+            qf[kk] = ok ? t * qm : (v8h)(f16)0;
         }
     }
 
@@ -190,53 +199,51 @@ __global__ void __launch_bounds__(NWV * 64, 8 / NWV) prefill_attn_kernel(AttnArg
                 for (int kk = 0; kk < HD / 16; ++kk)
                     s[sb] = mfma32(*reinterpret_cast<const v8h *>(kr + 16 * kk), qf[kk], s[sb]);
             }
-            // scale, mask, tile max.  A tile with every key live and visible to
-            // every row of the wave (no mask, inside the sequence, below the
-            // causal diagonal) skips the per-key tests: the same values.
+            // mask and tile max of the raw logits.  A tile with every key live
+            // and visible to every row of the wave (no mask, inside the
+            // sequence, below the causal diagonal) skips the per-key tests:
+            // the same values.
             float mt = -INFINITY;
             const bool full = !mb && k0 + KT <= a.T && (!a.causal || k0 + KT - 1 <= q0 + rgrp * 32);
             if (full) {
 #pragma unroll
                 for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const float x = s[sb][v] * a.c;
-                        s[sb][v] = x;
-                        mt = fmaxf(mt, x);
-                    }
+                    for (int v = 0; v < 16; ++v) mt = fmaxf(mt, s[sb][v]);
             } else {
 #pragma unroll
                 for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const int kr = 32 * sb + 8 * (v / 4) + 4 * g + (v % 4);
-                        float x = kbias[kr] == 0.f ? s[sb][v] * a.c : -INFINITY;
-                        if (a.causal && k0 + kr > qrow) x = -INFINITY;
+                        const bool vis = kbias[kr] == 0.f && !(a.causal && k0 + kr > qrow);
+                        const float x = vis ? s[sb][v] : -INFINITY;
                         s[sb][v] = x;
                         mt = fmaxf(mt, x);
                     }
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const float mn = fmaxf(m, mt);
-            const float mu = mn == -INFINITY ? 0.f : mn;
-            const float alpha = __builtin_amdgcn_exp2f(m - mu);
-            m = mn;
-            float ps = 0.f;
+            const float mtc = mt * a.c;   // c > 0: the max of the scaled logits
+            const bool grow = mtc > m + kRescale;
+            if (__builtin_amdgcn_ballot_w64(grow)) {
+                const float alpha = grow ? __builtin_amdgcn_exp2f(m - mtc) : 1.f;
+                m = grow ? mtc : m;
+                l *= alpha;
+#pragma unroll
+                for (int i = 0; i < HD / 32; ++i) o[i] *= alpha;
+            }
+            const float nmu = m == -INFINITY ? 0.f : -m;
+            float ps0 = 0.f, ps1 = 0.f;
             v8h pb[4];
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
-                    const float p = __builtin_amdgcn_exp2f(s[sb][v] - mu);
-                    ps += p;
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[sb][v], a.c, nmu));
+                    if (v & 1) ps1 += p; else ps0 += p;
                     pb[2 * sb + v / 8][v % 8] = (f16)p;
                 }
-            l = l * alpha + ps;
-            // alpha is exactly 1 wherever the running max did not move
-            if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-                for (int i = 0; i < HD / 32; ++i) o[i] *= alpha;
-            }
+            l += ps0 + ps1;
             // O^T += V^T P^T; PV step st covers keys 16 st .. 16 st + 15 of the tile
 #pragma unroll
             for (int st = 0; st < 4; ++st)
@@ -285,6 +292,7 @@ extern "C" int srq_prefill_attention(const void *q, const void *k, const void *v
     SRQ_CHECK_ARG(n_q_heads % n_kv_heads == 0,
                   "prefill_attention: n_q_heads=%lld is not a multiple of n_kv_heads=%lld",
                   (long long)n_q_heads, (long long)n_kv_heads);
+    SRQ_CHECK_ARG(__builtin_isfinite(sm_scale), "prefill_attention: sm_scale is not finite");
     if (batch == 0 || seq_len == 0 || n_q_heads == 0) return SRQ_OK;
     SRQ_CHECK_ARG(q && k && v && out, "prefill_attention: null pointer");
     SRQ_CHECK_ARG(seq_len <= (1 << 30) && n_q_heads <= 65535 && batch <= 65535,
@@ -312,7 +320,8 @@ extern "C" int srq_prefill_attention(const void *q, const void *k, const void *v
     a.T = (int)seq_len;
     a.Hq = (int)n_q_heads;
     a.group = (int)(n_q_heads / n_kv_heads);
-    a.c = sm_scale * 1.4426950408889634f;
+    a.c = (sm_scale == 0.f ? 1.f : fabsf(sm_scale)) * 1.4426950408889634f;
+    a.qmul = sm_scale > 0.f ? 1.f : sm_scale < 0.f ? -1.f : 0.f;
     a.causal = causal ? 1 : 0;
     // GQA groups of 2, 4 or 8 q heads share each staged K/V tile in 8-wave
     // blocks (32 8 / G query rows of the G heads) when that still gives a

@@ -75,6 +75,10 @@ def test_abi_version(lib):
     (lambda L: L.srq_qkv_decode_i4(None, None, None, None, 3, ctypes.c_float(1.0), 1,
                                    *[ctypes.c_void_p(256)] * 5, 2, 8, 2, 1, 0, 16, 128, None, 1,
                                    None), "cos/sin batch"),
+    # the scale goes into the exponent with its sign applied to q: it must be finite
+    (lambda L: L.srq_prefill_attention(None, None, None, None, 1, 4, 4, 4, 128, 512, 2048, 512,
+                                       2048, ctypes.c_float(float("nan")), 1, None, None),
+     "sm_scale"),
     # the no-allocation decode has nowhere to leave unmerged split-KV states
     (lambda L: L.srq_batch_decode_i4_noalloc(None, *[ctypes.c_void_p(256)] * 6, 2, 32, 8, 1, 0,
                                              64, 128, 4, None), "null output"),

@@ -93,6 +93,44 @@ def test_prefill_large_logits(C):
     _check(out, q, k, v, None, True, "large logits")
 
 
+@pytest.mark.parametrize("step", [0.004, 0.01, 0.03, -0.01])
+def test_prefill_rising_logits(C, step):
+    """Logits that rise along the keys by about 2, 5 or 16 (log2 units) per
+    64-key tile, or fall: the running max moves by less than its rescale
+    threshold on many tiles, so probabilities above 1 go through the fp16 PV
+    product and the row sum, and by more on others."""
+    B, T, Hq, Hkv = 1, 600, 4, 2
+    g = torch.Generator().manual_seed(17)
+    q = torch.full((B, T, Hq, 128), 0.5).half()
+    ramp = torch.arange(T, dtype=torch.float32) * step
+    k = (ramp[None, :, None, None] + 0.05 * torch.randn(B, T, Hkv, 128, generator=g)).half()
+    v = torch.randn(B, T, Hkv, 128, generator=g).half()
+    out = C.prefill_attention(q.cuda(), k.cuda(), v.cuda())
+    torch.cuda.synchronize()
+    _check(out, q, k, v, None, True, f"ramp step {step}")
+
+
+@pytest.mark.parametrize("scale", [0.3, -0.05, 0.0])
+def test_prefill_softmax_scale(C, scale):
+    """Any finite softmax_scale: larger than 1/sqrt(128), negative (the
+    softmax then favours the smallest q.k), and zero (the mean of the visible
+    V rows)."""
+    B, T, Hq, Hkv = 2, 260, 8, 2
+    q, k, v = _inputs(B, T, Hq, Hkv, seed=23)
+    mask = torch.ones(B, T, dtype=torch.int64)
+    mask[1, :50] = 0
+    out = C.prefill_attention(q.cuda(), k.cuda(), v.cuda(), mask.cuda(), softmax_scale=scale)
+    torch.cuda.synchronize()
+    want = oa.prefill(q.numpy(), k.numpy(), v.numpy(), mask.numpy(), True, sm_scale=scale)
+    np.testing.assert_allclose(to_np(out).astype(np.float64), want, rtol=1e-2, atol=1e-2)
+
+
+def test_prefill_rejects_nonfinite_scale(C):
+    q = torch.zeros(1, 4, 4, 128, dtype=torch.float16, device="cuda:0")
+    with pytest.raises(RuntimeError, match="sm_scale"):
+        C.prefill_attention(q, q, q, softmax_scale=float("nan"))
+
+
 def test_prefill_strided_qkv_slices(C):
     """q/k/v as column slices of one fused projection output."""
     B, T, Hq, Hkv = 2, 150, 8, 2
