@@ -59,7 +59,8 @@ def parse():
     p.add_argument("--profile", choices=PROFILE_WORKLOADS, default=None,
                    help="only run one workload a few times (for rocprofv3 counter passes): "
                         "the cfg2 QLinear at M = 2048, 128 or 8192, the cfg4 MLP at M = 512, "
-                        "the cfg5 MoE block or the cfg3 decode layer")
+                        "the cfg5 MoE block, the cfg3 decode layer or the prefill attention "
+                        "(Llama-70B heads, T = 8192)")
     p.add_argument("--cpu-rows", type=int, default=256,
                    help="rows of the CPU baseline sample")
     p.add_argument("--min-bytes", type=float, default=640e6,
@@ -123,7 +124,7 @@ def time_cpu_baseline(args, x, hadk, k, sign, wfq):
 
 COPY_BYTES = 1 << 30
 PROFILE_WORKLOADS = ("cfg2_M2048", "cfg2_M128", "cfg2_M8192", "cfg2_M16", "cfg4_M512",
-                     "cfg5_moe", "cfg3_decode")
+                     "cfg5_moe", "cfg3_decode", "prefill_T8192")
 
 
 def bench_decode_layer(args, dev):
@@ -638,6 +639,8 @@ def profile_workloads(args, dev):
         res = bench_mlp70b(dev, 512, args.seed + 30 + 512, reps=3, min_bytes=6e8)
     elif name == "cfg5_moe":
         res = bench_moe(dev, args.seed + 40, reps=3)
+    elif name == "prefill_T8192":
+        res = bench_prefill_attention(dev, 1, 8192, 64, 8, args.seed + 50 + 8192, reps=3)
     else:
         args.decode_steps, args.decode_layers = 3, 2
         res = bench_decode_layer(args, dev)
