@@ -23,9 +23,12 @@
 // exchange with lane l ^ 32; P^T becomes the B operand of the PV product
 // straight from the lane's registers if the 16 k-slots of each PV step are
 // assigned to keys in that same order (k-slot j of lane half g <-> key
-// 8(j/4) + 4g + j%4 of the 16-key step), and V^T is read from LDS in the
-// matching order (two 8-byte reads per operand).  V is transposed once,
-// when the tile is stored to LDS.
+// 8(j/4) + 4g + j%4 of the 16-key step).  V stays row-major in LDS and its
+// V^T operand comes from gfx950's transposing LDS read (ds_read_b64_tr_b16:
+// within each 16 lanes, lane 4a + b receives half b of the 8 bytes read by
+// lanes a, a + 4, a + 8, a + 12): lanes reading rows k0 + j / 4, columns
+// d + 4 (j % 4) (j = lane % 16) hand lane j the 4 keys k0..k0+3 of column
+// d + j, one group of 4 k-slots (two reads per operand).
 // Logits are q.k * sm_scale * log2(e); probabilities use exp2, P is rounded
 // to fp16 for the PV product (as flash-attn does), O and the row sum stay
 // fp32, and out = fp16(O / sum).  The scale c = |sm_scale| log2(e) is applied
@@ -42,11 +45,11 @@ namespace {
 constexpr int HD = 128;          // head dim
 constexpr int KT = 64;           // keys per tile
 constexpr int KS = HD + 8;       // Ks row stride (halves)
-// Vt row stride (halves): 34 dwords, so the 8-byte V^T operand reads of
-// consecutive lanes (rows 34 dwords apart) start on distinct even banks; a
-// 36-dword stride (KT + 8) repeats the bank pattern within a read and measured
-// 9x the bank-conflict cycles (Llama-70B heads, T = 8192: 1466 -> 1396 us)
-constexpr int VS = KT + 4;
+// Row-major V row stride (halves): 288 bytes, so the 4 rows x 32 bytes that
+// each 16 lanes of a transposing read touch lie on distinct banks (a
+// 272-byte stride measured 2-4% slower at T = 2048-8192)
+constexpr int VR = HD + 16;
+typedef short v4s __attribute__((vector_size(8)));
 constexpr float kRescale = 8.f;  // move the running max when it grows by more (log2 units)
 
 struct AttnArgs {
@@ -76,7 +79,7 @@ __global__ void __launch_bounds__(NWV * 64, 8 / NWV) prefill_attn_kernel(AttnArg
     constexpr int QB = 32 * NWV / GH;         // query rows per block
     static_assert(NWV % GH == 0 && (NT == 256 || NT == 512), "block shape");
     __shared__ __align__(16) f16 Ks_[2][KT * KS];
-    __shared__ __align__(16) f16 Vt_[2][HD * VS];
+    __shared__ __align__(16) f16 Vs_[2][KT * VR];
     __shared__ float kbias_[2][KT];
 
     const int tid = threadIdx.x;
@@ -117,76 +120,57 @@ __global__ void __launch_bounds__(NWV * 64, 8 / NWV) prefill_attn_kernel(AttnArg
     const int kv_end = a.causal ? min(a.T, q0 + QB) : a.T;
     const int ntiles = (kv_end + KT - 1) / KT;
 
-    // staging registers of one tile, NT threads: K row tid / KR, KH halves
-    // from (tid % KR) * KH; V keys 2 (tid % 32) + {0, 1}, VH dims from
-    // VH (tid / 32); key bias tid (< KT) (raw loads; the masking selects run
-    // at store time, after the MFMAs, so that no use of a loaded value
-    // forces its wait before them)
-    constexpr int KR = NT / KT, KH = HD / KR, VH = HD / (NT / 32);
-    v8h kx[KH / 8], vx0[VH / 8], vx1[VH / 8];
-    bool kok = false, vok0 = false, vok1 = false;
+    // staging registers of one tile, NT threads: row tid / KR of K and of V,
+    // KH halves from (tid % KR) * KH; key bias tid (< KT) (raw loads; the
+    // masking selects run at store time, after the MFMAs, so that no use of a
+    // loaded value forces its wait before them)
+    constexpr int KR = NT / KT, KH = HD / KR;
+    v8h kx[KH / 8], vx[KH / 8];
+    bool ok = false;
     float kbv = 0.f;
     auto load_tile = [&](int t) __attribute__((always_inline)) {
-        const int k0 = t * KT;
-        {
-            const int r = tid / KR, d0 = (tid % KR) * KH;
-            const int key = k0 + r;
-            kok = key < a.T && (!mb || mb[key] != 0);
-            const f16 *src = kb + (int64_t)(kok ? key : 0) * a.kv_tok + d0;
+        const int r = tid / KR, d0 = (tid % KR) * KH;
+        const int key = t * KT + r;
+        ok = key < a.T && (!mb || mb[key] != 0);
+        const int64_t off = (int64_t)(ok ? key : 0) * a.kv_tok + d0;
 #pragma unroll
-            for (int i = 0; i < KH / 8; ++i) kx[i] = *reinterpret_cast<const v8h *>(src + 8 * i);
-        }
-        {
-            const int kp = tid & 31, d0 = (tid >> 5) * VH;
-            const int key = k0 + 2 * kp;
-            vok0 = key < a.T && (!mb || mb[key] != 0);
-            vok1 = key + 1 < a.T && (!mb || mb[key + 1] != 0);
-            const f16 *s0 = vb + (int64_t)(vok0 ? key : 0) * a.kv_tok + d0;
-            const f16 *s1 = vb + (int64_t)(vok1 ? key + 1 : 0) * a.kv_tok + d0;
-#pragma unroll
-            for (int i = 0; i < VH / 8; ++i) {
-                vx0[i] = *reinterpret_cast<const v8h *>(s0 + 8 * i);
-                vx1[i] = *reinterpret_cast<const v8h *>(s1 + 8 * i);
-            }
+        for (int i = 0; i < KH / 8; ++i) {
+            kx[i] = *reinterpret_cast<const v8h *>(kb + off + 8 * i);
+            vx[i] = *reinterpret_cast<const v8h *>(vb + off + 8 * i);
         }
         if (tid < KT) {
-            const int key = k0 + tid;
-            const bool ok = key < a.T && (!mb || mb[key] != 0);
-            kbv = ok ? 0.f : -INFINITY;
+            const int kz = t * KT + tid;
+            const bool live = kz < a.T && (!mb || mb[kz] != 0);
+            kbv = live ? 0.f : -INFINITY;
         }
     };
-    // K row-major, V transposed (V^T rows d, columns keys)
-    auto store_tile = [&](int buf) __attribute__((always_inline)) {
-        {
-            const int r = tid / KR, d0 = (tid % KR) * KH;
+    // K and V row-major
+    auto store_tile = [&](int buf, int t) __attribute__((always_inline)) {
+        // a tile with every key live (no mask, inside the sequence; uniform
+        // over the block) needs no selects (T = 8192: 1376 -> 1347 us)
+        if ((mb || (t + 1) * KT > a.T) && !ok) {
 #pragma unroll
-            for (int i = 0; i < KH / 8; ++i)
-                *reinterpret_cast<v8h *>(&Ks_[buf][r * KS + d0 + 8 * i]) =
-                    kok ? kx[i] : (v8h)(f16)0;
+            for (int i = 0; i < KH / 8; ++i) kx[i] = vx[i] = (v8h)(f16)0;
         }
-        {
-            const int kp = tid & 31, d0 = (tid >> 5) * VH;
+        const int r = tid / KR, d0 = (tid % KR) * KH;
 #pragma unroll
-            for (int j = 0; j < VH; ++j) {
-                v2h pr;
-                pr[0] = vok0 ? vx0[j / 8][j % 8] : (f16)0;
-                pr[1] = vok1 ? vx1[j / 8][j % 8] : (f16)0;
-                *reinterpret_cast<v2h *>(&Vt_[buf][(d0 + j) * VS + 2 * kp]) = pr;
-            }
+        for (int i = 0; i < KH / 8; ++i) {
+            *reinterpret_cast<v8h *>(&Ks_[buf][r * KS + d0 + 8 * i]) = kx[i];
+            *reinterpret_cast<v8h *>(&Vs_[buf][r * VR + d0 + 8 * i]) = vx[i];
         }
         if (tid < KT) kbias_[buf][tid] = kbv;
     };
 
     if (ntiles > 0) {
         load_tile(0);
-        store_tile(0);
+        store_tile(0, 0);
     }
     __syncthreads();
     for (int t = 0; t < ntiles; ++t) {
         const int k0 = t * KT;
         const int buf = t & 1;
         const f16 *Ks = Ks_[buf];
-        const f16 *Vt = Vt_[buf];
+        const f16 *Vs = Vs_[buf];
         const float *kbias = kbias_[buf];
         if (t + 1 < ntiles) load_tile(t + 1);  // in flight during this tile's MFMAs
         // this tile's compute (returns early when no key is visible)
@@ -262,14 +246,21 @@ __global__ void __launch_bounds__(NWV * 64, 8 / NWV) prefill_attn_kernel(AttnArg
             for (int st = 0; st < 4; ++st)
 #pragma unroll
                 for (int db = 0; db < HD / 32; ++db) {
-                    const f16 *vr = &Vt[(32 * db + ln) * VS + 16 * st + 4 * g];
-                    v4h lo = *reinterpret_cast<const v4h *>(vr);
-                    v4h hi = *reinterpret_cast<const v4h *>(vr + 8);
-                    v8h av = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    // lane (16-lane group q, j = lane % 16) reads row 4 g + j / 4 (+ 8),
+                    // columns 16 (q & 1) + 4 (j % 4) of the block; the transposing read
+                    // hands lane l keys 4 g + 0..3 (+ 8) of column l % 32
+                    const f16 *vr = &Vs[(16 * st + 4 * g + ((lane & 15) >> 2)) * VR + 32 * db +
+                                        16 * ((lane >> 4) & 1) + 4 * (lane & 3)];
+                    v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s *)vr);
+                    v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) v4s *)(vr + 8 * VR));
+                    v4h l4 = __builtin_bit_cast(v4h, lo), h4 = __builtin_bit_cast(v4h, hi);
+                    v8h av = {l4[0], l4[1], l4[2], l4[3], h4[0], h4[1], h4[2], h4[3]};
                     o[db] = mfma32(av, pb[st], o[db]);
                 }
         }();
-        if (t + 1 < ntiles) store_tile(buf ^ 1);
+        if (t + 1 < ntiles) store_tile(buf ^ 1, t + 1);
         __syncthreads();
     }
 
