@@ -215,12 +215,13 @@ def _time_launches(launch, n, stream):
     return e0.elapsed_time(e1) / n
 
 
-def _time_graph(launch, n, reps=3):
-    """Average ms of `launch(i)`, i = 0 .. n-1, captured once into a HIP
-    graph and replayed `reps` times (HIP events around the replays): the
-    launches' GPU time without the host's per-call cost, which is of the
-    order of the small-M kernels themselves.  `launch` must issue its work
-    on the current stream."""
+def _time_graph(launch, n, reps=5):
+    """Ms per launch of `launch(i)`, i = 0 .. n-1, captured once into a HIP
+    graph: the median over `reps` replays, each between its own HIP events
+    (one disturbed replay, e.g. a clock-state change, does not move it) --
+    the launches' GPU time without the host's per-call cost, which is of
+    the order of the small-M kernels themselves.  `launch` must issue its
+    work on the current stream."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -235,14 +236,15 @@ def _time_graph(launch, n, reps=3):
     graph.replay()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(st)
-    for _ in range(reps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record(st)
+    for r in range(reps):
         graph.replay()
-    e1.record(st)
+        ev[r + 1].record(st)
     torch.cuda.synchronize()
     del graph
-    return e0.elapsed_time(e1) / (reps * n)
+    per = sorted(ev[r].elapsed_time(ev[r + 1]) for r in range(reps))
+    return per[reps // 2] / n
 
 
 def _roof(us, ops, nbytes):
