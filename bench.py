@@ -1,7 +1,7 @@
 """Benchmark of the SignRot W4A4 QLinear hot path on one MI355X.
 
-Default workload (the config the metric is quoted
-on): Llama-3-8B down_proj W4A4 prefill, M=2048 tokens, K=14336, N=4096.
+Default workload (config 2, the one the headline metric is quoted on):
+Llama-3-8B down_proj W4A4 prefill, M=2048 tokens, K=14336, N=4096.
 One step = one QLinear forward over one batch:
   had_sign_quant  (had_28 ⊗ H_512 rotation, SignRot sign, per-token int4
                    quantization + packing: one launch)
@@ -552,8 +552,9 @@ def bench_prefill_attention(dev, B, T, Hq, Hkv, seed, reps=20):
 
 
 def bench_configs(args, dev):
-    """The BASELINE.json configs other than the headline one, each at its
-    own shape (configs[0], the cfg2 M sweep, configs[3], configs[4]), the cfg2
+    """The benchmark configs other than the headline one, each at its own
+    shape (cfg1 q_proj at M=16, the cfg2 M sweep, the cfg4 70B MLP, the cfg5
+    MoE block), the cfg2
     QLinear with asymmetric activations and on the opt-in bf6 path, and the
     prefill attention (Llama-70B heads)."""
     out = {"cfg1_qproj_M16": bench_qlinear(dev, 16, 4096, 4096, args.seed + 10, n_out=4,
