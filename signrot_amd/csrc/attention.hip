@@ -87,8 +87,15 @@ __global__ void __launch_bounds__(NWV * 64, 8 / NWV) prefill_attn_kernel(AttnArg
     const int g = lane >> 5, ln = lane & 31;
     const int rgrp = wave / GH;               // this wave's 32-row group
     // heaviest causal tiles first
-    const int qtile = a.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    const int hq = (int)blockIdx.y * GH + wave % GH, b = blockIdx.z;
+    // dispatch order: the linear block id runs over the head groups fastest,
+    // so under a causal mask the heaviest q tiles of every head group go
+    // first and the light ones fill in behind them (with the q tile fastest,
+    // the first wave of blocks mixed heavy and light tiles of half the head
+    // groups: Llama-70B heads, T = 2048 / 8192: 139 -> 97 / 1299 -> 1225 us)
+    const int lin = (int)blockIdx.x + (int)gridDim.x * (int)blockIdx.y;
+    const int qt_lin = lin / (int)gridDim.y, hg = lin % (int)gridDim.y;
+    const int qtile = a.causal ? (int)gridDim.x - 1 - qt_lin : qt_lin;
+    const int hq = hg * GH + wave % GH, b = blockIdx.z;
     const int hk = hq / a.group;
     const int q0 = qtile * QB;
     const int qrow = q0 + rgrp * 32 + ln;          // this lane's query row
