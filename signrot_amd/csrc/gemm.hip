@@ -557,18 +557,21 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t tiles_n = (N + kBigBN - 1) / kBigBN;
     // XCD-aware tile order: workgroup b runs on XCD b % 8, and XCD x owns
-    // one (tiles_m / 4) x (tiles_n / 2) block of the tile grid (x % 4 picks
-    // the row block, x / 4 the column block), walked column-fastest.  The
+    // one (tiles_m / 2) x (tiles_n / 4) block of the tile grid (x % 2 picks
+    // the row block, x / 2 the column block), walked column-fastest.  The
     // 32 CUs of an XCD then share a few A row panels and B column panels in
-    // their L2 instead of each XCD reading all of B (measured: 3-12% faster
-    // at M = 2048 / 8192, less fabric traffic).  Other grids: row-major.
+    // their L2 instead of each XCD reading all of B (against row-major: 3-12%
+    // faster at M = 2048 / 8192, less fabric traffic).  At M = 2048 (32
+    // tiles of 256 x 128 per XCD) the 4 x 8 block reads 4 A and 8 B panels,
+    // 14.3 MB per XCD, against 18.4 MB for the 2 x 16 one.  Other grids:
+    // row-major.
     const int64_t tiles_m = (M + kBigBM - 1) / kBigBM;
     int64_t m0, n0;
-    if (tiles_m % 4 == 0 && tiles_n % 2 == 0) {
+    if (tiles_m % 2 == 0 && tiles_n % 4 == 0) {
         const int64_t x = blockIdx.x % 8, i = blockIdx.x / 8;
-        const int64_t bm = tiles_m / 4, bn = tiles_n / 2;
-        m0 = ((x % 4) * bm + i / bn) * kBigBM;
-        n0 = ((x / 4) * bn + i % bn) * kBigBN;
+        const int64_t bm = tiles_m / 2, bn = tiles_n / 4;
+        m0 = ((x % 2) * bm + i / bn) * kBigBM;
+        n0 = ((x / 2) * bn + i % bn) * kBigBN;
     } else {
         m0 = ((int64_t)blockIdx.x / tiles_n) * kBigBM;
         n0 = ((int64_t)blockIdx.x % tiles_n) * kBigBN;
