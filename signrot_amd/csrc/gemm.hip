@@ -557,21 +557,37 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t tiles_n = (N + kBigBN - 1) / kBigBN;
     // XCD-aware tile order: workgroup b runs on XCD b % 8, and XCD x owns
-    // one (tiles_m / 2) x (tiles_n / 4) block of the tile grid (x % 2 picks
-    // the row block, x / 2 the column block), walked column-fastest.  The
-    // 32 CUs of an XCD then share a few A row panels and B column panels in
-    // their L2 instead of each XCD reading all of B (against row-major: 3-12%
-    // faster at M = 2048 / 8192, less fabric traffic).  At M = 2048 (32
-    // tiles of 256 x 128 per XCD) the 4 x 8 block reads 4 A and 8 B panels,
-    // 14.3 MB per XCD, against 18.4 MB for the 2 x 16 one.  Other grids:
-    // row-major.
+    // one block of the tile grid, so the 32 CUs of an XCD share a few A row
+    // panels and B column panels in their L2 instead of each XCD reading all
+    // of B (against row-major: 3-12% faster at M = 2048 / 8192, less fabric
+    // traffic).  The grid splits into pm row parts x 8 / pm column parts,
+    // pm the divisor with the fewest panel rows per XCD: at M = 2048, K =
+    // 14336, N = 4096 (8 x 32 tiles) 4 x 8 blocks, 14.3 MB of panels per XCD
+    // against 18.4 for 2 x 16 (FETCH_SIZE 72.1 -> 57.7 MiB per launch); at
+    // M = 512, N = 57344 (2 x 448) each XCD holds both tile rows of its 56
+    // columns, so every B panel is fetched once.  Other grids: row-major.
     const int64_t tiles_m = (M + kBigBM - 1) / kBigBM;
     int64_t m0, n0;
-    if (tiles_m % 2 == 0 && tiles_n % 4 == 0) {
+    // the split of the tile grid into pm row parts x 8 / pm column parts
+    // with the fewest panel rows per XCD (pm = 0: none divides the grid)
+    int pm = 0;
+    int64_t best = 0;
+#pragma unroll
+    for (int c = 1; c <= 8; c *= 2) {
+        if (tiles_m % c || tiles_n % (8 / c)) continue;
+        const int64_t cost = (tiles_m / c) * kBigBM + (tiles_n / (8 / c)) * kBigBN;
+        if (!pm || cost < best) {
+            pm = c;
+            best = cost;
+        }
+    }
+    if (pm) {
+        // XCD x: row part x % pm, column part x / pm, walked row-fastest so
+        // the tiles sharing a B panel run in the same round
         const int64_t x = blockIdx.x % 8, i = blockIdx.x / 8;
-        const int64_t bm = tiles_m / 2, bn = tiles_n / 4;
-        m0 = ((x % 2) * bm + i / bn) * kBigBM;
-        n0 = ((x / 2) * bn + i % bn) * kBigBN;
+        const int64_t am = tiles_m / pm, bn = tiles_n / (8 / pm);
+        m0 = ((x % pm) * am + i % am) * kBigBM;
+        n0 = ((x / pm) * bn + i / am) * kBigBN;
     } else {
         m0 = ((int64_t)blockIdx.x / tiles_n) * kBigBM;
         n0 = ((int64_t)blockIdx.x % tiles_n) * kBigBN;
