@@ -31,6 +31,10 @@ GEMM_SHAPES = [
     # a ragged last batch, the cfg4 down-proj shapes)
     (1, 8192, 28672), (32, 8192, 28672), (16, 520, 20000), (7, 333, 40064),
     (25, 1000, 30016),
+    # 256 x 128 tile kernel: the tile grid split over the 8 XCDs into 1, 2, 4
+    # or 8 row parts (the split with the fewest panel rows per XCD), and
+    # row-major where no split divides the grid
+    (1024, 4096, 256), (2048, 512, 256),
     # 256 x 256 tile kernel (>= 256 such tiles): XCD-aware tile order, ragged
     # M and N with a K tail (row-major order), a grid of two waves of tiles
     (4096, 4096, 1024), (4352, 4160, 4128), (8192, 4096, 640),
