@@ -146,25 +146,36 @@ def test_prefill_strided_qkv_slices(C):
     _check(got, q.cpu(), k.cpu(), v.cpu(), None, True, "strided")
 
 
-def test_prefill_full_size_vs_fp32(C):
-    """Llama-70B heads at T = 2048 against a float32 torch reference on the
-    GPU (per kv-head group, explicit matmuls), tolerance 1e-2."""
-    B, T, Hq, Hkv = 1, 2048, 64, 8
-    g = torch.Generator(device="cuda:0").manual_seed(1)
+@pytest.mark.parametrize("B,T,masked", [(1, 2048, False), (1, 8192, False), (2, 3000, True)])
+def test_prefill_full_size_vs_fp32(C, B, T, masked):
+    """Llama-70B heads at full size (T = 2048 and 8192: the grids whose
+    blocks go out heaviest causal q tile first across the head groups; two
+    left-padded sequences at T = 3000) against a float32 torch reference on
+    the GPU (per kv-head group, explicit matmuls), tolerance 1e-2."""
+    Hq, Hkv = 64, 8
+    g = torch.Generator(device="cuda:0").manual_seed(T + B)
     q = torch.randn(B, T, Hq, 128, device="cuda:0", generator=g).half()
     k = torch.randn(B, T, Hkv, 128, device="cuda:0", generator=g).half()
     v = torch.randn(B, T, Hkv, 128, device="cuda:0", generator=g).half()
-    out = C.prefill_attention(q, k, v).float()
+    mask = None
+    if masked:
+        mask = torch.ones(B, T, dtype=torch.int64, device="cuda:0")
+        mask[1, : T // 4] = 0
+    out = C.prefill_attention(q, k, v, mask).float()
     causal = torch.ones(T, T, dtype=torch.bool, device="cuda:0").tril()
     G = Hq // Hkv
-    for h in range(0, Hq, 9):
-        qh = q[0, :, h].float()
-        kh = k[0, :, h // G].float()
-        vh = v[0, :, h // G].float()
-        s = (qh @ kh.t().contiguous()) * 128 ** -0.5
-        s = s.masked_fill(~causal, float("-inf"))
-        ref = torch.softmax(s, dim=-1) @ vh
-        torch.testing.assert_close(out[0, :, h], ref, rtol=1e-2, atol=1e-2)
+    for bb in range(B):
+        keep = causal if mask is None else causal & (mask[bb] != 0)[None, :]
+        live = torch.ones(T, dtype=torch.bool, device="cuda:0") if mask is None else mask[bb] != 0
+        for h in range(bb, Hq, 9):
+            qh = q[bb, :, h].float()
+            kh = k[bb, :, h // G].float()
+            vh = v[bb, :, h // G].float()
+            s = (qh @ kh.t().contiguous()) * 128 ** -0.5
+            s = s.masked_fill(~keep, float("-inf"))
+            ref = torch.softmax(s[live], dim=-1) @ vh
+            torch.testing.assert_close(out[bb, live, h], ref, rtol=1e-2, atol=1e-2)
+            assert torch.all(out[bb, ~live, h] == 0)
 
 
 def test_prefill_rejects_bad_shapes(C):
