@@ -86,14 +86,14 @@ __global__ void __launch_bounds__(NWV * 64, 8 / NWV) prefill_attn_kernel(AttnArg
     const int lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, ln = lane & 31;
     const int rgrp = wave / GH;               // this wave's 32-row group
-    // heaviest causal tiles first
     // dispatch order: the linear block id runs over the head groups fastest,
     // so under a causal mask the heaviest q tiles of every head group go
     // first and the light ones fill in behind them (with the q tile fastest,
     // the first wave of blocks mixed heavy and light tiles of half the head
     // groups: Llama-70B heads, T = 2048 / 8192: 139 -> 97 / 1299 -> 1225 us)
-    const int lin = (int)blockIdx.x + (int)gridDim.x * (int)blockIdx.y;
-    const int qt_lin = lin / (int)gridDim.y, hg = lin % (int)gridDim.y;
+    // (the host keeps gridDim.x * gridDim.y below 2^31)
+    const uint32_t lin = blockIdx.x + gridDim.x * blockIdx.y;
+    const int qt_lin = (int)(lin / gridDim.y), hg = (int)(lin % gridDim.y);
     const int qtile = a.causal ? (int)gridDim.x - 1 - qt_lin : qt_lin;
     const int hq = hg * GH + wave % GH, b = blockIdx.z;
     const int hk = hq / a.group;
@@ -340,8 +340,14 @@ extern "C" int srq_prefill_attention(const void *q, const void *k, const void *v
     // head (Llama-70B heads, T = 8192: 2012 -> 1528 us; T = 512 stays on
     // the 4-wave form: 25 against 31 us)
     hipStream_t st = (hipStream_t)stream;
+    bool fits = true;
     auto go = [&](auto kern, int nwv, int gh) {
         const int qb = 32 * nwv / gh;
+        // the kernel's linear block id over (q tile, head group) is 32-bit
+        if (srq_cdiv(seq_len, qb) * (n_q_heads / gh) >= (int64_t)1 << 31) {
+            fits = false;
+            return;
+        }
         dim3 grid((unsigned)srq_cdiv(seq_len, qb), (unsigned)(n_q_heads / gh), (unsigned)batch);
         kern<<<grid, nwv * 64, 0, st>>>(a);
     };
@@ -354,6 +360,7 @@ extern "C" int srq_prefill_attention(const void *q, const void *k, const void *v
     case 8: go(prefill_attn_kernel<8, 8>, 8, 8); break;
     default: go(prefill_attn_kernel<4, 1>, 4, 1); break;
     }
+    SRQ_CHECK_ARG(fits, "prefill_attention: seq_len x n_q_heads too large (q tiles x heads >= 2^31)");
     SRQ_LAUNCH_CHECK("prefill_attention");
     return SRQ_OK;
 }

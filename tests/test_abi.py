@@ -79,6 +79,12 @@ def test_abi_version(lib):
     (lambda L: L.srq_prefill_attention(None, None, None, None, 1, 4, 4, 4, 128, 512, 2048, 512,
                                        2048, ctypes.c_float(float("nan")), 1, None, None),
      "sm_scale"),
+    # the prefill kernel's linear block id over (q tile, head group) is 32-bit
+    (lambda L: L.srq_prefill_attention(*[ctypes.c_void_p(256)] * 3, None, 1, 1 << 30, 65528,
+                                       8191, 128, 65528 * 128, (1 << 30) * 65528 * 128,
+                                       8191 * 128, (1 << 30) * 8191 * 128,
+                                       ctypes.c_float(0.088), 1, ctypes.c_void_p(256), None),
+     "too large"),
     # the no-allocation decode has nowhere to leave unmerged split-KV states
     (lambda L: L.srq_batch_decode_i4_noalloc(None, *[ctypes.c_void_p(256)] * 6, 2, 32, 8, 1, 0,
                                              64, 128, 4, None), "null output"),
