@@ -451,7 +451,8 @@ int srq_merge_head_had_quant(const float *tmp, int64_t batch, int64_t n_heads, i
  * unpad / varlen / pad round trip of flash-attn).  Logits are
  * q.k * sm_scale for any finite sm_scale (negative or zero included; a
  * non-finite one is SRQ_EINVAL); fp32 softmax, P rounded to fp16 for the PV
- * product.
+ * product.  SRQ_EINVAL also for a launch grid of 2^31 or more query tiles x
+ * head groups per sequence (tens of millions of tokens).
  * Replaces the prefill call of transformers' _flash_attention_forward
  * (flash-attn 2) in e2e/quantized_llama/modeling_llama.py:81-90. */
 int srq_prefill_attention(const void *q, const void *k, const void *v,
