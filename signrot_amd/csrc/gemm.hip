@@ -1069,31 +1069,22 @@ constexpr int kStreamKW = 8;
 constexpr int kStreamS = 4;
 constexpr int kStreamMaxCb = 16;   // column blocks per workgroup
 
-// MoE rows split between the tiled grouped kernel (128-row tiles) and the
-// stream kernel's remainder pass: an expert with more than one tile whose
-// last tile would hold 1..32 rows leaves those rows to one weight-streaming
-// pass over its weights, so the grouped launch runs no near-empty tiles
-// (cfg5: the down launch's 320 tiles for 256 CUs become 256).  Both kernels
-// decide from the device-resident expert offsets, with this rule.
+// MoE rows past an expert's full 128-row tiles: when an expert has more
+// than one tile and its last tile would hold 1..32 rows, those rows ride on
+// its last full tile instead (the grouped kernel's producer waves compute
+// them from the same weight stages), so no near-empty tile streams the
+// expert's weights a second time (cfg5: the down launch's 320 tiles for 256
+// CUs become 256).
 constexpr int kMoeTile = 128, kMoeRemMax = 32;
-// at most this many experts take the split (each workgroup of the remainder
-// pass reads a bit per expert)
-constexpr int kMoeRemMaxP = 1024;
 SRQ_DEV int64_t moe_tiled_rows(int64_t r) {
     const int64_t q = r % kMoeTile;
     return (r > kMoeTile && q > 0 && q <= kMoeRemMax) ? r - q : r;
 }
-// The remainder pass's view of a MoE product (stream kernel, MOE = true):
-// the expert offsets [P + 1] of the rows, the expert count
-struct MoeRem {
-    const int32_t *offsets = nullptr;
-    int P = 0;
-};
 
-template <int MB, int NSUB, bool AUNP, bool UA, bool BATCH = false, bool MOE = false>
+template <int MB, int NSUB, bool AUNP, bool UA, bool BATCH = false>
 __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
-    const uint8_t *__restrict__ A_in, const uint8_t *__restrict__ B_in, int64_t M_in, int64_t N,
-    int64_t K, Epi e_in, MoeRem mr) {
+    const uint8_t *__restrict__ A, const uint8_t *__restrict__ B, int64_t M, int64_t N,
+    int64_t K, Epi e) {
     constexpr int KW = kStreamKW, S = kStreamS;
     __shared__ __attribute__((aligned(1024))) uint8_t ring[KW * S * 2048];
     __shared__ int sum[kStreamMaxCb][MB * 256];
@@ -1102,308 +1093,245 @@ __global__ __launch_bounds__(kStreamKW * 64) void gemm_stream_kernel(
     // BATCH: the A transposes after the first batch go through this area
     // (the ring then holds weight items in flight)
     __shared__ __attribute__((aligned(16))) uint8_t astage[BATCH ? KW * MB * 2048 : 16];
-    const int lane0 = threadIdx.x & 63;
-    const int wave0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t KB = K / 2;
-    // One pass over column blocks wg, wg + G, ... (at most kStreamMaxCb of
-    // them) of the product A [M, K/2] x B [N, K/2] with epilogue e; it
-    // starts and ends with the workgroup's LDS free
-    auto pass = [&](const uint8_t *A, const uint8_t *B, int64_t M, const Epi &e, int wg,
-                    int G) __attribute__((always_inline)) {
-        // MoE form: fresh lane and wave ids per pass, so nothing derived from
-        // them is hoisted out of its loops and held across passes (that
-        // spilled ~100 VGPRs)
-        int lane = lane0, wave = wave0;
-        if constexpr (MOE) asm volatile("" : "+v"(lane), "+s"(wave));
-        const int units = (int)((KB + 127) / 128);
-        const int per = (units + KW - 1) / KW;
-        const int u0 = wave * per;
-        const int nsub = max(0, min(per, units - u0));
-        // BATCH: the wave's units in batches of NSUB (A of one batch in
-        // registers at a time); a batch's units past nsub read as zeros
-        const int nbat = BATCH ? (per + NSUB - 1) / NSUB : 1;
-        const int ncb = (int)((N + 15) / 16);
-        const int ncb_mine = min(kStreamMaxCb, (ncb - wg + G - 1) / G);
-        if (ncb_mine <= 0) return;
-        const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
+    const int units = (int)((KB + 127) / 128);
+    const int per = (units + KW - 1) / KW;
+    const int u0 = wave * per;
+    const int nsub = max(0, min(per, units - u0));
+    // BATCH: the wave's units in batches of NSUB (A of one batch in
+    // registers at a time); a batch's units past nsub read as zeros
+    const int nbat = BATCH ? (per + NSUB - 1) / NSUB : 1;
+    const int ncb = (int)((N + 15) / 16);
+    const int G = gridDim.x;
+    const int ncb_mine = (ncb - (int)blockIdx.x + G - 1) / G;
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(A, M * KB), br = make_rsrc(B, N * KB);
 
-        for (int t = threadIdx.x; t < ncb_mine * MB * 256; t += KW * 64) (&sum[0][0])[t] = 0;
-        if (!e.C) {
-            for (int t = threadIdx.x; t < MB * 16; t += KW * 64) sal[t] = t < M ? (float)e.sa[t] : 0.f;
-            for (int t = threadIdx.x; t < ncb_mine * 16; t += KW * 64) {
-                const int64_t n = (int64_t)(wg + (t >> 4) * G) * 16 + (t & 15);
-                sbl[t] = n < N ? (float)e.sb[n] : 0.f;
-            }
+    for (int t = threadIdx.x; t < ncb_mine * MB * 256; t += KW * 64) (&sum[0][0])[t] = 0;
+    if (!e.C) {
+        for (int t = threadIdx.x; t < MB * 16; t += KW * 64) sal[t] = t < M ? (float)e.sa[t] : 0.f;
+        for (int t = threadIdx.x; t < ncb_mine * 16; t += KW * 64) {
+            const int64_t n = (int64_t)(blockIdx.x + (t >> 4) * G) * 16 + (t & 15);
+            sbl[t] = n < N ? (float)e.sb[n] : 0.f;
         }
+    }
 
-        // The residual (and bias) of the first column block this wave stores
-        // (j = wave), fetched now so the epilogue after the stream does not wait
-        // a memory round trip for them.
-        const int rr = lane & 15;
-        f16 res0[MB][4], bias0 = (f16)0;
-        if (!e.C && wave < ncb_mine) {
-            const int64_t gn = (int64_t)(wg + wave * G) * 16 + rr;
-            if (e.bias && gn < N) bias0 = e.bias[gn];
-    #pragma unroll
+    // The residual (and bias) of the first column block this wave stores
+    // (j = wave), fetched now so the epilogue after the stream does not wait
+    // a memory round trip for them.
+    const int rr = lane & 15;
+    f16 res0[MB][4], bias0 = (f16)0;
+    if (!e.C && wave < ncb_mine) {
+        const int64_t gn = (int64_t)(blockIdx.x + wave * G) * 16 + rr;
+        if (e.bias && gn < N) bias0 = e.bias[gn];
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = i * 16 + 4 * (lane >> 4) + r;
+                res0[i][r] = (e.res && m < M && gn < N) ? e.res[m * N + gn] : (f16)0;
+            }
+    }
+
+    // A: unit s of the wave's batch bt, row block i, chunk pair t; lane
+    // holds row 16 i + (lane & 15), logical chunk 4 t + (lane >> 4) of the
+    // unit, read line-friendly and transposed through the wave's staging
+    // area tb
+    v4i areg[NSUB][MB][2];
+    v4i aun[AUNP ? NSUB : 1][MB][2][2];
+    auto load_a = [&](int bt, uint8_t *tb) __attribute__((always_inline)) {
+        v4i raw[NSUB][MB][2];
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s)
+#pragma unroll
+            for (int h = 0; h < 2 * MB; ++h) {
+                const int64_t row = 8 * h + (lane >> 3);
+                const int su = bt * NSUB + s;
+                const int64_t kb = (int64_t)(u0 + su) * 128 + 16 * (lane & 7);
+                const bool ok = su < nsub && row < M && kb < KB;
+                raw[s][h >> 1][h & 1] = bload16(ar, ok ? (uint32_t)(row * KB + kb) : kOob);
+            }
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) {
+#pragma unroll
+            for (int h = 0; h < 2 * MB; ++h) {
+                const int row = 8 * h + (lane >> 3);
+                *(v4i *)(tb + row * 128 + 16 * ((lane & 7) ^ (row & 7))) = raw[s][h >> 1][h & 1];
+            }
+#pragma unroll
             for (int i = 0; i < MB; ++i)
-    #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int m = i * 16 + 4 * (lane >> 4) + r;
-                    res0[i][r] = (e.res && m < M && gn < N) ? e.res[m * N + gn] : (f16)0;
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int row = 16 * i + (lane & 15);
+                    areg[s][i][t] =
+                        *(const v4i *)(tb + row * 128 + 16 * ((4 * t + (lane >> 4)) ^ (row & 7)));
                 }
+            // this wave's reads of unit s land before unit s + 1 overwrites the slot
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
         }
-
-        // A: unit s of the wave's batch bt, row block i, chunk pair t; lane
-        // holds row 16 i + (lane & 15), logical chunk 4 t + (lane >> 4) of the
-        // unit, read line-friendly and transposed through the wave's staging
-        // area tb
-        v4i areg[NSUB][MB][2];
-        v4i aun[AUNP ? NSUB : 1][MB][2][2];
-        auto load_a = [&](int bt, uint8_t *tb) __attribute__((always_inline)) {
-            v4i raw[NSUB][MB][2];
-    #pragma unroll
-            for (int s = 0; s < NSUB; ++s)
-    #pragma unroll
-                for (int h = 0; h < 2 * MB; ++h) {
-                    const int64_t row = 8 * h + (lane >> 3);
-                    const int su = bt * NSUB + s;
-                    const int64_t kb = (int64_t)(u0 + su) * 128 + 16 * (lane & 7);
-                    const bool ok = su < nsub && row < M && kb < KB;
-                    raw[s][h >> 1][h & 1] = bload16(ar, ok ? (uint32_t)(row * KB + kb) : kOob);
-                }
-    #pragma unroll
-            for (int s = 0; s < NSUB; ++s) {
-    #pragma unroll
-                for (int h = 0; h < 2 * MB; ++h) {
-                    const int row = 8 * h + (lane >> 3);
-                    *(v4i *)(tb + row * 128 + 16 * ((lane & 7) ^ (row & 7))) = raw[s][h >> 1][h & 1];
-                }
-    #pragma unroll
-                for (int i = 0; i < MB; ++i)
-    #pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const int row = 16 * i + (lane & 15);
-                        areg[s][i][t] =
-                            *(const v4i *)(tb + row * 128 + 16 * ((4 * t + (lane >> 4)) ^ (row & 7)));
-                    }
-                // this wave's reads of unit s land before unit s + 1 overwrites the slot
-                __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-            }
-    #pragma unroll
-            for (int s = 0; s < NSUB; ++s)
-    #pragma unroll
-                for (int i = 0; i < MB; ++i)
-    #pragma unroll
-                    for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(areg[s][i][t]));
-            if (AUNP) {
-    #pragma unroll
-                for (int s = 0; s < (AUNP ? NSUB : 1); ++s)
-    #pragma unroll
-                    for (int i = 0; i < MB; ++i)
-    #pragma unroll
-                        for (int t = 0; t < 2; ++t) {
-                            aun[s][i][t][0] = unpack8a<UA>((u32)areg[s][i][t][0], (u32)areg[s][i][t][1]);
-                            aun[s][i][t][1] = unpack8a<UA>((u32)areg[s][i][t][2], (u32)areg[s][i][t][3]);
-                        }
-            }
-        };
-        load_a(0, ring + wave * (S * 2048));
-        __syncthreads();
-
-        // item = (batch, column block j, unit s); DMA instruction h covers rows
-        // 8 h + (lane >> 3).  Without batching the items are (j, s < nsub);
-        // with it every batch has NSUB units (those past nsub load zeros).
-        const uint32_t ring_w = (uint32_t)(uintptr_t)ring + (uint32_t)wave * (S * 2048);
-        const int per_bat = BATCH ? ncb_mine * NSUB : ncb_mine * nsub;
-        const int total = per_bat * nbat;
-        auto issue = [&](int item) {
-            const uint32_t lds = ring_w + (item % S) * 2048;
-            int64_t nrow0 = 0, kb0 = 0;
-            bool live = item < total;
-            if (live) {
-                int j, su;
-                if (BATCH) {
-                    const int bt = item / per_bat, rem = item - bt * per_bat;
-                    j = rem / NSUB;
-                    su = bt * NSUB + (rem - j * NSUB);
-                    live = su < nsub;
-                } else {
-                    j = item / nsub;
-                    su = item - j * nsub;
-                }
-                nrow0 = (int64_t)(wg + j * G) * 16;
-                kb0 = (int64_t)(u0 + su) * 128;
-            }
-    #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int r = 8 * h + (lane >> 3);
-                const int64_t row = nrow0 + r;
-                const int64_t kb = kb0 + 16 * ((lane & 7) ^ (r & 7));
-                const uint32_t off = (live && row < N && kb < KB) ? (uint32_t)(row * KB + kb) : kOob;
-                dma16(br, off, __builtin_amdgcn_readfirstlane(lds + h * 1024));
-            }
-        };
-
-        v4i acc[MB];
-    #pragma unroll
-        for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
-    #pragma unroll
-        for (int it = 0; it < S - 1; ++it) issue(it);
-
-        for (int bt = 0; bt < nbat; ++bt) {
-            // the next batch's A (the items already in flight keep streaming)
-            if (BATCH && bt > 0) load_a(bt, astage + wave * (MB * 2048));
-            for (int j = 0; j < ncb_mine; ++j) {
-    #pragma unroll
-                for (int s = 0; s < NSUB; ++s) {
-                    if (!BATCH && s >= nsub) break;
-                    const int it = bt * per_bat + j * (BATCH ? NSUB : nsub) + s;
-                    issue(it + S - 1);  // items past the end load zeros into a free stage
-                    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (S - 1)) : "memory");
-                    const uint8_t *st = ring + wave * (S * 2048) + (it % S) * 2048 + 128 * rr;
-                    v4i bw[2];
-    #pragma unroll
-                    for (int t = 0; t < 2; ++t)
-                        bw[t] = *(const v4i *)(st + 16 * ((4 * t + (lane >> 4)) ^ (rr & 7)));
-    #pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const v4i b0 = unpack8((u32)bw[t][0], (u32)bw[t][1]);
-                        const v4i b1 = unpack8((u32)bw[t][2], (u32)bw[t][3]);
-    #pragma unroll
-                        for (int i = 0; i < MB; ++i) {
-                            v4i a0, a1;
-                            if (AUNP) {
-                                a0 = aun[AUNP ? s : 0][i][t][0];
-                                a1 = aun[AUNP ? s : 0][i][t][1];
-                            } else {
-                                v4i w = areg[s][i][t];
-                                asm volatile("" : "+v"(w));  // unpack per use, not hoisted out of j
-                                a0 = unpack8a<UA>((u32)w[0], (u32)w[1]);
-                                a1 = unpack8a<UA>((u32)w[2], (u32)w[3]);
-                            }
-                            acc[i] = mfma16(a0, b0, acc[i]);
-                            acc[i] = mfma16(a1, b1, acc[i]);
-                        }
-                    }
-                }
-                if (nsub > 0) {
-                    int *sm = sum[j];
-    #pragma unroll
-                    for (int i = 0; i < MB; ++i)
-    #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            __hip_atomic_fetch_add(&sm[i * 256 + (4 * (lane >> 4) + r) * 16 + rr],
-                                                   acc[i][r], __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
-    #pragma unroll
-                for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
-            }
-        }
-        // the zero-fill DMAs of items past the end land before the block ends
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (e.swiglu) {
-            // lane rr < 8: output column 8 c + rr of column block c from gate
-            // column 16 c + rr and up column 16 c + rr + 8, each dequantized as
-            // the plain fp16 epilogue does, then swiglu1
-            for (int j = wave; j < ncb_mine; j += KW) {
-                const int *sm = sum[j];
-                const int64_t cb = wg + (int64_t)j * G;
-                const int c = rr & 7;
-                const float sbg = sbl[j * 16 + c], sbu = sbl[j * 16 + c + 8];
-    #pragma unroll
-                for (int i = 0; i < MB; ++i)
-    #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int m = i * 16 + 4 * (lane >> 4) + r;
-                        const int base = i * 256 + (4 * (lane >> 4) + r) * 16;
-                        if (rr < 8 && m < M && cb * 16 + 16 <= N) {
-                            const f16 g = f16_rn(((float)(sm[base + c] >> 8) * sal[m]) * sbg);
-                            const f16 u = f16_rn(((float)(sm[base + c + 8] >> 8) * sal[m]) * sbu);
-                            e.out[m * (N / 2) + cb * 8 + c] = swiglu1((float)g, (float)u);
-                        }
-                    }
-            }
-            return;
-        }
-        for (int j = wave; j < ncb_mine; j += KW) {
-            const int *sm = sum[j];
-            const int64_t gn = (int64_t)(wg + j * G) * 16 + rr;
-            const float sbv = e.C ? 0.f : sbl[j * 16 + rr];
-    #pragma unroll
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s)
+#pragma unroll
             for (int i = 0; i < MB; ++i)
-    #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int m = i * 16 + 4 * (lane >> 4) + r;
-                    const int raw = sm[i * 256 + (4 * (lane >> 4) + r) * 16 + rr];
-                    if (m < M && gn < N) {
-                        const int v = epi_val(e, raw, m, gn);
-                        if (e.C) {
-                            e.C[m * N + gn] = v;
-                        } else {
-                            const bool first = j == wave;
-                            f16 o = f16_rn(((float)v * sal[m]) * sbv);
-                            if (e.bias) o = f16_rn((float)o + (float)(first ? bias0 : e.bias[gn]));
-                            if (e.res)
-                                o = f16_rn((float)o + (float)(first ? res0[i][r] : e.res[m * N + gn]));
-                            e.out[m * N + gn] = o;
-                        }
+#pragma unroll
+                for (int t = 0; t < 2; ++t) asm volatile("" : "+v"(areg[s][i][t]));
+        if (AUNP) {
+#pragma unroll
+            for (int s = 0; s < (AUNP ? NSUB : 1); ++s)
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        aun[s][i][t][0] = unpack8a<UA>((u32)areg[s][i][t][0], (u32)areg[s][i][t][1]);
+                        aun[s][i][t][1] = unpack8a<UA>((u32)areg[s][i][t][2], (u32)areg[s][i][t][3]);
                     }
-                }
         }
     };
-    if constexpr (!MOE) {
-        pass(A_in, B_in, M_in, e_in, blockIdx.x, gridDim.x);
-    } else {
-        // the experts with a remainder pass, in order: every workgroup
-        // derives the same list (one bit per expert, flagged by the waves in
-        // parallel: one round of offset loads)
-        __shared__ unsigned long long rmask[(kMoeRemMaxP + 63) / 64];
-        const int nchunk = (mr.P + 63) / 64;
-        for (int c = wave0; c < nchunk; c += KW) {
-            const int x = 64 * c + lane0;
-            bool f = false;
-            if (x < mr.P) {
-                const int64_t r = mr.offsets[x + 1] - mr.offsets[x];
-                f = moe_tiled_rows(r) != r;
+    load_a(0, ring + wave * (S * 2048));
+    __syncthreads();
+
+    // item = (batch, column block j, unit s); DMA instruction h covers rows
+    // 8 h + (lane >> 3).  Without batching the items are (j, s < nsub);
+    // with it every batch has NSUB units (those past nsub load zeros).
+    const uint32_t ring_w = (uint32_t)(uintptr_t)ring + (uint32_t)wave * (S * 2048);
+    const int per_bat = BATCH ? ncb_mine * NSUB : ncb_mine * nsub;
+    const int total = per_bat * nbat;
+    auto issue = [&](int item) {
+        const uint32_t lds = ring_w + (item % S) * 2048;
+        int64_t nrow0 = 0, kb0 = 0;
+        bool live = item < total;
+        if (live) {
+            int j, su;
+            if (BATCH) {
+                const int bt = item / per_bat, rem = item - bt * per_bat;
+                j = rem / NSUB;
+                su = bt * NSUB + (rem - j * NSUB);
+                live = su < nsub;
+            } else {
+                j = item / nsub;
+                su = item - j * nsub;
             }
-            const unsigned long long m = __ballot(f);
-            if (lane0 == 0) rmask[c] = m;
+            nrow0 = (int64_t)(blockIdx.x + j * G) * 16;
+            kb0 = (int64_t)(u0 + su) * 128;
         }
-        __syncthreads();
-        int nrem = 0;
-        for (int c = 0; c < nchunk; ++c) nrem += __popcll(rmask[c]);
-        nrem = __builtin_amdgcn_readfirstlane(nrem);
-        // every expert gets spe workgroups (one at least); unit u = expert
-        // u % nrem, slice u / nrem of its column blocks (slice, slice + spe,
-        // ...), walked in passes of at most kStreamMaxCb column blocks, so
-        // one workgroup per CU streams any number of experts and columns
-        const int ncb = (int)((N + 15) / 16);
-        const int spe = max(1, (int)gridDim.x / max(nrem, 1));
-        for (int u = blockIdx.x; u < nrem * spe; u += gridDim.x) {
-            const int k = u % nrem, slice = u / nrem;
-            int c = 0, before = 0;
-            for (;; ++c) {
-                const int pc = __popcll(rmask[c]);
-                if (before + pc > k) break;
-                before += pc;
-            }
-            unsigned long long m = rmask[c];
-            for (int i = k - before; i > 0; --i) m &= m - 1;  // drop the lower set bits
-            const int x = __builtin_amdgcn_readfirstlane(64 * c + __builtin_ctzll(m));
-            const int64_t r0 = mr.offsets[x], r = mr.offsets[x + 1] - r0, full = moe_tiled_rows(r);
-            Epi e = e_in;
-            e.sa += r0 + full;
-            e.sb += (int64_t)x * N;
-            e.out += (r0 + full) * (e.swiglu ? N / 2 : N);
-            const uint8_t *A = A_in + (r0 + full) * KB, *B = B_in + (int64_t)x * N * KB;
-            const int mine = (ncb - slice + spe - 1) / spe;
-            for (int p0 = 0; p0 < mine; p0 += kStreamMaxCb) {
-                __syncthreads();  // the previous pass's LDS reads are done
-                pass(A, B, r - full, e, slice + p0 * spe, spe);
-            }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = 8 * h + (lane >> 3);
+            const int64_t row = nrow0 + r;
+            const int64_t kb = kb0 + 16 * ((lane & 7) ^ (r & 7));
+            const uint32_t off = (live && row < N && kb < KB) ? (uint32_t)(row * KB + kb) : kOob;
+            dma16(br, off, __builtin_amdgcn_readfirstlane(lds + h * 1024));
         }
+    };
+
+    v4i acc[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
+#pragma unroll
+    for (int it = 0; it < S - 1; ++it) issue(it);
+
+    for (int bt = 0; bt < nbat; ++bt) {
+        // the next batch's A (the items already in flight keep streaming)
+        if (BATCH && bt > 0) load_a(bt, astage + wave * (MB * 2048));
+        for (int j = 0; j < ncb_mine; ++j) {
+#pragma unroll
+            for (int s = 0; s < NSUB; ++s) {
+                if (!BATCH && s >= nsub) break;
+                const int it = bt * per_bat + j * (BATCH ? NSUB : nsub) + s;
+                issue(it + S - 1);  // items past the end load zeros into a free stage
+                asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * (S - 1)) : "memory");
+                const uint8_t *st = ring + wave * (S * 2048) + (it % S) * 2048 + 128 * rr;
+                v4i bw[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    bw[t] = *(const v4i *)(st + 16 * ((4 * t + (lane >> 4)) ^ (rr & 7)));
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const v4i b0 = unpack8((u32)bw[t][0], (u32)bw[t][1]);
+                    const v4i b1 = unpack8((u32)bw[t][2], (u32)bw[t][3]);
+#pragma unroll
+                    for (int i = 0; i < MB; ++i) {
+                        v4i a0, a1;
+                        if (AUNP) {
+                            a0 = aun[AUNP ? s : 0][i][t][0];
+                            a1 = aun[AUNP ? s : 0][i][t][1];
+                        } else {
+                            v4i w = areg[s][i][t];
+                            asm volatile("" : "+v"(w));  // unpack per use, not hoisted out of j
+                            a0 = unpack8a<UA>((u32)w[0], (u32)w[1]);
+                            a1 = unpack8a<UA>((u32)w[2], (u32)w[3]);
+                        }
+                        acc[i] = mfma16(a0, b0, acc[i]);
+                        acc[i] = mfma16(a1, b1, acc[i]);
+                    }
+                }
+            }
+            if (nsub > 0) {
+                int *sm = sum[j];
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        __hip_atomic_fetch_add(&sm[i * 256 + (4 * (lane >> 4) + r) * 16 + rr],
+                                               acc[i][r], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+#pragma unroll
+            for (int i = 0; i < MB; ++i) acc[i] = (v4i){0, 0, 0, 0};
+        }
+    }
+    // the zero-fill DMAs of items past the end land before the block ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (e.swiglu) {
+        // lane rr < 8: output column 8 c + rr of column block c from gate
+        // column 16 c + rr and up column 16 c + rr + 8, each dequantized as
+        // the plain fp16 epilogue does, then swiglu1
+        for (int j = wave; j < ncb_mine; j += KW) {
+            const int *sm = sum[j];
+            const int64_t cb = blockIdx.x + (int64_t)j * G;
+            const int c = rr & 7;
+            const float sbg = sbl[j * 16 + c], sbu = sbl[j * 16 + c + 8];
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = i * 16 + 4 * (lane >> 4) + r;
+                    const int base = i * 256 + (4 * (lane >> 4) + r) * 16;
+                    if (rr < 8 && m < M && cb * 16 + 16 <= N) {
+                        const f16 g = f16_rn(((float)(sm[base + c] >> 8) * sal[m]) * sbg);
+                        const f16 u = f16_rn(((float)(sm[base + c + 8] >> 8) * sal[m]) * sbu);
+                        e.out[m * (N / 2) + cb * 8 + c] = swiglu1((float)g, (float)u);
+                    }
+                }
+        }
+        return;
+    }
+    for (int j = wave; j < ncb_mine; j += KW) {
+        const int *sm = sum[j];
+        const int64_t gn = (int64_t)(blockIdx.x + j * G) * 16 + rr;
+        const float sbv = e.C ? 0.f : sbl[j * 16 + rr];
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = i * 16 + 4 * (lane >> 4) + r;
+                const int raw = sm[i * 256 + (4 * (lane >> 4) + r) * 16 + rr];
+                if (m < M && gn < N) {
+                    const int v = epi_val(e, raw, m, gn);
+                    if (e.C) {
+                        e.C[m * N + gn] = v;
+                    } else {
+                        const bool first = j == wave;
+                        f16 o = f16_rn(((float)v * sal[m]) * sbv);
+                        if (e.bias) o = f16_rn((float)o + (float)(first ? bias0 : e.bias[gn]));
+                        if (e.res)
+                            o = f16_rn((float)o + (float)(first ? res0[i][r] : e.res[m * N + gn]));
+                        e.out[m * N + gn] = o;
+                    }
+                }
+            }
     }
 }
 
@@ -1420,7 +1348,7 @@ bool launch_stream(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int
     if (cb_per > kStreamMaxCb) return false;
     const dim3 grid((unsigned)((ncb + cb_per - 1) / cb_per)), block(kStreamKW * 64);
 #define SRQ_STREAM(MB, NSUB, AUNP, BATCH) \
-    gemm_stream_kernel<MB, NSUB, AUNP, UA, BATCH><<<grid, block, 0, st>>>(a, b, M, N, K, e, MoeRem{})
+    gemm_stream_kernel<MB, NSUB, AUNP, UA, BATCH><<<grid, block, 0, st>>>(a, b, M, N, K, e)
     // per > 8 units per wave (K > 16384): A goes through registers in
     // batches of NSUB units (cfg4 down at M = 1 / 32: 54 us on the skinny
     // kernel before)
@@ -1438,35 +1366,6 @@ bool launch_stream(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int
     }
 #undef SRQ_STREAM
     return true;
-}
-
-// Workgroups of the remainder pass of a MoE product with P experts: one per
-// CU (each walks its share of every remainder expert's column blocks), or 0
-// where the split does not apply and the grouped launch tiles every row
-// (more than kMoeRemMaxP experts).
-int64_t moe_rem_blocks(int64_t P) { return P > kMoeRemMaxP ? 0 : 256; }
-
-// The remainder pass of a MoE product (signed A): one stream-kernel launch
-// of moe_rem_blocks workgroups that take the experts leaving 1..32 rows to
-// it (moe_tiled_rows), decided on the device from the offsets like the
-// grouped launch's rows, so the pair needs no host read.  With no remainder
-// anywhere every workgroup returns at once.
-void launch_moe_rem(const uint8_t *a, const uint8_t *b, const int32_t *offsets, int P,
-                    int64_t N, int64_t K, int64_t blocks, const Epi &e, hipStream_t st) {
-    const int64_t units = (K / 2 + 127) / 128;
-    const int64_t per = (units + kStreamKW - 1) / kStreamKW;
-    const dim3 grid((unsigned)blocks), block(kStreamKW * 64);
-    MoeRem mr;
-    mr.offsets = offsets;
-    mr.P = P;
-#define SRQ_MOE_REM(NSUB, AUNP, BATCH) \
-    gemm_stream_kernel<2, NSUB, AUNP, false, BATCH, true><<<grid, block, 0, st>>>(a, b, 0, N, K, e, mr)
-    if (per <= 2) SRQ_MOE_REM(2, true, false);
-    else if (per <= 4) SRQ_MOE_REM(4, false, false);
-    else if (per <= 7) SRQ_MOE_REM(7, false, false);
-    else if (per <= 8) SRQ_MOE_REM(8, false, false);
-    else SRQ_MOE_REM(7, false, true);
-#undef SRQ_MOE_REM
 }
 
 // ---------------------------------------------------------------------------
@@ -1504,7 +1403,9 @@ struct GroupedArgs {
     const int32_t *offsets;
     const uint8_t *A, *B;
     int64_t N, K;
-    // rows left to the remainder pass (moe_tiled_rows) are not tiled here
+    // expert-offset forms with symmetric A and at least two K steps: an
+    // expert's rows past its full tiles (moe_tiled_rows) ride on its last
+    // full tile (GroupedProb::xrows)
     int skip_rem;
     const f16 *sa, *sb;
     f16 *out;
@@ -1541,6 +1442,9 @@ struct GroupedProb {
     const uint8_t *a, *b;
     int32_t *c;
     int64_t m, n, k, lda_b, ldb_b, ldc, row0;
+    // rows m .. m + xrows - 1 of the problem (at most 32), computed by the
+    // producer waves of its last M tile
+    int64_t xrows;
 };
 
 SRQ_DEV int64_t uni(int64_t v) {
@@ -1551,6 +1455,7 @@ SRQ_DEV int64_t uni(int64_t v) {
 template <int FORM>
 SRQ_DEV GroupedProb grouped_prob(const GroupedArgs &g, int p) {
     GroupedProb r;
+    r.xrows = 0;
     if constexpr (FORM == kFormSplitK) {
         const int64_t kc0 = (int64_t)p * g.Kc;
         r.row0 = 0;
@@ -1591,7 +1496,11 @@ SRQ_DEV GroupedProb grouped_prob(const GroupedArgs &g, int p) {
         const int e = g.pair ? p >> 1 : p;
         r.row0 = uni(g.offsets[e]);
         r.m = uni(g.offsets[e + 1]) - r.row0;
-        if (g.skip_rem) r.m = moe_tiled_rows(r.m);
+        if (g.skip_rem) {
+            const int64_t t = moe_tiled_rows(r.m);
+            r.xrows = r.m - t;
+            r.m = t;
+        }
         r.n = g.N;
         r.k = g.K;
         r.lda_b = r.ldb_b = g.K / 2;
@@ -1625,7 +1534,7 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTG * kStage];
     __shared__ __attribute__((aligned(16))) uint8_t epi_lds[kCompute * kEpiTile];
 
-    const int lane = threadIdx.x & 63;
+    const int lane0 = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool producer = wave >= kCompute;
     const int pw = wave - kCompute;
@@ -1646,23 +1555,45 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             }
         }
         if (p >= g.P) break;
+        // lane laundered per tile: its derived LDS addresses are recomputed
+        // per tile, not held across the tile loop by both wave roles (that
+        // left the producers' extra-row code without registers)
+        int lane = lane0;
+        asm volatile("" : "+v"(lane));
         const int64_t tiles_n = (pr.n + kGrpBN - 1) / kGrpBN;
         const int64_t local = t - pstart;
         const int64_t m0 = (local / tiles_n) * kGrpBM, n0 = (local % tiles_n) * kGrpBN;
         const int64_t KB = pr.k / 2;
         const int steps = (int)((KB + KBB - 1) / KBB);
+        // the expert's last full tile, with its extra rows (signed
+        // expert-offset forms; the host asks for them only with two or more
+        // K steps)
+        constexpr bool kExtra = !UA && (FORM == kFormGeneral || FORM == kFormSwiglu);
+        const bool xt = kExtra && pr.xrows > 0 && m0 + kGrpBM == pr.m;
 
         if (producer) {
-            const __amdgpu_buffer_rsrc_t ar = make_rsrc(pr.a, pr.m * pr.lda_b);
-            const __amdgpu_buffer_rsrc_t br = make_rsrc(pr.b, pr.n * pr.ldb_b);
+            // (wave-uniform, stated: the tile loop's divergent epilogues can
+            // hide it from the compiler, which then puts them in VGPRs)
+            const __amdgpu_buffer_rsrc_t ar =
+                make_rsrc((const uint8_t *)uni((int64_t)pr.a), uni(pr.m * pr.lda_b));
+            const __amdgpu_buffer_rsrc_t br =
+                make_rsrc((const uint8_t *)uni((int64_t)pr.b), uni(pr.n * pr.ldb_b));
             uint32_t roff[kDmaPerWave];
             int jc[kDmaPerWave];
+            // 1 KiB block of DMA q of this wave: A rows then B rows 32 pw ..
+            // 32 pw + 31 of the stage (a producer's extra rows read only the
+            // B rows it loads itself)
+            constexpr int kAPer = kGrpBM / R / NPROD, kBPer = kGrpBN / R / NPROD;
+            static_assert(kAPer + kBPer == kDmaPerWave && kBPer * R == 32, "DMA blocks");
+            auto blk = [&](int q) {
+                return q < kAPer ? kAPer * pw + q : kGrpBM / R + kBPer * pw + (q - kAPer);
+            };
 #pragma unroll
             for (int q = 0; q < kDmaPerWave; ++q) {
-                const int i = pw * kDmaPerWave + q;
+                const int i = blk(q);
                 const int r = R * i + lane / C;
                 jc[q] = ((lane % C) ^ swz<KBB>(r)) * 16;
-                const bool isa = R * i < kGrpBM;
+                const bool isa = q < kAPer;
                 const int64_t row = isa ? m0 + r : n0 + r - kGrpBM;
                 roff[q] = row < (isa ? pr.m : pr.n)
                               ? (uint32_t)(row * (isa ? pr.lda_b : pr.ldb_b)) : kOob;
@@ -1670,18 +1601,147 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             auto issue = [&](int st, int sl) {
                 const int64_t kb0 = (int64_t)st * KBB;
                 const bool tail = kb0 + KBB > KB;
-#pragma unroll
-                for (int q = 0; q < kDmaPerWave; ++q) {
-                    const int i = pw * kDmaPerWave + q;
-                    const uint32_t dst = lds0 + sl * kStage + i * 1024;
+                auto one = [&](int q, __amdgpu_buffer_rsrc_t rs) __attribute__((always_inline)) {
+                    const uint32_t dst = lds0 + sl * kStage + blk(q) * 1024;
                     uint32_t off = roff[q] == kOob ? kOob : roff[q] + (uint32_t)kb0 + jc[q];
                     if (tail && kb0 + jc[q] >= KB) off = kOob;
-                    dma16(R * i < kGrpBM ? ar : br, off, dst);
-                }
+                    dma16(rs, off, dst);
+                };
+#pragma unroll
+                for (int q = 0; q < kAPer; ++q) one(q, ar);
+#pragma unroll
+                for (int q = kAPer; q < kDmaPerWave; ++q) one(q, br);
             };
 #pragma unroll
             for (int q = 0; q < NSTG - 1; ++q)
                 if (q < steps) issue(q, q);
+            if (kExtra && xt) {
+                // The expert's rows past its full tiles (1..32; at least two K
+                // steps): producer wave pw multiplies them with the tile's
+                // columns 32 pw .. 32 pw + 31, i.e. the B rows of each stage
+                // that it loads itself, against its own copy of their codes
+                // in NSTG 4 KiB slots of the epilogue area (idle during the K
+                // loop; four DMAs per step).  It reads only what it loaded,
+                // so its own waits suffice: it multiplies step s - 1 after
+                // barrier s, while the compute waves work on step s, and
+                // then refills that stage and slot.  The area is free once
+                // the compute waves' previous epilogue is done: on such a
+                // tile every wave meets one more barrier before the K loop,
+                // after which the producers load steps 0 and 1's codes.
+                static_assert(NSTG == 3, "extra-row schedule");
+                constexpr int kXSlot = kMoeRemMax * KBB;
+                constexpr int kXDma = kXSlot / 1024;  // DMAs per step
+                static_assert(NPROD * NSTG * kXSlot <= kCompute * kEpiTile, "extra-row slots");
+                const uint32_t xlds0 =
+                    (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)epi_lds +
+                    pw * (NSTG * kXSlot);
+                const uint8_t *xbase = epi_lds + pw * (NSTG * kXSlot);
+                const __amdgpu_buffer_rsrc_t xr = make_rsrc(
+                    (const uint8_t *)uni((int64_t)(pr.a + pr.m * pr.lda_b)), uni(pr.xrows * pr.lda_b));
+                uint32_t xoff[kXDma];
+                int xjc[kXDma];
+#pragma unroll
+                for (int b = 0; b < kXDma; ++b) {
+                    const int xrow = R * b + lane / C;
+                    xjc[b] = ((lane % C) ^ swz<KBB>(xrow)) * 16;
+                    xoff[b] = xrow < pr.xrows ? (uint32_t)(xrow * pr.lda_b) : kOob;
+                }
+                auto issue_x = [&](int st) {
+                    const int64_t kb0 = (int64_t)st * KBB;
+#pragma unroll
+                    for (int b = 0; b < kXDma; ++b) {
+                        const uint32_t off = (xoff[b] == kOob || kb0 + xjc[b] >= KB)
+                                                 ? kOob : xoff[b] + (uint32_t)kb0 + xjc[b];
+                        dma16(xr, off, xlds0 + (st % NSTG) * kXSlot + b * 1024);
+                    }
+                };
+                const int rr = lane & 31, gx = lane >> 5;
+                const int rb = kGrpBM + 32 * pw + rr;  // this wave's B rows of a stage
+                v16i xacc = (v16i){};
+                auto extra = [&](int st) {
+                    const uint8_t *stg = smem + (st % NSTG) * kStage;
+                    const uint8_t *xs = xbase + (st % NSTG) * kXSlot;
+#pragma unroll
+                    for (int pp = 0; pp < KBB / 32; ++pp) {
+                        const int j = 2 * pp + gx;
+                        const v4i fa =
+                            *reinterpret_cast<const v4i *>(xs + rr * KBB + ((j ^ swz<KBB>(rr)) << 4));
+                        const v4i fb =
+                            *reinterpret_cast<const v4i *>(stg + rb * KBB + ((j ^ swz<KBB>(rb)) << 4));
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+                            xacc = mfma32i8(unpack8a<UA>((u32)fa[2 * h], (u32)fa[2 * h + 1]),
+                                            unpack8((u32)fb[2 * h], (u32)fb[2 * h + 1]), xacc);
+                    }
+                };
+                __builtin_amdgcn_s_barrier();  // the epilogue area is free
+                asm volatile("" ::: "memory");
+                issue_x(0);
+                issue_x(1);
+                for (int s = 0; s < steps; ++s) {
+                    // this wave's LDS reads of step s - 2 are done before its
+                    // stage and slot are refilled below, and its loads of step
+                    // s are done, later ones may fly (step 0: step 1's DMAs
+                    // and steps 0 and 1's codes newer; later: step s + 1's
+                    // DMAs and codes newer, if any)
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    if (s == 0)
+                        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave + 2 * kXDma) : "memory");
+                    else
+                        ring_wait<kDmaPerWave + kXDma, NSTG - 2>(min(NSTG - 2, steps - 1 - s));
+                    __builtin_amdgcn_s_barrier();
+                    asm volatile("" ::: "memory");
+                    if (s > 0) extra(s - 1);
+                    if (s + NSTG - 1 < steps) {
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                        issue(s + NSTG - 1, (s + NSTG - 1) % NSTG);
+                        issue_x(s + NSTG - 1);
+                    }
+                }
+                extra(steps - 1);
+                // end of tile: every wave is done with every stage and slot
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                // fp16 outputs of the extra rows, from the 32x32 accumulator
+                // layout (lane: column rr, rows 8 (v / 4) + 4 gx + v % 4), with
+                // the arithmetic of the tile's LDS-staged epilogue
+                const int64_t ex = p;
+                const f16 *sa = g.sa + pr.row0 + pr.m;
+                const int64_t col = n0 + 32 * pw + rr;
+                if constexpr (FORM == kFormSwiglu) {
+                    // columns in blocks of 8 gate then 8 up: a gate lane takes
+                    // its up value from the lane 8 above
+                    const int jj = rr & 15;
+                    const int64_t gn0 = col - jj;
+                    const bool on = jj < 8 && gn0 + 16 <= pr.n;
+                    const float sbg = on ? (float)g.sb[ex * g.N + gn0 + jj] : 0.f;
+                    const float sbu = on ? (float)g.sb[ex * g.N + gn0 + 8 + jj] : 0.f;
+                    f16 *out = g.out + (pr.row0 + pr.m) * (g.N / 2) + gn0 / 2 + jj;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int ua = __shfl_down(xacc[v], 8, 64);
+                        const int m = 8 * (v / 4) + 4 * gx + v % 4;
+                        if (on && m < pr.xrows) {
+                            const float sav = (float)sa[m];
+                            const f16 gh = f16_rn((float)(xacc[v] >> 8) * sav * sbg);
+                            const f16 uh = f16_rn((float)(ua >> 8) * sav * sbu);
+                            out[m * (g.N / 2)] = swiglu1((float)gh, (float)uh);
+                        }
+                    }
+                } else {
+                    const bool on = col < pr.n;
+                    const float sbv = on ? (float)g.sb[ex * g.N + col] : 0.f;
+                    f16 *out = g.out + (pr.row0 + pr.m) * g.N + col;
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) {
+                        const int m = 8 * (v / 4) + 4 * gx + v % 4;
+                        if (on && m < pr.xrows)
+                            out[m * g.N] = f16_rn((float)(xacc[v] >> (UA ? 4 : 8)) * (float)sa[m] * sbv);
+                    }
+                }
+                continue;
+            }
             for (int s = 0; s < steps; ++s) {
                 // this wave's DMA of step s is done (later steps may fly);
                 // after the barrier every wave's is, and step s - 1's stage
@@ -1702,6 +1762,13 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){};
+        if (kExtra && xt) {
+            // the extra-row tile's first barrier (see the producers): this
+            // wave's epilogue LDS reads are done
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
         for (int s = 0; s < steps; ++s) {
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
@@ -2158,16 +2225,8 @@ extern "C" int srq_w4a4_linear_moe(const void *A, const void *a_scale, const voi
     g.sa = (const f16 *)a_scale;
     g.sb = (const f16 *)b_scale;
     g.out = (f16 *)out;
-    const int64_t rem_blocks = moe_rem_blocks(num_experts);
-    g.skip_rem = rem_blocks > 0;
+    g.skip_rem = K > 2 * kGrpKBB;  // at least two K steps (the extra rows' schedule)
     gemm_grouped_kernel<4, false><<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
-    if (rem_blocks) {
-        Epi e{};
-        e.sa = g.sa;
-        e.sb = g.sb;
-        e.out = g.out;
-        launch_moe_rem(g.A, g.B, expert_offsets, g.P, N, K, rem_blocks, e, (hipStream_t)stream);
-    }
     SRQ_LAUNCH_CHECK("w4a4_linear_moe");
     return SRQ_OK;
 }
@@ -2201,18 +2260,9 @@ extern "C" int srq_w4a4_linear_moe_swiglu(const void *A, const void *a_scale, co
     g.sa = (const f16 *)a_scale;
     g.sb = (const f16 *)b_scale;
     g.out = (f16 *)out;
-    const int64_t rem_blocks = moe_rem_blocks(num_experts);
-    g.skip_rem = rem_blocks > 0;
+    g.skip_rem = K > 2 * kGrpKBB;  // at least two K steps (the extra rows' schedule)
     gemm_grouped_kernel<4, false, kFormSwiglu>
         <<<dim3(kGroupedGrid), dim3(512), 0, (hipStream_t)stream>>>(g);
-    if (rem_blocks) {
-        Epi e{};
-        e.sa = g.sa;
-        e.sb = g.sb;
-        e.out = g.out;
-        e.swiglu = 1;
-        launch_moe_rem(g.A, g.B, expert_offsets, g.P, N, K, rem_blocks, e, (hipStream_t)stream);
-    }
     SRQ_LAUNCH_CHECK("w4a4_linear_moe_swiglu");
     return SRQ_OK;
 }

@@ -151,13 +151,13 @@ def test_matmul_grouped_vs_oracle(C):
         assert_bitexact(c[off[e]:off[e + 1]], want[e], f"problem {e}")
 
 
-# Experts past one 128-row tile with 1..32 rows left over send those rows
-# through the weight-streaming remainder pass; 33+ left over, exact tiles and
-# single tiles stay in the grouped launch.  The cases put every kind of expert
-# side by side, at the MoE down shape too, with every expert taking the pass
-# (several passes of column blocks per workgroup), with more such experts
-# than workgroups, and past 1024 experts (where the grouped launch tiles
-# every row).
+# Experts past one 128-row tile with 1..32 rows left over compute those rows
+# on their last full tile (the grouped kernel's producer waves); 33+ left
+# over, exact tiles and single tiles are tiled as they are.  The cases put
+# every kind of expert side by side, at the MoE down shape too, with every
+# expert taking extra rows, with many experts, at the fewest K steps that
+# allow it (two) and with a ragged last K step, and at K <= 256 (one step:
+# every row tiled).
 REM_COUNTS = [160, 161, 257, 0, 100, 128, 140, 288, 33, 129, 1, 416]
 
 
@@ -166,11 +166,13 @@ REM_COUNTS = [160, 161, 257, 0, 100, 128, 140, 288, 33, 129, 1, 416]
                                         ([0, 0], 128, 128), ([1], 4096, 14336),
                                         (REM_COUNTS, 1000, 800), (REM_COUNTS, 4096, 14336),
                                         ([129, 0, 150], 16, 64), ([1025] * 4, 300, 2048),
-                                        ([140] * 8, 14336, 4096), ([131] * 300, 40, 64),
-                                        ([131] * 1025, 16, 64)],
+                                        ([140] * 8, 14336, 4096), ([131] * 300, 40, 1024),
+                                        ([131] * 1025, 16, 64), ([140, 129, 160], 200, 512),
+                                        ([150, 33, 161, 288], 64, 288)],
                          ids=["small", "cfg5-gate", "empty", "one-row", "rem-kinds",
-                              "rem-down", "rem-narrow", "rem-one-row", "rem-all-passes",
-                              "rem-300-experts", "1025-experts"])
+                              "rem-down", "rem-narrow", "rem-one-row", "rem-all-experts",
+                              "rem-300-experts", "1025-experts", "rem-two-steps",
+                              "rem-ragged-k"])
 def test_w4a4_linear_moe(C, counts, n, k):
     torch.manual_seed(sum(counts) + n)
     a, b = _grouped_inputs(None, counts, n, k)
@@ -519,7 +521,7 @@ def test_swiglu_had_sign_quant_moe(C, rows, n, K, experts, clip, with_sign):
                                        ([123, 127, 123, 122, 123, 126, 136, 144], 14336, 4096),
                                        ([700, 1], 1024, 2048), (REM_COUNTS, 1008, 800),
                                        ([130, 131, 160, 99], 14336, 4096),
-                                       ([140] * 8, 14336, 4096)])
+                                       ([140] * 8, 14336, 4096), ([140, 161, 129], 48, 512)])
 def test_w4a4_linear_moe_swiglu_equals_gate_up_then_swiglu(C, counts, n, k):
     """The SwiGLU epilogue of the grouped gate/up launch over interleaved
     weights: bit-identical to the two projections followed by srq_swiglu."""
