@@ -475,12 +475,18 @@ SRQ_DEV void store_block_lds32_swiglu(const Epi &e, int64_t M, int64_t N, int64_
 }
 
 // One K step of a compute wave: the stage holds BM A rows then the B rows.
-template <int FM, int FN, int KBB, int BM = kBigBM, bool UA = false>
-SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN]) {
+// XJ >= 0 (the grouped kernel's extra-row tiles): also the 32 rows at xs
+// (same row layout as the stage) times this wave's B block XJ, into xacc,
+// from the B operands already unpacked for the tile.
+template <int FM, int FN, int KBB, int BM = kBigBM, bool UA = false, int XJ = -1>
+SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN],
+                         const uint8_t *xs = nullptr, v16i *xacc = nullptr) {
     constexpr int NPP = KBB / 32;  // 16-byte fragment fetches per step
+    constexpr int NX = XJ >= 0 ? 1 : 0;
+    static_assert(XJ < FN, "extra block");
     const int rr = lane & 31;
     const int g = lane >> 5;
-    v4i fa[2][FM], fb[2][FN];
+    v4i fa[2][FM], fb[2][FN], fx[2][1];
     auto fetch = [&](int pp, int slot) {
         const int j = 2 * pp + g;
 #pragma unroll
@@ -493,12 +499,14 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
             const int r = BM + wn * (FN * 32) + jn * 32 + rr;
             fb[slot][jn] = *reinterpret_cast<const v4i *>(stage + r * KBB + ((j ^ swz<KBB>(r)) << 4));
         }
+        if constexpr (NX)
+            fx[slot][0] = *reinterpret_cast<const v4i *>(xs + rr * KBB + ((j ^ swz<KBB>(rr)) << 4));
     };
     // K slice s = 2 pp + h: bytes 8h .. 8h + 7 of the 16-byte fragments of
     // fetch pp.  Software pipeline: the nibble unpacking of slice s + 1 is
     // interleaved with the MFMAs of slice s (one MFMA, then its share of
     // the unpacking VALU work), so the vector and matrix pipes overlap.
-    v4i ua[2][FM], ub[2][FN];
+    v4i ua[2][FM], ub[2][FN], ux[2][1];
     auto unpack = [&](int sl, int buf) {
         const int pp = sl >> 1, h = sl & 1;
 #pragma unroll
@@ -507,6 +515,8 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
 #pragma unroll
         for (int jn = 0; jn < FN; ++jn)
             ub[buf][jn] = unpack8((u32)fb[pp & 1][jn][2 * h], (u32)fb[pp & 1][jn][2 * h + 1]);
+        if constexpr (NX)
+            ux[buf][0] = unpack8a<UA>((u32)fx[pp & 1][0][2 * h], (u32)fx[pp & 1][0][2 * h + 1]);
     };
     fetch(0, 0);
     unpack(0, 0);
@@ -519,14 +529,16 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
 #pragma unroll
             for (int jn = 0; jn < FN; ++jn)
                 acc[i][jn] = mfma32i8(ua[sl & 1][i], ub[sl & 1][jn], acc[i][jn]);
+        if constexpr (NX) *xacc = mfma32i8(ux[sl & 1][0], ub[sl & 1][XJ < 0 ? 0 : XJ], *xacc);
         if (sl + 1 < 2 * NPP) unpack(sl + 1, (sl + 1) & 1);
         if ((sl & 1) == 0 && pp + 1 < NPP)
-            __builtin_amdgcn_sched_group_barrier(0x100, FM + FN, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, FM + FN + NX, 0);
         // unpack8 is 6 VALU; spread a slice's (FM + FN) of them over its
         // FM * FN MFMAs
-        constexpr int kValuPerMfma = (6 * (FM + FN) + FM * FN - 1) / (FM * FN);
+        constexpr int kMf = FM * FN + NX;
+        constexpr int kValuPerMfma = (6 * (FM + FN + NX) + kMf - 1) / kMf;
 #pragma unroll
-        for (int m = 0; m < FM * FN; ++m) {
+        for (int m = 0; m < kMf; ++m) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             if (sl + 1 < 2 * NPP) __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);
         }
@@ -1617,98 +1629,118 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                 if (q < steps) issue(q, q);
             if (kExtra && xt) {
                 // The expert's rows past its full tiles (1..32; at least two K
-                // steps): producer wave pw multiplies them with the tile's
-                // columns 32 pw .. 32 pw + 31, i.e. the B rows of each stage
-                // that it loads itself, against its own copy of their codes
-                // in NSTG 4 KiB slots of the epilogue area (idle during the K
-                // loop; four DMAs per step).  It reads only what it loaded,
-                // so its own waits suffice: it multiplies step s - 1 after
-                // barrier s, while the compute waves work on step s, and
-                // then refills that stage and slot.  The area is free once
-                // the compute waves' previous epilogue is done: on such a
-                // tile every wave meets one more barrier before the K loop,
-                // after which the producers load steps 0 and 1's codes.
-                static_assert(NSTG == 3, "extra-row schedule");
+                // steps): the compute waves multiply them with the B operands
+                // they unpack for the tile.  Their codes stream into NSTG
+                // 4 KiB slots of the epilogue area (idle during the K loop),
+                // one 1 KiB DMA (8 rows) per producer per step in the stage
+                // layout, waited before barrier s like step s's stage.  The
+                // area is free once the compute waves' previous epilogue is
+                // done: on such a tile every wave meets one more barrier
+                // before the K loop, after which steps 0 and 1's codes load.
+                static_assert(NSTG == 3 && NPROD * R == kMoeRemMax, "extra-row schedule");
                 constexpr int kXSlot = kMoeRemMax * KBB;
-                constexpr int kXDma = kXSlot / 1024;  // DMAs per step
-                static_assert(NPROD * NSTG * kXSlot <= kCompute * kEpiTile, "extra-row slots");
+                static_assert(NSTG * kXSlot <= kCompute * kEpiTile, "extra-row slots");
                 const uint32_t xlds0 =
-                    (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)epi_lds +
-                    pw * (NSTG * kXSlot);
-                const uint8_t *xbase = epi_lds + pw * (NSTG * kXSlot);
+                    (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)epi_lds;
+                const int xrow = R * pw + lane / C;
+                const int xjc = ((lane % C) ^ swz<KBB>(xrow)) * 16;
                 const __amdgpu_buffer_rsrc_t xr = make_rsrc(
                     (const uint8_t *)uni((int64_t)(pr.a + pr.m * pr.lda_b)), uni(pr.xrows * pr.lda_b));
-                uint32_t xoff[kXDma];
-                int xjc[kXDma];
-#pragma unroll
-                for (int b = 0; b < kXDma; ++b) {
-                    const int xrow = R * b + lane / C;
-                    xjc[b] = ((lane % C) ^ swz<KBB>(xrow)) * 16;
-                    xoff[b] = xrow < pr.xrows ? (uint32_t)(xrow * pr.lda_b) : kOob;
-                }
+                const uint32_t xoff = xrow < pr.xrows ? (uint32_t)(xrow * pr.lda_b) : kOob;
                 auto issue_x = [&](int st) {
                     const int64_t kb0 = (int64_t)st * KBB;
-#pragma unroll
-                    for (int b = 0; b < kXDma; ++b) {
-                        const uint32_t off = (xoff[b] == kOob || kb0 + xjc[b] >= KB)
-                                                 ? kOob : xoff[b] + (uint32_t)kb0 + xjc[b];
-                        dma16(xr, off, xlds0 + (st % NSTG) * kXSlot + b * 1024);
-                    }
-                };
-                const int rr = lane & 31, gx = lane >> 5;
-                const int rb = kGrpBM + 32 * pw + rr;  // this wave's B rows of a stage
-                v16i xacc = (v16i){};
-                auto extra = [&](int st) {
-                    const uint8_t *stg = smem + (st % NSTG) * kStage;
-                    const uint8_t *xs = xbase + (st % NSTG) * kXSlot;
-#pragma unroll
-                    for (int pp = 0; pp < KBB / 32; ++pp) {
-                        const int j = 2 * pp + gx;
-                        const v4i fa =
-                            *reinterpret_cast<const v4i *>(xs + rr * KBB + ((j ^ swz<KBB>(rr)) << 4));
-                        const v4i fb =
-                            *reinterpret_cast<const v4i *>(stg + rb * KBB + ((j ^ swz<KBB>(rb)) << 4));
-#pragma unroll
-                        for (int h = 0; h < 2; ++h)
-                            xacc = mfma32i8(unpack8a<UA>((u32)fa[2 * h], (u32)fa[2 * h + 1]),
-                                            unpack8((u32)fb[2 * h], (u32)fb[2 * h + 1]), xacc);
-                    }
+                    const uint32_t off =
+                        (xoff == kOob || kb0 + xjc >= KB) ? kOob : xoff + (uint32_t)kb0 + xjc;
+                    dma16(xr, off, xlds0 + (st % NSTG) * kXSlot + pw * 1024);
                 };
                 __builtin_amdgcn_s_barrier();  // the epilogue area is free
                 asm volatile("" ::: "memory");
                 issue_x(0);
                 issue_x(1);
                 for (int s = 0; s < steps; ++s) {
-                    // this wave's LDS reads of step s - 2 are done before its
-                    // stage and slot are refilled below, and its loads of step
-                    // s are done, later ones may fly (step 0: step 1's DMAs
-                    // and steps 0 and 1's codes newer; later: step s + 1's
-                    // DMAs and codes newer, if any)
-                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                    if (s == 0)
-                        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerWave + 2 * kXDma) : "memory");
-                    else
-                        ring_wait<kDmaPerWave + kXDma, NSTG - 2>(min(NSTG - 2, steps - 1 - s));
+                    // this wave's DMA and codes of step s are done, later
+                    // ones may fly (step 0: step 1's codes newer; later: step
+                    // s + 1's DMA and codes newer, if any)
+                    if (s == 0) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+                    else ring_wait<kDmaPerWave + 1, NSTG - 2>(min(NSTG - 2, steps - 1 - s));
                     __builtin_amdgcn_s_barrier();
                     asm volatile("" ::: "memory");
-                    if (s > 0) extra(s - 1);
                     if (s + NSTG - 1 < steps) {
-                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                         issue(s + NSTG - 1, (s + NSTG - 1) % NSTG);
                         issue_x(s + NSTG - 1);
                     }
                 }
-                extra(steps - 1);
-                // end of tile: every wave is done with every stage and slot
+                // end of tile: every compute wave is done with every stage
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                continue;
+            }
+            for (int s = 0; s < steps; ++s) {
+                // this wave's DMA of step s is done (later steps may fly);
+                // after the barrier every wave's is, and step s - 1's stage
+                // is free for step s + NSTG - 1
+                ring_wait<kDmaPerWave, NSTG - 2>(min(NSTG - 2, steps - 1 - s));
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                if (s + NSTG - 1 < steps) issue(s + NSTG - 1, (s + NSTG - 1) % NSTG);
+            }
+            // end of tile: every compute wave is done with every stage
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            continue;
+        }
+
+        v16i acc[FM][FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){};
+        v16i xacc = (v16i){};  // extra-row tiles: the extra rows x B block wm
+        bool xdone = false;
+        if constexpr (kExtra) {
+            if (xt) {
+                // the extra-row tile's first barrier (see the producers): this
+                // wave's epilogue LDS reads are done
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
-                // fp16 outputs of the extra rows, from the 32x32 accumulator
-                // layout (lane: column rr, rows 8 (v / 4) + 4 gx + v % 4), with
-                // the arithmetic of the tile's LDS-staged epilogue
+                static_assert(WGN * FN * 32 == kGrpBN && FN == 2 && kCompute / WGN == 2,
+                              "wave wm takes B block wm of its columns");
+                constexpr int kXSlot = kMoeRemMax * KBB;
+                auto xloop = [&](auto xj) __attribute__((always_inline)) {
+                    for (int s = 0; s < steps; ++s) {
+                        __builtin_amdgcn_s_barrier();
+                        asm volatile("" ::: "memory");
+                        big_compute<FM, FN, KBB, kGrpBM, UA, decltype(xj)::value>(
+                            smem + (s % NSTG) * kStage, wm, wn, lane, acc,
+                            epi_lds + (s % NSTG) * kXSlot, &xacc);
+                    }
+                };
+                if (wm == 0) xloop(std::integral_constant<int, 0>{});
+                else xloop(std::integral_constant<int, 1>{});
+                xdone = true;
+            }
+        }
+        if (!xdone) {
+            for (int s = 0; s < steps; ++s) {
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                big_compute<FM, FN, KBB, kGrpBM, UA>(smem + (s % NSTG) * kStage, wm, wn, lane, acc);
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if constexpr (kExtra) {
+            if (xt) {
+                // fp16 outputs of the extra rows from the 32x32 accumulator
+                // layout (lane: column rr of B block wm of this wave's
+                // columns, rows 8 (v / 4) + 4 gx + v % 4), with the arithmetic
+                // of the tile's LDS-staged epilogue
+                const int rr = lane & 31, gx = lane >> 5;
                 const int64_t ex = p;
                 const f16 *sa = g.sa + pr.row0 + pr.m;
-                const int64_t col = n0 + 32 * pw + rr;
+                const int64_t col = n0 + wn * (FN * 32) + wm * 32 + rr;
                 if constexpr (FORM == kFormSwiglu) {
                     // columns in blocks of 8 gate then 8 up: a gate lane takes
                     // its up value from the lane 8 above
@@ -1740,43 +1772,8 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                             out[m * g.N] = f16_rn((float)(xacc[v] >> (UA ? 4 : 8)) * (float)sa[m] * sbv);
                     }
                 }
-                continue;
             }
-            for (int s = 0; s < steps; ++s) {
-                // this wave's DMA of step s is done (later steps may fly);
-                // after the barrier every wave's is, and step s - 1's stage
-                // is free for step s + NSTG - 1
-                ring_wait<kDmaPerWave, NSTG - 2>(min(NSTG - 2, steps - 1 - s));
-                __builtin_amdgcn_s_barrier();
-                asm volatile("" ::: "memory");
-                if (s + NSTG - 1 < steps) issue(s + NSTG - 1, (s + NSTG - 1) % NSTG);
-            }
-            // end of tile: every compute wave is done with every stage
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            continue;
         }
-
-        v16i acc[FM][FN];
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){};
-        if (kExtra && xt) {
-            // the extra-row tile's first barrier (see the producers): this
-            // wave's epilogue LDS reads are done
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-        }
-        for (int s = 0; s < steps; ++s) {
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            big_compute<FM, FN, KBB, kGrpBM, UA>(smem + (s % NSTG) * kStage, wm, wn, lane, acc);
-        }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
 
         if (g.out) {
             // fp16 (expert-offset form): rows row0 + m of the [R, N] output,
