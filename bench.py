@@ -58,9 +58,10 @@ def parse():
                         "2048, 8192) and print its results")
     p.add_argument("--profile", choices=PROFILE_WORKLOADS, default=None,
                    help="only run one workload a few times (for rocprofv3 counter passes): "
-                        "the cfg2 QLinear at M = 2048, 128 or 8192, the cfg4 MLP at M = 512, "
-                        "the cfg5 MoE block, the cfg3 decode layer or the prefill attention "
-                        "(Llama-70B heads, T = 8192)")
+                        "the cfg2 QLinear at M = 2048, 128, 16 or 8192, the cfg4 MLP at M = "
+                        "512, the cfg5 MoE block, the cfg3 decode layer, the prefill attention "
+                        "(Llama-70B heads, T = 8192) or the cfg2 QLinear on the bf6 path at "
+                        "M = 2048")
     p.add_argument("--cpu-rows", type=int, default=256,
                    help="rows of the CPU baseline sample")
     p.add_argument("--min-bytes", type=float, default=640e6,
@@ -124,7 +125,7 @@ def time_cpu_baseline(args, x, hadk, k, sign, wfq):
 
 COPY_BYTES = 1 << 30
 PROFILE_WORKLOADS = ("cfg2_M2048", "cfg2_M128", "cfg2_M8192", "cfg2_M16", "cfg4_M512",
-                     "cfg5_moe", "cfg3_decode", "prefill_T8192")
+                     "cfg5_moe", "cfg3_decode", "prefill_T8192", "cfg2_bf6_M2048")
 
 
 def bench_decode_layer(args, dev):
@@ -644,6 +645,8 @@ def profile_workloads(args, dev):
         res = bench_moe(dev, args.seed + 40, reps=3)
     elif name == "prefill_T8192":
         res = bench_prefill_attention(dev, 1, 8192, 64, 8, args.seed + 50 + 8192, reps=3)
+    elif name == "cfg2_bf6_M2048":
+        res = bench_qlinear_bf6(dev, 2048, 14336, 4096, args.seed + 26, reps=5, min_bytes=6e8)
     else:
         args.decode_steps, args.decode_layers = 3, 2
         res = bench_decode_layer(args, dev)
