@@ -475,18 +475,18 @@ SRQ_DEV void store_block_lds32_swiglu(const Epi &e, int64_t M, int64_t N, int64_
 }
 
 // One K step of a compute wave: the stage holds BM A rows then the B rows.
-// XJ >= 0 (the grouped kernel's extra-row tiles): also the 32 rows at xs
-// (same row layout as the stage) times this wave's B block XJ, into xacc,
-// from the B operands already unpacked for the tile.
-template <int FM, int FN, int KBB, int BM = kBigBM, bool UA = false, int XJ = -1>
+// XJ >= 0 (the grouped kernel's extra-row tiles): also the XB blocks of 32
+// rows at xs (same row layout as the stage) times this wave's B block XJ,
+// into xacc[0 .. XB - 1], from the B operands already unpacked for the tile.
+template <int FM, int FN, int KBB, int BM = kBigBM, bool UA = false, int XJ = -1, int XB = 1>
 SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&acc)[FM][FN],
                          const uint8_t *xs = nullptr, v16i *xacc = nullptr) {
     constexpr int NPP = KBB / 32;  // 16-byte fragment fetches per step
-    constexpr int NX = XJ >= 0 ? 1 : 0;
+    constexpr int NX = XJ >= 0 ? XB : 0;
     static_assert(XJ < FN, "extra block");
     const int rr = lane & 31;
     const int g = lane >> 5;
-    v4i fa[2][FM], fb[2][FN], fx[2][1];
+    v4i fa[2][FM], fb[2][FN], fx[2][XB];
     auto fetch = [&](int pp, int slot) {
         const int j = 2 * pp + g;
 #pragma unroll
@@ -499,14 +499,17 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
             const int r = BM + wn * (FN * 32) + jn * 32 + rr;
             fb[slot][jn] = *reinterpret_cast<const v4i *>(stage + r * KBB + ((j ^ swz<KBB>(r)) << 4));
         }
-        if constexpr (NX)
-            fx[slot][0] = *reinterpret_cast<const v4i *>(xs + rr * KBB + ((j ^ swz<KBB>(rr)) << 4));
+#pragma unroll
+        for (int xb = 0; xb < NX; ++xb) {
+            const int r = 32 * xb + rr;
+            fx[slot][xb] = *reinterpret_cast<const v4i *>(xs + r * KBB + ((j ^ swz<KBB>(r)) << 4));
+        }
     };
     // K slice s = 2 pp + h: bytes 8h .. 8h + 7 of the 16-byte fragments of
     // fetch pp.  Software pipeline: the nibble unpacking of slice s + 1 is
     // interleaved with the MFMAs of slice s (one MFMA, then its share of
     // the unpacking VALU work), so the vector and matrix pipes overlap.
-    v4i ua[2][FM], ub[2][FN], ux[2][1];
+    v4i ua[2][FM], ub[2][FN], ux[2][XB];
     auto unpack = [&](int sl, int buf) {
         const int pp = sl >> 1, h = sl & 1;
 #pragma unroll
@@ -515,8 +518,9 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
 #pragma unroll
         for (int jn = 0; jn < FN; ++jn)
             ub[buf][jn] = unpack8((u32)fb[pp & 1][jn][2 * h], (u32)fb[pp & 1][jn][2 * h + 1]);
-        if constexpr (NX)
-            ux[buf][0] = unpack8a<UA>((u32)fx[pp & 1][0][2 * h], (u32)fx[pp & 1][0][2 * h + 1]);
+#pragma unroll
+        for (int xb = 0; xb < NX; ++xb)
+            ux[buf][xb] = unpack8a<UA>((u32)fx[pp & 1][xb][2 * h], (u32)fx[pp & 1][xb][2 * h + 1]);
     };
     fetch(0, 0);
     unpack(0, 0);
@@ -529,7 +533,9 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
 #pragma unroll
             for (int jn = 0; jn < FN; ++jn)
                 acc[i][jn] = mfma32i8(ua[sl & 1][i], ub[sl & 1][jn], acc[i][jn]);
-        if constexpr (NX) *xacc = mfma32i8(ux[sl & 1][0], ub[sl & 1][XJ < 0 ? 0 : XJ], *xacc);
+#pragma unroll
+        for (int xb = 0; xb < NX; ++xb)
+            xacc[xb] = mfma32i8(ux[sl & 1][xb], ub[sl & 1][XJ < 0 ? 0 : XJ], xacc[xb]);
         if (sl + 1 < 2 * NPP) unpack(sl + 1, (sl + 1) & 1);
         if ((sl & 1) == 0 && pp + 1 < NPP)
             __builtin_amdgcn_sched_group_barrier(0x100, FM + FN + NX, 0);
@@ -1082,12 +1088,12 @@ constexpr int kStreamS = 4;
 constexpr int kStreamMaxCb = 16;   // column blocks per workgroup
 
 // MoE rows past an expert's full 128-row tiles: when an expert has more
-// than one tile and its last tile would hold 1..32 rows, those rows ride on
+// than one tile and its last tile would hold 1..64 rows, those rows ride on
 // its last full tile instead (the grouped kernel's producer waves compute
 // them from the same weight stages), so no near-empty tile streams the
 // expert's weights a second time (cfg5: the down launch's 320 tiles for 256
 // CUs become 256).
-constexpr int kMoeTile = 128, kMoeRemMax = 32;
+constexpr int kMoeTile = 128, kMoeRemMax = 64;
 SRQ_DEV int64_t moe_tiled_rows(int64_t r) {
     const int64_t q = r % kMoeTile;
     return (r > kMoeTile && q > 0 && q <= kMoeRemMax) ? r - q : r;
@@ -1454,8 +1460,8 @@ struct GroupedProb {
     const uint8_t *a, *b;
     int32_t *c;
     int64_t m, n, k, lda_b, ldb_b, ldc, row0;
-    // rows m .. m + xrows - 1 of the problem (at most 32), computed by the
-    // producer waves of its last M tile
+    // rows m .. m + xrows - 1 of the problem (at most kMoeRemMax), computed
+    // on its last M tile
     int64_t xrows;
 };
 
@@ -1628,30 +1634,39 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             for (int q = 0; q < NSTG - 1; ++q)
                 if (q < steps) issue(q, q);
             if (kExtra && xt) {
-                // The expert's rows past its full tiles (1..32; at least two K
+                // The expert's rows past its full tiles (1..64; at least two K
                 // steps): the compute waves multiply them with the B operands
                 // they unpack for the tile.  Their codes stream into NSTG
-                // 4 KiB slots of the epilogue area (idle during the K loop),
-                // one 1 KiB DMA (8 rows) per producer per step in the stage
-                // layout, waited before barrier s like step s's stage.  The
+                // 8 KiB slots of the epilogue area (idle during the K loop),
+                // two 1 KiB DMAs (8 rows each) per producer per step in the
+                // stage layout, waited before barrier s like step s's stage.  The
                 // area is free once the compute waves' previous epilogue is
                 // done: on such a tile every wave meets one more barrier
                 // before the K loop, after which steps 0 and 1's codes load.
-                static_assert(NSTG == 3 && NPROD * R == kMoeRemMax, "extra-row schedule");
                 constexpr int kXSlot = kMoeRemMax * KBB;
+                constexpr int kXDma = kMoeRemMax / R / NPROD;  // DMAs per producer per step
+                static_assert(NSTG == 3 && kXDma * R * NPROD == kMoeRemMax, "extra-row schedule");
                 static_assert(NSTG * kXSlot <= kCompute * kEpiTile, "extra-row slots");
                 const uint32_t xlds0 =
                     (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)epi_lds;
-                const int xrow = R * pw + lane / C;
-                const int xjc = ((lane % C) ^ swz<KBB>(xrow)) * 16;
                 const __amdgpu_buffer_rsrc_t xr = make_rsrc(
                     (const uint8_t *)uni((int64_t)(pr.a + pr.m * pr.lda_b)), uni(pr.xrows * pr.lda_b));
-                const uint32_t xoff = xrow < pr.xrows ? (uint32_t)(xrow * pr.lda_b) : kOob;
+                uint32_t xoff[kXDma];
+                int xjc[kXDma];
+#pragma unroll
+                for (int q = 0; q < kXDma; ++q) {
+                    const int xrow = R * (kXDma * pw + q) + lane / C;
+                    xjc[q] = ((lane % C) ^ swz<KBB>(xrow)) * 16;
+                    xoff[q] = xrow < pr.xrows ? (uint32_t)(xrow * pr.lda_b) : kOob;
+                }
                 auto issue_x = [&](int st) {
                     const int64_t kb0 = (int64_t)st * KBB;
-                    const uint32_t off =
-                        (xoff == kOob || kb0 + xjc >= KB) ? kOob : xoff + (uint32_t)kb0 + xjc;
-                    dma16(xr, off, xlds0 + (st % NSTG) * kXSlot + pw * 1024);
+#pragma unroll
+                    for (int q = 0; q < kXDma; ++q) {
+                        const uint32_t off = (xoff[q] == kOob || kb0 + xjc[q] >= KB)
+                                                 ? kOob : xoff[q] + (uint32_t)kb0 + xjc[q];
+                        dma16(xr, off, xlds0 + (st % NSTG) * kXSlot + (kXDma * pw + q) * 1024);
+                    }
                 };
                 __builtin_amdgcn_s_barrier();  // the epilogue area is free
                 asm volatile("" ::: "memory");
@@ -1661,8 +1676,8 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                     // this wave's DMA and codes of step s are done, later
                     // ones may fly (step 0: step 1's codes newer; later: step
                     // s + 1's DMA and codes newer, if any)
-                    if (s == 0) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-                    else ring_wait<kDmaPerWave + 1, NSTG - 2>(min(NSTG - 2, steps - 1 - s));
+                    if (s == 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kXDma) : "memory");
+                    else ring_wait<kDmaPerWave + kXDma, NSTG - 2>(min(NSTG - 2, steps - 1 - s));
                     __builtin_amdgcn_s_barrier();
                     asm volatile("" ::: "memory");
                     if (s + NSTG - 1 < steps) {
@@ -1695,7 +1710,8 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) acc[i][j] = (v16i){};
-        v16i xacc = (v16i){};  // extra-row tiles: the extra rows x B block wm
+        // extra-row tiles: extra rows 32 xb .. 32 xb + 31 x B block wm
+        v16i xacc[2] = {(v16i){}, (v16i){}};
         bool xdone = false;
         if constexpr (kExtra) {
             if (xt) {
@@ -1707,17 +1723,26 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                 static_assert(WGN * FN * 32 == kGrpBN && FN == 2 && kCompute / WGN == 2,
                               "wave wm takes B block wm of its columns");
                 constexpr int kXSlot = kMoeRemMax * KBB;
-                auto xloop = [&](auto xj) __attribute__((always_inline)) {
+                static_assert(kMoeRemMax == 64, "one or two extra blocks");
+                auto xloop = [&](auto xj, auto xb) __attribute__((always_inline)) {
                     for (int s = 0; s < steps; ++s) {
                         __builtin_amdgcn_s_barrier();
                         asm volatile("" ::: "memory");
-                        big_compute<FM, FN, KBB, kGrpBM, UA, decltype(xj)::value>(
-                            smem + (s % NSTG) * kStage, wm, wn, lane, acc,
-                            epi_lds + (s % NSTG) * kXSlot, &xacc);
+                        big_compute<FM, FN, KBB, kGrpBM, UA, decltype(xj)::value,
+                                    decltype(xb)::value>(smem + (s % NSTG) * kStage, wm, wn, lane,
+                                                         acc, epi_lds + (s % NSTG) * kXSlot, xacc);
                     }
                 };
-                if (wm == 0) xloop(std::integral_constant<int, 0>{});
-                else xloop(std::integral_constant<int, 1>{});
+                using I0 = std::integral_constant<int, 0>;
+                using I1 = std::integral_constant<int, 1>;
+                using I2 = std::integral_constant<int, 2>;
+                if (pr.xrows > 32) {
+                    if (wm == 0) xloop(I0{}, I2{});
+                    else xloop(I1{}, I2{});
+                } else {
+                    if (wm == 0) xloop(I0{}, I1{});
+                    else xloop(I1{}, I1{});
+                }
                 xdone = true;
             }
         }
@@ -1735,8 +1760,9 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             if (xt) {
                 // fp16 outputs of the extra rows from the 32x32 accumulator
                 // layout (lane: column rr of B block wm of this wave's
-                // columns, rows 8 (v / 4) + 4 gx + v % 4), with the arithmetic
-                // of the tile's LDS-staged epilogue
+                // columns, rows 32 xb + 8 (v / 4) + 4 gx + v % 4; block 1 is
+                // zero unless there are more than 32), with the arithmetic of
+                // the tile's LDS-staged epilogue
                 const int rr = lane & 31, gx = lane >> 5;
                 const int64_t ex = p;
                 const f16 *sa = g.sa + pr.row0 + pr.m;
@@ -1751,26 +1777,31 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                     const float sbu = on ? (float)g.sb[ex * g.N + gn0 + 8 + jj] : 0.f;
                     f16 *out = g.out + (pr.row0 + pr.m) * (g.N / 2) + gn0 / 2 + jj;
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int ua = __shfl_down(xacc[v], 8, 64);
-                        const int m = 8 * (v / 4) + 4 * gx + v % 4;
-                        if (on && m < pr.xrows) {
-                            const float sav = (float)sa[m];
-                            const f16 gh = f16_rn((float)(xacc[v] >> 8) * sav * sbg);
-                            const f16 uh = f16_rn((float)(ua >> 8) * sav * sbu);
-                            out[m * (g.N / 2)] = swiglu1((float)gh, (float)uh);
+                    for (int xb = 0; xb < 2; ++xb)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const int ua = __shfl_down(xacc[xb][v], 8, 64);
+                            const int m = 32 * xb + 8 * (v / 4) + 4 * gx + v % 4;
+                            if (on && m < pr.xrows) {
+                                const float sav = (float)sa[m];
+                                const f16 gh = f16_rn((float)(xacc[xb][v] >> 8) * sav * sbg);
+                                const f16 uh = f16_rn((float)(ua >> 8) * sav * sbu);
+                                out[m * (g.N / 2)] = swiglu1((float)gh, (float)uh);
+                            }
                         }
-                    }
                 } else {
                     const bool on = col < pr.n;
                     const float sbv = on ? (float)g.sb[ex * g.N + col] : 0.f;
                     f16 *out = g.out + (pr.row0 + pr.m) * g.N + col;
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) {
-                        const int m = 8 * (v / 4) + 4 * gx + v % 4;
-                        if (on && m < pr.xrows)
-                            out[m * g.N] = f16_rn((float)(xacc[v] >> (UA ? 4 : 8)) * (float)sa[m] * sbv);
-                    }
+                    for (int xb = 0; xb < 2; ++xb)
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const int m = 32 * xb + 8 * (v / 4) + 4 * gx + v % 4;
+                            if (on && m < pr.xrows)
+                                out[m * g.N] = f16_rn((float)(xacc[xb][v] >> (UA ? 4 : 8)) *
+                                                      (float)sa[m] * sbv);
+                        }
                 }
             }
         }

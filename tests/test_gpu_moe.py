@@ -151,14 +151,15 @@ def test_matmul_grouped_vs_oracle(C):
         assert_bitexact(c[off[e]:off[e + 1]], want[e], f"problem {e}")
 
 
-# Experts past one 128-row tile with 1..32 rows left over compute those rows
-# on their last full tile (the grouped kernel's producer waves); 33+ left
-# over, exact tiles and single tiles are tiled as they are.  The cases put
+# Experts past one 128-row tile with 1..64 rows left over compute those rows
+# on their last full tile (one or two extra 32-row blocks of the grouped
+# kernel's compute waves); 65+ left over, exact tiles and single tiles are
+# tiled as they are.  The cases put
 # every kind of expert side by side, at the MoE down shape too, with every
 # expert taking extra rows, with many experts, at the fewest K steps that
 # allow it (two) and with a ragged last K step, and at K <= 256 (one step:
 # every row tiled).
-REM_COUNTS = [160, 161, 257, 0, 100, 128, 140, 288, 33, 129, 1, 416]
+REM_COUNTS = [160, 161, 257, 0, 100, 128, 140, 288, 33, 129, 1, 416, 170, 192, 193]
 
 
 @pytest.mark.parametrize("counts,n,k", [([3, 0, 5, 1], 300, 768),
@@ -521,7 +522,8 @@ def test_swiglu_had_sign_quant_moe(C, rows, n, K, experts, clip, with_sign):
                                        ([123, 127, 123, 122, 123, 126, 136, 144], 14336, 4096),
                                        ([700, 1], 1024, 2048), (REM_COUNTS, 1008, 800),
                                        ([130, 131, 160, 99], 14336, 4096),
-                                       ([140] * 8, 14336, 4096), ([140, 161, 129], 48, 512)])
+                                       ([140] * 8, 14336, 4096), ([140, 161, 129], 48, 512),
+                                       ([170, 192, 193, 224, 160], 2048, 1024)])
 def test_w4a4_linear_moe_swiglu_equals_gate_up_then_swiglu(C, counts, n, k):
     """The SwiGLU epilogue of the grouped gate/up launch over interleaved
     weights: bit-identical to the two projections followed by srq_swiglu."""
