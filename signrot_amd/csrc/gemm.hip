@@ -1895,21 +1895,53 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t *__res
                                                             int S, int64_t M, int64_t N,
                                                             Epi e) {
     const int64_t MN = M * N;
+    const int sh = e.ua ? 4 : 8;
     for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V; i < MN;
          i += (int64_t)gridDim.x * 256 * V) {
+        // the S partials, 8 loads in flight at a time (one at a time, each
+        // waited before the next, took ~2x as long)
         int acc[V] = {};
-        for (int s = 0; s < S; ++s) {
+        for (int s0 = 0; s0 < S; s0 += 8) {
             if constexpr (V == 4) {
-                const v4i p = *reinterpret_cast<const v4i *>(ws + s * MN + i);
+                v4i p[8];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) acc[k] += p[k];
+                for (int k = 0; k < 8; ++k)
+                    p[k] = s0 + k < S ? *reinterpret_cast<const v4i *>(ws + (s0 + k) * MN + i)
+                                      : (v4i){};
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[q] += p[k][q];
             } else {
-                acc[0] += ws[s * MN + i];
+                int p[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) p[k] = s0 + k < S ? ws[(s0 + k) * MN + i] : 0;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[0] += p[k];
             }
         }
+        if (V == 4 && !e.C && N % 4 == 0) {
+            // the four outputs share a row: store_one's arithmetic with every
+            // operand loaded before the first store (a store may alias them,
+            // so store_one per output waited a round trip for each)
+            const int64_t m = i / N, n = i - m * N;
+            f16 o[V];
 #pragma unroll
-        for (int k = 0; k < V; ++k)
-            store_one(e, N, (i + k) / N, (i + k) % N, (int)((u32)acc[k] << (e.ua ? 4 : 8)));
+            for (int k = 0; k < V; ++k) {
+                const int v = epi_val(e, (int)((u32)acc[k] << sh), m, n + k);
+                const float a = (float)v * (float)e.sa[m];
+                f16 x = f16_rn(a * (float)e.sb[n + k]);
+                if (e.bias) x = f16_rn((float)x + (float)e.bias[n + k]);
+                if (e.res) x = f16_rn((float)x + (float)e.res[m * N + n + k]);
+                o[k] = x;
+            }
+#pragma unroll
+            for (int k = 0; k < V; ++k) e.out[m * N + n + k] = o[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < V; ++k)
+                store_one(e, N, (i + k) / N, (i + k) % N, (int)((u32)acc[k] << sh));
+        }
     }
 }
 
