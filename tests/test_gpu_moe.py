@@ -320,12 +320,13 @@ def test_block_nan_token():
 
 
 @pytest.mark.parametrize("T,k,H", [(512, 2, 4096), (33, 1, 64), (7, 2, 8), (100, 4, 256),
-                                   (0, 2, 64)])
+                                   (0, 2, 64), (20, 8, 128), (16, 10, 64)])
 def test_moe_combine_matches_torch(C, T, k, H):
     """srq_moe_combine against (y[inv].view(T, k, H) * w.unsqueeze(-1)).sum(1)
     in torch fp16 (moe.py:226-230): bit for bit for k <= 2 (fp32 sums of
-    two products are order-free); for k = 4 within one fp16 ulp (torch's
-    reduction order is its own)."""
+    two products are order-free); for k = 4, 8 and 10 (past the kernel's
+    batched choices) within one fp16 ulp (torch's reduction order is its
+    own)."""
     g = torch.Generator(device=DEV).manual_seed(T * k + H)
     y = torch.randn(T * k, H, generator=g, device=DEV).half()
     w = torch.rand(T, k, generator=g, device=DEV).half()
