@@ -1089,10 +1089,10 @@ constexpr int kStreamMaxCb = 16;   // column blocks per workgroup
 
 // MoE rows past an expert's full 128-row tiles: when an expert has more
 // than one tile and its last tile would hold 1..64 rows, those rows ride on
-// its last full tile instead (the grouped kernel's producer waves compute
-// them from the same weight stages), so no near-empty tile streams the
-// expert's weights a second time (cfg5: the down launch's 320 tiles for 256
-// CUs become 256).
+// its last full tile instead (the grouped kernel's compute waves multiply
+// them with the B operands they unpack for that tile; the producer waves
+// stage their codes), so no mostly empty tile streams the expert's weights
+// a second time (cfg5: the down launch's 320 tiles for 256 CUs become 256).
 constexpr int kMoeTile = 128, kMoeRemMax = 64;
 SRQ_DEV int64_t moe_tiled_rows(int64_t r) {
     const int64_t q = r % kMoeTile;
@@ -1396,7 +1396,9 @@ bool launch_stream(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int
 // with a running prefix sum.  Producers and compute waves walk the same
 // sequence, so their barrier counts agree: K steps plus one end-of-tile
 // barrier per tile (after it the stages are free for the next tile's
-// prologue).  Rows past a problem's m and chunks past its k read as zeros.
+// prologue), and one more before the K loop of a tile with extra rows
+// (GroupedProb::xrows).  Rows past a problem's m and chunks past its k read
+// as zeros.
 
 constexpr int kGrpBM = 128, kGrpBN = 128;
 static_assert(kGrpBM == kMoeTile, "the MoE remainder rule assumes the grouped kernel's tile rows");
