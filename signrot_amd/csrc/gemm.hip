@@ -1600,9 +1600,8 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
                 make_rsrc((const uint8_t *)uni((int64_t)pr.b), uni(pr.n * pr.ldb_b));
             uint32_t roff[kDmaPerWave];
             int jc[kDmaPerWave];
-            // 1 KiB block of DMA q of this wave: A rows then B rows 32 pw ..
-            // 32 pw + 31 of the stage (a producer's extra rows read only the
-            // B rows it loads itself)
+            // 1 KiB block of DMA q of this wave: its A rows then its B rows,
+            // 32 pw .. 32 pw + 31 of each, of the stage
             constexpr int kAPer = kGrpBM / R / NPROD, kBPer = kGrpBN / R / NPROD;
             static_assert(kAPer + kBPer == kDmaPerWave && kBPer * R == 32, "DMA blocks");
             auto blk = [&](int q) {
