@@ -91,6 +91,10 @@ struct Epi {
     // columns and out [M, N / 2] receives swiglu(gate, up) of each pair
     // (C, bias, res and zr null)
     int swiglu;
+    // swiglu output row stride in elements, 0 for N / 2 (read by the big
+    // and grouped kernels' LDS swiglu epilogues only: launch_gemm's column
+    // split)
+    int64_t ldo;
 };
 
 // The int32 product of output (m, n) from the MFMA accumulator: sum(a * w),
@@ -297,7 +301,7 @@ SRQ_DEV void store_block_lds_impl(const Epi &e, int64_t M, int64_t N, int64_t mb
             v8h o;
 #pragma unroll
             for (int k = 0; k < 8; ++k) o[k] = swiglu1((float)gv[k], (float)uv[k]);
-            *reinterpret_cast<v8h *>(e.out + gm * (N / 2) + gs0 / 2) = o;
+            *reinterpret_cast<v8h *>(e.out + gm * (e.ldo ? e.ldo : N / 2) + gs0 / 2) = o;
         }
         return;
     }
@@ -470,7 +474,7 @@ SRQ_DEV void store_block_lds32_swiglu(const Epi &e, int64_t M, int64_t N, int64_
             const f16 uh = f16_rn((float)(ua >> 8) * sa * sbu[k]);
             o[k] = swiglu1((float)gh, (float)uh);
         }
-        *reinterpret_cast<v8h *>(e.out + gm * (N / 2) + gn0 / 2) = o;
+        *reinterpret_cast<v8h *>(e.out + gm * (e.ldo ? e.ldo : N / 2) + gn0 / 2) = o;
     }
 }
 
@@ -1447,6 +1451,7 @@ struct GroupedArgs {
     int64_t M;
     const f16 *bias, *res;
     int swiglu;  // dense form: the columns are blocks of 8 gate, 8 up; out [M, N/2]
+    int64_t ldo;  // dense swiglu form: Epi::ldo
     // split-K form (the SPLITK instantiation): problem p is the dense
     // product over K codes [p Kc, min((p + 1) Kc, K)), its int32 partial
     // (shifted down like the dense accumulator) at ws_c + p M N
@@ -1828,6 +1833,7 @@ __global__ __launch_bounds__(64 * (4 + NPROD), 1) void gemm_grouped_kernel(Group
             if constexpr (DENSE) {
                 e.bias = g.bias;
                 e.res = g.res;
+                e.ldo = g.ldo;
             }
             if (sw)
                 store_block_lds32_swiglu<32, FM, FN>(
@@ -2044,15 +2050,36 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         g.zr = e.zr;
         g.ws = e.ws;
         g.swiglu = e.swiglu;
+        g.ldo = e.ldo;
         const int64_t tiles = srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN);
         gemm_grouped_kernel<4, UA, kFormDense>
             <<<dim3((unsigned)std::min<int64_t>(tiles, kGroupedGrid)), dim3(512), 0, st>>>(g);
     } else if (M >= 1024 || srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) >= 512) {
-        const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
+        const int64_t tm = srq_cdiv(M, kBigBM), tiles = tm * srq_cdiv(N, kBigBN);
+        const int64_t rem = tiles % 256;
         // 4 compute waves (128 x 64 each) + 4 producer waves (8 compute
         // waves of 64 x 64, two per SIMD, measured no faster)
-        gemm_big_kernel<4, 2, 2, 4, 2, 128, 3, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(
-            a, b, M, N, K, e);
+        if (e.swiglu && !e.ldo && M < 1024 && rem && rem <= 128 && rem % tm == 0 &&
+            srq_cdiv(M, kGrpBM) * (rem / tm) * (kBigBN / kGrpBN) >= 128) {
+            // a last round over at most half the CUs: its columns (whole
+            // 128-column tiles) take the grouped kernel's dense form, which
+            // spreads 128 x 128 tiles over every CU, and the rest runs in
+            // whole rounds (cfg4 M = 512 gate/up: 768 + 256 tiles instead of
+            // 3.5 rounds of 256); both write the [M, N / 2] output at its
+            // own row stride
+            const int64_t tail = rem / tm * kBigBN, head = N - tail;
+            Epi eh = e;
+            eh.ldo = N / 2;
+            gemm_big_kernel<4, 2, 2, 4, 2, 128, 3, UA>
+                <<<dim3((unsigned)(tiles - rem)), dim3(512), 0, st>>>(a, b, M, head, K, eh);
+            Epi et = eh;
+            et.out = e.out + head / 2;
+            et.sb = e.sb + head;
+            launch_gemm<UA>(a, b + head * (K / 2), M, tail, K, et, st);
+        } else {
+            gemm_big_kernel<4, 2, 2, 4, 2, 128, 3, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(
+                a, b, M, N, K, e);
+        }
     } else {
         // mid-size M: the tile shrinks with M so the grid still covers the
         // 256 CUs (at N = 4096: 256 workgroups for M = 128, 256, 512); the

@@ -261,7 +261,11 @@ def test_qkv_decode_i4_argument_errors():
     # every other kernel of the dispatch: ring (the skinny kernel is skipped),
     # dense grouped, big, 256 x 256 square tiles
     (48, 896, 1024), (70, 256, 256), (600, 512, 2048), (128, 14336, 4096), (300, 4096, 1024),
-    (1100, 1504, 1024), (4096, 4096, 512), (2048, 14336, 512)])
+    (1100, 1504, 1024), (4096, 4096, 512), (2048, 14336, 512),
+    # big-kernel grids with a last round over at most half the CUs: those
+    # columns on the dense grouped form (the cfg4 70B gate/up at M = 512; a
+    # ragged M)
+    (512, 28672, 8192), (300, 20480, 512)])
 def test_w4a4_linear_swiglu_equals_linear_then_swiglu(M, ffn, K):
     """The SwiGLU epilogue of the gate/up projection, on every kernel the
     shape dispatches to: bit-identical to the fp16 gate/up GEMM outputs fed
