@@ -558,11 +558,13 @@ SRQ_DEV void big_compute(const uint8_t *stage, int wm, int wn, int lane, v16i (&
 
 // WGM x WGN compute waves, each FM x FN blocks of 32 x 32 (a (32 FM) x
 // (32 FN) wave tile), plus NPROD producer waves; the block tile is always
-// kBigBM x kBigBN.
+// kBigBM x kBigBN.  Kc > 0: split-K form, workgroup row blockIdx.y takes
+// codes [y Kc, (y + 1) Kc) of K and stores its int32 partials (e.C, shifted
+// down like the dense accumulator) at e.C + y M N.
 template <int NPROD, int WGM, int WGN, int FM, int FN, int KBB, int NSTG, bool UA>
 __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
     const uint8_t *__restrict__ A, const uint8_t *__restrict__ B, int64_t M, int64_t N,
-    int64_t K, Epi e) {
+    int64_t K, Epi e, int64_t Kc) {
     static_assert(WGM * FM * 32 == kBigBM && WGN * FN * 32 == kBigBN, "block tile");
     static_assert(NSTG == 3, "the producers' vmcnt waits assume one step in flight beyond the next");
     constexpr int kCompute = WGM * WGN;
@@ -615,7 +617,11 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
         n0 = ((int64_t)blockIdx.x % tiles_n) * kBigBN;
     }
     const int64_t KB = K / 2;
-    const int steps = (int)((KB + KBB - 1) / KBB);
+    // this workgroup's K bytes [kbase, kend) of every row
+    const int64_t kbase = Kc ? (int64_t)blockIdx.y * (Kc / 2) : 0;
+    const int64_t kend = Kc ? min(kbase + Kc / 2, KB) : KB;
+    const int steps = (int)((kend - kbase + KBB - 1) / KBB);
+    if (Kc) e.C += (int64_t)blockIdx.y * M * N;
 
     if (wave >= kCompute) {
         // ---- producer: DMA block i = kDmaPerWave * pw + q covers stage rows
@@ -641,14 +647,14 @@ __global__ __launch_bounds__(64 * (WGM * WGN + NPROD), 1) void gemm_big_kernel(
             roff[q] = row < (isa ? M : N) ? (uint32_t)(row * KB) : kOob;
         }
         auto issue = [&](int st, int sl) {
-            const int64_t kb0 = (int64_t)st * KBB;
-            const bool tail = kb0 + KBB > KB;
+            const int64_t kb0 = kbase + (int64_t)st * KBB;
+            const bool tail = kb0 + KBB > kend;
 #pragma unroll
             for (int q = 0; q < kDmaPerWave; ++q) {
                 const int i = pw * kDmaPerWave + q;
                 const uint32_t dst = lds0 + sl * kStage + i * 1024;
                 uint32_t off = roff[q] == kOob ? kOob : roff[q] + (uint32_t)kb0 + jc[q];
-                if (tail && kb0 + jc[q] >= KB) off = kOob;
+                if (tail && kb0 + jc[q] >= kend) off = kOob;
                 dma16(kRowsPerDma * i < kBigBM ? ar : br, off, dst);
             }
         };
@@ -1961,12 +1967,26 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const int32_t *__res
 struct SplitK {
     int S = 0;
     int64_t Kc = 0;
+    bool big = false;  // the big kernel's 256 x 128 tiles, grid (tiles, S)
 };
 SplitK splitk_plan(int64_t M, int64_t N, int64_t K, bool fp16_out) {
     SplitK p;
     if (!fp16_out || M <= 64 || M >= 1024 || K < 2048) return p;
     const int64_t tiles = srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN);
-    if (tiles >= 192 || srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) >= 512) return p;
+    const int64_t big = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
+    if (tiles >= 192 && big >= 64 && big <= 128 && 256 % big == 0 && K / (256 / big) >= 4096) {
+        // enough 128 x 128 tiles for the dense grouped form, but 256 / big
+        // K-chunks of 256 x 128 tiles cover the CUs exactly, and the bigger
+        // tile unpacks fewer nibbles per MFMA (the grouped kernel's compute
+        // waves are bound by that issue)
+        p.S = (int)(256 / big);
+        p.Kc = srq_cdiv(srq_cdiv(K, p.S), 256) * 256;
+        p.S = (int)srq_cdiv(K, p.Kc);
+        p.big = true;
+        if (p.S < 2) p = SplitK{};
+        return p;
+    }
+    if (tiles >= 192 || big >= 512) return p;
     int64_t S = std::min<int64_t>(256 / tiles, K / 1792);
     if (S < 2 || tiles * S < 128) return p;
     const int64_t Kc = srq_cdiv(srq_cdiv(K, S), 256) * 256;
@@ -1978,6 +1998,19 @@ SplitK splitk_plan(int64_t M, int64_t N, int64_t K, bool fp16_out) {
 int64_t splitk_bytes(int64_t M, int64_t N, int64_t K, bool fp16_out) {
     const SplitK p = splitk_plan(M, N, K, fp16_out);
     return p.S ? (int64_t)p.S * M * N * 4 : 0;
+}
+
+// The S partials at ws summed into e's epilogue.
+void splitk_reduce(const void *ws, int S, int64_t M, int64_t N, const Epi &e, hipStream_t st) {
+    if ((M * N) % 4 == 0) {
+        const int64_t blocks = std::min<int64_t>(srq_cdiv(M * N / 4, 256), 2048);
+        splitk_reduce_kernel<4><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+            (const int32_t *)ws, S, M, N, e);
+    } else {
+        const int64_t blocks = std::min<int64_t>(srq_cdiv(M * N, 256), 2048);
+        splitk_reduce_kernel<1><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
+            (const int32_t *)ws, S, M, N, e);
+    }
 }
 
 // Kernel choice by shape; UA: A holds unsigned nibbles (Epi::ua).  With a
@@ -2005,6 +2038,17 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         // enough 256 x 256 tiles to cover the 256 CUs
         const int64_t tiles = srq_cdiv(M, kSqBM) * srq_cdiv(N, kSqBN);
         gemm_sq_kernel<128, 2, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(a, b, M, N, K, e);
+    } else if (sk.S && sk.big && !e.swiglu && ws_bytes >= (int64_t)sk.S * M * N * 4) {
+        // split-K on the big kernel: S rows of workgroups over K-chunks
+        // write int32 partials, then one pass sums them and runs the
+        // epilogue
+        Epi ep{};
+        ep.C = (int32_t *)ws;
+        ep.ua = e.ua;
+        const int64_t tiles = srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN);
+        gemm_big_kernel<4, 2, 2, 4, 2, 128, 3, UA>
+            <<<dim3((unsigned)tiles, (unsigned)sk.S), dim3(512), 0, st>>>(a, b, M, N, K, ep, sk.Kc);
+        splitk_reduce(ws, sk.S, M, N, e, st);
     } else if (sk.S && !e.swiglu && ws_bytes >= (int64_t)sk.S * M * N * 4) {
         // split-K: S dense problems over K-chunks write int32 partials,
         // then one pass sums them and runs the epilogue
@@ -2020,15 +2064,7 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
         const int64_t tiles = srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN) * sk.S;
         gemm_grouped_kernel<4, UA, kFormSplitK>
             <<<dim3((unsigned)std::min<int64_t>(tiles, kGroupedGrid)), dim3(512), 0, st>>>(g);
-        if ((M * N) % 4 == 0) {
-            const int64_t blocks = std::min<int64_t>(srq_cdiv(M * N / 4, 256), 2048);
-            splitk_reduce_kernel<4><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-                (const int32_t *)ws, sk.S, M, N, e);
-        } else {
-            const int64_t blocks = std::min<int64_t>(srq_cdiv(M * N, 256), 2048);
-            splitk_reduce_kernel<1><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(
-                (const int32_t *)ws, sk.S, M, N, e);
-        }
+        splitk_reduce(ws, sk.S, M, N, e, st);
     } else if (M < 1024 && !e.C && srq_cdiv(M, kGrpBM) * srq_cdiv(N, kGrpBN) >= 192 &&
                srq_cdiv(M, kBigBM) * srq_cdiv(N, kBigBN) < 512) {
         // mid-size M with enough 128 x 128 tiles to fill the CUs: the grouped
@@ -2071,14 +2107,14 @@ void launch_gemm(const uint8_t *a, const uint8_t *b, int64_t M, int64_t N, int64
             Epi eh = e;
             eh.ldo = N / 2;
             gemm_big_kernel<4, 2, 2, 4, 2, 128, 3, UA>
-                <<<dim3((unsigned)(tiles - rem)), dim3(512), 0, st>>>(a, b, M, head, K, eh);
+                <<<dim3((unsigned)(tiles - rem)), dim3(512), 0, st>>>(a, b, M, head, K, eh, 0);
             Epi et = eh;
             et.out = e.out + head / 2;
             et.sb = e.sb + head;
             launch_gemm<UA>(a, b + head * (K / 2), M, tail, K, et, st);
         } else {
             gemm_big_kernel<4, 2, 2, 4, 2, 128, 3, UA><<<dim3((unsigned)tiles), dim3(512), 0, st>>>(
-                a, b, M, N, K, e);
+                a, b, M, N, K, e, 0);
         }
     } else {
         // mid-size M: the tile shrinks with M so the grid still covers the

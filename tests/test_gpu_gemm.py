@@ -126,7 +126,10 @@ def test_w4a4_linear_residual_dense_grouped(C, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(128, 4096, 14336), (128, 14336, 4096), (200, 4100, 8192),
                                    (100, 14336, 4640), (512, 4096, 14336), (65, 1032, 28672),
-                                   (99, 1001, 28672)])
+                                   (99, 1001, 28672),
+                                   # the big kernel's split: the cfg4 70B down_proj at M = 512;
+                                   # ragged M with K chunks of 4352 and 3968 codes
+                                   (512, 8192, 28672), (300, 8192, 8320)])
 def test_w4a4_linear_split_k(C, M, N, K):
     """Mid-size M with few output tiles: the workspace entry points split K
     into int32 partials; the result is bit for bit the plain entry point's
