@@ -113,8 +113,9 @@ int srq_w4a4_linear_swiglu(const void *A, const void *a_scale, const void *B,
 
 /* Workspace form of srq_w4a4_linear (and of srq_w4a4_linear_residual
  * below, with residual): bit-identical outputs.  For mid-size M (65 ..
- * 1023) whose 128 x 128 output tiles are too few to fill the GPU, the
- * product is split over K into int32 partials in `workspace` (device
+ * 1023) whose output tiles are too few to fill the GPU (under 192 of
+ * 128 x 128, or 64 or 128 of 256 x 128 with K chunks of at least 4096
+ * codes), the product is split over K into int32 partials in `workspace` (device
  * memory, srq_w4a4_linear_ws_bytes(M, N, K) bytes, 0 when the shape is not
  * split) and summed by a second pass before the epilogue; with a smaller
  * workspace the call runs as srq_w4a4_linear.  No counterpart in the
