@@ -705,13 +705,15 @@ def main():
     stream = torch.cuda.current_stream()
 
     def step(i):
+        # on the current stream at call time (the capture stream under
+        # graph capture)
         j = i % nsets
+        cs = torch.cuda.current_stream().cuda_stream
         _native.call("srq_had_sign_quant", xs[j].data_ptr(), M, K, k,
                      hadk.data_ptr() if hadk is not None else None, sign.data_ptr(), 0, 1.0,
-                     qbufs[j].data_ptr(), sbufs[j].data_ptr(), stream.cuda_stream)
+                     qbufs[j].data_ptr(), sbufs[j].data_ptr(), cs)
         _native.call("srq_w4a4_linear", qbufs[j].data_ptr(), sbufs[j].data_ptr(),
-                     wqs[j].data_ptr(), ws.data_ptr(), None, M, N, K, outs[j].data_ptr(),
-                     stream.cuda_stream)
+                     wqs[j].data_ptr(), ws.data_ptr(), None, M, N, K, outs[j].data_ptr(), cs)
 
     # correctness guard on the measured buffers: fused path == module path
     from signrot_amd.functional import kernel
@@ -724,6 +726,8 @@ def main():
         step(i)
     torch.cuda.synchronize()
 
+    # eager: the K steps launched one call at a time (reported beside the
+    # timed figure)
     t_start = torch.cuda.Event(enable_timing=True)
     t_stop = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -732,8 +736,28 @@ def main():
         step(i)
     t_stop.record(stream)
     torch.cuda.synchronize()
-    total_ms = t_start.elapsed_time(t_stop)
-    ms_step = total_ms / args.steps
+    ms_step_eager = t_start.elapsed_time(t_stop) / args.steps
+
+    # timed: the K steps captured once into a HIP graph (as a serving loop
+    # runs them, without the host's per-launch cost between kernels),
+    # replayed once untimed, then exactly once between HIP events
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for i in range(args.steps):
+            step(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    graph.replay()
+    t_stop.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t_start.elapsed_time(t_stop) / args.steps
+    del graph
+    # the replayed graph computed what the eager steps did
+    assert torch.equal(qbufs[0], q_ref) and torch.equal(sbufs[0], s_ref)
 
     # per-kernel averages: each kernel alone, back to back, over the same
     # rotating buffers, HIP events on the launch stream around the loop
@@ -784,6 +808,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 5),
+        "timing": "hip_graph",
+        "ms_per_step_eager": round(ms_step_eager, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
